@@ -1,0 +1,198 @@
+/*
+ * staleynet_gemm.h — C ABI of the MI355X (gfx950) GEMM library that stands in
+ * for StaleyNET's `staleynet-cuda` GEMM entry point.
+ *
+ * Every product the reference's model issues goes through one call,
+ *   Gpu::matmul(&self, spec: &MatmulSpec, left: &Tensor, right: &Tensor,
+ *               output: &mut Tensor) -> GpuResult
+ * (reference: crates/staleynet-cuda/src/ops/matmul.rs:144-171), on a `Gpu`
+ * that owns one device context and one stream (crates/staleynet-cuda/src/device.rs:129-208).
+ * This header exports exactly that surface with plain pointers and sizes so a
+ * Rust `-sys` crate (or any C FFI) can bind it; no GPU-runtime or framework
+ * types appear in any signature.
+ *
+ * Semantics kept from the reference:
+ *   output[b] = scale * op(left[b]) * op(right[b])            (overwrite)
+ *   output[b] = output[b] + scale * op(left[b]) * op(right[b]) (accumulate)
+ * op(X) is X or X^T per the operand's storage; element (r, c) of logical
+ * matrix b of an operand with `Transposed` storage lives at
+ * b*batch_stride + c*rows + r, otherwise at b*batch_stride + r*cols + c
+ * (ops/matmul.rs:24-32). The output is always row-major with row stride
+ * `cols` (kernels/matmul.rs:161-163). A batch stride of 0 broadcasts one
+ * matrix. Calls are asynchronous on the context's stream; errors in a kernel
+ * surface at the next synchronising call.
+ *
+ * Status convention: 0 is success; negative values are this library's own
+ * validation errors (SN_ERR_*); positive values are HIP runtime error codes
+ * passed through unchanged. No function aborts the process.
+ *
+ * Threading: a context is not internally locked, like the reference's `Gpu`
+ * (tests share it behind a mutex, tests/kernels_match_reference.rs:14-23).
+ */
+#ifndef STALEYNET_GEMM_H
+#define STALEYNET_GEMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes -------------------------------------------------------- */
+#define SN_OK 0
+/* A required pointer argument was null (a null operand is allowed only when
+ * the spec needs zero elements of it). */
+#define SN_ERR_NULL_ARGUMENT (-1)
+/* "matmul: left operand too small" (ops/matmul.rs:147). */
+#define SN_ERR_LEFT_TOO_SMALL (-2)
+/* "matmul: right operand too small" (ops/matmul.rs:148). */
+#define SN_ERR_RIGHT_TOO_SMALL (-3)
+/* "matmul: output too small" (ops/matmul.rs:149). */
+#define SN_ERR_OUTPUT_TOO_SMALL (-4)
+/* batch_count == 0: the reference's `required_len` underflows
+ * (ops/matmul.rs:139-141) and panics; here it is reported instead. */
+#define SN_ERR_EMPTY_BATCH (-5)
+/* A size or index computation does not fit in 64 bits, or a dimension is too
+ * large for the kernels' 32-bit tile counters. */
+#define SN_ERR_OVERFLOW (-6)
+/* An enum field holds an unknown value, or the combination is not supported
+ * (for example a causal mask on a non-square-compatible product). */
+#define SN_ERR_UNSUPPORTED (-7)
+/* The output overlaps an input. The reference's borrow rules make this
+ * impossible (`&mut Tensor` vs `&Tensor`); a C caller must be told. */
+#define SN_ERR_ALIASING (-8)
+/* No usable GPU at the requested ordinal. */
+#define SN_ERR_NO_DEVICE (-9)
+/* The context's split-K workspace cannot hold the partial sums this product
+ * needs (only possible with a workspace smaller than the default). */
+#define SN_ERR_WORKSPACE (-10)
+
+/* ---- enums (carried as uint32_t in structs) ------------------------------ */
+/* Storage (ops/matmul.rs:15-22). */
+#define SN_ROW_MAJOR 0u
+#define SN_TRANSPOSED 1u
+/* WriteMode and its kernel flag (ops/mod.rs:253-269). */
+#define SN_OVERWRITE 0u
+#define SN_ACCUMULATE 1u
+/* Causal masks: an extension with no reference counterpart; 0 keeps the
+ * reference's dense behaviour. A causal [query, key] matrix has its element
+ * (q, k) visible iff k <= q + query_offset, the rule of the reference's
+ * causal_softmax (kernels/attention.rs:160), with q counted within each
+ * matrix of the batch.
+ *   SN_MASK_CAUSAL_OUTPUT: the output is such a matrix (scores S = Q K^T and
+ *     dP = dO V^T, attention.rs:206-209, 239-242). Masked outputs are not
+ *     computed; they are written as 0 when overwriting and left unchanged
+ *     when accumulating (the product is treated as 0 there).
+ *   SN_MASK_CAUSAL_LEFT: the left operand, as stored, is such a matrix
+ *     (P or dS, attention.rs:212-213, 244-260) and is treated as 0 where
+ *     masked; whole masked tiles of the inner dimension are skipped. With
+ *     Transposed storage op(left) = P^T, so the mask applies to (k, r). */
+#define SN_MASK_NONE 0u
+#define SN_MASK_CAUSAL_OUTPUT 1u
+#define SN_MASK_CAUSAL_LEFT 2u
+/* Per-call precision override; DEFAULT uses the context's kernel choice. */
+#define SN_PRECISION_DEFAULT 0u
+#define SN_PRECISION_F32 1u
+#define SN_PRECISION_BF16 2u
+/* Kernel selection, the role of the reference's MatmulKernel
+ * (device.rs:38-67; public field Gpu::matmul_kernel, device.rs:144):
+ *   SN_KERNEL_MFMA_F32  fp32 matrix-core GEMM (default; the role of Blocked)
+ *   SN_KERNEL_MFMA_BF16 inputs rounded to bf16 (nearest-even), fp32
+ *                       accumulation (the role of TensorCore's TF32)
+ *   SN_KERNEL_SIMPLE    one thread per output, k summed in order with
+ *                       separately rounded products (the role of Naive);
+ *                       a slow cross-check, bit-identical to the reference's
+ *                       CPU loop. */
+#define SN_KERNEL_MFMA_F32 0u
+#define SN_KERNEL_MFMA_BF16 1u
+#define SN_KERNEL_SIMPLE 2u
+
+/* MatmulSpec (ops/matmul.rs:56-82) field for field, plus the extensions
+ * `mask`, `query_offset` and `precision` (zero = reference behaviour).
+ * Fill it with sn_matmul_spec_new() and adjust fields, as the reference's
+ * builders do (MatmulSpec::new + left_transposed/right_transposed/
+ * accumulate/scaled/batched, ops/matmul.rs:84-122). */
+typedef struct sn_matmul_spec {
+    size_t rows;          /* rows of op(left) and of the output */
+    size_t cols;          /* columns of op(right) and of the output */
+    size_t inner;         /* columns of op(left) = rows of op(right) */
+    uint32_t left_storage;  /* SN_ROW_MAJOR or SN_TRANSPOSED */
+    uint32_t right_storage; /* SN_ROW_MAJOR or SN_TRANSPOSED */
+    size_t batch_count;   /* BatchStrides::count */
+    size_t batch_left;    /* elements between consecutive left matrices (0 broadcasts) */
+    size_t batch_right;   /* elements between consecutive right matrices (0 broadcasts) */
+    size_t batch_output;  /* elements between consecutive outputs */
+    float scale;          /* multiplier applied to the product */
+    uint32_t write;       /* SN_OVERWRITE or SN_ACCUMULATE */
+    uint32_t mask;        /* SN_MASK_* (extension) */
+    uint32_t precision;   /* SN_PRECISION_* (extension) */
+    size_t query_offset;  /* positions cached before query 0 (extension, masks only) */
+} sn_matmul_spec;
+
+typedef struct sn_context sn_context;
+
+/* `MatmulSpec::new(rows, cols, inner)`: row-major operands, unbatched
+ * (BatchStrides::SINGLE), overwrite, scale 1 (ops/matmul.rs:86-97). */
+sn_matmul_spec sn_matmul_spec_new(size_t rows, size_t cols, size_t inner);
+
+/* `Gpu::new(ordinal)` (device.rs:148-155): selects the device, creates one
+ * stream and a split-K workspace of the default size (256 MiB; every
+ * product of the reference's model configurations fits in it). */
+int sn_context_create(int ordinal, sn_context **out);
+/* The same with an explicit workspace size in bytes (0 disables split-K). */
+int sn_context_create_with_workspace(int ordinal, size_t workspace_bytes, sn_context **out);
+int sn_context_destroy(sn_context *context);
+/* `Gpu::bind_to_current_thread` (device.rs:157-161): makes the context's
+ * device current on the calling thread. */
+int sn_context_bind(sn_context *context);
+/* `gpu.matmul_kernel = kernel` / read it back (device.rs:144). */
+int sn_context_set_kernel(sn_context *context, uint32_t kernel);
+int sn_context_get_kernel(const sn_context *context, uint32_t *kernel);
+/* The context's stream as an opaque handle (a hipStream_t), for callers
+ * that time work with events on the stream it runs on. */
+void *sn_context_stream(sn_context *context);
+/* `MatmulKernel::tolerance` (device.rs:56-66): the largest relative error,
+ * in the reference test's metric, that the kernel's arithmetic allows
+ * against the reference's f32 product (1e-5 f32, 2e-2 bf16 inputs);
+ * NaN for an unknown kernel. */
+float sn_kernel_tolerance(uint32_t kernel);
+
+/* ---- buffers (device.rs:163-192) ----------------------------------------- */
+/* `Gpu::synchronize`: blocks until all queued work has finished. */
+int sn_synchronize(sn_context *context);
+/* `Gpu::zeros`: a zero-filled device buffer of `count` floats. */
+int sn_alloc_zeroed(sn_context *context, size_t count, float **out);
+/* Releases a buffer from sn_alloc_zeroed / sn_upload. */
+int sn_free(sn_context *context, float *buffer);
+/* `Gpu::upload`: a new device buffer holding `count` host floats. */
+int sn_upload(sn_context *context, const float *host, size_t count, float **out);
+/* `Gpu::download`: copies `count` floats back to the host (synchronising). */
+int sn_download(sn_context *context, const float *device, size_t count, float *host);
+/* `Gpu::copy_from_host`: overwrites an existing buffer (synchronising). */
+int sn_copy_from_host(sn_context *context, float *device, const float *host, size_t count);
+/* `Gpu::fill_zero`: zeroes `count` floats in stream order. */
+int sn_fill_zero(sn_context *context, float *device, size_t count);
+
+/* ---- the GEMM ------------------------------------------------------------ */
+/* The host-side checks of `Gpu::matmul` (ops/matmul.rs:147-149) as a pure
+ * function: returns SN_OK or the SN_ERR_* code the call would return. The
+ * lengths are element counts of the buffers passed for each operand. */
+int sn_matmul_validate(const sn_matmul_spec *spec, size_t left_len, size_t right_len, size_t output_len);
+
+/* `Gpu::matmul` (ops/matmul.rs:146-171): validates, then enqueues the
+ * product on the context's stream and returns without waiting. Nothing is
+ * allocated. A spec with rows or cols of 0 writes nothing; inner = 0 writes
+ * scale*0 (overwrite) or leaves the output (accumulate), as the reference's
+ * loops do. */
+int sn_matmul(sn_context *context, const sn_matmul_spec *spec, const float *left, size_t left_len,
+              const float *right, size_t right_len, float *output, size_t output_len);
+
+/* A short English description of a status code (never null). */
+const char *sn_status_string(int status);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STALEYNET_GEMM_H */

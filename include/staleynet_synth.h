@@ -1,0 +1,31 @@
+/*
+ * staleynet_synth.h — seeded synthetic inputs for benchmarks and tests.
+ *
+ * No counterpart in the reference: its weights are drawn on the host
+ * (crates/staleynet-model/src/random.rs) and its GEMM bench multiplies
+ * zero-filled operands (crates/staleynet-cli/src/commands/bench.rs:131-138).
+ * This generator fills device memory directly so that multi-gigabyte inputs
+ * are resident in HBM before a timed region starts.
+ */
+#ifndef STALEYNET_SYNTH_H
+#define STALEYNET_SYNTH_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Enqueues on `stream` (a hipStream_t, e.g. from sn_context_stream) a fill of
+ * `count` floats at `device` with mean + std * N(0, 1) deviates: SplitMix64
+ * counters + Box-Muller, keyed by (seed, stream_id). Returns 0, -1 for a null
+ * buffer, or a HIP error code. */
+int sn_fill_normal(void *stream, float *device, size_t count, uint64_t seed, uint64_t stream_id, float mean,
+                   float stddev);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STALEYNET_SYNTH_H */

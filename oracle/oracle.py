@@ -1,0 +1,149 @@
+"""ctypes view of the CPU oracle (test infrastructure only).
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline
+leg import this module, and only to check or time against the GPU path; the
+product library never routes through it. The arithmetic lives in
+``oracle/matmul_oracle.c`` and follows the reference's CPU GEMM,
+``crates/staleynet-cuda/src/reference.rs:10-38``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIBRARY_PATH = os.path.join(_HERE, "liboracle.so")
+
+_size = ctypes.c_size_t
+_f32p = ctypes.POINTER(ctypes.c_float)
+_f64p = ctypes.POINTER(ctypes.c_double)
+_u64p = ctypes.POINTER(ctypes.c_uint64)
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Loads ``liboracle.so`` (built by ``make -C oracle``)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIBRARY_PATH):
+            raise FileNotFoundError(f"{LIBRARY_PATH} is missing: run `make -C oracle` (or __graft_entry__.build())")
+        lib = ctypes.CDLL(LIBRARY_PATH)
+        common = [_size, _size, _size, ctypes.c_int, ctypes.c_int]
+        lib.oracle_matmul.argtypes = common + [_size, _size, _size, _size, ctypes.c_float, ctypes.c_int,
+                                               _f32p, _f32p, _f32p]
+        lib.oracle_matmul.restype = None
+        lib.oracle_matmul_rows.argtypes = common + [_size, _size, _size, _size, ctypes.c_float, ctypes.c_int,
+                                                    _f32p, _f32p, _f32p, _size, _size]
+        lib.oracle_matmul_rows.restype = None
+        lib.oracle_matmul_elements.argtypes = common + [_size, _size, ctypes.c_float, ctypes.c_int, _f32p, _f32p,
+                                                        _size, _u64p, _u64p, _u64p, _f32p, _f32p]
+        lib.oracle_matmul_elements.restype = None
+        lib.oracle_matmul_f64.argtypes = common + [_size, _size, ctypes.c_double, ctypes.c_int, _f32p, _f32p,
+                                                   _size, _u64p, _u64p, _u64p, _f32p, _f64p]
+        lib.oracle_matmul_f64.restype = None
+        lib.oracle_random_values.argtypes = [_size, ctypes.c_uint64, _f32p]
+        lib.oracle_random_values.restype = None
+        lib.oracle_relative_error.argtypes = [_f32p, _f32p, _size]
+        lib.oracle_relative_error.restype = ctypes.c_float
+        lib.oracle_causal_softmax.argtypes = [_f32p, _size, _size, _size, ctypes.c_float, _size]
+        lib.oracle_causal_softmax.restype = None
+        lib.oracle_softmax_backward.argtypes = [_f32p, _f32p, _size, _size]
+        lib.oracle_softmax_backward.restype = None
+        _lib = lib
+    return _lib
+
+
+def _f32(array: np.ndarray):
+    assert array.dtype == np.float32 and array.flags["C_CONTIGUOUS"]
+    return array.ctypes.data_as(_f32p)
+
+
+def _u64(array: np.ndarray):
+    assert array.dtype == np.uint64 and array.flags["C_CONTIGUOUS"]
+    return array.ctypes.data_as(_u64p)
+
+
+@dataclass(frozen=True)
+class Product:
+    """The fields of the reference's ``MatmulSpec`` (ops/matmul.rs:58-82) the oracle needs."""
+
+    rows: int
+    cols: int
+    inner: int
+    left_transposed: bool = False
+    right_transposed: bool = False
+    count: int = 1
+    batch_left: int = 0
+    batch_right: int = 0
+    batch_output: int = 0
+    scale: float = 1.0
+    accumulate: bool = False
+
+    def _head(self):
+        return (self.rows, self.cols, self.inner, int(self.left_transposed), int(self.right_transposed))
+
+
+def matmul(p: Product, left: np.ndarray, right: np.ndarray, output: np.ndarray) -> None:
+    """``reference::matmul`` on host arrays; ``output`` is updated in place."""
+    load().oracle_matmul(*p._head(), p.count, p.batch_left, p.batch_right, p.batch_output, p.scale,
+                         int(p.accumulate), _f32(left), _f32(right), _f32(output))
+
+
+def matmul_rows(p: Product, left, right, output, row_begin: int, row_end: int) -> None:
+    """``reference::matmul`` restricted to rows ``[row_begin, row_end)`` of every matrix."""
+    load().oracle_matmul_rows(*p._head(), p.count, p.batch_left, p.batch_right, p.batch_output, p.scale,
+                              int(p.accumulate), _f32(left), _f32(right), _f32(output), row_begin, row_end)
+
+
+def matmul_elements(p: Product, left, right, batch, row, col, previous=None) -> np.ndarray:
+    """Reference-order values at the given (batch, row, col) positions."""
+    batch, row, col = (np.ascontiguousarray(x, dtype=np.uint64) for x in (batch, row, col))
+    n = batch.size
+    prev = np.zeros(n, np.float32) if previous is None else np.ascontiguousarray(previous, np.float32)
+    out = np.empty(n, np.float32)
+    load().oracle_matmul_elements(*p._head(), p.batch_left, p.batch_right, p.scale, int(p.accumulate),
+                                  _f32(left), _f32(right), n, _u64(batch), _u64(row), _u64(col), _f32(prev),
+                                  _f32(out))
+    return out
+
+
+def matmul_elements_f64(p: Product, left, right, batch, row, col, previous=None) -> np.ndarray:
+    """The same positions accumulated in f64 (an error yardstick, not the parity target)."""
+    batch, row, col = (np.ascontiguousarray(x, dtype=np.uint64) for x in (batch, row, col))
+    n = batch.size
+    prev = np.zeros(n, np.float32) if previous is None else np.ascontiguousarray(previous, np.float32)
+    out = np.empty(n, np.float64)
+    load().oracle_matmul_f64(*p._head(), p.batch_left, p.batch_right, float(p.scale), int(p.accumulate),
+                             _f32(left), _f32(right), n, _u64(batch), _u64(row), _u64(col), _f32(prev),
+                             out.ctypes.data_as(_f64p))
+    return out
+
+
+def random_values(count: int, seed: int) -> np.ndarray:
+    """The reference test's LCG values in [-1, 1) (kernels_match_reference.rs:26-38)."""
+    out = np.empty(count, np.float32)
+    load().oracle_random_values(count, seed, _f32(out))
+    return out
+
+
+def relative_error(expected: np.ndarray, actual: np.ndarray) -> float:
+    """The reference test's metric (kernels_match_reference.rs:41-52)."""
+    expected = np.ascontiguousarray(expected, np.float32).ravel()
+    actual = np.ascontiguousarray(actual, np.float32).ravel()
+    assert expected.size == actual.size
+    return float(load().oracle_relative_error(_f32(expected), _f32(actual), expected.size))
+
+
+def causal_softmax(scores: np.ndarray, queries: int, keys: int, scale: float, query_offset: int) -> None:
+    """``reference::causal_softmax`` in place on ``[rows, keys]`` (reference.rs:101-119)."""
+    assert scores.size % keys == 0
+    load().oracle_causal_softmax(_f32(scores), scores.size // keys, queries, keys, scale, query_offset)
+
+
+def softmax_backward(probabilities: np.ndarray, grad: np.ndarray, cols: int) -> None:
+    """``reference::softmax_backward`` in place on ``grad`` (reference.rs:122-137)."""
+    assert probabilities.size == grad.size and grad.size % cols == 0
+    load().oracle_softmax_backward(_f32(probabilities), _f32(grad), grad.size // cols, cols)

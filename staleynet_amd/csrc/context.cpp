@@ -1,0 +1,357 @@
+// The C ABI (include/staleynet_gemm.h): device context, buffers, validation
+// and the GEMM dispatcher. Mirrors the reference's `Gpu` handle
+// (crates/staleynet-cuda/src/device.rs:129-208) and `Gpu::matmul`
+// (crates/staleynet-cuda/src/ops/matmul.rs:144-171).
+#include "staleynet_gemm.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <new>
+
+#include "gemm_internal.h"
+
+struct sn_context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    uint32_t kernel = SN_KERNEL_MFMA_F32;
+    sn::Env env;
+};
+
+namespace {
+
+constexpr size_t kDefaultWorkspaceBytes = size_t(256) << 20;
+// Dimensions above this would overflow the kernels' 32-bit tile counters.
+constexpr size_t kMaxDimension = size_t(1) << 31;
+
+int status(hipError_t err) { return err == hipSuccess ? SN_OK : int(err); }
+
+bool mul_overflows(size_t a, size_t b, size_t* out) { return __builtin_mul_overflow(a, b, out); }
+
+// `(count - 1) * stride + per_matrix` (ops/matmul.rs:139-141), or false on
+// overflow. `count` is at least 1 here.
+bool required_len(size_t count, size_t stride, size_t per_matrix, size_t* out) {
+    size_t span;
+    if (mul_overflows(count - 1, stride, &span)) return false;
+    return !__builtin_add_overflow(span, per_matrix, out);
+}
+
+struct Lengths {
+    size_t left, right, output;
+};
+
+int check_spec(const sn_matmul_spec* spec, Lengths* need) {
+    if (spec == nullptr) return SN_ERR_NULL_ARGUMENT;
+    if (spec->batch_count == 0) return SN_ERR_EMPTY_BATCH;
+    if (spec->left_storage > SN_TRANSPOSED || spec->right_storage > SN_TRANSPOSED) return SN_ERR_UNSUPPORTED;
+    if (spec->write > SN_ACCUMULATE || spec->mask > SN_MASK_CAUSAL_LEFT) return SN_ERR_UNSUPPORTED;
+    if (spec->precision > SN_PRECISION_BF16) return SN_ERR_UNSUPPORTED;
+    if (spec->rows >= kMaxDimension || spec->cols >= kMaxDimension || spec->inner >= kMaxDimension ||
+        spec->batch_count >= kMaxDimension)
+        return SN_ERR_OVERFLOW;
+    if (spec->query_offset >= (size_t(1) << 62)) return SN_ERR_OVERFLOW;
+    size_t left_per, right_per, out_per;
+    if (mul_overflows(spec->rows, spec->inner, &left_per) || mul_overflows(spec->inner, spec->cols, &right_per) ||
+        mul_overflows(spec->rows, spec->cols, &out_per))
+        return SN_ERR_OVERFLOW;
+    if (!required_len(spec->batch_count, spec->batch_left, left_per, &need->left) ||
+        !required_len(spec->batch_count, spec->batch_right, right_per, &need->right) ||
+        !required_len(spec->batch_count, spec->batch_output, out_per, &need->output))
+        return SN_ERR_OVERFLOW;
+    // Byte offsets must stay below 2^63 for the kernels' signed arithmetic.
+    const size_t limit = size_t(1) << 60;
+    if (need->left >= limit || need->right >= limit || need->output >= limit) return SN_ERR_OVERFLOW;
+    return SN_OK;
+}
+
+bool overlaps(const float* a, size_t a_len, const float* b, size_t b_len) {
+    if (a_len == 0 || b_len == 0) return false;
+    const uintptr_t a0 = reinterpret_cast<uintptr_t>(a), b0 = reinterpret_cast<uintptr_t>(b);
+    return a0 < b0 + b_len * sizeof(float) && b0 < a0 + a_len * sizeof(float);
+}
+
+}  // namespace
+
+extern "C" {
+
+sn_matmul_spec sn_matmul_spec_new(size_t rows, size_t cols, size_t inner) {
+    sn_matmul_spec spec;
+    std::memset(&spec, 0, sizeof(spec));
+    spec.rows = rows;
+    spec.cols = cols;
+    spec.inner = inner;
+    spec.left_storage = SN_ROW_MAJOR;
+    spec.right_storage = SN_ROW_MAJOR;
+    spec.batch_count = 1;
+    spec.scale = 1.0f;
+    spec.write = SN_OVERWRITE;
+    spec.mask = SN_MASK_NONE;
+    spec.precision = SN_PRECISION_DEFAULT;
+    return spec;
+}
+
+int sn_context_create_with_workspace(int ordinal, size_t workspace_bytes, sn_context** out) {
+    if (out == nullptr) return SN_ERR_NULL_ARGUMENT;
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || ordinal < 0 || ordinal >= count) return SN_ERR_NO_DEVICE;
+    hipError_t err = hipSetDevice(ordinal);
+    if (err != hipSuccess) return status(err);
+    sn_context* ctx = new (std::nothrow) sn_context();
+    if (ctx == nullptr) return SN_ERR_OVERFLOW;
+    ctx->device = ordinal;
+    hipDeviceProp_t prop;
+    err = hipGetDeviceProperties(&prop, ordinal);
+    if (err == hipSuccess && prop.multiProcessorCount > 0) ctx->env.cu_count = prop.multiProcessorCount;
+    if (err == hipSuccess) err = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    if (err == hipSuccess && workspace_bytes > 0) {
+        void* ws = nullptr;
+        err = hipMalloc(&ws, workspace_bytes);
+        if (err == hipSuccess) {
+            ctx->env.workspace = static_cast<float*>(ws);
+            ctx->env.workspace_bytes = workspace_bytes;
+        }
+    }
+    if (err != hipSuccess) {
+        sn_context_destroy(ctx);
+        return status(err);
+    }
+    *out = ctx;
+    return SN_OK;
+}
+
+int sn_context_create(int ordinal, sn_context** out) {
+    return sn_context_create_with_workspace(ordinal, kDefaultWorkspaceBytes, out);
+}
+
+int sn_context_destroy(sn_context* ctx) {
+    if (ctx == nullptr) return SN_OK;
+    hipError_t first = hipSetDevice(ctx->device);
+    if (ctx->stream != nullptr) {
+        hipError_t err = hipStreamSynchronize(ctx->stream);
+        if (first == hipSuccess) first = err;
+        err = hipStreamDestroy(ctx->stream);
+        if (first == hipSuccess) first = err;
+    }
+    if (ctx->env.workspace != nullptr) {
+        hipError_t err = hipFree(ctx->env.workspace);
+        if (first == hipSuccess) first = err;
+    }
+    delete ctx;
+    return status(first);
+}
+
+int sn_context_bind(sn_context* ctx) {
+    if (ctx == nullptr) return SN_ERR_NULL_ARGUMENT;
+    return status(hipSetDevice(ctx->device));
+}
+
+int sn_context_set_kernel(sn_context* ctx, uint32_t kernel) {
+    if (ctx == nullptr) return SN_ERR_NULL_ARGUMENT;
+    if (kernel > SN_KERNEL_SIMPLE) return SN_ERR_UNSUPPORTED;
+    ctx->kernel = kernel;
+    return SN_OK;
+}
+
+int sn_context_get_kernel(const sn_context* ctx, uint32_t* kernel) {
+    if (ctx == nullptr || kernel == nullptr) return SN_ERR_NULL_ARGUMENT;
+    *kernel = ctx->kernel;
+    return SN_OK;
+}
+
+void* sn_context_stream(sn_context* ctx) { return ctx == nullptr ? nullptr : static_cast<void*>(ctx->stream); }
+
+float sn_kernel_tolerance(uint32_t kernel) {
+    switch (kernel) {
+        case SN_KERNEL_MFMA_F32:
+        case SN_KERNEL_SIMPLE:
+            return 1e-5f;
+        case SN_KERNEL_MFMA_BF16:
+            return 2e-2f;
+        default:
+            return NAN;
+    }
+}
+
+int sn_synchronize(sn_context* ctx) {
+    if (ctx == nullptr) return SN_ERR_NULL_ARGUMENT;
+    hipError_t err = hipSetDevice(ctx->device);
+    if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);
+    return status(err);
+}
+
+int sn_alloc_zeroed(sn_context* ctx, size_t count, float** out) {
+    if (ctx == nullptr || out == nullptr) return SN_ERR_NULL_ARGUMENT;
+    *out = nullptr;
+    size_t bytes;
+    if (mul_overflows(count, sizeof(float), &bytes)) return SN_ERR_OVERFLOW;
+    if (bytes == 0) return SN_OK;
+    hipError_t err = hipSetDevice(ctx->device);
+    void* p = nullptr;
+    if (err == hipSuccess) err = hipMalloc(&p, bytes);
+    if (err == hipSuccess) err = hipMemsetAsync(p, 0, bytes, ctx->stream);
+    if (err != hipSuccess) {
+        if (p != nullptr) (void)hipFree(p);
+        return status(err);
+    }
+    *out = static_cast<float*>(p);
+    return SN_OK;
+}
+
+int sn_free(sn_context* ctx, float* buffer) {
+    if (ctx == nullptr) return SN_ERR_NULL_ARGUMENT;
+    if (buffer == nullptr) return SN_OK;
+    hipError_t err = hipSetDevice(ctx->device);
+    if (err == hipSuccess) err = hipFree(buffer);
+    return status(err);
+}
+
+int sn_upload(sn_context* ctx, const float* host, size_t count, float** out) {
+    if (ctx == nullptr || out == nullptr || (host == nullptr && count > 0)) return SN_ERR_NULL_ARGUMENT;
+    *out = nullptr;
+    size_t bytes;
+    if (mul_overflows(count, sizeof(float), &bytes)) return SN_ERR_OVERFLOW;
+    if (bytes == 0) return SN_OK;
+    hipError_t err = hipSetDevice(ctx->device);
+    void* p = nullptr;
+    if (err == hipSuccess) err = hipMalloc(&p, bytes);
+    if (err == hipSuccess) err = hipMemcpyAsync(p, host, bytes, hipMemcpyHostToDevice, ctx->stream);
+    if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);
+    if (err != hipSuccess) {
+        if (p != nullptr) (void)hipFree(p);
+        return status(err);
+    }
+    *out = static_cast<float*>(p);
+    return SN_OK;
+}
+
+int sn_download(sn_context* ctx, const float* device, size_t count, float* host) {
+    if (ctx == nullptr) return SN_ERR_NULL_ARGUMENT;
+    if (count == 0) return SN_OK;
+    if (device == nullptr || host == nullptr) return SN_ERR_NULL_ARGUMENT;
+    size_t bytes;
+    if (mul_overflows(count, sizeof(float), &bytes)) return SN_ERR_OVERFLOW;
+    hipError_t err = hipSetDevice(ctx->device);
+    if (err == hipSuccess) err = hipMemcpyAsync(host, device, bytes, hipMemcpyDeviceToHost, ctx->stream);
+    if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);
+    return status(err);
+}
+
+int sn_copy_from_host(sn_context* ctx, float* device, const float* host, size_t count) {
+    if (ctx == nullptr) return SN_ERR_NULL_ARGUMENT;
+    if (count == 0) return SN_OK;
+    if (device == nullptr || host == nullptr) return SN_ERR_NULL_ARGUMENT;
+    size_t bytes;
+    if (mul_overflows(count, sizeof(float), &bytes)) return SN_ERR_OVERFLOW;
+    hipError_t err = hipSetDevice(ctx->device);
+    if (err == hipSuccess) err = hipMemcpyAsync(device, host, bytes, hipMemcpyHostToDevice, ctx->stream);
+    if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);
+    return status(err);
+}
+
+int sn_fill_zero(sn_context* ctx, float* device, size_t count) {
+    if (ctx == nullptr) return SN_ERR_NULL_ARGUMENT;
+    if (count == 0) return SN_OK;
+    if (device == nullptr) return SN_ERR_NULL_ARGUMENT;
+    size_t bytes;
+    if (mul_overflows(count, sizeof(float), &bytes)) return SN_ERR_OVERFLOW;
+    hipError_t err = hipSetDevice(ctx->device);
+    if (err == hipSuccess) err = hipMemsetAsync(device, 0, bytes, ctx->stream);
+    return status(err);
+}
+
+int sn_matmul_validate(const sn_matmul_spec* spec, size_t left_len, size_t right_len, size_t output_len) {
+    Lengths need;
+    const int rc = check_spec(spec, &need);
+    if (rc != SN_OK) return rc;
+    if (left_len < need.left) return SN_ERR_LEFT_TOO_SMALL;
+    if (right_len < need.right) return SN_ERR_RIGHT_TOO_SMALL;
+    if (output_len < need.output) return SN_ERR_OUTPUT_TOO_SMALL;
+    return SN_OK;
+}
+
+int sn_matmul(sn_context* ctx, const sn_matmul_spec* spec, const float* left, size_t left_len, const float* right,
+              size_t right_len, float* output, size_t output_len) {
+    if (ctx == nullptr) return SN_ERR_NULL_ARGUMENT;
+    int rc = sn_matmul_validate(spec, left_len, right_len, output_len);
+    if (rc != SN_OK) return rc;
+    Lengths need;
+    check_spec(spec, &need);
+    if ((need.left > 0 && left == nullptr) || (need.right > 0 && right == nullptr) ||
+        (need.output > 0 && output == nullptr))
+        return SN_ERR_NULL_ARGUMENT;
+    if (overlaps(output, need.output, left, need.left) || overlaps(output, need.output, right, need.right))
+        return SN_ERR_ALIASING;
+    if (spec->rows == 0 || spec->cols == 0) return SN_OK;
+
+    sn::Problem p;
+    p.a = left;
+    p.b = right;
+    p.c = output;
+    p.m = int64_t(spec->rows);
+    p.n = int64_t(spec->cols);
+    p.k = int64_t(spec->inner);
+    // Left [rows, inner]: row-major is K-contiguous (ld = inner); transposed
+    // storage keeps it as [inner, rows] (ld = rows). Right [inner, cols]:
+    // row-major is N-contiguous (ld = cols); transposed is [cols, inner],
+    // K-contiguous (ld = inner). See ops/matmul.rs:24-32.
+    p.a_k_contiguous = spec->left_storage == SN_ROW_MAJOR;
+    p.lda = p.a_k_contiguous ? p.k : p.m;
+    p.b_k_contiguous = spec->right_storage == SN_TRANSPOSED;
+    p.ldb = p.b_k_contiguous ? p.k : p.n;
+    p.batch = int64_t(spec->batch_count);
+    p.stride_a = int64_t(spec->batch_left);
+    p.stride_b = int64_t(spec->batch_right);
+    p.stride_c = int64_t(spec->batch_output);
+    p.scale = spec->scale;
+    p.accumulate = spec->write == SN_ACCUMULATE;
+    p.mask = spec->mask;
+    p.query_offset = int64_t(spec->query_offset);
+
+    uint32_t kernel = ctx->kernel;
+    if (spec->precision == SN_PRECISION_F32 && kernel == SN_KERNEL_MFMA_BF16) kernel = SN_KERNEL_MFMA_F32;
+    if (spec->precision == SN_PRECISION_BF16) kernel = SN_KERNEL_MFMA_BF16;
+
+    hipError_t err = hipSetDevice(ctx->device);
+    if (err != hipSuccess) return status(err);
+    if (kernel == SN_KERNEL_SIMPLE) return status(sn::launch_gemm_simple(p, ctx->stream));
+    const bool bf16 = kernel == SN_KERNEL_MFMA_BF16;
+    if (!bf16 && sn::gemv_applies(p)) return status(sn::launch_gemv(p, ctx->env, ctx->stream));
+    if (sn::gemm_workspace_bytes(p, bf16, ctx->env) > ctx->env.workspace_bytes) return SN_ERR_WORKSPACE;
+    return status(bf16 ? sn::launch_gemm_bf16(p, ctx->env, ctx->stream) : sn::launch_gemm_f32(p, ctx->env, ctx->stream));
+}
+
+const char* sn_status_string(int code) {
+    switch (code) {
+        case SN_OK:
+            return "success";
+        case SN_ERR_NULL_ARGUMENT:
+            return "a required pointer argument is null";
+        case SN_ERR_LEFT_TOO_SMALL:
+            return "matmul: left operand too small";
+        case SN_ERR_RIGHT_TOO_SMALL:
+            return "matmul: right operand too small";
+        case SN_ERR_OUTPUT_TOO_SMALL:
+            return "matmul: output too small";
+        case SN_ERR_EMPTY_BATCH:
+            return "matmul: batch count is zero";
+        case SN_ERR_OVERFLOW:
+            return "matmul: a size or offset overflows";
+        case SN_ERR_UNSUPPORTED:
+            return "matmul: unsupported spec field value";
+        case SN_ERR_ALIASING:
+            return "matmul: output overlaps an input";
+        case SN_ERR_NO_DEVICE:
+            return "no GPU at the requested ordinal";
+        case SN_ERR_WORKSPACE:
+            return "matmul: split-K workspace too small";
+        default:
+            break;
+    }
+    if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
+    return "unknown status";
+}
+
+}  // extern "C"

@@ -1,0 +1,50 @@
+// Internal interface between the C-ABI layer (context.cpp) and the kernels.
+// Not installed; the public surface is include/staleynet_gemm.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace sn {
+
+// One (batched) product in the kernels' terms. "K-contiguous" means element
+// (row, k) of the operand is at base[row * ld + k]; otherwise it is at
+// base[k * ld + row]. For the left operand "row" is an output row (M), for
+// the right operand an output column (N).
+struct Problem {
+    const float* a = nullptr;
+    const float* b = nullptr;
+    float* c = nullptr;
+    int64_t m = 0, n = 0, k = 0;
+    bool a_k_contiguous = true;  // left stored row-major
+    bool b_k_contiguous = false; // right stored transposed
+    int64_t lda = 0, ldb = 0;    // stride of the non-contiguous index
+    int64_t batch = 1;
+    int64_t stride_a = 0, stride_b = 0, stride_c = 0;
+    float scale = 1.0f;
+    bool accumulate = false;
+    uint32_t mask = 0;           // SN_MASK_*
+    int64_t query_offset = 0;
+};
+
+// What a launch may use beyond its operands: the context's split-K scratch
+// and the device's compute-unit count (for sizing grids).
+struct Env {
+    float* workspace = nullptr;
+    size_t workspace_bytes = 0;
+    int cu_count = 256;
+};
+
+// Launchers; each returns hipSuccess or the launch error.
+hipError_t launch_gemm_f32(const Problem& p, const Env& env, hipStream_t stream);
+hipError_t launch_gemm_bf16(const Problem& p, const Env& env, hipStream_t stream);
+hipError_t launch_gemm_simple(const Problem& p, hipStream_t stream);
+// Decode-shaped products (few rows, right operand N-contiguous); returns
+// hipErrorNotSupported when the shape is not one it handles.
+hipError_t launch_gemv(const Problem& p, const Env& env, hipStream_t stream);
+bool gemv_applies(const Problem& p);
+
+// Bytes of split-K workspace launch_gemm_* would use for `p` (0 = none).
+size_t gemm_workspace_bytes(const Problem& p, bool bf16, const Env& env);
+
+}  // namespace sn

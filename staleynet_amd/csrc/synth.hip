@@ -1,0 +1,55 @@
+// Seeded synthetic inputs in device memory: element i of stream `stream`
+// under `seed` is a normal deviate mean + std * z, z from the Box-Muller
+// transform of two uniforms drawn by SplitMix64 (Steele, Lea and Flood,
+// "Fast splittable pseudorandom number generators", OOPSLA 2014) at counter
+// positions 2*(i/2) and 2*(i/2)+1. Counter-based, so any element can be
+// produced independently and the same (seed, stream, count) always yields
+// the same bytes. A bench/test utility with no reference counterpart (the
+// reference draws its weights on the host, crates/staleynet-model/src/random.rs).
+#include "staleynet_synth.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+
+namespace {
+
+__host__ __device__ inline uint64_t splitmix64_mix(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+constexpr uint64_t kGamma = 0x9E3779B97F4A7C15ull;
+
+__global__ __launch_bounds__(256) void fill_normal_kernel(float* out, uint64_t count, uint64_t base, float mean,
+                                                          float stddev) {
+    const uint64_t pairs = (count + 1) / 2;
+    for (uint64_t pair = blockIdx.x * uint64_t(blockDim.x) + threadIdx.x; pair < pairs;
+         pair += uint64_t(gridDim.x) * blockDim.x) {
+        const uint64_t z1 = splitmix64_mix(base + (2 * pair + 1) * kGamma);
+        const uint64_t z2 = splitmix64_mix(base + (2 * pair + 2) * kGamma);
+        const float u1 = float((z1 >> 40) + 1) * (1.0f / 16777216.0f);  // (0, 1]
+        const float u2 = float(z2 >> 40) * (1.0f / 16777216.0f);        // [0, 1)
+        const float radius = sqrtf(-2.0f * logf(u1));
+        float s, c;
+        sincosf(6.28318530717958647692f * u2, &s, &c);
+        out[2 * pair] = mean + stddev * (radius * c);
+        if (2 * pair + 1 < count) out[2 * pair + 1] = mean + stddev * (radius * s);
+    }
+}
+
+}  // namespace
+
+extern "C" int sn_fill_normal(void* stream, float* device, size_t count, uint64_t seed, uint64_t stream_id,
+                              float mean, float stddev) {
+    if (count == 0) return 0;
+    if (device == nullptr) return -1;
+    const uint64_t base = splitmix64_mix(seed) ^ splitmix64_mix(stream_id + 0x632BE59BD9B4E019ull);
+    const uint64_t pairs = (count + 1) / 2;
+    const uint64_t grid = std::min<uint64_t>((pairs + 255) / 256, 65536);
+    hipLaunchKernelGGL(fill_normal_kernel, dim3(unsigned(grid)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       device, uint64_t(count), base, mean, stddev);
+    return int(hipGetLastError());
+}

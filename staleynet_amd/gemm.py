@@ -1,0 +1,417 @@
+"""Python view of the gfx950 GEMM library, shaped like the reference's host API.
+
+Mirrors ``staleynet-cuda``'s GEMM surface so that callers and tests read like
+the reference's own:
+
+* ``Storage``, ``BatchStrides``, ``WriteMode`` and ``MatmulSpec`` with its
+  builders (``crates/staleynet-cuda/src/ops/matmul.rs:14-142``,
+  ``ops/mod.rs:251-269``);
+* ``MatmulKernel`` and its ``tolerance`` (``device.rs:38-67``);
+* ``Gpu`` with ``zeros/upload/download/copy_from_host/fill_zero/synchronize``
+  and ``matmul`` (``device.rs:129-208``, ``ops/matmul.rs:144-171``);
+* ``Shape`` and ``Tensor`` (``device.rs:210-275``).
+
+Every call goes through the C ABI in ``include/staleynet_gemm.h``
+(``libstaleynet_gemm.so``, built by ``staleynet_amd/build.py``). There is no
+fallback: if the library is missing, loading raises.
+
+Errors: the reference panics on undersized operands with
+"matmul: left operand too small" etc.; here ``matmul`` raises
+``MatmulPanic`` (an ``AssertionError``) with the same messages. Runtime
+failures raise ``GpuError`` carrying the HIP status.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+import os
+from dataclasses import dataclass, field, replace
+
+import numpy as np
+
+PACKAGE_DIR = os.path.dirname(os.path.abspath(__file__))
+LIBRARY_PATH = os.path.join(PACKAGE_DIR, "libstaleynet_gemm.so")
+
+# Status codes (include/staleynet_gemm.h).
+SN_OK = 0
+SN_ERR_NULL_ARGUMENT = -1
+SN_ERR_LEFT_TOO_SMALL = -2
+SN_ERR_RIGHT_TOO_SMALL = -3
+SN_ERR_OUTPUT_TOO_SMALL = -4
+SN_ERR_EMPTY_BATCH = -5
+SN_ERR_OVERFLOW = -6
+SN_ERR_UNSUPPORTED = -7
+SN_ERR_ALIASING = -8
+SN_ERR_NO_DEVICE = -9
+SN_ERR_WORKSPACE = -10
+
+_VALIDATION_CODES = {SN_ERR_LEFT_TOO_SMALL, SN_ERR_RIGHT_TOO_SMALL, SN_ERR_OUTPUT_TOO_SMALL, SN_ERR_EMPTY_BATCH,
+                     SN_ERR_OVERFLOW, SN_ERR_UNSUPPORTED, SN_ERR_ALIASING, SN_ERR_NULL_ARGUMENT}
+
+
+class Storage(enum.IntEnum):
+    """How an operand is laid out relative to the logical matrix (ops/matmul.rs:15-22)."""
+
+    RowMajor = 0
+    Transposed = 1
+
+
+class WriteMode(enum.IntEnum):
+    """Overwrite or add into the output (ops/mod.rs:253-260); the value is the kernel flag."""
+
+    Overwrite = 0
+    Accumulate = 1
+
+
+class Mask(enum.IntEnum):
+    """Causal masks (an extension; ``None_`` is the reference's dense product)."""
+
+    None_ = 0
+    CausalOutput = 1
+    CausalLeft = 2
+
+
+class Precision(enum.IntEnum):
+    """Per-call precision override (an extension)."""
+
+    Default = 0
+    F32 = 1
+    Bf16 = 2
+
+
+class MatmulKernel(enum.IntEnum):
+    """Which GEMM implementation ``Gpu.matmul`` uses (the role of device.rs:38-54)."""
+
+    MfmaF32 = 0
+    MfmaBf16 = 1
+    Simple = 2
+
+    def tolerance(self) -> float:
+        """Largest relative error the kernel's arithmetic allows (device.rs:56-66)."""
+        return float(_library().sn_kernel_tolerance(int(self)))
+
+
+@dataclass(frozen=True)
+class BatchStrides:
+    """Element offsets between consecutive matrices of a batch (ops/matmul.rs:35-54)."""
+
+    count: int
+    left: int
+    right: int
+    output: int
+
+
+BatchStrides.SINGLE = BatchStrides(count=1, left=0, right=0, output=0)
+
+
+@dataclass(frozen=True)
+class MatmulSpec:
+    """Full description of one (batched) GEMM (ops/matmul.rs:56-142)."""
+
+    rows: int
+    cols: int
+    inner: int
+    left: Storage = Storage.RowMajor
+    right: Storage = Storage.RowMajor
+    batch: BatchStrides = field(default_factory=lambda: BatchStrides.SINGLE)
+    scale: float = 1.0
+    write: WriteMode = WriteMode.Overwrite
+    mask: Mask = Mask.None_
+    query_offset: int = 0
+    precision: Precision = Precision.Default
+
+    @staticmethod
+    def new(rows: int, cols: int, inner: int) -> "MatmulSpec":
+        """``[rows, inner] · [inner, cols]``, row-major, unbatched, overwrite, scale 1."""
+        return MatmulSpec(rows, cols, inner)
+
+    def left_transposed(self) -> "MatmulSpec":
+        return replace(self, left=Storage.Transposed)
+
+    def right_transposed(self) -> "MatmulSpec":
+        return replace(self, right=Storage.Transposed)
+
+    def accumulate(self) -> "MatmulSpec":
+        return replace(self, write=WriteMode.Accumulate)
+
+    def scaled(self, scale: float) -> "MatmulSpec":
+        return replace(self, scale=scale)
+
+    def batched(self, strides: BatchStrides) -> "MatmulSpec":
+        return replace(self, batch=strides)
+
+    def causal_output(self, query_offset: int = 0) -> "MatmulSpec":
+        """Outputs (q, k) with k > q + query_offset are not computed (written 0 / left unchanged)."""
+        return replace(self, mask=Mask.CausalOutput, query_offset=query_offset)
+
+    def causal_left(self, query_offset: int = 0) -> "MatmulSpec":
+        """The stored left [query, key] matrix is 0 where k > q + query_offset."""
+        return replace(self, mask=Mask.CausalLeft, query_offset=query_offset)
+
+    def with_precision(self, precision: Precision) -> "MatmulSpec":
+        return replace(self, precision=precision)
+
+    def required_len(self, stride: int, per_matrix: int) -> int:
+        """Elements an operand of ``per_matrix`` elements must hold (ops/matmul.rs:139-141)."""
+        return (self.batch.count - 1) * stride + per_matrix
+
+    def lengths(self) -> tuple[int, int, int]:
+        """Elements the left, right and output buffers must hold."""
+        return (self.required_len(self.batch.left, self.rows * self.inner),
+                self.required_len(self.batch.right, self.inner * self.cols),
+                self.required_len(self.batch.output, self.rows * self.cols))
+
+    def flops(self) -> int:
+        """Algorithmic floating-point operations, ``2·rows·cols·inner`` per matrix."""
+        return 2 * self.rows * self.cols * self.inner * self.batch.count
+
+    def to_c(self) -> "CMatmulSpec":
+        return CMatmulSpec(self.rows, self.cols, self.inner, int(self.left), int(self.right), self.batch.count,
+                           self.batch.left, self.batch.right, self.batch.output, float(self.scale), int(self.write),
+                           int(self.mask), int(self.precision), self.query_offset)
+
+
+class CMatmulSpec(ctypes.Structure):
+    """``sn_matmul_spec`` (include/staleynet_gemm.h)."""
+
+    _fields_ = [("rows", ctypes.c_size_t), ("cols", ctypes.c_size_t), ("inner", ctypes.c_size_t),
+                ("left_storage", ctypes.c_uint32), ("right_storage", ctypes.c_uint32),
+                ("batch_count", ctypes.c_size_t), ("batch_left", ctypes.c_size_t),
+                ("batch_right", ctypes.c_size_t), ("batch_output", ctypes.c_size_t),
+                ("scale", ctypes.c_float), ("write", ctypes.c_uint32), ("mask", ctypes.c_uint32),
+                ("precision", ctypes.c_uint32), ("query_offset", ctypes.c_size_t)]
+
+
+class GpuError(RuntimeError):
+    """A failed call into the library; ``status`` is the C status code."""
+
+    def __init__(self, status: int, what: str = ""):
+        self.status = status
+        super().__init__(f"{what + ': ' if what else ''}{status_string(status)} (status {status})")
+
+
+class MatmulPanic(AssertionError):
+    """The reference's ``assert!`` panics in ``Gpu::matmul`` (ops/matmul.rs:147-149)."""
+
+    def __init__(self, status: int):
+        self.status = status
+        super().__init__(status_string(status))
+
+
+_lib = None
+_F32P = ctypes.POINTER(ctypes.c_float)
+
+
+def _library() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIBRARY_PATH):
+            raise FileNotFoundError(
+                f"{LIBRARY_PATH} is missing; build it with `python -c 'import __graft_entry__ as g; g.build()'`")
+        lib = ctypes.CDLL(LIBRARY_PATH)
+        ctx = ctypes.c_void_p
+        size = ctypes.c_size_t
+        lib.sn_matmul_spec_new.argtypes = [size, size, size]
+        lib.sn_matmul_spec_new.restype = CMatmulSpec
+        lib.sn_context_create.argtypes = [ctypes.c_int, ctypes.POINTER(ctx)]
+        lib.sn_context_create_with_workspace.argtypes = [ctypes.c_int, size, ctypes.POINTER(ctx)]
+        lib.sn_context_destroy.argtypes = [ctx]
+        lib.sn_context_bind.argtypes = [ctx]
+        lib.sn_context_set_kernel.argtypes = [ctx, ctypes.c_uint32]
+        lib.sn_context_get_kernel.argtypes = [ctx, ctypes.POINTER(ctypes.c_uint32)]
+        lib.sn_context_stream.argtypes = [ctx]
+        lib.sn_context_stream.restype = ctypes.c_void_p
+        lib.sn_kernel_tolerance.argtypes = [ctypes.c_uint32]
+        lib.sn_kernel_tolerance.restype = ctypes.c_float
+        lib.sn_synchronize.argtypes = [ctx]
+        lib.sn_alloc_zeroed.argtypes = [ctx, size, ctypes.POINTER(_F32P)]
+        lib.sn_free.argtypes = [ctx, ctypes.c_void_p]
+        lib.sn_upload.argtypes = [ctx, _F32P, size, ctypes.POINTER(_F32P)]
+        lib.sn_download.argtypes = [ctx, ctypes.c_void_p, size, _F32P]
+        lib.sn_copy_from_host.argtypes = [ctx, ctypes.c_void_p, _F32P, size]
+        lib.sn_fill_zero.argtypes = [ctx, ctypes.c_void_p, size]
+        lib.sn_matmul_validate.argtypes = [ctypes.POINTER(CMatmulSpec), size, size, size]
+        lib.sn_matmul.argtypes = [ctx, ctypes.POINTER(CMatmulSpec), ctypes.c_void_p, size, ctypes.c_void_p, size,
+                                  ctypes.c_void_p, size]
+        lib.sn_status_string.argtypes = [ctypes.c_int]
+        lib.sn_status_string.restype = ctypes.c_char_p
+        lib.sn_fill_normal.argtypes = [ctypes.c_void_p, ctypes.c_void_p, size, ctypes.c_uint64, ctypes.c_uint64,
+                                       ctypes.c_float, ctypes.c_float]
+        for name in ("sn_context_create", "sn_context_create_with_workspace", "sn_context_destroy",
+                     "sn_context_bind", "sn_context_set_kernel", "sn_context_get_kernel", "sn_synchronize",
+                     "sn_alloc_zeroed", "sn_free", "sn_upload", "sn_download", "sn_copy_from_host", "sn_fill_zero",
+                     "sn_matmul_validate", "sn_matmul", "sn_fill_normal"):
+            getattr(lib, name).restype = ctypes.c_int
+        _lib = lib
+    return _lib
+
+
+def library() -> ctypes.CDLL:
+    """The loaded ``libstaleynet_gemm.so`` (raises if it has not been built)."""
+    return _library()
+
+
+def status_string(status: int) -> str:
+    return _library().sn_status_string(int(status)).decode()
+
+
+def validate(spec: MatmulSpec, left_len: int, right_len: int, output_len: int) -> int:
+    """``sn_matmul_validate``: the host checks of ``Gpu::matmul`` as a pure function."""
+    c = spec.to_c()
+    return int(_library().sn_matmul_validate(ctypes.byref(c), left_len, right_len, output_len))
+
+
+@dataclass(frozen=True)
+class Shape:
+    """Rows × columns of a row-major matrix (device.rs:210-243)."""
+
+    rows: int
+    cols: int
+
+    @staticmethod
+    def new(rows: int, cols: int) -> "Shape":
+        return Shape(rows, cols)
+
+    @staticmethod
+    def vector(cols: int) -> "Shape":
+        return Shape(1, cols)
+
+    def __len__(self) -> int:
+        return self.rows * self.cols
+
+
+class Tensor:
+    """A row-major f32 matrix in device memory owned by a ``Gpu`` (device.rs:245-275)."""
+
+    def __init__(self, gpu: "Gpu", pointer: int, shape: Shape):
+        self._gpu = gpu
+        self.pointer = pointer
+        self._shape = shape
+
+    def shape(self) -> Shape:
+        return self._shape
+
+    def __len__(self) -> int:
+        return len(self._shape)
+
+    def reshaped(self, shape: Shape) -> "Tensor":
+        assert len(shape) == len(self._shape), f"reshape {self._shape} -> {shape} changes size"
+        out = Tensor(self._gpu, self.pointer, shape)
+        self.pointer = 0  # ownership moves, as in the reference
+        return out
+
+    def free(self) -> None:
+        if self.pointer and self._gpu._ctx:
+            self._gpu._check(_library().sn_free(self._gpu._ctx, ctypes.c_void_p(self.pointer)), "free")
+        self.pointer = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Gpu:
+    """One device, one stream (``Gpu::new``, device.rs:147-155)."""
+
+    def __init__(self, ordinal: int = 0, workspace_bytes: int | None = None):
+        lib = _library()
+        handle = ctypes.c_void_p()
+        if workspace_bytes is None:
+            rc = lib.sn_context_create(ordinal, ctypes.byref(handle))
+        else:
+            rc = lib.sn_context_create_with_workspace(ordinal, workspace_bytes, ctypes.byref(handle))
+        if rc != SN_OK:
+            raise GpuError(rc, f"Gpu::new({ordinal})")
+        self._ctx = handle
+
+    @staticmethod
+    def new(ordinal: int = 0) -> "Gpu":
+        return Gpu(ordinal)
+
+    def close(self) -> None:
+        if self._ctx:
+            rc = _library().sn_context_destroy(self._ctx)
+            self._ctx = None
+            if rc != SN_OK:
+                raise GpuError(rc, "destroy")
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc: int, what: str) -> None:
+        if rc != SN_OK:
+            raise GpuError(rc, what)
+
+    @property
+    def matmul_kernel(self) -> MatmulKernel:
+        value = ctypes.c_uint32()
+        self._check(_library().sn_context_get_kernel(self._ctx, ctypes.byref(value)), "get kernel")
+        return MatmulKernel(value.value)
+
+    @matmul_kernel.setter
+    def matmul_kernel(self, kernel: MatmulKernel) -> None:
+        self._check(_library().sn_context_set_kernel(self._ctx, int(kernel)), "set kernel")
+
+    @property
+    def stream(self) -> int:
+        """The context's ``hipStream_t`` as an integer handle."""
+        return int(_library().sn_context_stream(self._ctx) or 0)
+
+    def bind_to_current_thread(self) -> None:
+        self._check(_library().sn_context_bind(self._ctx), "bind")
+
+    def synchronize(self) -> None:
+        self._check(_library().sn_synchronize(self._ctx), "synchronize")
+
+    def zeros(self, shape: Shape) -> Tensor:
+        out = _F32P()
+        self._check(_library().sn_alloc_zeroed(self._ctx, len(shape), ctypes.byref(out)), "zeros")
+        return Tensor(self, ctypes.cast(out, ctypes.c_void_p).value or 0, shape)
+
+    def upload(self, shape: Shape, values) -> Tensor:
+        host = np.ascontiguousarray(values, dtype=np.float32).ravel()
+        assert host.size == len(shape), f"upload: {host.size} values for shape {shape}"
+        out = _F32P()
+        self._check(_library().sn_upload(self._ctx, host.ctypes.data_as(_F32P), host.size, ctypes.byref(out)),
+                    "upload")
+        return Tensor(self, ctypes.cast(out, ctypes.c_void_p).value or 0, shape)
+
+    def download(self, tensor: Tensor) -> np.ndarray:
+        host = np.empty(len(tensor), np.float32)
+        self._check(_library().sn_download(self._ctx, ctypes.c_void_p(tensor.pointer), host.size,
+                                           host.ctypes.data_as(_F32P)), "download")
+        return host
+
+    def copy_from_host(self, tensor: Tensor, values) -> None:
+        host = np.ascontiguousarray(values, dtype=np.float32).ravel()
+        assert host.size == len(tensor)
+        self._check(_library().sn_copy_from_host(self._ctx, ctypes.c_void_p(tensor.pointer),
+                                                 host.ctypes.data_as(_F32P), host.size), "copy_from_host")
+
+    def fill_zero(self, tensor: Tensor) -> None:
+        self._check(_library().sn_fill_zero(self._ctx, ctypes.c_void_p(tensor.pointer), len(tensor)), "fill_zero")
+
+    def fill_normal(self, tensor: Tensor, seed: int, stream_id: int, mean: float = 0.0, std: float = 1.0) -> None:
+        """Seeded N(mean, std²) values (include/staleynet_synth.h), enqueued on this context's stream."""
+        rc = _library().sn_fill_normal(ctypes.c_void_p(self.stream), ctypes.c_void_p(tensor.pointer), len(tensor),
+                                       seed, stream_id, mean, std)
+        self._check(rc, "fill_normal")
+
+    def matmul(self, spec: MatmulSpec, left: Tensor, right: Tensor, output: Tensor) -> None:
+        """``Gpu::matmul``: enqueue ``output = scale·op(left)·op(right) (+ output)``."""
+        self.matmul_raw(spec, left.pointer, len(left), right.pointer, len(right), output.pointer, len(output))
+
+    def matmul_raw(self, spec: MatmulSpec, left: int, left_len: int, right: int, right_len: int, output: int,
+                   output_len: int) -> None:
+        """``sn_matmul`` on raw device pointers (for buffers owned elsewhere)."""
+        c = spec.to_c()
+        rc = _library().sn_matmul(self._ctx, ctypes.byref(c), ctypes.c_void_p(left), left_len,
+                                  ctypes.c_void_p(right), right_len, ctypes.c_void_p(output), output_len)
+        if rc in _VALIDATION_CODES:
+            raise MatmulPanic(rc)
+        self._check(rc, "matmul")

@@ -1,0 +1,147 @@
+"""CPU checks of the C-ABI library: it loads, exports every declared entry
+point, and its host-side validation mirrors ``Gpu::matmul``'s asserts
+(crates/staleynet-cuda/src/ops/matmul.rs:147-149) with distinct codes. No
+GPU work is issued here."""
+import ctypes
+import hashlib
+import json
+import os
+import re
+
+import numpy as np
+import pytest
+
+from staleynet_amd import gemm
+from staleynet_amd.gemm import BatchStrides, MatmulSpec, Shape, Storage, WriteMode
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    names = []
+    for header in sorted(os.listdir(os.path.join(ROOT, "include"))):
+        if not header.endswith(".h"):
+            continue
+        text = open(os.path.join(ROOT, "include", header)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names += re.findall(r"\b(sn_[a-z0-9_]+)\s*\(", text)
+    return sorted(set(names))
+
+
+def test_library_exports_every_declared_entry_point():
+    lib = gemm.library()
+    names = declared_functions()
+    assert "sn_matmul" in names and "sn_matmul_validate" in names and len(names) >= 20
+    for name in names:
+        assert hasattr(lib, name), f"{name} is declared in include/ but not exported"
+
+
+def test_spec_new_matches_the_reference_defaults():
+    # MatmulSpec::new (ops/matmul.rs:86-97; test :178-188).
+    spec = gemm.library().sn_matmul_spec_new(2, 3, 4)
+    assert (spec.rows, spec.cols, spec.inner) == (2, 3, 4)
+    assert spec.left_storage == 0 and spec.right_storage == 0
+    assert (spec.batch_count, spec.batch_left, spec.batch_right, spec.batch_output) == (1, 0, 0, 0)
+    assert spec.scale == 1.0 and spec.write == 0 and spec.mask == 0 and spec.precision == 0
+
+
+def test_python_builders_set_the_expected_fields():
+    # ops/matmul.rs:190-207
+    spec = (MatmulSpec.new(2, 3, 4).left_transposed().right_transposed().accumulate().scaled(0.25)
+            .batched(BatchStrides(count=3, left=8, right=12, output=6)))
+    assert spec.left == Storage.Transposed and spec.right == Storage.Transposed
+    assert spec.write == WriteMode.Accumulate and spec.scale == 0.25
+    assert spec.batch == BatchStrides(3, 8, 12, 6)
+    assert BatchStrides.SINGLE == BatchStrides(1, 0, 0, 0)
+
+
+def test_required_len_accounts_for_the_batch_stride():
+    # ops/matmul.rs:209-216
+    spec = MatmulSpec.new(2, 3, 4).batched(BatchStrides(count=3, left=8, right=0, output=6))
+    assert spec.required_len(8, 8) == 24
+    assert spec.required_len(0, 8) == 8
+    assert spec.required_len(6, 6) == 18
+
+
+def test_validate_accepts_exact_lengths_and_reports_each_undersized_operand():
+    spec = MatmulSpec.new(5, 7, 3).batched(BatchStrides(count=2, left=15, right=0, output=35))
+    left, right, out = spec.lengths()
+    assert (left, right, out) == (30, 21, 70)
+    assert gemm.validate(spec, left, right, out) == gemm.SN_OK
+    assert gemm.validate(spec, left - 1, right, out) == gemm.SN_ERR_LEFT_TOO_SMALL
+    assert gemm.validate(spec, left, right - 1, out) == gemm.SN_ERR_RIGHT_TOO_SMALL
+    assert gemm.validate(spec, left, right, out - 1) == gemm.SN_ERR_OUTPUT_TOO_SMALL
+    # The reference asserts left, then right, then output.
+    assert gemm.validate(spec, 0, 0, 0) == gemm.SN_ERR_LEFT_TOO_SMALL
+
+
+def test_validate_reports_empty_batches_overflow_and_unknown_enums():
+    assert gemm.validate(MatmulSpec.new(2, 2, 2).batched(BatchStrides(0, 4, 4, 4)), 99, 99, 99) == \
+        gemm.SN_ERR_EMPTY_BATCH
+    huge = MatmulSpec.new(1 << 30, 1 << 30, 1 << 30)
+    assert gemm.validate(huge, 1 << 62, 1 << 62, 1 << 62) == gemm.SN_ERR_OVERFLOW
+    wrap = MatmulSpec.new(2, 2, 2).batched(BatchStrides(3, 1 << 63, 0, 4))
+    assert gemm.validate(wrap, 1 << 62, 99, 99) == gemm.SN_ERR_OVERFLOW
+    c = MatmulSpec.new(2, 2, 2).to_c()
+    c.left_storage = 2
+    assert gemm.library().sn_matmul_validate(ctypes.byref(c), 4, 4, 4) == gemm.SN_ERR_UNSUPPORTED
+    c = MatmulSpec.new(2, 2, 2).to_c()
+    c.mask = 9
+    assert gemm.library().sn_matmul_validate(ctypes.byref(c), 4, 4, 4) == gemm.SN_ERR_UNSUPPORTED
+
+
+def test_zero_sized_products_validate():
+    assert gemm.validate(MatmulSpec.new(0, 5, 3), 0, 15, 0) == gemm.SN_OK
+    assert gemm.validate(MatmulSpec.new(4, 5, 0), 0, 0, 20) == gemm.SN_OK
+
+
+def test_null_spec_and_null_context_are_errors_not_crashes():
+    lib = gemm.library()
+    assert lib.sn_matmul_validate(None, 0, 0, 0) == gemm.SN_ERR_NULL_ARGUMENT
+    spec = MatmulSpec.new(1, 1, 1).to_c()
+    assert lib.sn_matmul(None, ctypes.byref(spec), None, 1, None, 1, None, 1) == gemm.SN_ERR_NULL_ARGUMENT
+    assert lib.sn_synchronize(None) == gemm.SN_ERR_NULL_ARGUMENT
+    assert lib.sn_context_destroy(None) == gemm.SN_OK
+
+
+def test_status_strings_carry_the_reference_panic_messages():
+    assert gemm.status_string(gemm.SN_ERR_LEFT_TOO_SMALL) == "matmul: left operand too small"
+    assert gemm.status_string(gemm.SN_ERR_RIGHT_TOO_SMALL) == "matmul: right operand too small"
+    assert gemm.status_string(gemm.SN_ERR_OUTPUT_TOO_SMALL) == "matmul: output too small"
+    for code in range(-10, 1):
+        assert gemm.status_string(code)
+
+
+def test_kernel_tolerances_follow_the_reference_convention():
+    assert gemm.MatmulKernel.MfmaF32.tolerance() == pytest.approx(1e-5)
+    assert gemm.MatmulKernel.Simple.tolerance() == pytest.approx(1e-5)
+    assert gemm.MatmulKernel.MfmaBf16.tolerance() == pytest.approx(2e-2)
+
+
+def test_shape_helpers():
+    assert len(Shape.new(3, 4)) == 12 and Shape.vector(5) == Shape(1, 5)
+
+
+def test_oracle_reproduces_the_committed_sweep_vectors():
+    # The same vectors the GPU tests compare against; a change in the oracle build shows here first.
+    from oracle import oracle
+    import sys
+    sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
+    import make_golden
+
+    golden = json.load(open(os.path.join(ROOT, "tests", "golden", "sweep_oracle.json")))["cases"]
+    for record in golden:
+        out = make_golden.oracle_output(record)
+        assert hashlib.sha256(out.astype("<f4").tobytes()).hexdigest() == record["sha256"]
+        assert out[:8].tolist() == record["first"]
+
+
+def test_context_creation_without_a_gpu_fails_cleanly():
+    lib = gemm.library()
+    count = ctypes.c_int(0)
+    hip = ctypes.CDLL("libamdhip64.so")
+    if hip.hipGetDeviceCount(ctypes.byref(count)) == 0 and count.value > 0:
+        pytest.skip("a GPU is present")
+    handle = ctypes.c_void_p()
+    assert lib.sn_context_create(0, ctypes.byref(handle)) == gemm.SN_ERR_NO_DEVICE
+    assert not handle.value

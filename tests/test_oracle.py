@@ -1,0 +1,215 @@
+"""Pins the CPU oracle (oracle/matmul_oracle.c) before anything is checked against it.
+
+Each check is chosen so that a plausible mistake in the restatement of
+``reference::matmul`` (crates/staleynet-cuda/src/reference.rs:19-38) fails:
+the reference's own known-answer tests, an order-sensitive case, exact
+integer arithmetic, transpose/broadcast/scale/accumulate identities and an
+f64 error bound.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from oracle import oracle
+from oracle.oracle import Product
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def kats():
+    with open(os.path.join(GOLDEN, "reference_kats.json")) as f:
+        return json.load(f)
+
+
+def run(product: Product, left, right, output):
+    left = np.asarray(left, np.float32)
+    right = np.asarray(right, np.float32)
+    out = np.asarray(output, np.float32).copy()
+    oracle.matmul(product, left, right, out)
+    return out
+
+
+# ---- the reference's known-answer tests (reference.rs:177-232) -------------
+
+@pytest.mark.parametrize("case", [c["name"] for c in json.load(open(os.path.join(GOLDEN, "reference_kats.json")))["matmul"]])
+def test_reference_known_answers(case):
+    kat = next(c for c in kats()["matmul"] if c["name"] == case)
+    s = kat["spec"]
+    product = Product(s["rows"], s["cols"], s["inner"], s.get("left_transposed", False),
+                      s.get("right_transposed", False), s.get("count", 1), s.get("batch_left", 0),
+                      s.get("batch_right", 0), s.get("batch_output", 0), s.get("scale", 1.0),
+                      s.get("accumulate", False))
+    out = run(product, kat["left"], kat["right"], kat["initial"])
+    assert out.tolist() == kat["expected"]  # exact: every value is an exact small integer/half
+
+
+def test_softmax_known_answers():
+    data = kats()
+    for kat in data["causal_softmax"]:
+        scores = np.asarray(kat["scores"], np.float32)
+        oracle.causal_softmax(scores, kat["queries"], kat["keys"], kat["scale"], kat["query_offset"])
+        for index, value in kat["expected"].items():
+            assert abs(scores[int(index)] - value) <= 1e-6
+        for row in range(scores.size // kat["keys"]):
+            assert abs(scores[row * kat["keys"]:(row + 1) * kat["keys"]].sum() - 1.0) <= 1e-6
+    kat = data["softmax_backward"]
+    grad = np.asarray(kat["grad"], np.float32)
+    oracle.softmax_backward(np.asarray(kat["probabilities"], np.float32), grad, kat["cols"])
+    assert np.allclose(grad, kat["expected"], atol=1e-6, rtol=0)
+
+
+def test_causal_softmax_with_offset_orders_and_masks():
+    # reference.rs:283-293: scale 0.5, offset 1, rows of [1, 2, 3].
+    scores = np.asarray([1, 2, 3, 1, 2, 3], np.float32)
+    oracle.causal_softmax(scores, 2, 3, 0.5, 1)
+    assert scores[0] < scores[1] and scores[2] == 0.0
+    assert scores[3] < scores[4] < scores[5]
+    assert abs(scores[:3].sum() - 1) <= 1e-6 and abs(scores[3:].sum() - 1) <= 1e-6
+
+
+# ---- summation order ---------------------------------------------------------
+
+def test_sum_is_sequential_in_k_with_f32_rounding():
+    # 2^24 + 1 rounds to 2^24 in f32, so summing k in order gives 0, while
+    # the exact value (or any order that adds -2^24 before +1) gives 1.
+    out = run(Product(1, 1, 3), [2.0 ** 24, 1.0, -(2.0 ** 24)], [1.0, 1.0, 1.0], [7.0])
+    assert out[0] == 0.0
+    # Reversing k changes the result: the oracle does not reorder.
+    out = run(Product(1, 1, 3), [-(2.0 ** 24), 1.0, 2.0 ** 24], [1.0, 1.0, 1.0], [7.0])
+    assert out[0] == 1.0
+
+
+def test_products_are_rounded_before_the_sum():
+    # x = 1 + 2^-12: x·x = 1 + 2^-11 + 2^-24 exactly, which rounds (ties to
+    # even) to 1 + 2^-11. Summing [1·c, x·x] with c = -(1 + 2^-11) gives 0 when
+    # the product is rounded first; a fused multiply-add would keep 2^-24.
+    x = np.float32(1 + 2.0 ** -12)
+    c = np.float32(-(1 + 2.0 ** -11))
+    out = run(Product(1, 1, 2), [1.0, x], [c, x], [5.0])
+    assert out[0] == 0.0
+
+
+def test_scaled_sum_is_rounded_before_it_is_added_to_previous():
+    # s = 1 + 2^-23: scale·sum = s·s = 1 + 2^-22 + 2^-46 rounds to 1 + 2^-22,
+    # so prev + scale·sum = 0 for prev = -(1 + 2^-22); fusing would give 2^-46.
+    s = np.float32(1 + 2.0 ** -23)
+    out = run(Product(1, 1, 1, scale=float(s), accumulate=True), [s], [1.0], [-(1 + 2.0 ** -22)])
+    assert out[0] == 0.0
+
+
+# ---- exact integer arithmetic --------------------------------------------------
+
+@pytest.mark.parametrize("left_t", [False, True])
+@pytest.mark.parametrize("right_t", [False, True])
+def test_integer_inputs_match_exact_integer_products(left_t, right_t):
+    rng = np.random.default_rng(7)
+    rows, cols, inner, count = 13, 11, 17, 3
+    a = rng.integers(-8, 9, size=(count, rows, inner))
+    b = rng.integers(-8, 9, size=(count, inner, cols))
+    prev = rng.integers(-50, 51, size=(count, rows, cols))
+    stored_a = np.ascontiguousarray(np.swapaxes(a, 1, 2) if left_t else a).astype(np.float32).ravel()
+    stored_b = np.ascontiguousarray(np.swapaxes(b, 1, 2) if right_t else b).astype(np.float32).ravel()
+    product = Product(rows, cols, inner, left_t, right_t, count, rows * inner, inner * cols, rows * cols, 2.0, True)
+    out = run(product, stored_a, stored_b, prev.astype(np.float32).ravel())
+    expected = prev + 2 * np.einsum("bij,bjk->bik", a, b)
+    assert np.array_equal(out, expected.astype(np.float32).ravel())
+
+
+# ---- identities over random inputs ------------------------------------------
+
+def _random(count, seed):
+    return oracle.random_values(count, seed)
+
+
+def test_transposed_storage_equals_explicit_transpose_bitwise():
+    rows, cols, inner = 9, 14, 23
+    a = _random(rows * inner, 1).reshape(rows, inner)
+    b = _random(inner * cols, 2).reshape(inner, cols)
+    base = run(Product(rows, cols, inner), a.ravel(), b.ravel(), np.zeros(rows * cols))
+    both = run(Product(rows, cols, inner, True, True), np.ascontiguousarray(a.T).ravel(),
+               np.ascontiguousarray(b.T).ravel(), np.zeros(rows * cols))
+    assert np.array_equal(base, both)
+
+
+def test_zero_batch_stride_broadcasts():
+    rows, cols, inner, count = 5, 6, 7, 4
+    a = _random(count * rows * inner, 3)
+    b = _random(inner * cols, 4)
+    out = run(Product(rows, cols, inner, count=count, batch_left=rows * inner, batch_right=0,
+                      batch_output=rows * cols), a, b, np.zeros(count * rows * cols))
+    for i in range(count):
+        single = run(Product(rows, cols, inner), a[i * rows * inner:(i + 1) * rows * inner], b,
+                     np.zeros(rows * cols))
+        assert np.array_equal(out[i * rows * cols:(i + 1) * rows * cols], single)
+
+
+def test_power_of_two_scale_is_exact_and_accumulate_adds_previous():
+    rows, cols, inner = 8, 8, 33
+    a, b, prev = _random(rows * inner, 5), _random(inner * cols, 6), _random(rows * cols, 7)
+    plain = run(Product(rows, cols, inner), a, b, np.zeros(rows * cols))
+    scaled = run(Product(rows, cols, inner, scale=0.25), a, b, np.zeros(rows * cols))
+    assert np.array_equal(scaled, (plain * np.float32(0.25)).astype(np.float32))
+    acc = run(Product(rows, cols, inner, scale=0.7, accumulate=True), a, b, prev)
+    over = run(Product(rows, cols, inner, scale=0.7), a, b, np.zeros(rows * cols))
+    assert np.array_equal(acc, (prev + over).astype(np.float32))
+
+
+def test_error_against_f64_is_within_the_sequential_bound():
+    # |fl(sum) - sum| <= (k-1)·u·Σ|a||b| + k·u·Σ|a||b| for sequential f32 sums, u = 2^-24.
+    rows, cols, inner = 4, 5, 4096
+    a, b = _random(rows * inner, 8), _random(inner * cols, 9)
+    p = Product(rows, cols, inner)
+    out = run(p, a, b, np.zeros(rows * cols))
+    r, c = np.meshgrid(np.arange(rows), np.arange(cols), indexing="ij")
+    truth = oracle.matmul_elements_f64(p, a, b, np.zeros(r.size), r.ravel(), c.ravel())
+    mags = np.abs(a.reshape(rows, inner).astype(np.float64)) @ np.abs(b.reshape(inner, cols).astype(np.float64))
+    bound = 2 * inner * 2.0 ** -24 * mags.ravel()
+    assert np.all(np.abs(out.astype(np.float64) - truth) <= bound)
+    assert np.max(np.abs(out - truth)) > 0  # f32 rounding is visible at this size
+
+
+def test_elements_and_rows_agree_with_the_full_product():
+    rows, cols, inner, count = 7, 9, 31, 2
+    a, b, prev = _random(count * rows * inner, 10), _random(count * inner * cols, 11), _random(count * rows * cols, 12)
+    p = Product(rows, cols, inner, True, False, count, rows * inner, inner * cols, rows * cols, 0.7, True)
+    full = run(p, a, b, prev)
+    part = prev.copy()
+    oracle.matmul_rows(p, a, b, part, 2, 5)
+    rows_mask = np.zeros((count, rows, cols), bool)
+    rows_mask[:, 2:5, :] = True
+    assert np.array_equal(part.reshape(count, rows, cols)[rows_mask], full.reshape(count, rows, cols)[rows_mask])
+    assert np.array_equal(part.reshape(count, rows, cols)[~rows_mask], prev.reshape(count, rows, cols)[~rows_mask])
+    bi, ri, ci = np.meshgrid(np.arange(count), np.arange(rows), np.arange(cols), indexing="ij")
+    got = oracle.matmul_elements(p, a, b, bi.ravel(), ri.ravel(), ci.ravel(), prev)
+    assert np.array_equal(got, full)
+
+
+# ---- the test harness pieces -------------------------------------------------
+
+def test_random_values_follow_knuths_mmix_lcg():
+    # kernels_match_reference.rs:26-38 with Python integers as the arbitrary-precision check.
+    mult, inc, mask = 6364136223846793005, 1442695040888963407, (1 << 64) - 1
+    for seed in (0, 1, 2, 3, 12345):
+        state = (seed * mult + inc) & mask
+        expected = []
+        for _ in range(100):
+            state = (state * mult + inc) & mask
+            expected.append((state >> 40) / 2.0 ** 24 * 2.0 - 1.0)
+        got = oracle.random_values(100, seed)
+        assert got.tolist() == expected  # every step is exact in f32
+    values = oracle.random_values(1 << 16, 1)
+    assert values.min() >= -1.0 and values.max() < 1.0
+    assert abs(values.mean()) < 0.01 and abs(values.var() - 1 / 3) < 0.01
+
+
+def test_relative_error_follows_the_reference_metric():
+    expected = np.asarray([1.0, -4.0, 2.0], np.float32)
+    actual = np.asarray([1.5, -4.0, 1.0], np.float32)
+    assert oracle.relative_error(expected, actual) == pytest.approx(1.0 / 4.0)
+    # The magnitude floor is f32::EPSILON.
+    assert oracle.relative_error(np.zeros(3, np.float32), np.full(3, 1e-7, np.float32)) == pytest.approx(
+        1e-7 / np.finfo(np.float32).eps)
+    # Like Rust's f32::max, a NaN difference is skipped by the fold.
+    assert oracle.relative_error(expected, np.asarray([np.nan, -4.0, 2.0], np.float32)) == 0.0

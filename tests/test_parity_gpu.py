@@ -1,0 +1,226 @@
+"""GPU parity against the CPU oracle, through the C ABI.
+
+The sweep mirrors the reference's own GPU test,
+``matmul_matches_reference_for_every_storage_and_kernel``
+(crates/staleynet-cuda/tests/kernels_match_reference.rs:54-91): ragged sizes
+x batch {1, 3} x {NN, TN, NT, TT}, scale 0.7, accumulate onto LCG values,
+relative error below the kernel's tolerance. The oracle's outputs are also
+checked against the committed vectors (tests/golden/sweep_oracle.json).
+Edge cases the reference leaves implicit are added: empty products,
+undersized/aliased operands, unaligned operands (the scalar-load path),
+split-K, broadcast batches and the causal-mask extension.
+"""
+import hashlib
+import json
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import oracle
+from staleynet_amd.gemm import (BatchStrides, MatmulKernel, MatmulPanic, MatmulSpec, Shape, SN_ERR_ALIASING,
+                                SN_ERR_EMPTY_BATCH, SN_ERR_LEFT_TOO_SMALL, SN_ERR_OUTPUT_TOO_SMALL)
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(HERE, "golden"))
+import make_golden  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+KERNELS = [MatmulKernel.MfmaF32, MatmulKernel.Simple]
+GOLDEN = {(c["rows"], c["cols"], c["inner"], c["batch"], c["variant"]): c
+          for c in json.load(open(os.path.join(HERE, "golden", "sweep_oracle.json")))["cases"]}
+
+
+def to_product(spec: MatmulSpec) -> oracle.Product:
+    return oracle.Product(spec.rows, spec.cols, spec.inner, bool(spec.left), bool(spec.right), spec.batch.count,
+                          spec.batch.left, spec.batch.right, spec.batch.output, spec.scale, bool(spec.write))
+
+
+def run_gpu(gpu, spec, left, right, initial, kernel=MatmulKernel.MfmaF32):
+    gpu.matmul_kernel = kernel
+    try:
+        lt = gpu.upload(Shape.vector(left.size), left)
+        rt = gpu.upload(Shape.vector(right.size), right)
+        out = gpu.upload(Shape.vector(initial.size), initial)
+        gpu.matmul(spec, lt, rt, out)
+        return gpu.download(out)
+    finally:
+        gpu.matmul_kernel = MatmulKernel.MfmaF32
+
+
+def expected_for(spec, left, right, initial):
+    out = initial.copy()
+    oracle.matmul(to_product(spec), left, right, out)
+    return out
+
+
+def check(expected, actual, tolerance, what=""):
+    assert np.all(np.isfinite(actual)), f"{what}: non-finite output"
+    error = oracle.relative_error(expected, actual)
+    assert error < tolerance, f"{what}: relative error {error}"
+    return error
+
+
+@pytest.mark.parametrize("case", list(make_golden.sweep_cases()),
+                         ids=lambda c: f"{c['rows']}x{c['cols']}x{c['inner']}-b{c['batch']}-{c['variant']}")
+def test_matmul_matches_reference_for_every_storage_and_kernel(gpu, case):
+    rows, cols, inner, batch = case["rows"], case["cols"], case["inner"], case["batch"]
+    spec = MatmulSpec.new(rows, cols, inner).batched(
+        BatchStrides(count=batch, left=rows * inner, right=inner * cols, output=rows * cols)).scaled(0.7).accumulate()
+    if case["left_t"]:
+        spec = spec.left_transposed()
+    if case["right_t"]:
+        spec = spec.right_transposed()
+    left = oracle.random_values(batch * rows * inner, 1)
+    right = oracle.random_values(batch * inner * cols, 2)
+    initial = oracle.random_values(batch * rows * cols, 3)
+    expected = expected_for(spec, left, right, initial)
+    golden = GOLDEN[(rows, cols, inner, batch, case["variant"])]
+    assert hashlib.sha256(expected.astype("<f4").tobytes()).hexdigest() == golden["sha256"]
+    for kernel in KERNELS:
+        actual = run_gpu(gpu, spec, left, right, initial, kernel)
+        check(expected, actual, kernel.tolerance(), f"{kernel.name} {spec}")
+        if kernel == MatmulKernel.Simple:
+            # Same order, same separately rounded operations as the reference loop.
+            assert np.array_equal(expected, actual)
+
+
+def test_empty_products_follow_the_reference_loops(gpu):
+    initial = oracle.random_values(20, 3)
+    # rows = 0: nothing is written.
+    out = run_gpu(gpu, MatmulSpec.new(0, 5, 3), np.zeros(1, np.float32), oracle.random_values(15, 2), initial)
+    assert np.array_equal(out, initial)
+    # inner = 0: the sum is 0, so overwrite stores scale*0 and accumulate keeps the previous value.
+    out = run_gpu(gpu, MatmulSpec.new(4, 5, 0).scaled(0.7), np.zeros(1, np.float32), np.zeros(1, np.float32), initial)
+    assert np.array_equal(out, np.zeros(20, np.float32))
+    out = run_gpu(gpu, MatmulSpec.new(4, 5, 0).accumulate(), np.zeros(1, np.float32), np.zeros(1, np.float32),
+                  initial)
+    assert np.array_equal(out, initial)
+
+
+def test_invalid_specs_raise_the_reference_panics(gpu):
+    left = gpu.upload(Shape.vector(6), np.ones(6))
+    right = gpu.upload(Shape.vector(6), np.ones(6))
+    out = gpu.zeros(Shape.vector(4))
+    with pytest.raises(MatmulPanic, match="left operand too small") as info:
+        gpu.matmul(MatmulSpec.new(2, 2, 4), left, right, out)
+    assert info.value.status == SN_ERR_LEFT_TOO_SMALL
+    with pytest.raises(MatmulPanic, match="output too small") as info:
+        gpu.matmul(MatmulSpec.new(3, 2, 2), left, right, out)
+    assert info.value.status == SN_ERR_OUTPUT_TOO_SMALL
+    with pytest.raises(MatmulPanic) as info:
+        gpu.matmul(MatmulSpec.new(2, 2, 2).batched(BatchStrides(0, 4, 4, 4)), left, right, out)
+    assert info.value.status == SN_ERR_EMPTY_BATCH
+    with pytest.raises(MatmulPanic) as info:
+        gpu.matmul(MatmulSpec.new(2, 2, 2), left, right, left)
+    assert info.value.status == SN_ERR_ALIASING
+    gpu.synchronize()
+    assert np.array_equal(gpu.download(out), np.zeros(4, np.float32))
+
+
+@pytest.mark.parametrize("variant", ["NN", "TN", "NT", "TT"])
+def test_unaligned_operands_take_the_scalar_path(gpu, variant):
+    # Operands that start 1 float past an aligned address cannot use 128-bit loads.
+    rows, cols, inner = 96, 80, 68
+    spec = MatmulSpec.new(rows, cols, inner).scaled(1.5)
+    if variant[0] == "T":
+        spec = spec.left_transposed()
+    if variant[1] == "T":
+        spec = spec.right_transposed()
+    left = oracle.random_values(rows * inner + 1, 4)
+    right = oracle.random_values(inner * cols + 1, 5)
+    initial = np.zeros(rows * cols + 1, np.float32)
+    expected = expected_for(spec, left[1:].copy(), right[1:].copy(), initial[1:].copy())
+    lt = gpu.upload(Shape.vector(left.size), left)
+    rt = gpu.upload(Shape.vector(right.size), right)
+    out = gpu.upload(Shape.vector(initial.size), initial)
+    gpu.matmul_raw(spec, lt.pointer + 4, left.size - 1, rt.pointer + 4, right.size - 1, out.pointer + 4,
+                   initial.size - 1)
+    actual = gpu.download(out)
+    assert actual[0] == 0.0
+    check(expected, actual[1:], 1e-5, variant)
+
+
+@pytest.mark.parametrize("variant", ["NN", "TN", "NT"])
+def test_split_k_matches_for_long_inner_dimensions(gpu, variant):
+    # Few output tiles and a long K: the dispatcher splits K and reduces in order.
+    rows, cols, inner = 200, 300, 8192
+    spec = MatmulSpec.new(rows, cols, inner).scaled(0.5).accumulate()
+    if variant[0] == "T":
+        spec = spec.left_transposed()
+    if variant[1] == "T":
+        spec = spec.right_transposed()
+    left = oracle.random_values(rows * inner, 6)
+    right = oracle.random_values(inner * cols, 7)
+    initial = oracle.random_values(rows * cols, 8)
+    expected = expected_for(spec, left, right, initial)
+    check(expected, run_gpu(gpu, spec, left, right, initial), 1e-5, variant)
+
+
+def test_broadcast_batches_and_the_narrow_tile(gpu):
+    # N = 64 uses the 256x64 tile; the right operand is shared by every matrix.
+    rows, cols, inner, count = 300, 64, 200, 3
+    spec = MatmulSpec.new(rows, cols, inner).batched(BatchStrides(count, rows * inner, 0, rows * cols))
+    left = oracle.random_values(count * rows * inner, 9)
+    right = oracle.random_values(inner * cols, 10)
+    initial = np.zeros(count * rows * cols, np.float32)
+    expected = expected_for(spec, left, right, initial)
+    actual = run_gpu(gpu, spec, left, right, initial)
+    check(expected, actual, 1e-5)
+    # Broadcasting the left operand instead.
+    spec = MatmulSpec.new(rows, cols, inner).batched(BatchStrides(count, 0, inner * cols, rows * cols))
+    right = oracle.random_values(count * inner * cols, 11)
+    left = oracle.random_values(rows * inner, 12)
+    check(expected_for(spec, left, right, initial), run_gpu(gpu, spec, left, right, initial), 1e-5)
+
+
+def causal_visible(queries, keys, offset):
+    q = np.arange(queries)[:, None]
+    k = np.arange(keys)[None, :]
+    return k <= q + offset
+
+
+@pytest.mark.parametrize("offset", [0, 37])
+@pytest.mark.parametrize("accumulate", [False, True])
+def test_causal_output_mask(gpu, offset, accumulate):
+    # S = Q·Kᵀ per head (attention.rs:206-209) with masked tiles skipped.
+    t, h, count = 300, 64, 2
+    spec = MatmulSpec.new(t, t, h).right_transposed().batched(BatchStrides(count, t * h, t * h, t * t))
+    if accumulate:
+        spec = spec.accumulate()
+    q = oracle.random_values(count * t * h, 13)
+    k = oracle.random_values(count * t * h, 14)
+    initial = oracle.random_values(count * t * t, 15)
+    dense = expected_for(spec, q, k, initial).reshape(count, t, t)
+    actual = run_gpu(gpu, spec.causal_output(offset), q, k, initial).reshape(count, t, t)
+    visible = np.broadcast_to(causal_visible(t, t, offset), dense.shape)
+    check(dense[visible], actual[visible], 1e-5)
+    masked = actual[~visible]
+    if accumulate:
+        assert np.array_equal(masked, initial.reshape(count, t, t)[~visible])
+    else:
+        assert np.all(masked == 0.0)
+
+
+@pytest.mark.parametrize("offset", [0, 45])
+@pytest.mark.parametrize("transposed", [False, True])
+def test_causal_left_mask(gpu, offset, transposed):
+    # O = P·V (NN) and dV = Pᵀ·dO (TN) with P causal (attention.rs:212-213, 244-247).
+    # The masked part of P holds large garbage that must not reach the result.
+    t, h, count = 280, 64, 2
+    p = oracle.random_values(count * t * t, 16).reshape(count, t, t)
+    visible = causal_visible(t, t, offset)
+    p_clean = np.where(visible, p, 0).astype(np.float32)
+    p_dirty = np.where(visible, p, 1e4).astype(np.float32)
+    v = oracle.random_values(count * t * h, 17)
+    spec = MatmulSpec.new(t, h, t).batched(BatchStrides(count, t * t, t * h, t * h)).scaled(0.125)
+    if transposed:
+        spec = spec.left_transposed()
+    initial = np.zeros(count * t * h, np.float32)
+    expected = expected_for(spec, p_clean.ravel(), v, initial)
+    actual = run_gpu(gpu, spec.causal_left(offset), p_dirty.ravel(), v, initial)
+    check(expected, actual, 1e-5)
+    simple = run_gpu(gpu, spec.causal_left(offset), p_dirty.ravel(), v, initial, MatmulKernel.Simple)
+    check(expected, simple, 1e-6)
