@@ -147,3 +147,36 @@ def softmax_backward(probabilities: np.ndarray, grad: np.ndarray, cols: int) -> 
     """``reference::softmax_backward`` in place on ``grad`` (reference.rs:122-137)."""
     assert probabilities.size == grad.size and grad.size % cols == 0
     load().oracle_softmax_backward(_f32(probabilities), _f32(grad), grad.size // cols, cols)
+
+
+def _workers(workers):
+    return max(1, workers or min(16, os.cpu_count() or 1))
+
+
+def matmul_parallel(p: Product, left, right, output, workers: int | None = None) -> None:
+    """``matmul`` with output rows split across threads (ctypes releases the
+    GIL); every element is computed exactly as in the serial loop."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    n = _workers(workers)
+    bounds = [p.rows * i // n for i in range(n + 1)]
+    with ThreadPoolExecutor(n) as pool:
+        list(pool.map(lambda i: matmul_rows(p, left, right, output, bounds[i], bounds[i + 1]), range(n)))
+
+
+def matmul_elements_parallel(p: Product, left, right, batch, row, col, previous=None, workers=None, f64=False):
+    """``matmul_elements`` (or its f64 twin) with the positions split across threads."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    batch, row, col = (np.ascontiguousarray(x, dtype=np.uint64) for x in (batch, row, col))
+    prev = None if previous is None else np.ascontiguousarray(previous, np.float32)
+    n = _workers(workers)
+    bounds = [batch.size * i // n for i in range(n + 1)]
+    fn = matmul_elements_f64 if f64 else matmul_elements
+
+    def part(i):
+        s = slice(bounds[i], bounds[i + 1])
+        return fn(p, left, right, batch[s], row[s], col[s], None if prev is None else prev[s])
+
+    with ThreadPoolExecutor(n) as pool:
+        return np.concatenate(list(pool.map(part, range(n))))

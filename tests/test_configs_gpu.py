@@ -1,0 +1,220 @@
+"""GPU parity at the BASELINE configurations' shapes, through the C ABI.
+
+Inputs are seeded synthetic data generated in device memory (the same bytes
+are downloaded for the oracle): activations and gradients ~N(0,1), weights
+~N(0,0.02). Each product is the one the reference's model issues:
+``Linear::forward`` (NN), ``Linear::backward`` (TN dW with accumulate, NT dX)
+in crates/staleynet-model/src/layers/linear.rs:43-63, the 16-codebook head
+(gpt.rs:72), the attention products (layers/attention.rs:197-267) and the
+cached decode products (attention.rs:274-320).
+
+Comparison, in the reference test's metric max|Δ|/max|expected|
+(kernels_match_reference.rs:41-52), bound 1e-5 for fp32:
+* config 0 (7.1M, M = 2048): every output of every product;
+* configs 1 and 2 (M = 8192, 32768): 65536 sampled outputs per product,
+  each computed by the oracle in the reference's order; the error against
+  an f64 sum is recorded beside it;
+* config 3 (causal attention, T = 2048, h = 64): every output of every head
+  of a 4-head batch (config 3's per-head shape; its 192 heads repeat it);
+* config 4 (decode, M in {1, 4, 16}): every output.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle
+from staleynet_amd.gemm import BatchStrides, MatmulSpec, Shape
+
+pytestmark = pytest.mark.gpu
+
+TOLERANCE = 1e-5
+SEED = 1234
+SAMPLES = 65536
+MODELS = {
+    "c0": dict(tokens=4 * 512, width=256, ffn=1024),
+    "c1": dict(tokens=8 * 1024, width=512, ffn=2048),
+    "c2": dict(tokens=16 * 2048, width=768, ffn=3072),
+}
+HEAD = 16 * 1024
+
+
+def linears(model):
+    d, f = model["width"], model["ffn"]
+    return {"qkv": (d, 3 * d), "out": (d, d), "up": (d, f), "down": (f, d), "head": (d, HEAD)}
+
+
+def product_of(spec: MatmulSpec) -> oracle.Product:
+    return oracle.Product(spec.rows, spec.cols, spec.inner, bool(spec.left), bool(spec.right), spec.batch.count,
+                          spec.batch.left, spec.batch.right, spec.batch.output, spec.scale, bool(spec.write))
+
+
+def normal(gpu, shape, stream, std=1.0):
+    t = gpu.zeros(shape)
+    gpu.fill_normal(t, SEED, stream, 0.0, std)
+    return t
+
+
+def compare(spec, left, right, previous, actual, full: bool, rng):
+    """Relative error of `actual` against the oracle (all outputs or a sample)."""
+    product = product_of(spec)
+    if full:
+        expected = previous.copy() if spec.write else np.zeros_like(actual)
+        oracle.matmul_parallel(product, left, right, expected)
+        assert np.all(np.isfinite(actual))
+        return oracle.relative_error(expected, actual), None
+    total = spec.batch.count * spec.rows * spec.cols
+    picks = rng.choice(total, size=min(SAMPLES, total), replace=False)
+    b, rest = np.divmod(picks, spec.rows * spec.cols)
+    r, c = np.divmod(rest, spec.cols)
+    flat = b * spec.batch.output + r * spec.cols + c
+    prev = previous[flat] if spec.write else None
+    expected = oracle.matmul_elements_parallel(product, left, right, b, r, c, prev)
+    truth = oracle.matmul_elements_parallel(product, left, right, b, r, c, prev, f64=True)
+    got = actual[flat]
+    assert np.all(np.isfinite(got))
+    f64_error = float(np.max(np.abs(got.astype(np.float64) - truth)) / np.max(np.abs(truth)))
+    return oracle.relative_error(expected, got), f64_error
+
+
+@pytest.mark.parametrize("config,layer", [(c, l) for c in MODELS for l in ("qkv", "out", "up", "down", "head")])
+def test_linear_products_match_the_oracle(gpu, config, layer):
+    model = MODELS[config]
+    m = model["tokens"]
+    inputs, outputs = linears(model)[layer]
+    base = 10 * list(MODELS).index(config) + 3 * ["qkv", "out", "up", "down", "head"].index(layer)
+    x = normal(gpu, Shape(m, inputs), base + 0)
+    w = normal(gpu, Shape(inputs, outputs), base + 1, 0.02)
+    dy = normal(gpu, Shape(m, outputs), base + 2)
+    dw = normal(gpu, Shape(inputs, outputs), base + 3, 0.01)  # a gradient accumulated earlier
+    y, dx = gpu.zeros(Shape(m, outputs)), gpu.zeros(Shape(m, inputs))
+    dw_before = gpu.download(dw)
+
+    forward = MatmulSpec.new(m, outputs, inputs)
+    weight_grad = MatmulSpec.new(inputs, outputs, m).left_transposed().accumulate()
+    input_grad = MatmulSpec.new(m, inputs, outputs).right_transposed()
+    gpu.matmul(forward, x, w, y)
+    gpu.matmul(weight_grad, x, dy, dw)
+    gpu.matmul(input_grad, dy, w, dx)
+    xh, wh, dyh = gpu.download(x), gpu.download(w), gpu.download(dy)
+
+    full = config == "c0"
+    rng = np.random.default_rng(base)
+    results = {}
+    for name, spec, left, right, prev, out in (("NN", forward, xh, wh, None, y),
+                                                ("TN", weight_grad, xh, dyh, dw_before, dw),
+                                                ("NT", input_grad, dyh, wh, None, dx)):
+        error, f64_error = compare(spec, left, right, prev, gpu.download(out), full, rng)
+        results[name] = (error, f64_error)
+        assert error < TOLERANCE, f"{config} {layer} {name}: relative error {error} (f64 {f64_error})"
+    print(f"{config} {layer}: " + ", ".join(f"{k} {e:.2e}" + (f" (f64 {f:.2e})" if f is not None else "")
+                                            for k, (e, f) in results.items()))
+
+
+# ---- config 3: causal attention -------------------------------------------------------------
+
+T, H, HEADS = 2048, 64, 4
+
+
+@pytest.fixture(scope="module")
+def attention(gpu):
+    """Q, K, V, dO ~ N(0,1); P = causal softmax of seeded scores at scale 1/8
+    (reference.rs:101-119); dS = softmax backward of P and a seeded dP
+    (reference.rs:122-137). Row-major [heads·T, ·] as attention.rs:56-95 lays them out."""
+    q = normal(gpu, Shape(HEADS * T, H), 100)
+    k = normal(gpu, Shape(HEADS * T, H), 101)
+    v = normal(gpu, Shape(HEADS * T, H), 102)
+    do = normal(gpu, Shape(HEADS * T, H), 103)
+    scores = normal(gpu, Shape(HEADS * T, T), 104)
+    upstream = normal(gpu, Shape(HEADS * T, T), 105)
+    p = gpu.download(scores)
+    oracle.causal_softmax(p, T, T, 0.125, 0)
+    ds = gpu.download(upstream)
+    oracle.softmax_backward(p, ds, T)
+    host = {"q": gpu.download(q), "k": gpu.download(k), "v": gpu.download(v), "do": gpu.download(do), "p": p,
+            "ds": ds}
+    dev = {"q": q, "k": k, "v": v, "do": do, "p": gpu.upload(Shape(HEADS * T, T), p),
+           "ds": gpu.upload(Shape(HEADS * T, T), ds)}
+    return host, dev
+
+
+def attention_specs():
+    head, score = T * H, T * T
+    per_head = lambda left, right, out: BatchStrides(HEADS, left, right, out)  # noqa: E731
+    s = 0.125
+    # (name, spec, left, right, output kind) following attention.rs:206-260.
+    return [
+        ("scores", MatmulSpec.new(T, T, H).right_transposed().batched(per_head(head, head, score)), "q", "k", "out"),
+        ("mix", MatmulSpec.new(T, H, T).batched(per_head(score, head, head)), "p", "v", "left"),
+        ("prob_grad", MatmulSpec.new(T, T, H).right_transposed().batched(per_head(head, head, score)), "do", "v",
+         "out"),
+        ("value_grad", MatmulSpec.new(T, H, T).left_transposed().batched(per_head(score, head, head)), "p", "do",
+         "left"),
+        ("query_grad", MatmulSpec.new(T, H, T).scaled(s).batched(per_head(score, head, head)), "ds", "k", "left"),
+        ("key_grad", MatmulSpec.new(T, H, T).left_transposed().scaled(s).batched(per_head(score, head, head)), "ds",
+         "q", "left"),
+    ]
+
+
+@pytest.mark.parametrize("masked", [False, True], ids=["dense", "causal"])
+@pytest.mark.parametrize("index", range(6), ids=[a[0] for a in attention_specs()])
+def test_attention_products_match_the_oracle(gpu, attention, index, masked):
+    host, dev = attention
+    name, spec, left, right, kind = attention_specs()[index]
+    if masked:
+        spec = spec.causal_output() if kind == "out" else spec.causal_left()
+    out = gpu.zeros(Shape(HEADS * spec.rows, spec.cols))
+    gpu.matmul(spec, dev[left], dev[right], out)
+    actual = gpu.download(out)
+    expected = np.zeros_like(actual)
+    oracle.matmul_parallel(product_of(spec), host[left], host[right], expected)
+    assert np.all(np.isfinite(actual))
+    if masked and kind == "out":
+        q = np.arange(T)[:, None]
+        visible = np.broadcast_to(np.arange(T)[None, :] <= q, (HEADS, T, T)).ravel()
+        error = oracle.relative_error(expected[visible], actual[visible])
+        assert np.all(actual[~visible] == 0.0)
+    else:
+        error = oracle.relative_error(expected, actual)
+    assert error < TOLERANCE, f"{name} masked={masked}: relative error {error}"
+
+
+# ---- config 4: decode shapes ----------------------------------------------------------------
+
+@pytest.mark.parametrize("rows", [1, 4, 16])
+@pytest.mark.parametrize("inputs,outputs", [(768, 2304), (768, 768), (768, 3072), (3072, 768), (768, HEAD)])
+def test_decode_products_match_the_oracle(gpu, rows, inputs, outputs):
+    x = normal(gpu, Shape(rows, inputs), 200 + rows)
+    w = normal(gpu, Shape(inputs, outputs), 210, 0.02)
+    y = gpu.zeros(Shape(rows, outputs))
+    spec = MatmulSpec.new(rows, outputs, inputs)
+    gpu.matmul(spec, x, w, y)
+    error, _ = compare(spec, gpu.download(x), gpu.download(w), None, gpu.download(y), True, None)
+    assert error < TOLERANCE
+
+
+@pytest.mark.parametrize("cached", [0, 700, 1407])
+def test_cached_decode_attention_matches_the_oracle(gpu, cached):
+    # forward_cached (attention.rs:300-316): one new position against a cache
+    # of capacity 1408 per head; scores masked at query_offset = cached.
+    heads, capacity, n = 12, 1408, 1
+    q = normal(gpu, Shape(heads * n, H), 300)
+    keys = normal(gpu, Shape(heads * capacity, H), 301)
+    values = normal(gpu, Shape(heads * capacity, H), 302)
+    scores_spec = MatmulSpec.new(n, capacity, H).right_transposed().batched(
+        BatchStrides(heads, n * H, capacity * H, n * capacity))
+    scores = gpu.zeros(Shape(heads * n, capacity))
+    gpu.matmul(scores_spec.causal_output(cached), q, keys, scores)
+    s = gpu.download(scores)
+    dense = np.zeros_like(s)
+    qh, kh, vh = gpu.download(q), gpu.download(keys), gpu.download(values)
+    oracle.matmul(product_of(scores_spec), qh, kh, dense)
+    visible = np.broadcast_to(np.arange(capacity)[None, :] <= cached, (heads, capacity)).ravel()
+    assert oracle.relative_error(dense[visible], s[visible]) < TOLERANCE
+    assert np.all(s[~visible] == 0.0)
+    p = s.copy()
+    oracle.causal_softmax(p, n, capacity, 0.125, cached)
+    mix_spec = MatmulSpec.new(n, H, capacity).batched(BatchStrides(heads, n * capacity, capacity * H, n * H))
+    out = gpu.zeros(Shape(heads * n, H))
+    gpu.matmul(mix_spec.causal_left(cached), gpu.upload(Shape(heads * n, capacity), p), values, out)
+    expected = np.zeros(heads * n * H, np.float32)
+    oracle.matmul(product_of(mix_spec), p, vh, expected)
+    assert oracle.relative_error(expected, gpu.download(out)) < TOLERANCE

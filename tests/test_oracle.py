@@ -213,3 +213,16 @@ def test_relative_error_follows_the_reference_metric():
         1e-7 / np.finfo(np.float32).eps)
     # Like Rust's f32::max, a NaN difference is skipped by the fold.
     assert oracle.relative_error(expected, np.asarray([np.nan, -4.0, 2.0], np.float32)) == 0.0
+
+
+def test_parallel_drivers_are_bit_identical_to_the_serial_loop():
+    rows, cols, inner, count = 64, 50, 70, 2
+    p = Product(rows, cols, inner, True, False, count, rows * inner, inner * cols, rows * cols, 0.7, True)
+    a, b, c = _random(count * rows * inner, 1), _random(count * inner * cols, 2), _random(count * rows * cols, 3)
+    serial = run(p, a, b, c)
+    threaded = c.copy()
+    oracle.matmul_parallel(p, a, b, threaded, workers=5)
+    assert np.array_equal(serial, threaded)
+    bi, ri, ci = np.meshgrid(np.arange(count), np.arange(rows), np.arange(cols), indexing="ij")
+    picked = oracle.matmul_elements_parallel(p, a, b, bi.ravel(), ri.ravel(), ci.ravel(), c, workers=7)
+    assert np.array_equal(serial, picked)
