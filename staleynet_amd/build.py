@@ -71,6 +71,27 @@ def build_oracle() -> str:
     return os.path.join(oracle_dir, "liboracle.so")
 
 
+CPP_TESTS = ["kernels_match_reference"]
+
+
+def build_cpp_tests() -> list[str]:
+    """Builds the C++ parity tests (tests/cpp) against the library, the C++
+    host mirror (host/staleynet_cuda.hpp) and the oracle. Run from the tests."""
+    tests_dir = os.path.join(REPO_ROOT, "tests", "cpp")
+    oracle_dir = os.path.join(REPO_ROOT, "oracle")
+    outputs = []
+    for name in CPP_TESTS:
+        out = os.path.join(tests_dir, name)
+        _run(["g++", "-std=c++17", "-O2", "-Wall", "-Wextra", f"-I{INCLUDE}", f"-I{os.path.join(PACKAGE_DIR, 'host')}",
+              os.path.join(tests_dir, name + ".cpp"), "-o", out,
+              f"-L{PACKAGE_DIR}", "-lstaleynet_gemm", f"-L{oracle_dir}", "-loracle",
+              "-L/opt/rocm/lib", "-Wl,-rpath-link,/opt/rocm/lib",
+              "-Wl,-rpath,$ORIGIN/../../staleynet_amd:$ORIGIN/../../oracle"])
+        outputs.append(out)
+    return outputs
+
+
 if __name__ == "__main__":
     print(build())
     print(build_oracle())
+    print(build_cpp_tests())

@@ -21,330 +21,26 @@
 //  * Fragments: within a 16-deep chunk, lane half h feeds k = 8h + s to
 //    MFMA s (s = 0..7), i.e. k-groups 2h and 2h+1: two ds_read_b128 per
 //    32-row fragment. A and B use the same assignment, so products pair.
-//  * Global loads are 128-bit and coalesced along whichever dimension is
-//    contiguous in memory. A K-contiguous operand is read as 8 lanes per row
-//    (128 contiguous bytes); an operand contiguous along M or N (left stored
-//    transposed, right stored row-major) is read as 4x4 blocks, 8 lanes on
-//    8 k-quads of one 4-row group, and transposed in registers on the way
-//    into LDS. One kernel body serves NN, NT, TN and TT.
+//  * Global loads are 128-bit buffer loads, coalesced along whichever
+//    dimension is contiguous in memory (see the loaders in gemm_common.h):
+//    no per-lane branches; out-of-range lanes read 0. One kernel body serves
+//    NN, NT, TN and TT; an operand contiguous along M or N is transposed in
+//    registers on its way into LDS.
 //  * Double-buffered LDS; the next tile is prefetched into registers while
 //    the current one is multiplied: one barrier per BK step.
-//  * Grid: blockIdx.x enumerates output tiles, remapped so each XCD (the
-//    dispatcher deals workgroups round-robin over 8 XCDs, each with its own
-//    L2) receives a contiguous run of whole K splits, each walked as a
+//  * Grid: blockIdx.x enumerates (split, tile) pairs, remapped so each XCD
+//    (the dispatcher deals workgroups round-robin over 8 XCDs, each with its
+//    own L2) receives a contiguous run of whole K splits, each walked as a
 //    grouped raster; y = matrix of the batch. Split-K partial sums go to the
-//    context's workspace
-//    and a second kernel adds them in split order (deterministic).
+//    context's workspace and a second kernel adds them in split order
+//    (deterministic).
 //  * Masks: causal output tiles that are entirely masked are not multiplied;
 //    causal left operands limit each tile's K range to the visible part.
-#include "gemm_internal.h"
-#include "staleynet_gemm.h"
-
-#include <algorithm>
+#include "gemm_common.h"
 
 namespace sn {
+namespace gemm {
 namespace {
-
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-
-constexpr int kXcds = 8;
-constexpr int kGroupM = 8;
-
-// Buffer addressing: a 128-bit descriptor (base, record bound, format) in
-// scalar registers plus a 32-bit per-lane byte offset. Loads at an offset
-// past the bound return 0 and stores there are dropped, so edge tiles and
-// partial K-steps select kOutOfRange instead of branching per lane.
-constexpr int32_t kRecords = 0x7FFFFFFF;
-constexpr int32_t kOutOfRange = int32_t(0x80000000u);
-constexpr int32_t kRawBufferFormat = 0x00020000;  // 32-bit data format, gfx9 family
-// Per-lane offsets stay below this many bytes (checked on the host).
-constexpr int64_t kMaxBufferOffset = (int64_t(1) << 31) - 256;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const float* base) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, kRecords, kRawBufferFormat);
-}
-
-__device__ __forceinline__ f32x4 buffer_load4(__amdgpu_buffer_rsrc_t rsrc, int32_t offset) {
-    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, 0));
-}
-
-__device__ __forceinline__ float buffer_load1(__amdgpu_buffer_rsrc_t rsrc, int32_t offset) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, offset, 0, 0));
-}
-
-__device__ __forceinline__ void buffer_store1(__amdgpu_buffer_rsrc_t rsrc, int32_t offset, float value) {
-    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, value), rsrc, offset, 0, 0);
-}
-
-struct Args {
-    const float* a;
-    const float* b;
-    float* c;
-    float* ws;
-    int64_t m, n, k;
-    int64_t lda, ldb;
-    int64_t stride_a, stride_b, stride_c;
-    int64_t k_per_split;
-    int64_t batch_base;
-    int64_t query_offset;
-    int32_t tiles_m, tiles_n;
-    int32_t splits;
-    int32_t accumulate;
-    int32_t mask;
-    float scale;
-};
-
-template <int BM_, int BN_, int BK_, int WAVES_M_, int WAVES_N_>
-struct Tile {
-    static constexpr int BM = BM_, BN = BN_, BK = BK_;
-    static constexpr int WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
-    static constexpr int THREADS = 64 * WAVES_M * WAVES_N;
-    static constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
-    static constexpr int FM = WTM / 32, FN = WTN / 32;
-    static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile is whole 32x32 blocks");
-    static_assert(BK == 32, "the loaders' lane mappings assume 8 k-groups per tile");
-};
-
-// LDS geometry of one operand tile: BK/4 planes (k-groups) of ROWS + 1
-// slots; slot (g, r) holds k = 4g .. 4g+3 of row r.
-template <int ROWS, int BK>
-struct Planes {
-    static constexpr int PLANE = ROWS + 1;
-    static constexpr int GROUPS = BK / 4;
-    static constexpr int SLOTS = GROUPS * PLANE;
-};
-
-// Operand loaders. Each stages a ROWS x BK tile of one operand per K-step
-// through registers into the LDS layout above. `init` runs once per tile,
-// `load` issues the global reads for the K-step starting at k0 (reading 0
-// outside the matrix), `store` writes the registers to one LDS stage.
-//
-// K-contiguous operands (element (r, k) at base[r * ld + k]): vector v of a
-// thread is row idx / 8, k-group idx % 8 (idx = tid + v * THREADS), so the 8
-// lanes of a row read 128 contiguous bytes and write 8 different k-groups.
-//
-// Row-contiguous operands (element (r, k) at base[k * ld + r]): block v of a
-// thread is k-quad idx % 8 and rows 4 * (idx / 8) .. +3, read as four 16-byte
-// row pieces and written transposed, one slot per row.
-
-// Scalar fallback for operands that are unaligned or too large for 32-bit
-// buffer offsets: one bounds check per element.
-template <int ROWS, int BK, int THREADS>
-struct KContiguousScalarLoader {
-    using P = Planes<ROWS, BK>;
-    static constexpr int TOTAL = ROWS * P::GROUPS;
-    static constexpr int PER_THREAD = (TOTAL + THREADS - 1) / THREADS;
-    f32x4 reg[PER_THREAD];
-
-    __device__ __forceinline__ void init(int64_t, int64_t, int64_t, int) {}
-
-    __device__ __forceinline__ void load(const float* __restrict__ base, int64_t ld, int64_t row0, int64_t rows,
-                                         int64_t k0, int64_t k_total, int tid) {
-#pragma unroll
-        for (int v = 0; v < PER_THREAD; ++v) {
-            const int idx = tid + v * THREADS;
-            const int64_t gr = row0 + idx / P::GROUPS;
-            const int64_t gk = k0 + (idx % P::GROUPS) * 4;
-            f32x4 x = {0.f, 0.f, 0.f, 0.f};
-            if ((TOTAL % THREADS == 0 || idx < TOTAL) && gr < rows) {
-                const float* src = base + gr * ld + gk;
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (gk + e < k_total) x[e] = src[e];
-            }
-            reg[v] = x;
-        }
-    }
-
-    // Zeroes elements (r, k) with k > r + offset (a causal [query, key]
-    // operand stored row-major: r = query, k = key).
-    __device__ __forceinline__ void mask_keys_after_query(int64_t row0, int64_t k0, int64_t offset, int tid) {
-#pragma unroll
-        for (int v = 0; v < PER_THREAD; ++v) {
-            const int idx = tid + v * THREADS;
-            const int64_t gr = row0 + idx / P::GROUPS;
-            const int64_t gk = k0 + (idx % P::GROUPS) * 4;
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (gk + e > gr + offset) reg[v][e] = 0.f;
-        }
-    }
-
-    __device__ __forceinline__ void store(float* lds, int tid) const {
-#pragma unroll
-        for (int v = 0; v < PER_THREAD; ++v) {
-            const int idx = tid + v * THREADS;
-            if (TOTAL % THREADS == 0 || idx < TOTAL) {
-                const int slot = (idx % P::GROUPS) * P::PLANE + idx / P::GROUPS;
-                *reinterpret_cast<f32x4*>(lds + 4 * slot) = reg[v];
-            }
-        }
-    }
-};
-
-// 128-bit buffer loads; needs K % 4 == 0, ld % 4 == 0 and a 16-byte aligned
-// base, so a vector is either wholly inside the matrix or wholly outside.
-template <int ROWS, int BK, int THREADS>
-struct KContiguousBufferLoader : KContiguousScalarLoader<ROWS, BK, THREADS> {
-    using Base = KContiguousScalarLoader<ROWS, BK, THREADS>;
-    using P = typename Base::P;
-    using Base::PER_THREAD;
-    using Base::TOTAL;
-    using Base::reg;
-    int32_t offset[PER_THREAD];  // bytes from the K-step's tile origin; kOutOfRange past the last row
-
-    __device__ __forceinline__ void init(int64_t ld, int64_t row0, int64_t rows, int tid) {
-#pragma unroll
-        for (int v = 0; v < PER_THREAD; ++v) {
-            const int idx = tid + v * THREADS;
-            const int r = idx / P::GROUPS;
-            const bool valid = (TOTAL % THREADS == 0 || idx < TOTAL) && row0 + r < rows;
-            offset[v] = valid ? int32_t((r * ld + (idx % P::GROUPS) * 4) * 4) : kOutOfRange;
-        }
-    }
-
-    __device__ __forceinline__ void load(const float* __restrict__ base, int64_t ld, int64_t row0, int64_t,
-                                         int64_t k0, int64_t k_total, int tid) {
-        const __amdgpu_buffer_rsrc_t rsrc = buffer_of(base + row0 * ld + k0);
-        const bool k_valid = k0 + (tid % P::GROUPS) * 4 < k_total;  // the same k-group for every v
-#pragma unroll
-        for (int v = 0; v < PER_THREAD; ++v) reg[v] = buffer_load4(rsrc, k_valid ? offset[v] : kOutOfRange);
-    }
-};
-
-template <int ROWS, int BK, int THREADS>
-struct RowContiguousScalarLoader {
-    using P = Planes<ROWS, BK>;
-    static constexpr int TOTAL = P::GROUPS * (ROWS / 4);
-    static constexpr int PER_THREAD = (TOTAL + THREADS - 1) / THREADS;
-    static_assert(ROWS % 4 == 0, "tile is whole 4-row groups");
-    f32x4 reg[PER_THREAD][4];  // [v][kk]: rows 4q..4q+3 at k = 4g + kk
-
-    __device__ __forceinline__ void init(int64_t, int64_t, int64_t, int) {}
-
-    __device__ __forceinline__ void load(const float* __restrict__ base, int64_t ld, int64_t row0, int64_t rows,
-                                         int64_t k0, int64_t k_total, int tid) {
-#pragma unroll
-        for (int v = 0; v < PER_THREAD; ++v) {
-            const int idx = tid + v * THREADS;
-            const int64_t gr = row0 + (idx / P::GROUPS) * 4;
-#pragma unroll
-            for (int kk = 0; kk < 4; ++kk) {
-                const int64_t gk = k0 + (idx % P::GROUPS) * 4 + kk;
-                f32x4 x = {0.f, 0.f, 0.f, 0.f};
-                if ((TOTAL % THREADS == 0 || idx < TOTAL) && gk < k_total) {
-                    const float* src = base + gk * ld + gr;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        if (gr + e < rows) x[e] = src[e];
-                }
-                reg[v][kk] = x;
-            }
-        }
-    }
-
-    // Zeroes elements (r, k) with r > k + offset (a causal [query, key]
-    // operand stored row-major and read transposed: r = key, k = query).
-    __device__ __forceinline__ void mask_keys_after_query(int64_t row0, int64_t k0, int64_t offset, int tid) {
-#pragma unroll
-        for (int v = 0; v < PER_THREAD; ++v) {
-            const int idx = tid + v * THREADS;
-            const int64_t gr = row0 + (idx / P::GROUPS) * 4;
-#pragma unroll
-            for (int kk = 0; kk < 4; ++kk) {
-                const int64_t gk = k0 + (idx % P::GROUPS) * 4 + kk;
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (gr + e > gk + offset) reg[v][kk][e] = 0.f;
-            }
-        }
-    }
-
-    __device__ __forceinline__ void store(float* lds, int tid) const {
-#pragma unroll
-        for (int v = 0; v < PER_THREAD; ++v) {
-            const int idx = tid + v * THREADS;
-            if (TOTAL % THREADS == 0 || idx < TOTAL) {
-                const int first = (idx % P::GROUPS) * P::PLANE + (idx / P::GROUPS) * 4;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    f32x4 t = {reg[v][0][e], reg[v][1][e], reg[v][2][e], reg[v][3][e]};
-                    *reinterpret_cast<f32x4*>(lds + 4 * (first + e)) = t;
-                }
-            }
-        }
-    }
-};
-
-// 128-bit buffer loads; needs rows % 4 == 0, ld % 4 == 0 and a 16-byte
-// aligned base.
-template <int ROWS, int BK, int THREADS>
-struct RowContiguousBufferLoader : RowContiguousScalarLoader<ROWS, BK, THREADS> {
-    using Base = RowContiguousScalarLoader<ROWS, BK, THREADS>;
-    using P = typename Base::P;
-    using Base::PER_THREAD;
-    using Base::TOTAL;
-    using Base::reg;
-    int32_t offset[PER_THREAD][4];  // bytes from the K-step's tile origin; kOutOfRange past the last row
-
-    __device__ __forceinline__ void init(int64_t ld, int64_t row0, int64_t rows, int tid) {
-#pragma unroll
-        for (int v = 0; v < PER_THREAD; ++v) {
-            const int idx = tid + v * THREADS;
-            const int r = (idx / P::GROUPS) * 4;
-            const bool valid = (TOTAL % THREADS == 0 || idx < TOTAL) && row0 + r < rows;
-#pragma unroll
-            for (int kk = 0; kk < 4; ++kk)
-                offset[v][kk] = valid ? int32_t((((idx % P::GROUPS) * 4 + kk) * ld + r) * 4) : kOutOfRange;
-        }
-    }
-
-    __device__ __forceinline__ void load(const float* __restrict__ base, int64_t ld, int64_t row0, int64_t,
-                                         int64_t k0, int64_t k_total, int tid) {
-        const __amdgpu_buffer_rsrc_t rsrc = buffer_of(base + k0 * ld + row0);
-        const int64_t k_first = k0 + (tid % P::GROUPS) * 4;  // the same k-quad for every v
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-            const bool k_valid = k_first + kk < k_total;
-#pragma unroll
-            for (int v = 0; v < PER_THREAD; ++v) reg[v][kk] = buffer_load4(rsrc, k_valid ? offset[v][kk] : kOutOfRange);
-        }
-    }
-};
-
-template <bool K_CONTIGUOUS, bool BUFFER, int ROWS, int BK, int THREADS>
-using LoaderFor = typename std::conditional<
-    K_CONTIGUOUS,
-    typename std::conditional<BUFFER, KContiguousBufferLoader<ROWS, BK, THREADS>,
-                              KContiguousScalarLoader<ROWS, BK, THREADS>>::type,
-    typename std::conditional<BUFFER, RowContiguousBufferLoader<ROWS, BK, THREADS>,
-                              RowContiguousScalarLoader<ROWS, BK, THREADS>>::type>::type;
-
-// Block id -> (K split, tile row, tile column). Consecutive workgroup ids
-// land on different XCDs, so ids are first regrouped so that each XCD holds
-// one contiguous range; that range covers whole K splits in turn (the tiles
-// of a split share its slices of A and B) and, within a split, walks a
-// raster grouped kGroupM tile rows high, keeping the A rows and B columns an
-// XCD reuses in its own L2.
-__device__ __forceinline__ void tile_coordinates(int bid, int blocks, int tiles_m, int tiles_n, int& split, int& tm,
-                                                 int& tn) {
-    const int xcd = bid % kXcds;
-    const int local = bid / kXcds;
-    const int q = blocks / kXcds;
-    const int r = blocks % kXcds;
-    const int linear = (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + local;
-    const int tiles = tiles_m * tiles_n;
-    split = linear / tiles;
-    const int id = linear % tiles;
-    const int per_group = kGroupM * tiles_n;
-    const int group = id / per_group;
-    const int first_m = group * kGroupM;
-    const int group_rows = min(tiles_m - first_m, kGroupM);
-    const int within = id % per_group;
-    tm = first_m + within % group_rows;
-    tn = within / group_rows;
-}
 
 template <class T>
 __device__ __forceinline__ void multiply_tile(const float* __restrict__ lds_a, const float* __restrict__ lds_b,
@@ -386,14 +82,6 @@ __device__ __forceinline__ void multiply_tile(const float* __restrict__ lds_a, c
     }
 }
 
-// The reference's combine (kernels/matmul.rs:166-168), the product and the
-// sum rounded separately as the reference rounds them.
-__device__ __forceinline__ void write_output(float* dst, float sum, float scale, bool accumulate) {
-#pragma clang fp contract(off)
-    const float scaled = scale * sum;
-    *dst = accumulate ? *dst + scaled : scaled;
-}
-
 template <class T, bool A_K, bool B_K, bool BUF>
 __global__ __launch_bounds__(T::THREADS) void gemm_f32_kernel(Args args) {
     using PA = Planes<T::BM, T::BK>;
@@ -414,19 +102,12 @@ __global__ __launch_bounds__(T::THREADS) void gemm_f32_kernel(Args args) {
     const int64_t n0 = int64_t(tn) * T::BN;
 
     const int64_t row_last = min(m0 + T::BM, args.m) - 1;
-    const bool output_causal = args.mask == int(SN_MASK_CAUSAL_OUTPUT);
     const bool left_causal = args.mask == int(SN_MASK_CAUSAL_LEFT);
     float* c_batch = args.c + batch * args.stride_c;
 
-    if (output_causal && n0 > row_last + args.query_offset) {
+    if (args.mask == int(SN_MASK_CAUSAL_OUTPUT) && n0 > row_last + args.query_offset) {
         // Every output of this tile is masked: the product is 0 there.
-        if (!args.accumulate) {
-            for (int e = tid; e < T::BM * T::BN; e += T::THREADS) {
-                const int64_t r = m0 + e / T::BN;
-                const int64_t col = n0 + e % T::BN;
-                if (r < args.m && col < args.n) c_batch[r * args.n + col] = 0.f;
-            }
-        }
+        if (!args.accumulate) zero_tile<T>(args, c_batch, m0, n0, tid);
         return;
     }
 
@@ -483,58 +164,9 @@ __global__ __launch_bounds__(T::THREADS) void gemm_f32_kernel(Args args) {
         }
     }
 
-    // Accumulator element r of a 32x32 block holds row 8(r/4) + 4*half + r%4
-    // and column lane%32 of that block.
-    const int col_in_block = lane & 31;
-    const int half = lane >> 5;
-    const bool accumulate = args.accumulate != 0;
     const bool partial = args.splits > 1;
     float* out = partial ? args.ws + ((blockIdx.y * int64_t(args.splits) + split) * args.m) * args.n : c_batch;
-    if constexpr (BUF) {
-        // Offsets from the tile origin; kOutOfRange drops stores outside the matrix.
-        const __amdgpu_buffer_rsrc_t rsrc = buffer_of(out + m0 * args.n + n0);
-#pragma unroll
-        for (int i = 0; i < T::FM; ++i)
-#pragma unroll
-            for (int j = 0; j < T::FN; ++j)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int row = wave_m * T::WTM + 32 * i + 8 * (r / 4) + 4 * half + (r % 4);
-                    const int col = wave_n * T::WTN + 32 * j + col_in_block;
-                    const bool inside = m0 + row < args.m && n0 + col < args.n;
-                    const int32_t offset = inside ? int32_t((row * args.n + col) * 4) : kOutOfRange;
-                    const float sum = acc[i][j][r];
-                    if (partial) {
-                        buffer_store1(rsrc, offset, sum);
-                    } else if (output_causal && n0 + col > m0 + row + args.query_offset) {
-                        if (!accumulate) buffer_store1(rsrc, offset, 0.f);
-                    } else {
-#pragma clang fp contract(off)
-                        const float scaled = args.scale * sum;
-                        buffer_store1(rsrc, offset, accumulate ? buffer_load1(rsrc, offset) + scaled : scaled);
-                    }
-                }
-    } else {
-#pragma unroll
-        for (int i = 0; i < T::FM; ++i)
-#pragma unroll
-            for (int j = 0; j < T::FN; ++j)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int64_t row = m0 + wave_m * T::WTM + 32 * i + 8 * (r / 4) + 4 * half + (r % 4);
-                    const int64_t col = n0 + wave_n * T::WTN + 32 * j + col_in_block;
-                    if (row < args.m && col < args.n) {
-                        float* dst = out + row * args.n + col;
-                        if (partial) {
-                            *dst = acc[i][j][r];
-                        } else if (output_causal && col > row + args.query_offset) {
-                            if (!accumulate) *dst = 0.f;
-                        } else {
-                            write_output(dst, acc[i][j][r], args.scale, accumulate);
-                        }
-                    }
-                }
-    }
+    write_tile<T, BUF>(args, acc, out, m0, n0, wave_m, wave_n, lane, partial);
 }
 
 // Adds the split partial sums of each output in split order, then applies
@@ -556,74 +188,9 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
     }
 }
 
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-
-// Buffer loads take 128 bits at a time, so the contiguous dimension, the
-// leading dimension and the batch stride must be multiples of 4 floats and
-// the base 16-byte aligned; per-lane offsets within one K-step tile must
-// also fit the 31-bit range.
-bool buffer_ok(const float* base, bool k_contiguous, int64_t rows, int64_t k, int64_t ld, int64_t stride,
-               int tile_rows, int bk) {
-    const int64_t contiguous = k_contiguous ? k : rows;
-    const int64_t span = k_contiguous ? (int64_t(tile_rows) * ld + bk) * 4 : (int64_t(bk) * ld + tile_rows) * 4;
-    return aligned16(base) && contiguous % 4 == 0 && ld % 4 == 0 && stride % 4 == 0 && span < kMaxBufferOffset;
-}
-
-struct Plan {
-    int tiles_m, tiles_n;
-    int splits;
-    int64_t k_per_split;
-};
-
-template <class T>
-Plan plan_for(const Problem& p, const Env& env) {
-    Plan plan;
-    plan.tiles_m = int((p.m + T::BM - 1) / T::BM);
-    plan.tiles_n = int((p.n + T::BN - 1) / T::BN);
-    plan.splits = 1;
-    plan.k_per_split = std::max<int64_t>(p.k, 1);
-    const int64_t tiles = int64_t(plan.tiles_m) * plan.tiles_n * p.batch;
-    // Products whose output tiles cannot fill every CU a few times over
-    // (the K = 32768 weight gradients) split K instead, in BK-aligned slices
-    // of at least 8 steps, as far as the workspace allows.
-    const int64_t target = int64_t(env.cu_count) * 3;
-    const int64_t k_steps = (p.k + T::BK - 1) / T::BK;
-    if (p.mask == SN_MASK_NONE && tiles < target && k_steps >= 16 && p.batch == 1) {
-        int64_t splits = std::min<int64_t>((target + tiles - 1) / tiles, k_steps / 8);
-        const int64_t per_split_bytes = p.m * p.n * int64_t(sizeof(float));
-        if (per_split_bytes > 0) splits = std::min<int64_t>(splits, int64_t(env.workspace_bytes) / per_split_bytes);
-        if (splits >= 2) {
-            const int64_t steps_per_split = (k_steps + splits - 1) / splits;
-            plan.k_per_split = steps_per_split * T::BK;
-            plan.splits = int((p.k + plan.k_per_split - 1) / plan.k_per_split);
-        }
-    }
-    return plan;
-}
-
 template <class T, bool A_K, bool B_K, bool BUF>
 hipError_t launch_tiles(const Problem& p, const Env& env, const Plan& plan, hipStream_t stream) {
-    Args args;
-    args.a = p.a;
-    args.b = p.b;
-    args.c = p.c;
-    args.ws = env.workspace;
-    args.m = p.m;
-    args.n = p.n;
-    args.k = p.k;
-    args.lda = p.lda;
-    args.ldb = p.ldb;
-    args.stride_a = p.stride_a;
-    args.stride_b = p.stride_b;
-    args.stride_c = p.stride_c;
-    args.k_per_split = plan.k_per_split;
-    args.query_offset = p.query_offset;
-    args.tiles_m = plan.tiles_m;
-    args.tiles_n = plan.tiles_n;
-    args.splits = plan.splits;
-    args.accumulate = p.accumulate ? 1 : 0;
-    args.mask = int(p.mask);
-    args.scale = p.scale;
+    Args args = make_args<T>(p, env, plan);
     const int64_t tile_count = int64_t(plan.tiles_m) * plan.tiles_n * plan.splits;
     // Work-items per grid dimension must stay below 2^32.
     if (tile_count * T::THREADS >= (int64_t(1) << 32)) return hipErrorInvalidConfiguration;
@@ -631,27 +198,18 @@ hipError_t launch_tiles(const Problem& p, const Env& env, const Plan& plan, hipS
     for (int64_t first = 0; first < p.batch; first += 65535) {
         const int64_t count = std::min<int64_t>(65535, p.batch - first);
         args.batch_base = first;
-        hipLaunchKernelGGL((gemm_f32_kernel<T, A_K, B_K, BUF>), dim3(blocks, unsigned(count)),
-                           dim3(T::THREADS), 0, stream, args);
+        hipLaunchKernelGGL((gemm_f32_kernel<T, A_K, B_K, BUF>), dim3(blocks, unsigned(count)), dim3(T::THREADS), 0,
+                           stream, args);
         hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
     }
-    if (plan.splits > 1) {
-        const int64_t total = p.m * p.n * p.batch;
-        const int64_t grid = std::min<int64_t>((total + 255) / 256, int64_t(env.cu_count) * 16);
-        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(unsigned(grid)), dim3(256), 0, stream, env.workspace, p.c, p.m,
-                           p.n, p.batch, plan.splits, p.stride_c, p.scale, p.accumulate ? 1 : 0);
-        return hipGetLastError();
-    }
+    if (plan.splits > 1) return launch_splitk_reduce(p, env, plan.splits, stream);
     return hipSuccess;
 }
 
 template <class T, bool A_K, bool B_K>
 hipError_t dispatch_path(const Problem& p, const Env& env, const Plan& plan, hipStream_t stream) {
-    const bool buffers = buffer_ok(p.a, A_K, p.m, p.k, p.lda, p.stride_a, T::BM, T::BK) &&
-                         buffer_ok(p.b, B_K, p.n, p.k, p.ldb, p.stride_b, T::BN, T::BK) &&
-                         (int64_t(T::BM) * p.n + T::BN) * 4 < kMaxBufferOffset;
-    if (buffers) return launch_tiles<T, A_K, B_K, true>(p, env, plan, stream);
+    if (buffers_ok<T>(p)) return launch_tiles<T, A_K, B_K, true>(p, env, plan, stream);
     return launch_tiles<T, A_K, B_K, false>(p, env, plan, stream);
 }
 
@@ -671,15 +229,28 @@ bool use_narrow(const Problem& p) { return p.n <= 64; }
 
 }  // namespace
 
-size_t gemm_workspace_bytes(const Problem& p, bool bf16, const Env& env) {
-    (void)bf16;
+hipError_t launch_splitk_reduce(const Problem& p, const Env& env, int splits, hipStream_t stream) {
+    const int64_t total = p.m * p.n * p.batch;
+    const int64_t grid = std::min<int64_t>((total + 255) / 256, int64_t(env.cu_count) * 16);
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(unsigned(grid)), dim3(256), 0, stream, env.workspace, p.c, p.m,
+                       p.n, p.batch, splits, p.stride_c, p.scale, p.accumulate ? 1 : 0);
+    return hipGetLastError();
+}
+
+size_t f32_workspace_bytes(const Problem& p, const Env& env) {
     const Plan plan = use_narrow(p) ? plan_for<TileNarrow>(p, env) : plan_for<TileSquare>(p, env);
     return plan.splits > 1 ? size_t(plan.splits) * size_t(p.m) * size_t(p.n) * sizeof(float) : 0;
 }
 
+}  // namespace gemm
+
 hipError_t launch_gemm_f32(const Problem& p, const Env& env, hipStream_t stream) {
-    if (use_narrow(p)) return dispatch_layout<TileNarrow>(p, env, stream);
-    return dispatch_layout<TileSquare>(p, env, stream);
+    if (gemm::use_narrow(p)) return gemm::dispatch_layout<gemm::TileNarrow>(p, env, stream);
+    return gemm::dispatch_layout<gemm::TileSquare>(p, env, stream);
+}
+
+size_t gemm_workspace_bytes(const Problem& p, bool bf16, const Env& env) {
+    return bf16 ? gemm::bf16_workspace_bytes(p, env) : gemm::f32_workspace_bytes(p, env);
 }
 
 }  // namespace sn

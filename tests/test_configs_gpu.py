@@ -218,3 +218,29 @@ def test_cached_decode_attention_matches_the_oracle(gpu, cached):
     expected = np.zeros(heads * n * H, np.float32)
     oracle.matmul(product_of(mix_spec), p, vh, expected)
     assert oracle.relative_error(expected, gpu.download(out)) < TOLERANCE
+
+
+# ---- bf16-input variant at config 2 ----------------------------------------------------------
+
+@pytest.mark.parametrize("layer", ["qkv", "down"])
+def test_bf16_products_within_the_stated_tolerance(gpu, layer):
+    """bf16 inputs with fp32 accumulation against the fp32 oracle: max relative
+    error below 2e-2 (the variant's stated tolerance)."""
+    from staleynet_amd.gemm import Precision
+    model = MODELS["c2"]
+    m = model["tokens"]
+    inputs, outputs = linears(model)[layer]
+    x = normal(gpu, Shape(m, inputs), 400)
+    w = normal(gpu, Shape(inputs, outputs), 401, 0.02)
+    dy = normal(gpu, Shape(m, outputs), 402)
+    y, dx, dw = gpu.zeros(Shape(m, outputs)), gpu.zeros(Shape(m, inputs)), gpu.zeros(Shape(inputs, outputs))
+    specs = [(MatmulSpec.new(m, outputs, inputs), x, w, y),
+             (MatmulSpec.new(inputs, outputs, m).left_transposed().accumulate(), x, dy, dw),
+             (MatmulSpec.new(m, inputs, outputs).right_transposed(), dy, w, dx)]
+    host = {id(x): gpu.download(x), id(w): gpu.download(w), id(dy): gpu.download(dy)}
+    rng = np.random.default_rng(7)
+    for spec, left, right, out in specs:
+        gpu.matmul(spec.with_precision(Precision.Bf16), left, right, out)
+        error, _ = compare(spec, host[id(left)], host[id(right)], np.zeros(len(out), np.float32),
+                           gpu.download(out), False, rng)
+        assert error < 2e-2, f"bf16 {layer} {spec}: relative error {error}"

@@ -28,7 +28,7 @@ import make_golden  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
-KERNELS = [MatmulKernel.MfmaF32, MatmulKernel.Simple]
+KERNELS = [MatmulKernel.MfmaF32, MatmulKernel.MfmaBf16, MatmulKernel.Simple]
 GOLDEN = {(c["rows"], c["cols"], c["inner"], c["batch"], c["variant"]): c
           for c in json.load(open(os.path.join(HERE, "golden", "sweep_oracle.json")))["cases"]}
 
@@ -224,3 +224,52 @@ def test_causal_left_mask(gpu, offset, transposed):
     check(expected, actual, 1e-5)
     simple = run_gpu(gpu, spec.causal_left(offset), p_dirty.ravel(), v, initial, MatmulKernel.Simple)
     check(expected, simple, 1e-6)
+
+
+# ---- bf16-input variant ---------------------------------------------------------
+
+@pytest.mark.parametrize("variant", ["NN", "TN", "NT", "TT"])
+def test_bf16_is_exact_on_bf16_representable_integers(gpu, variant):
+    # Integers of magnitude <= 16 are exact in bf16, their products are exact,
+    # and every partial sum stays below 2^24, so any summation order gives the
+    # exact result: a wrong lane layout or a wrong k pairing cannot hide.
+    rows, cols, inner = 96, 160, 200
+    rng = np.random.default_rng(11)
+    left = rng.integers(-16, 17, size=rows * inner).astype(np.float32)
+    right = rng.integers(-16, 17, size=inner * cols).astype(np.float32)
+    spec = MatmulSpec.new(rows, cols, inner)
+    if variant[0] == "T":
+        spec = spec.left_transposed()
+    if variant[1] == "T":
+        spec = spec.right_transposed()
+    initial = np.zeros(rows * cols, np.float32)
+    expected = expected_for(spec, left, right, initial)
+    actual = run_gpu(gpu, spec, left, right, initial, MatmulKernel.MfmaBf16)
+    assert np.array_equal(expected, actual)
+
+
+def test_bf16_inputs_round_to_nearest_even(gpu):
+    # A times the identity returns A rounded to bf16 (7 stored mantissa bits).
+    # Expected values follow from IEEE roundTiesToEven by hand:
+    u = 2.0 ** -7  # bf16 ulp in [1, 2)
+    cases = [
+        (1.0, 1.0),
+        (1 + 2.0 ** -8, 1.0),                      # halfway, 1.0 is even
+        (1 + 3 * 2.0 ** -8, 1 + 2 * u),            # halfway between 1+u (odd) and 1+2u (even)
+        (1 + 2.0 ** -8 + 2.0 ** -20, 1 + u),       # just above halfway
+        (1 + 2.0 ** -8 - 2.0 ** -20, 1.0),         # just below halfway
+        (-(1 + 3 * 2.0 ** -8), -(1 + 2 * u)),
+        (3.0, 3.0),
+        (1.0 / 3.0, 0.333984375),                  # 0x3EAB: 0.01010101 01010101... rounds up
+        (float(np.finfo(np.float32).max), float("inf")),
+        (2.0 ** -100 * 1.5, 2.0 ** -100 * 1.5),    # exact, small exponent
+        (0.0, 0.0),
+    ]
+    k = 16
+    a = np.zeros((len(cases), k), np.float32)
+    a[:, 0] = [c[0] for c in cases]
+    eye = np.eye(k, dtype=np.float32)
+    spec = MatmulSpec.new(len(cases), k, k)
+    out = run_gpu(gpu, spec, a.ravel(), eye.ravel(), np.zeros(len(cases) * k, np.float32), MatmulKernel.MfmaBf16)
+    got = out.reshape(len(cases), k)[:, 0]
+    assert got.tolist() == [np.float32(c[1]) for c in cases]
