@@ -1,21 +1,27 @@
 """Benchmark of the GEMM hot path on one MI355X.
 
-Workload (BASELINE.json metric, config 2): the 111.5M model's training GEMM
-set, exactly as the reference's model issues it through ``Gpu::matmul``:
-12 blocks x {QKV 768->2304, out-proj 768->768, FFN up 768->3072, FFN down
-3072->768}, each as forward NN (``Linear::forward``, linear.rs:43-48),
-input-gradient NT and weight-gradient TN with accumulate
-(``Linear::backward``, linear.rs:51-63), plus the 16-codebook head
-768->16384 (gpt.rs:72) in the same three forms; M = 16 x 2048 = 32768
-tokens. 19.173 TFLOP of algorithmic work per step. Inputs are seeded
-synthetic data resident in HBM before timing (activations and gradients
-~N(0,1), weights ~N(0,0.02)).
+Headline workload (BASELINE.json metric, config 2): the 111.5M model's
+training GEMM set, exactly as the reference's model issues it through
+``Gpu::matmul``:
+- 12 blocks x {QKV 768->2304, out-proj 768->768, FFN up 768->3072, FFN down 3072->768};
+- plus the 16-codebook head 768->16384 (gpt.rs:72);
+- each as forward NN (``Linear::forward``, linear.rs:43-48), input-gradient NT and
+  weight-gradient TN with accumulate (``Linear::backward``, linear.rs:51-63);
+- M = 16 x 2048 = 32768 tokens: 147 products, 19.173 TFLOP of algorithmic work per step.
 
-A "step" is one pass over that set. The line printed is the driver's JSON
-contract plus ``roofline`` (the forward NN kernel, timed per launch with HIP
-events on the library's stream) and ``cpu_baseline`` (the reference's CPU
-matmul restated bit-for-bit in oracle/, on one host core, over a bounded
-row sample of every GEMM of the set, scaled to the full set).
+Inputs are seeded synthetic data resident in HBM before timing (activations and
+gradients ~N(0,1), weights ~N(0,0.02)). A "step" is one pass over that set, timed
+with HIP events on the library's stream.
+
+The printed JSON line is the driver's contract plus:
+- ``roofline``: the forward-NN kernel, timed per launch with HIP events;
+- ``cpu_baseline``: the reference's CPU matmul restated bit-for-bit in oracle/, on one
+  host core, over a bounded row sample of every GEMM of the set, scaled to the full set;
+- ``bf16``: the same set with bf16-rounded inputs and fp32 accumulation;
+- ``attention``: config 3's six causal attention products, 192 heads x T = 2048 x h = 64;
+- ``decode``: config 4's M in {1, 4, 16} products against the 111.5M weights, replayed
+  from a HIP graph over a weight pool larger than the 256 MB Infinity Cache, and one
+  decode token's 49 products in sequence.
 """
 from __future__ import annotations
 
@@ -31,13 +37,14 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-from staleynet_amd.gemm import BatchStrides, Gpu, MatmulSpec, Shape  # noqa: E402
+from staleynet_amd.gemm import BatchStrides, Gpu, MatmulSpec, Precision, Shape  # noqa: E402
 
 # MI355X published peaks (dense): fp32 matrix 157.3 TFLOP/s, bf16 2.5 PFLOP/s, HBM 8 TB/s.
 PEAK_FP32_TFLOPS = 157.3
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
 SEED = 1234
+METRIC = "GEMM TFLOP/s and % fp32 MFMA peak (111.5M train set); decode GEMV GB/s, 1 GPU"
 
 
 class HipEvents:
@@ -68,7 +75,50 @@ class HipEvents:
         self.hip.hipEventDestroy(event)
 
 
-# ---- the workload ---------------------------------------------------------------
+class HipGraph:
+    """Stream capture of a sequence of library calls into a HIP graph, so a
+    launch-bound sequence (decode GEMVs) replays without per-call host cost.
+    The library issues no memset or allocation inside sn_matmul, so every
+    captured node is a kernel."""
+
+    CAPTURE_RELAXED = 2
+
+    def __init__(self, stream: int, record):
+        hip = ctypes.CDLL("libamdhip64.so")
+        self.hip, self.stream = hip, ctypes.c_void_p(stream)
+        graph = ctypes.c_void_p()
+        assert hip.hipStreamBeginCapture(self.stream, self.CAPTURE_RELAXED) == 0
+        try:
+            record()
+        finally:
+            assert hip.hipStreamEndCapture(self.stream, ctypes.byref(graph)) == 0
+        self.graph = graph
+        self.exec = ctypes.c_void_p()
+        assert hip.hipGraphInstantiate(ctypes.byref(self.exec), graph, None, None, 0) == 0
+
+    def launch(self) -> None:
+        assert self.hip.hipGraphLaunch(self.exec, self.stream) == 0
+
+    def close(self) -> None:
+        self.hip.hipGraphExecDestroy(self.exec)
+        self.hip.hipGraphDestroy(self.graph)
+
+
+def timed(events: HipEvents, stream: int, body, repeats: int) -> float:
+    """Milliseconds per repeat of `body`, events on `stream` around all repeats."""
+    start, end = events.create(), events.create()
+    events.device_synchronize()
+    events.record(start, stream)
+    for _ in range(repeats):
+        body()
+    events.record(end, stream)
+    ms = events.elapsed_ms(start, end) / repeats
+    events.destroy(start)
+    events.destroy(end)
+    return ms
+
+
+# ---- the training GEMM set ------------------------------------------------------------
 
 MODEL_111M = dict(name="111.5M", blocks=12, width=768, ffn=3072, heads_width=16 * 1024, tokens=16 * 2048)
 
@@ -83,13 +133,10 @@ def linear_products(tokens: int, inputs: int, outputs: int):
 
 
 def training_set(model=MODEL_111M):
-    """(label, layout, spec, operands) for every GEMM of one training step's set."""
-    m, d, f = model["tokens"], model["width"], model["ffn"]
+    """(label, inputs, outputs) for every Linear of one training step."""
+    d, f = model["width"], model["ffn"]
     layers = [("qkv", d, 3 * d), ("out", d, d), ("up", d, f), ("down", f, d)]
-    items = []
-    for block in range(model["blocks"]):
-        for name, inputs, outputs in layers:
-            items.append((f"b{block}.{name}", inputs, outputs))
+    items = [(f"b{block}.{name}", i, o) for block in range(model["blocks"]) for name, i, o in layers]
     items.append(("head", d, model["heads_width"]))
     return items
 
@@ -117,8 +164,7 @@ class LinearBuffers:
 
 
 def build_set(gpu: Gpu, model=MODEL_111M):
-    calls = []
-    buffers = []
+    calls, buffers = [], []
     for index, (label, inputs, outputs) in enumerate(training_set(model)):
         buf = LinearBuffers(gpu, model["tokens"], inputs, outputs, 16 * index)
         buffers.append(buf)
@@ -128,16 +174,160 @@ def build_set(gpu: Gpu, model=MODEL_111M):
     return calls, buffers
 
 
-def run_step(gpu: Gpu, calls, events=None, marks=None, stream=0):
+def run_step(gpu: Gpu, calls, precision=Precision.Default, events=None, marks=None, stream=0):
     for i, (_, _, spec, (left, right, out)) in enumerate(calls):
         if marks is not None:
             events.record(marks[i], stream)
-        gpu.matmul(spec, left, right, out)
+        gpu.matmul(spec.with_precision(precision) if precision else spec, left, right, out)
     if marks is not None:
         events.record(marks[len(calls)], stream)
 
 
-# ---- CPU baseline -----------------------------------------------------------------
+def measure_set(gpu: Gpu, events: HipEvents, calls, steps: int, warmup: int, precision=Precision.Default):
+    """Step time over `steps` steps and per-launch times from events between launches."""
+    stream = gpu.stream
+    for _ in range(warmup):
+        run_step(gpu, calls, precision)
+    events.device_synchronize()
+    marks = [[events.create() for _ in range(len(calls) + 1)] for _ in range(steps)]
+    start, end = events.create(), events.create()
+    events.record(start, stream)
+    for step in range(steps):
+        run_step(gpu, calls, precision, events, marks[step], stream)
+    events.record(end, stream)
+    events.device_synchronize()
+    ms_per_step = events.elapsed_ms(start, end) / steps
+    per_call = np.array([[events.elapsed_ms(marks[s][i], marks[s][i + 1]) for i in range(len(calls))]
+                         for s in range(steps)]).mean(axis=0)
+    for row in marks:
+        for e in row:
+            events.destroy(e)
+    return ms_per_step, per_call
+
+
+def summarize_set(calls, per_call_ms, peak):
+    layouts, shapes = {}, {}
+    for i, (_, layout, spec, _) in enumerate(calls):
+        entry = layouts.setdefault(layout, {"flops": 0, "ms": 0.0, "launches": 0})
+        entry["flops"] += spec.flops()
+        entry["ms"] += per_call_ms[i]
+        entry["launches"] += 1
+        key = f"{layout} {spec.rows}x{spec.cols}x{spec.inner}"
+        s = shapes.setdefault(key, [0.0, 0, spec.flops()])
+        s[0] += per_call_ms[i]
+        s[1] += 1
+    per_layout = {k: {"tflops": round(v["flops"] / (v["ms"] * 1e-3) / 1e12, 2), "ms_per_step": round(v["ms"], 3),
+                      "frac_peak": round(v["flops"] / (v["ms"] * 1e-3) / 1e12 / peak, 4)}
+                  for k, v in layouts.items()}
+    per_shape = {k: round(v[2] / (v[0] / v[1] * 1e-3) / 1e12, 1) for k, v in shapes.items()}
+    return layouts, per_layout, per_shape
+
+
+def bf16_roofline_tflops(spec: MatmulSpec) -> float:
+    """min(bf16 dense peak, algorithmic intensity x HBM bandwidth) with fp32 operands in HBM."""
+    m, n, k = spec.rows, spec.cols, spec.inner
+    bytes_moved = 4 * (m * k + k * n + m * n * (2 if spec.write else 1))
+    return min(PEAK_BF16_TFLOPS, spec.flops() / bytes_moved * PEAK_HBM_GBS / 1e3)
+
+
+# ---- config 3: causal attention ---------------------------------------------------------
+
+def measure_attention(gpu: Gpu, events: HipEvents, repeats: int = 3):
+    """The six attention products of attention.rs:206-260 for 16 x 12 heads, T = 2048, h = 64,
+    dense (the reference's calls) and with the causal-mask extension."""
+    heads, t, h = 16 * 12, 2048, 64
+    head_block, score_block = t * h, t * t
+    per_head = lambda l, r, o: BatchStrides(heads, l, r, o)  # noqa: E731
+    q, k, v, do = (gpu.zeros(Shape(heads * t, h)) for _ in range(4))
+    p, ds = gpu.zeros(Shape(heads * t, t)), gpu.zeros(Shape(heads * t, t))
+    for i, tensor in enumerate((q, k, v, do, p, ds)):
+        gpu.fill_normal(tensor, SEED, 900 + i)
+    s_out, dp_out = gpu.zeros(Shape(heads * t, t)), gpu.zeros(Shape(heads * t, t))
+    o, dv, dq, dk = (gpu.zeros(Shape(heads * t, h)) for _ in range(4))
+    scores = MatmulSpec.new(t, t, h).right_transposed().batched(per_head(head_block, head_block, score_block))
+    mix = MatmulSpec.new(t, h, t).batched(per_head(score_block, head_block, head_block))
+    transposed_mix = MatmulSpec.new(t, h, t).left_transposed().batched(per_head(score_block, head_block, head_block))
+    products = [
+        ("scores Q.K^T", scores, q, k, s_out, "out"),
+        ("mix P.V", mix, p, v, o, "left"),
+        ("dP = dO.V^T", scores, do, v, dp_out, "out"),
+        ("dV = P^T.dO", transposed_mix, p, do, dv, "left"),
+        ("dQ = s.dS.K", mix.scaled(0.125), ds, k, dq, "left"),
+        ("dK = s.dS^T.Q", transposed_mix.scaled(0.125), ds, q, dk, "left"),
+    ]
+    causal_flops = 2 * h * t * (t + 1) // 2 * heads  # visible (q, k) pairs only
+    dense_flops = 2 * h * t * t * heads
+    result = {"shape": "16x12 heads, T=2048, h=64, fp32", "causal_gflop_per_product": round(causal_flops / 1e9, 2),
+              "products": {}}
+    total = {"dense": 0.0, "causal": 0.0}
+    for name, spec, left, right, out, kind in products:
+        masked = spec.causal_output() if kind == "out" else spec.causal_left()
+        dense_ms = timed(events, gpu.stream, lambda: gpu.matmul(spec, left, right, out), repeats)
+        causal_ms = timed(events, gpu.stream, lambda: gpu.matmul(masked, left, right, out), repeats)
+        total["dense"] += dense_ms
+        total["causal"] += causal_ms
+        result["products"][name] = {
+            "dense_ms": round(dense_ms, 3), "dense_tflops": round(dense_flops / (dense_ms * 1e-3) / 1e12, 1),
+            "causal_ms": round(causal_ms, 3),
+            "causal_tflops_on_visible_work": round(causal_flops / (causal_ms * 1e-3) / 1e12, 1)}
+    result["all_six"] = {"dense_ms": round(total["dense"], 3), "causal_ms": round(total["causal"], 3),
+                         "causal_tflops_on_visible_work": round(6 * causal_flops / (total["causal"] * 1e-3) / 1e12, 1),
+                         "dense_tflops": round(6 * dense_flops / (total["dense"] * 1e-3) / 1e12, 1)}
+    return result
+
+
+# ---- config 4: decode ------------------------------------------------------------------
+
+DECODE_SHAPES = [("qkv", 768, 2304), ("out", 768, 768), ("up", 768, 3072), ("down", 3072, 768),
+                 ("head", 768, 16 * 1024)]
+
+
+def decode_bytes(m: int, k: int, n: int) -> int:
+    """Algorithmic bytes of one decode product: read W and x, write y (fp32)."""
+    return 4 * (k * n + m * k + m * n)
+
+
+def measure_decode(gpu: Gpu, events: HipEvents, pool_bytes: int = 640 << 20, repeats: int = 3):
+    """GB/s of y[M,N] = x[M,K] W[K,N] per shape, W drawn from a pool larger than the
+    256 MB Infinity Cache so reads come from HBM; launches replayed from a HIP graph.
+    Then one token's sequence (12 blocks x 4 products + head, distinct weights, M = 1)."""
+    result = {"per_shape_gbs": {}, "method": "HIP-graph replay, fp32 weights rotated through a "
+              f"{pool_bytes >> 20} MB pool (> 256 MB MALL); bytes = 4(KN + MK + MN)"}
+    for m in (1, 4, 16):
+        for name, k, n in DECODE_SHAPES:
+            copies = max(2, -(-pool_bytes // (4 * k * n)))
+            pool = [gpu.zeros(Shape(k, n)) for _ in range(copies)]
+            for i, w in enumerate(pool):
+                gpu.fill_normal(w, SEED, 1000 + i, 0.0, 0.02)
+            x, y = gpu.zeros(Shape(m, k)), gpu.zeros(Shape(m, n))
+            gpu.fill_normal(x, SEED, 999)
+            spec = MatmulSpec.new(m, n, k)
+            graph = HipGraph(gpu.stream, lambda: [gpu.matmul(spec, x, w, y) for w in pool])
+            graph.launch()
+            ms = timed(events, gpu.stream, graph.launch, repeats) / copies
+            graph.close()
+            result["per_shape_gbs"][f"M={m} {name} {k}x{n}"] = round(decode_bytes(m, k, n) / (ms * 1e-3) / 1e9, 1)
+            for w in pool:
+                w.free()
+    # One decode token: every product of the 12 blocks and the head, each weight distinct.
+    layers = [(k, n) for _ in range(12) for _, k, n in DECODE_SHAPES[:4]] + [DECODE_SHAPES[4][1:]]
+    weights = []
+    for i, (k, n) in enumerate(layers):
+        w = gpu.zeros(Shape(k, n))
+        gpu.fill_normal(w, SEED, 2000 + i, 0.0, 0.02)
+        weights.append((w, gpu.zeros(Shape(1, k)), gpu.zeros(Shape(1, n)), MatmulSpec.new(1, n, k)))
+    token_bytes = sum(decode_bytes(1, k, n) for k, n in layers)
+    graph = HipGraph(gpu.stream, lambda: [gpu.matmul(spec, x, w, y) for w, x, y, spec in weights])
+    graph.launch()
+    ms = timed(events, gpu.stream, graph.launch, 5)
+    graph.close()
+    result["token_sequence"] = {"products": len(layers), "mb_per_token": round(token_bytes / 1e6, 1),
+                                "us_per_token": round(ms * 1e3, 1),
+                                "gbs": round(token_bytes / (ms * 1e-3) / 1e9, 1)}
+    return result
+
+
+# ---- CPU baseline -----------------------------------------------------------------------
 
 def cpu_baseline(gpu: Gpu, calls, budget_s: float):
     """Times the oracle (reference::matmul restated in C, one core) on a row
@@ -151,10 +341,7 @@ def cpu_baseline(gpu: Gpu, calls, budget_s: float):
         distinct.setdefault(key, [spec, ops, 0])
         distinct[key][2] += 1
     per_gemm_budget = budget_s / len(distinct)
-    projected_s = 0.0
-    sampled_flops = 0
-    sampled_s = 0.0
-    samples = []
+    projected_s, sampled_flops, sampled_s, samples = 0.0, 0, 0.0, []
     for (layout, rows, cols, inner), (spec, (left, right, out), count) in distinct.items():
         a = gpu.download(left)
         b = gpu.download(right)
@@ -178,7 +365,18 @@ def cpu_baseline(gpu: Gpu, calls, budget_s: float):
     return projected_s, sampled_flops, sampled_s, samples
 
 
-# ---- main --------------------------------------------------------------------------
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+# ---- main -------------------------------------------------------------------------------
 
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
@@ -187,69 +385,35 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=1)
     parser.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline sampling")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    parser.add_argument("--no-extras", action="store_true", help="only the fp32 set (bf16, attention, decode off)")
     args = parser.parse_args()
 
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (the GEMM path has no multi-GPU component); got --gpus {args.gpus}",
-              file=sys.stderr)
+        print(f"bench.py measures one GPU only: the GEMM path runs on one device and its sharding is a design "
+              f"note, not a measured path; got --gpus {args.gpus}", file=sys.stderr)
         return 2
 
     gpu = Gpu(0)
     events = HipEvents()
-    stream = gpu.stream
     calls, _buffers = build_set(gpu)
     set_flops = sum(spec.flops() for _, _, spec, _ in calls)
 
-    for _ in range(args.warmup):
-        run_step(gpu, calls)
-    events.device_synchronize()
-
-    marks = [[events.create() for _ in range(len(calls) + 1)] for _ in range(args.steps)]
-    start, end = events.create(), events.create()
-    events.device_synchronize()
-    events.record(start, stream)
-    for step in range(args.steps):
-        run_step(gpu, calls, events, marks[step], stream)
-    events.record(end, stream)
-    events.device_synchronize()
-    total_ms = events.elapsed_ms(start, end)
-    ms_per_step = total_ms / args.steps
-
-    per_call_ms = np.zeros((args.steps, len(calls)))
-    for step in range(args.steps):
-        for i in range(len(calls)):
-            per_call_ms[step, i] = events.elapsed_ms(marks[step][i], marks[step][i + 1])
-    mean_ms = per_call_ms.mean(axis=0)
-
-    layouts = {}
-    for i, (label, layout, spec, _) in enumerate(calls):
-        entry = layouts.setdefault(layout, {"flops": 0, "ms": 0.0, "launches": 0})
-        entry["flops"] += spec.flops()
-        entry["ms"] += mean_ms[i]
-        entry["launches"] += 1
-    per_layout = {k: {"tflops": v["flops"] / (v["ms"] * 1e-3) / 1e12, "ms_per_step": v["ms"],
-                      "frac_fp32_peak": v["flops"] / (v["ms"] * 1e-3) / 1e12 / PEAK_FP32_TFLOPS}
-                  for k, v in layouts.items()}
-    shapes = {}
-    for i, (label, layout, spec, _) in enumerate(calls):
-        key = f"{layout} {spec.rows}x{spec.cols}x{spec.inner}"
-        entry = shapes.setdefault(key, [0.0, 0, spec.flops()])
-        entry[0] += mean_ms[i]
-        entry[1] += 1
-    per_shape = {k: round(v[2] / (v[0] / v[1] * 1e-3) / 1e12, 2) for k, v in shapes.items()}
-
+    ms_per_step, per_call = measure_set(gpu, events, calls, args.steps, args.warmup)
+    layouts, per_layout, per_shape = summarize_set(calls, per_call, PEAK_FP32_TFLOPS)
     nn = layouts["NN"]
     nn_flops_per_launch = nn["flops"] / nn["launches"]
     nn_ms_per_launch = nn["ms"] / nn["launches"]
     achieved = nn_flops_per_launch / (nn_ms_per_launch * 1e-3) / 1e12
-    roofline = {"kernel": "gemm_f32_kernel<Tile<128,128,16,2,2>, A k-contiguous, B n-contiguous> (all forward NN)",
+    roofline = {"kernel": "gemm_f32_kernel<Tile<128,128,32,2,2>, A K-contiguous, B N-contiguous, buffer loads> "
+                          "(every forward NN product of the set)",
                 "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "traffic": None,
-                "launch_ms_mean": round(nn_ms_per_launch, 4), "flops_per_launch": nn_flops_per_launch}
+                "launch_ms_mean": round(nn_ms_per_launch, 4), "flops_per_launch": nn_flops_per_launch,
+                "launches_per_step": nn["launches"]}
 
     value = set_flops / (ms_per_step * 1e-3) / 1e12
     result = {
-        "metric": "GEMM TFLOP/s and % fp32 MFMA peak (111.5M train set); decode GEMV GB/s, 1 GPU",
+        "metric": METRIC,
         "value": round(value, 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -266,9 +430,23 @@ def main() -> int:
                    "gemms_per_step": len(calls), "tflop_per_step": round(set_flops / 1e12, 4)},
         "frac_fp32_peak": round(value / PEAK_FP32_TFLOPS, 4),
         "roofline": roofline,
-        "per_layout": {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in per_layout.items()},
+        "per_layout": per_layout,
         "per_shape_tflops": per_shape,
     }
+
+    if not args.no_extras:
+        bf16_steps = max(1, min(args.steps, 3))
+        bf16_ms, bf16_calls = measure_set(gpu, events, calls, bf16_steps, 1, Precision.Bf16)
+        bf16_tflops = set_flops / (bf16_ms * 1e-3) / 1e12
+        attainable = set_flops / sum(spec.flops() / (bf16_roofline_tflops(spec) * 1e12) for _, _, spec, _ in calls) / 1e12
+        _, bf16_layout, _ = summarize_set(calls, bf16_calls, PEAK_BF16_TFLOPS)
+        result["bf16"] = {"value": round(bf16_tflops, 2), "unit": "TFLOP/s", "ms_per_step": round(bf16_ms, 3),
+                          "frac_bf16_peak": round(bf16_tflops / PEAK_BF16_TFLOPS, 4),
+                          "roofline_min_peak_or_ai_x_hbm": round(attainable, 1),
+                          "frac_roofline": round(bf16_tflops / attainable, 4), "per_layout": bf16_layout,
+                          "inputs": "fp32 in HBM, rounded to bf16 (nearest-even) in LDS; fp32 accumulation"}
+        result["attention"] = measure_attention(gpu, events)
+        result["decode"] = measure_decode(gpu, events)
 
     if not args.no_cpu:
         projected_s, sampled_flops, sampled_s, samples = cpu_baseline(gpu, calls, args.cpu_budget)
@@ -276,23 +454,11 @@ def main() -> int:
             "value": round(set_flops / projected_s / 1e12, 8), "unit": "TFLOP/s", "cores": 1, "kind": "port",
             "sample": f"reference::matmul restated in C (oracle/), single thread, same input bytes; "
                       f"{sampled_flops / 1e9:.1f} GFLOP over row samples of the {len(samples)} distinct GEMMs "
-                      f"({sampled_s:.1f} s), scaled linearly in rows to the full set: "
-                      f"{projected_s:.0f} s per step",
+                      f"({sampled_s:.1f} s), scaled linearly in rows to the full set: {projected_s:.0f} s per step",
             "host_cpu": _cpu_model(), "host_threads": os.cpu_count()}
     print(json.dumps(result))
     gpu.close()
     return 0
-
-
-def _cpu_model() -> str:
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return "unknown"
 
 
 if __name__ == "__main__":

@@ -23,6 +23,7 @@ struct sn_context {
 namespace {
 
 constexpr size_t kDefaultWorkspaceBytes = size_t(256) << 20;
+constexpr size_t kCounterCount = 16384;
 // Dimensions above this would overflow the kernels' 32-bit tile counters.
 constexpr size_t kMaxDimension = size_t(1) << 31;
 
@@ -106,6 +107,16 @@ int sn_context_create_with_workspace(int ordinal, size_t workspace_bytes, sn_con
     err = hipGetDeviceProperties(&prop, ordinal);
     if (err == hipSuccess && prop.multiProcessorCount > 0) ctx->env.cu_count = prop.multiProcessorCount;
     if (err == hipSuccess) err = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    if (err == hipSuccess) {
+        void* counters = nullptr;
+        err = hipMalloc(&counters, kCounterCount * sizeof(uint32_t));
+        if (err == hipSuccess) {
+            ctx->env.counters = static_cast<uint32_t*>(counters);
+            ctx->env.counter_count = kCounterCount;
+            err = hipMemsetAsync(counters, 0, kCounterCount * sizeof(uint32_t), ctx->stream);
+            if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);
+        }
+    }
     if (err == hipSuccess && workspace_bytes > 0) {
         void* ws = nullptr;
         err = hipMalloc(&ws, workspace_bytes);
@@ -137,6 +148,10 @@ int sn_context_destroy(sn_context* ctx) {
     }
     if (ctx->env.workspace != nullptr) {
         hipError_t err = hipFree(ctx->env.workspace);
+        if (first == hipSuccess) first = err;
+    }
+    if (ctx->env.counters != nullptr) {
+        hipError_t err = hipFree(ctx->env.counters);
         if (first == hipSuccess) first = err;
     }
     delete ctx;
@@ -318,7 +333,7 @@ int sn_matmul(sn_context* ctx, const sn_matmul_spec* spec, const float* left, si
     if (err != hipSuccess) return status(err);
     if (kernel == SN_KERNEL_SIMPLE) return status(sn::launch_gemm_simple(p, ctx->stream));
     const bool bf16 = kernel == SN_KERNEL_MFMA_BF16;
-    if (!bf16 && sn::gemv_applies(p)) return status(sn::launch_gemv(p, ctx->env, ctx->stream));
+    if (!bf16 && sn::gemv_applies(p, ctx->env)) return status(sn::launch_gemv(p, ctx->env, ctx->stream));
     if (sn::gemm_workspace_bytes(p, bf16, ctx->env) > ctx->env.workspace_bytes) return SN_ERR_WORKSPACE;
     return status(bf16 ? sn::launch_gemm_bf16(p, ctx->env, ctx->stream) : sn::launch_gemm_f32(p, ctx->env, ctx->stream));
 }

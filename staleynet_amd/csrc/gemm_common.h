@@ -49,6 +49,22 @@ __device__ __forceinline__ void buffer_store1(__amdgpu_buffer_rsrc_t rsrc, int32
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, value), rsrc, offset, 0, 0);
 }
 
+// Device-coherent 128-bit accesses (cache policy SC1: the device-scope bit
+// the gfx942/gfx950 memory model sets on agent-scope atomic loads and
+// stores). They are read and written where every XCD sees them, so data
+// handed between workgroups on different XCDs needs no L2 write-back or
+// invalidate, only completion ordering.
+constexpr int32_t kDeviceCoherent = 16;
+
+__device__ __forceinline__ f32x4 buffer_load4_coherent(__amdgpu_buffer_rsrc_t rsrc, int32_t offset) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, kDeviceCoherent));
+}
+
+__device__ __forceinline__ void buffer_store4_coherent(__amdgpu_buffer_rsrc_t rsrc, int32_t offset, f32x4 value) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, value), rsrc, offset, 0, kDeviceCoherent);
+}
+
 // f32 -> bf16, round to nearest, ties to even (IEEE 754 roundTiesToEven on
 // the 16 dropped bits); NaN stays a (quiet) NaN.
 __device__ __forceinline__ uint32_t bf16_bits(float value) {

@@ -27,11 +27,14 @@ struct Problem {
     int64_t query_offset = 0;
 };
 
-// What a launch may use beyond its operands: the context's split-K scratch
-// and the device's compute-unit count (for sizing grids).
+// What a launch may use beyond its operands: the context's split-K scratch,
+// its arrival counters (zero between calls; a kernel that increments one
+// resets it before it ends) and the device's compute-unit count.
 struct Env {
     float* workspace = nullptr;
     size_t workspace_bytes = 0;
+    uint32_t* counters = nullptr;
+    size_t counter_count = 0;
     int cu_count = 256;
 };
 
@@ -42,7 +45,7 @@ hipError_t launch_gemm_simple(const Problem& p, hipStream_t stream);
 // Decode-shaped products (few rows, right operand N-contiguous); returns
 // hipErrorNotSupported when the shape is not one it handles.
 hipError_t launch_gemv(const Problem& p, const Env& env, hipStream_t stream);
-bool gemv_applies(const Problem& p);
+bool gemv_applies(const Problem& p, const Env& env);
 
 // Bytes of split-K workspace launch_gemm_* would use for `p` (0 = none).
 size_t gemm_workspace_bytes(const Problem& p, bool bf16, const Env& env);

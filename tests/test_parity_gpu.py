@@ -273,3 +273,29 @@ def test_bf16_inputs_round_to_nearest_even(gpu):
     out = run_gpu(gpu, spec, a.ravel(), eye.ravel(), np.zeros(len(cases) * k, np.float32), MatmulKernel.MfmaBf16)
     got = out.reshape(len(cases), k)[:, 0]
     assert got.tolist() == [np.float32(c[1]) for c in cases]
+
+
+# ---- decode-shaped products (few rows, row-major weight) ------------------------------
+
+@pytest.mark.parametrize("rows,cols,inner", [(1, 8, 1), (3, 100, 37), (5, 772, 1000), (16, 260, 4100),
+                                             (7, 2304, 768), (2, 12, 20000)])
+@pytest.mark.parametrize("accumulate", [False, True])
+def test_few_row_products_match_the_oracle(gpu, rows, cols, inner, accumulate):
+    spec = MatmulSpec.new(rows, cols, inner).scaled(0.7)
+    if accumulate:
+        spec = spec.accumulate()
+    left = oracle.random_values(rows * inner, 21)
+    right = oracle.random_values(inner * cols, 22)
+    initial = oracle.random_values(rows * cols, 23)
+    expected = expected_for(spec, left, right, initial)
+    check(expected, run_gpu(gpu, spec, left, right, initial), 1e-5, f"{rows}x{cols}x{inner}")
+
+
+def test_batched_few_row_products(gpu):
+    # One query row per head against per-head weights (batch stride on both operands).
+    heads, cols, inner = 12, 64, 1408
+    spec = MatmulSpec.new(1, cols, inner).batched(BatchStrides(heads, inner, inner * cols, cols))
+    left = oracle.random_values(heads * inner, 24)
+    right = oracle.random_values(heads * inner * cols, 25)
+    initial = np.zeros(heads * cols, np.float32)
+    check(expected_for(spec, left, right, initial), run_gpu(gpu, spec, left, right, initial), 1e-5)
