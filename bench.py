@@ -376,6 +376,111 @@ def _cpu_model() -> str:
     return "unknown"
 
 
+# ---- rocprofv3 summaries ----------------------------------------------------------------
+
+# The roofline kernel: fp32 MFMA, 128x128 tile, A K-contiguous, B N-contiguous, buffer loads.
+NN_KERNEL_KEY = "Tile<128, 128, 32, 2, 2>, true, false, true>"
+COPY_KERNEL_KEY = "copy_kernel("
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "gemm_f32_nn_111M_hbm_traffic.txt")
+
+
+def load_traffic(path: str = TRAFFIC_SUMMARY):
+    """HBM bytes per NN launch from the committed PMC summary, or None without one."""
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def _short(name: str) -> str:
+    name = name.replace("sn::gemm::", "").replace("(anonymous namespace)::", "").replace("sn::", "")
+    return name.split("(")[0] if "(" in name else name
+
+
+def _per_dispatch(csv_path: str, counter: str):
+    """{kernel name: [counter value per dispatch, in dispatch order]} from a counter_collection.csv."""
+    import csv
+    out = {}
+    with open(csv_path, newline="") as f:
+        rows = sorted((r for r in csv.DictReader(f) if r["Counter_Name"] == counter),
+                      key=lambda r: int(r["Dispatch_Id"]))
+    for r in rows:
+        out.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+    return out
+
+
+def summarize_pmc(fetch_csv: str, write_csv: str, copy_mib: int) -> str:
+    """HBM traffic of the NN kernel per launch: FETCH_SIZE and WRITE_SIZE (KiB per dispatch), each
+    divided by what the same counter reads for the plain copy kernel per byte it moves."""
+    fetch, write = _per_dispatch(fetch_csv, "FETCH_SIZE"), _per_dispatch(write_csv, "WRITE_SIZE")
+    pick = lambda table, key: next(v for k, v in table.items() if key in k)  # noqa: E731
+    copy_bytes = copy_mib << 20
+    f_copy, w_copy = pick(fetch, COPY_KERNEL_KEY), pick(write, COPY_KERNEL_KEY)
+    f_factor = f_copy[-1] * 1024 / copy_bytes
+    w_factor = w_copy[-1] * 1024 / copy_bytes
+    f_nn, w_nn = pick(fetch, NN_KERNEL_KEY), pick(write, NN_KERNEL_KEY)
+    nn_calls = [spec for _, layout, spec in _set_specs() if layout == "NN"]
+    assert len(f_nn) == len(w_nn) == len(nn_calls), (len(f_nn), len(w_nn), len(nn_calls))
+    lines = [f"copy kernel ({copy_mib} MiB read + {copy_mib} MiB written): FETCH_SIZE {f_copy[-1]:.0f} KiB, "
+             f"WRITE_SIZE {w_copy[-1]:.0f} KiB -> factors {f_factor:.4f} (fetch), {w_factor:.4f} (write)",
+             "", "NN launches of one step, grouped by shape (means per launch):",
+             f"{'shape MxNxK':>22} {'launches':>8} {'algorithmic MB':>15} {'HBM read MB':>12} {'HBM write MB':>13} "
+             f"{'traffic/alg':>11}"]
+    groups = {}
+    for spec, f, w in zip(nn_calls, f_nn, w_nn):
+        g = groups.setdefault((spec.rows, spec.cols, spec.inner), [0, 0.0, 0.0])
+        g[0] += 1
+        g[1] += f * 1024 / f_factor
+        g[2] += w * 1024 / w_factor
+    for (m, n, k), (count, rd, wr) in groups.items():
+        alg = 4 * (m * k + k * n + m * n)
+        lines.append(f"{f'{m}x{n}x{k}':>22} {count:>8} {alg / 1e6:>15.1f} {rd / count / 1e6:>12.1f} "
+                     f"{wr / count / 1e6:>13.1f} {(rd + wr) / count / alg:>11.3f}")
+    traffic = sum(f * 1024 / f_factor + w * 1024 / w_factor for f, w in zip(f_nn, w_nn)) / len(f_nn)
+    algorithmic = sum(4 * (s.rows * s.inner + s.inner * s.cols + s.rows * s.cols) for s in nn_calls) / len(nn_calls)
+    lines += ["", f"raw counter means per NN launch: FETCH_SIZE {sum(f_nn) / len(f_nn):.0f} KiB, "
+              f"WRITE_SIZE {sum(w_nn) / len(w_nn):.0f} KiB",
+              f"mean over the {len(nn_calls)} NN launches: algorithmic {algorithmic / 1e6:.1f} MB, "
+              f"HBM traffic {traffic / 1e6:.1f} MB ({traffic / algorithmic:.3f}x)",
+              f"traffic_bytes_per_launch: {int(round(traffic))}",
+              f"algorithmic_bytes_per_launch: {int(round(algorithmic))}"]
+    return "\n".join(lines)
+
+
+def summarize_trace(stats_csv: str, bench_json: str = "") -> str:
+    """Kernel table from rocprofv3's kernel_stats.csv; with the bench line of the same run, the NN
+    kernel's rocprof average beside the HIP-event mean bench.py reported."""
+    import csv
+    with open(stats_csv, newline="") as f:
+        rows = list(csv.DictReader(f))
+    lines = [f"{'kernel':<78} {'calls':>6} {'avg us':>9} {'min us':>9} {'max us':>9} {'total ms':>9} {'%':>6}"]
+    for r in rows:
+        lines.append(f"{_short(r['Name'])[:78]:<78} {int(r['Calls']):>6} {float(r['AverageNs']) / 1e3:>9.1f} "
+                     f"{float(r['MinNs']) / 1e3:>9.1f} {float(r['MaxNs']) / 1e3:>9.1f} "
+                     f"{float(r['TotalDurationNs']) / 1e6:>9.2f} {float(r['Percentage']):>6.2f}")
+    nn = next((r for r in rows if NN_KERNEL_KEY in r["Name"]), None)
+    if nn is not None and bench_json:
+        with open(bench_json) as f:
+            line = json.loads([x for x in f.read().splitlines() if x.startswith("{")][-1])
+        event_ms = line["roofline"]["launch_ms_mean"]
+        prof_ms = float(nn["AverageNs"]) / 1e6
+        lines += ["", f"NN roofline kernel: rocprof average {prof_ms:.4f} ms over {nn['Calls']} launches; "
+                  f"bench.py HIP-event mean {event_ms:.4f} ms (ratio {event_ms / prof_ms:.3f})"]
+    return "\n".join(lines)
+
+
+def _set_specs():
+    """(label, layout, spec) of every product of the set, in launch order, without a GPU."""
+    model = MODEL_111M
+    for label, inputs, outputs in training_set(model):
+        for layout, spec in linear_products(model["tokens"], inputs, outputs):
+            yield label, layout, spec
+
+
 # ---- main -------------------------------------------------------------------------------
 
 def main() -> int:
@@ -386,7 +491,20 @@ def main() -> int:
     parser.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline sampling")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--no-extras", action="store_true", help="only the fp32 set (bf16, attention, decode off)")
+    parser.add_argument("--copy-calibration-mib", type=int, default=0,
+                        help="run one plain copy of this many MiB first (the PMC byte-counter calibration)")
+    parser.add_argument("--summarize-trace", nargs="+", metavar=("KERNEL_STATS_CSV", "BENCH_JSON"),
+                        help="print a kernel table from a rocprofv3 --stats run and exit (no GPU)")
+    parser.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                        help="print the NN kernel's HBM traffic from two --pmc runs and exit (no GPU)")
     args = parser.parse_args()
+
+    if args.summarize_trace:
+        print(summarize_trace(*args.summarize_trace[:2]))
+        return 0
+    if args.summarize_pmc:
+        print(summarize_pmc(*args.summarize_pmc, args.copy_calibration_mib or 1024))
+        return 0
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: the GEMM path runs on one device and its sharding is a design "
@@ -395,6 +513,14 @@ def main() -> int:
 
     gpu = Gpu(0)
     events = HipEvents()
+    if args.copy_calibration_mib:
+        src = gpu.zeros(Shape(args.copy_calibration_mib << 18, 1))
+        dst = gpu.zeros(Shape(args.copy_calibration_mib << 18, 1))
+        gpu.fill_normal(src, SEED, 3000)
+        gpu.copy_device(dst, src)
+        gpu.synchronize()
+        src.free()
+        dst.free()
     calls, _buffers = build_set(gpu)
     set_flops = sum(spec.flops() for _, _, spec, _ in calls)
 
@@ -407,9 +533,13 @@ def main() -> int:
     roofline = {"kernel": "gemm_f32_kernel<Tile<128,128,32,2,2>, A K-contiguous, B N-contiguous, buffer loads> "
                           "(every forward NN product of the set)",
                 "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "traffic": None,
+                "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "traffic": load_traffic(),
                 "launch_ms_mean": round(nn_ms_per_launch, 4), "flops_per_launch": nn_flops_per_launch,
-                "launches_per_step": nn["launches"]}
+                "launches_per_step": nn["launches"],
+                "traffic_unit": "HBM bytes per launch (PMC FETCH_SIZE + WRITE_SIZE, copy-calibrated; "
+                                "profiles/gemm_f32_nn_111M_hbm_traffic.txt)",
+                "algorithmic_bytes_per_launch": int(sum(4 * (s.rows * s.inner + s.inner * s.cols + s.rows * s.cols)
+                                                        for _, y, s, _ in calls if y == "NN") / nn["launches"])}
 
     value = set_flops / (ms_per_step * 1e-3) / 1e12
     result = {

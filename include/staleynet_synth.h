@@ -24,6 +24,13 @@ extern "C" {
 int sn_fill_normal(void *stream, float *device, size_t count, uint64_t seed, uint64_t stream_id, float mean,
                    float stddev);
 
+/* Enqueues on `stream` a copy of `count` floats from `src` to `dst` (both
+ * device memory, 16-byte aligned, count a multiple of 4, not overlapping).
+ * A plain streaming kernel used to calibrate hardware byte counters. Returns
+ * 0, -1 for a null buffer, -7 for a misaligned buffer or count, or a HIP
+ * error code. */
+int sn_copy_device(void *stream, float *dst, const float *src, size_t count);
+
 #ifdef __cplusplus
 }
 #endif

@@ -40,7 +40,28 @@ __global__ __launch_bounds__(256) void fill_normal_kernel(float* out, uint64_t c
     }
 }
 
+// Plain streaming copy, 16 bytes per lane per iteration: the known-size
+// kernel that hardware byte counters are calibrated against.
+__global__ __launch_bounds__(256) void copy_kernel(float4* __restrict__ dst, const float4* __restrict__ src,
+                                                   uint64_t vectors) {
+    for (uint64_t i = blockIdx.x * uint64_t(blockDim.x) + threadIdx.x; i < vectors;
+         i += uint64_t(gridDim.x) * blockDim.x)
+        dst[i] = src[i];
+}
+
 }  // namespace
+
+extern "C" int sn_copy_device(void* stream, float* dst, const float* src, size_t count) {
+    if (count == 0) return 0;
+    if (dst == nullptr || src == nullptr) return -1;
+    if (count % 4 != 0 || reinterpret_cast<uintptr_t>(dst) % 16 != 0 || reinterpret_cast<uintptr_t>(src) % 16 != 0)
+        return -7;
+    const uint64_t vectors = count / 4;
+    const uint64_t grid = std::min<uint64_t>((vectors + 255) / 256, 8192);
+    hipLaunchKernelGGL(copy_kernel, dim3(unsigned(grid)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       reinterpret_cast<float4*>(dst), reinterpret_cast<const float4*>(src), vectors);
+    return int(hipGetLastError());
+}
 
 extern "C" int sn_fill_normal(void* stream, float* device, size_t count, uint64_t seed, uint64_t stream_id,
                               float mean, float stddev) {

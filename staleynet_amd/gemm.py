@@ -237,10 +237,11 @@ def _library() -> ctypes.CDLL:
         lib.sn_status_string.restype = ctypes.c_char_p
         lib.sn_fill_normal.argtypes = [ctypes.c_void_p, ctypes.c_void_p, size, ctypes.c_uint64, ctypes.c_uint64,
                                        ctypes.c_float, ctypes.c_float]
+        lib.sn_copy_device.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, size]
         for name in ("sn_context_create", "sn_context_create_with_workspace", "sn_context_destroy",
                      "sn_context_bind", "sn_context_set_kernel", "sn_context_get_kernel", "sn_synchronize",
                      "sn_alloc_zeroed", "sn_free", "sn_upload", "sn_download", "sn_copy_from_host", "sn_fill_zero",
-                     "sn_matmul_validate", "sn_matmul", "sn_fill_normal"):
+                     "sn_matmul_validate", "sn_matmul", "sn_fill_normal", "sn_copy_device"):
             getattr(lib, name).restype = ctypes.c_int
         _lib = lib
     return _lib
@@ -401,6 +402,13 @@ class Gpu:
         rc = _library().sn_fill_normal(ctypes.c_void_p(self.stream), ctypes.c_void_p(tensor.pointer), len(tensor),
                                        seed, stream_id, mean, std)
         self._check(rc, "fill_normal")
+
+    def copy_device(self, dst: Tensor, src: Tensor) -> None:
+        """Device-to-device copy by a plain streaming kernel (include/staleynet_synth.h), on this stream."""
+        assert len(dst) == len(src), f"copy_device: {len(src)} values into {len(dst)}"
+        rc = _library().sn_copy_device(ctypes.c_void_p(self.stream), ctypes.c_void_p(dst.pointer),
+                                       ctypes.c_void_p(src.pointer), len(src))
+        self._check(rc, "copy_device")
 
     def matmul(self, spec: MatmulSpec, left: Tensor, right: Tensor, output: Tensor) -> None:
         """``Gpu::matmul``: enqueue ``output = scale·op(left)·op(right) (+ output)``."""
