@@ -61,9 +61,9 @@ __global__ __launch_bounds__(T::THREADS) void gemm_bf16_kernel(Args args) {
     const int wave_m = wave / T::WAVES_N;
     const int wave_n = wave % T::WAVES_N;
 
-    int split, tm, tn;
-    tile_coordinates(blockIdx.x, gridDim.x, args.tiles_m, args.tiles_n, split, tm, tn);
-    const int64_t batch = args.batch_base + blockIdx.y;
+    int batch_local, split, tm, tn;
+    tile_coordinates(blockIdx.x, gridDim.x, args.tiles_m, args.tiles_n, args.splits, batch_local, split, tm, tn);
+    const int64_t batch = args.batch_base + batch_local;
     const int64_t m0 = int64_t(tm) * T::BM;
     const int64_t n0 = int64_t(tn) * T::BN;
 
@@ -130,20 +130,20 @@ __global__ __launch_bounds__(T::THREADS) void gemm_bf16_kernel(Args args) {
     }
 
     const bool partial = args.splits > 1;
-    float* out = partial ? args.ws + ((blockIdx.y * int64_t(args.splits) + split) * args.m) * args.n : c_batch;
+    float* out = partial ? args.ws + ((batch_local * int64_t(args.splits) + split) * args.m) * args.n : c_batch;
     write_tile<T, BUF>(args, acc, out, m0, n0, wave_m, wave_n, lane, partial);
 }
 
 template <class T, bool A_K, bool B_K, bool BUF>
 hipError_t launch_tiles_bf16(const Problem& p, const Env& env, const Plan& plan, hipStream_t stream) {
     Args args = make_args<T>(p, env, plan);
-    const int64_t tile_count = int64_t(plan.tiles_m) * plan.tiles_n * plan.splits;
-    if (tile_count * T::THREADS >= (int64_t(1) << 32)) return hipErrorInvalidConfiguration;
-    const int blocks = int(tile_count);
-    for (int64_t first = 0; first < p.batch; first += 65535) {
-        const int64_t count = std::min<int64_t>(65535, p.batch - first);
+    const int64_t per_batch = int64_t(plan.tiles_m) * plan.tiles_n * plan.splits;
+    const int64_t chunk = batches_per_launch(per_batch, T::THREADS, p.batch);
+    if (chunk < 1) return hipErrorInvalidConfiguration;
+    for (int64_t first = 0; first < p.batch; first += chunk) {
+        const int64_t count = std::min<int64_t>(chunk, p.batch - first);
         args.batch_base = first;
-        hipLaunchKernelGGL((gemm_bf16_kernel<T, A_K, B_K, BUF>), dim3(blocks, unsigned(count)), dim3(T::THREADS), 0,
+        hipLaunchKernelGGL((gemm_bf16_kernel<T, A_K, B_K, BUF>), dim3(unsigned(count * per_batch)), dim3(T::THREADS), 0,
                            stream, args);
         hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;

@@ -373,22 +373,27 @@ using LoaderFor = typename std::conditional<
     typename std::conditional<BUFFER, RowContiguousBufferLoader<ROWS, BK, THREADS>,
                               RowContiguousScalarLoader<ROWS, BK, THREADS>>::type>::type;
 
-// Block id -> (K split, tile row, tile column). Consecutive workgroup ids
-// land on different XCDs, so ids are first regrouped so that each XCD holds
-// one contiguous range; that range covers whole K splits in turn (the tiles
-// of a split share its slices of A and B) and, within a split, walks a
-// raster grouped kGroupM tile rows high, keeping the A rows and B columns an
-// XCD reuses in its own L2.
-__device__ __forceinline__ void tile_coordinates(int bid, int blocks, int tiles_m, int tiles_n, int& split, int& tm,
-                                                 int& tn) {
+// Block id -> (matrix of the batch, K split, tile row, tile column). The
+// grid enumerates (batch, split, tile) with the batch outermost. Consecutive
+// workgroup ids land on different XCDs, so ids are first regrouped so that
+// each XCD holds one contiguous range: whole matrices of a batch (attention
+// heads: every XCD gets the same mix of causally full and empty tiles, and a
+// head's operands stay in one L2), or whole K splits of one product (the
+// tiles of a split share its slices of A and B). Within a split the tiles
+// are walked as a raster grouped kGroupM tile rows high, keeping the A rows
+// and B columns an XCD reuses in its own L2.
+__device__ __forceinline__ void tile_coordinates(int bid, int blocks, int tiles_m, int tiles_n, int splits, int& batch,
+                                                 int& split, int& tm, int& tn) {
     const int xcd = bid % kXcds;
     const int local = bid / kXcds;
     const int q = blocks / kXcds;
     const int r = blocks % kXcds;
     const int linear = (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + local;
     const int tiles = tiles_m * tiles_n;
-    split = linear / tiles;
-    const int id = linear % tiles;
+    batch = linear / (tiles * splits);
+    const int in_batch = linear % (tiles * splits);
+    split = in_batch / tiles;
+    const int id = in_batch % tiles;
     const int per_group = kGroupM * tiles_n;
     const int group = id / per_group;
     const int first_m = group * kGroupM;
@@ -396,6 +401,14 @@ __device__ __forceinline__ void tile_coordinates(int bid, int blocks, int tiles_
     const int within = id % per_group;
     tm = first_m + within % group_rows;
     tn = within / group_rows;
+}
+
+// Matrices of a batch per launch: the grid's x dimension holds
+// batches x splits x tiles workgroups and must stay below 2^32 work-items.
+// 0 when one matrix alone exceeds that.
+inline int64_t batches_per_launch(int64_t per_batch, int threads, int64_t batch) {
+    const int64_t fit = ((int64_t(1) << 32) - 1) / threads / per_batch;
+    return fit < batch ? fit : batch;
 }
 
 // The reference's combine (kernels/matmul.rs:166-168), the product and the
@@ -500,9 +513,12 @@ struct Plan {
     int64_t k_per_split;
 };
 
-// Products whose output tiles cannot fill every CU a few times over (the
-// K = 32768 weight gradients) split K instead, in BK-aligned slices of at
-// least 8 steps, as far as the workspace allows.
+// Products whose output tiles cannot fill every CU twice over (the
+// K = 32768 weight gradients: 36 to 768 tiles of 128x128) split K instead,
+// into enough BK-aligned slices of at least 8 steps for about eight
+// workgroups per CU, as far as the workspace allows. Measured on the
+// c2 weight gradients, eight per CU beats three (+2 to +8 %) and matches
+// twelve; more slices only add partial sums to write and add.
 template <class T>
 Plan plan_for(const Problem& p, const Env& env) {
     Plan plan;
@@ -511,9 +527,10 @@ Plan plan_for(const Problem& p, const Env& env) {
     plan.splits = 1;
     plan.k_per_split = std::max<int64_t>(p.k, 1);
     const int64_t tiles = int64_t(plan.tiles_m) * plan.tiles_n * p.batch;
-    const int64_t target = int64_t(env.cu_count) * 3;
+    const int64_t threshold = int64_t(env.cu_count) * 4;
+    const int64_t target = int64_t(env.cu_count) * 8;
     const int64_t k_steps = (p.k + T::BK - 1) / T::BK;
-    if (p.mask == SN_MASK_NONE && tiles < target && k_steps >= 16 && p.batch == 1) {
+    if (p.mask == SN_MASK_NONE && tiles < threshold && k_steps >= 16 && p.batch == 1) {
         int64_t splits = std::min<int64_t>((target + tiles - 1) / tiles, k_steps / 8);
         const int64_t per_split_bytes = p.m * p.n * int64_t(sizeof(float));
         if (per_split_bytes > 0) splits = std::min<int64_t>(splits, int64_t(env.workspace_bytes) / per_split_bytes);

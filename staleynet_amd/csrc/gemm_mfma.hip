@@ -28,10 +28,10 @@
 //    registers on its way into LDS.
 //  * Double-buffered LDS; the next tile is prefetched into registers while
 //    the current one is multiplied: one barrier per BK step.
-//  * Grid: blockIdx.x enumerates (split, tile) pairs, remapped so each XCD
+//  * Grid: blockIdx.x enumerates (batch, split, tile), remapped so each XCD
 //    (the dispatcher deals workgroups round-robin over 8 XCDs, each with its
-//    own L2) receives a contiguous run of whole K splits, each walked as a
-//    grouped raster; y = matrix of the batch. Split-K partial sums go to the
+//    own L2) receives a contiguous run of whole matrices or whole K splits,
+//    each walked as a grouped raster. Split-K partial sums go to the
 //    context's workspace and a second kernel adds them in split order
 //    (deterministic).
 //  * Masks: causal output tiles that are entirely masked are not multiplied;
@@ -95,9 +95,9 @@ __global__ __launch_bounds__(T::THREADS) void gemm_f32_kernel(Args args) {
     const int wave_m = wave / T::WAVES_N;
     const int wave_n = wave % T::WAVES_N;
 
-    int split, tm, tn;
-    tile_coordinates(blockIdx.x, gridDim.x, args.tiles_m, args.tiles_n, split, tm, tn);
-    const int64_t batch = args.batch_base + blockIdx.y;
+    int batch_local, split, tm, tn;
+    tile_coordinates(blockIdx.x, gridDim.x, args.tiles_m, args.tiles_n, args.splits, batch_local, split, tm, tn);
+    const int64_t batch = args.batch_base + batch_local;
     const int64_t m0 = int64_t(tm) * T::BM;
     const int64_t n0 = int64_t(tn) * T::BN;
 
@@ -165,7 +165,7 @@ __global__ __launch_bounds__(T::THREADS) void gemm_f32_kernel(Args args) {
     }
 
     const bool partial = args.splits > 1;
-    float* out = partial ? args.ws + ((blockIdx.y * int64_t(args.splits) + split) * args.m) * args.n : c_batch;
+    float* out = partial ? args.ws + ((batch_local * int64_t(args.splits) + split) * args.m) * args.n : c_batch;
     write_tile<T, BUF>(args, acc, out, m0, n0, wave_m, wave_n, lane, partial);
 }
 
@@ -191,14 +191,13 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 template <class T, bool A_K, bool B_K, bool BUF>
 hipError_t launch_tiles(const Problem& p, const Env& env, const Plan& plan, hipStream_t stream) {
     Args args = make_args<T>(p, env, plan);
-    const int64_t tile_count = int64_t(plan.tiles_m) * plan.tiles_n * plan.splits;
-    // Work-items per grid dimension must stay below 2^32.
-    if (tile_count * T::THREADS >= (int64_t(1) << 32)) return hipErrorInvalidConfiguration;
-    const int blocks = int(tile_count);
-    for (int64_t first = 0; first < p.batch; first += 65535) {
-        const int64_t count = std::min<int64_t>(65535, p.batch - first);
+    const int64_t per_batch = int64_t(plan.tiles_m) * plan.tiles_n * plan.splits;
+    const int64_t chunk = batches_per_launch(per_batch, T::THREADS, p.batch);
+    if (chunk < 1) return hipErrorInvalidConfiguration;
+    for (int64_t first = 0; first < p.batch; first += chunk) {
+        const int64_t count = std::min<int64_t>(chunk, p.batch - first);
         args.batch_base = first;
-        hipLaunchKernelGGL((gemm_f32_kernel<T, A_K, B_K, BUF>), dim3(blocks, unsigned(count)), dim3(T::THREADS), 0,
+        hipLaunchKernelGGL((gemm_f32_kernel<T, A_K, B_K, BUF>), dim3(unsigned(count * per_batch)), dim3(T::THREADS), 0,
                            stream, args);
         hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
@@ -223,7 +222,7 @@ hipError_t dispatch_layout(const Problem& p, const Env& env, hipStream_t stream)
 }
 
 using TileSquare = Tile<128, 128, 32, 2, 2>;  // 4 waves of 64x64
-using TileNarrow = Tile<256, 64, 32, 4, 1>;   // N <= 64 (attention head dim)
+using TileNarrow = Tile<128, 64, 32, 4, 1>;   // N <= 64 (attention head dim): 3 workgroups per CU
 
 bool use_narrow(const Problem& p) { return p.n <= 64; }
 
