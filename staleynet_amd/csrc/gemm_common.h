@@ -570,6 +570,11 @@ Args make_args(const Problem& p, const Env& env, const Plan& plan) {
     return args;
 }
 
+// The direct-to-LDS fp32 kernel (gemm_dma.hip): whether it serves `p`
+// (aligned operands) and its launcher.
+bool dma_applies(const Problem& p);
+hipError_t launch_gemm_f32_dma(const Problem& p, const Env& env, hipStream_t stream);
+
 // Adds the split-K partial sums in split order and applies the combine
 // (defined in gemm_mfma.hip).
 hipError_t launch_splitk_reduce(const Problem& p, const Env& env, int splits, hipStream_t stream);

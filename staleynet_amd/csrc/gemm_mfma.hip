@@ -244,6 +244,7 @@ size_t f32_workspace_bytes(const Problem& p, const Env& env) {
 }  // namespace gemm
 
 hipError_t launch_gemm_f32(const Problem& p, const Env& env, hipStream_t stream) {
+    if (gemm::dma_applies(p)) return gemm::launch_gemm_f32_dma(p, env, stream);
     if (gemm::use_narrow(p)) return gemm::dispatch_layout<gemm::TileNarrow>(p, env, stream);
     return gemm::dispatch_layout<gemm::TileSquare>(p, env, stream);
 }

@@ -143,6 +143,26 @@ def test_unaligned_operands_take_the_scalar_path(gpu, variant):
     check(expected, actual[1:], 1e-5, variant)
 
 
+@pytest.mark.parametrize("variant", ["NN", "TN", "NT", "TT"])
+@pytest.mark.parametrize("rows,cols,inner,batch", [(132, 196, 100, 3), (260, 132, 36, 1), (128, 128, 32, 2),
+                                                   (36, 516, 4, 1), (520, 60, 292, 2), (24, 40, 1028, 1)])
+def test_aligned_ragged_shapes_load_straight_into_lds(gpu, variant, rows, cols, inner, batch):
+    # Sizes that are multiples of 4 but not of the 128x128x32 tile: 16-byte-aligned
+    # operands take the direct-to-LDS kernel, whose edge tiles and last partial
+    # K-step are padded by out-of-range loads that write zeros into LDS.
+    spec = MatmulSpec.new(rows, cols, inner).batched(
+        BatchStrides(batch, rows * inner, inner * cols, rows * cols)).scaled(0.7).accumulate()
+    if variant[0] == "T":
+        spec = spec.left_transposed()
+    if variant[1] == "T":
+        spec = spec.right_transposed()
+    left = oracle.random_values(batch * rows * inner, 21)
+    right = oracle.random_values(batch * inner * cols, 22)
+    initial = oracle.random_values(batch * rows * cols, 23)
+    expected = expected_for(spec, left, right, initial)
+    check(expected, run_gpu(gpu, spec, left, right, initial), 1e-5, f"{variant} {spec}")
+
+
 @pytest.mark.parametrize("variant", ["NN", "TN", "NT"])
 def test_split_k_matches_for_long_inner_dimensions(gpu, variant):
     # Few output tiles and a long K: the dispatcher splits K and reduces in order.
@@ -160,7 +180,7 @@ def test_split_k_matches_for_long_inner_dimensions(gpu, variant):
 
 
 def test_broadcast_batches_and_the_narrow_tile(gpu):
-    # N = 64 uses the 256x64 tile; the right operand is shared by every matrix.
+    # N = 64 uses the 128x64 tile; the right operand is shared by every matrix.
     rows, cols, inner, count = 300, 64, 200, 3
     spec = MatmulSpec.new(rows, cols, inner).batched(BatchStrides(count, rows * inner, 0, rows * cols))
     left = oracle.random_values(count * rows * inner, 9)
