@@ -21,11 +21,14 @@
 //  * Fragments: within a 16-deep chunk, lane half h feeds k = 8h + s to
 //    MFMA s (s = 0..7), i.e. k-groups 2h and 2h+1: two ds_read_b128 per
 //    32-row fragment. A and B use the same assignment, so products pair.
-//  * Global loads are 128-bit buffer loads, coalesced along whichever
-//    dimension is contiguous in memory (see the loaders in gemm_common.h):
-//    no per-lane branches; out-of-range lanes read 0. One kernel body serves
-//    NN, NT, TN and TT; an operand contiguous along M or N is transposed in
-//    registers on its way into LDS.
+//  * This kernel serves operands that 128-bit loads cannot: a base that is
+//    not 16-byte aligned, or a contiguous dimension, leading dimension or
+//    batch stride that is not a multiple of 4 floats. Global loads are then
+//    scalar, coalesced along whichever dimension is contiguous in memory
+//    (the scalar loaders in gemm_common.h), and edges are guarded per lane.
+//    Aligned operands take gemm_dma.hip, which loads straight into LDS. One
+//    kernel body serves NN, NT, TN and TT; an operand contiguous along M or
+//    N is transposed in registers on its way into LDS.
 //  * Double-buffered LDS; the next tile is prefetched into registers while
 //    the current one is multiplied: one barrier per BK step.
 //  * Grid: blockIdx.x enumerates (batch, split, tile), remapped so each XCD
@@ -208,7 +211,7 @@ hipError_t launch_tiles(const Problem& p, const Env& env, const Plan& plan, hipS
 
 template <class T, bool A_K, bool B_K>
 hipError_t dispatch_path(const Problem& p, const Env& env, const Plan& plan, hipStream_t stream) {
-    if (buffers_ok<T>(p)) return launch_tiles<T, A_K, B_K, true>(p, env, plan, stream);
+    // Operands that allow 128-bit loads never get here (gemm_dma.hip).
     return launch_tiles<T, A_K, B_K, false>(p, env, plan, stream);
 }
 
