@@ -7,22 +7,35 @@
 // tile would leave most of its rows idle; the product is bound by reading W
 // once from HBM, so this kernel streams W and is judged against 8 TB/s.
 //
-// Design (one launch, one memory round trip per workgroup):
-//  * A workgroup of 4 waves owns 256 output columns and a 64-row slice of K;
-//    each lane owns 4 consecutive columns. Every wave issues all 16 of its
-//    row loads (16 bytes each, 1 KB contiguous per wave-row) before the
-//    first multiply, so a workgroup's whole slice is in flight at once.
-//  * x's slice is staged in LDS and read as a broadcast.
-//  * The 4 waves' partial sums are added in wave order through LDS.
-//  * K slices beyond the first go to separate workgroups. Each writes its
-//    partial sums to the split-K workspace with device-coherent stores
-//    (agent-scope atomics: written through to where every XCD reads them),
-//    waits for them to complete and increments its column block's arrival
-//    counter; the workgroup that arrives last reads the partials with
+// Design (one launch). Reads, not arithmetic, set the time, and an MI355X CU
+// sustains only about 16 GB/s of loads (its outstanding misses over the
+// memory latency), so the first rule is to keep every CU streaming:
+//  * A workgroup of 4 waves owns a slab of 64 columns; a lane owns 4
+//    consecutive columns, 16 lanes read one 256-byte row piece and one wave
+//    load covers 4 rows. A pass is 16 (8, 4 for more rows of x) 16-byte
+//    loads in flight per lane, rows dealt to the waves in groups of 4; the
+//    next pass's loads are issued before the current one is multiplied (two
+//    register sets, loads issued unconditionally so that the compiler's
+//    wait counts stay exact).
+//  * x's rows of the pass are staged in LDS (double-buffered with the passes)
+//    and read as broadcasts. A pass's x loads are issued before its W loads:
+//    load counters complete in order, so writing x to LDS then never waits
+//    for W.
+//  * Partial sums of a wave's row lanes are added with cross-lane moves, then
+//    the 4 waves' in wave order through LDS: a fixed order.
+//  * With a slab per CU or more (the 16-codebook head: 256 slabs), each slab
+//    streams the whole of K. Narrower weights (768 to 3072 columns: 12 to 48
+//    slabs) split K into slices of whole 16-row groups, for 128-192
+//    workgroups. Each slice writes its partial sums with
+//    device-coherent stores (agent-scope: written through to where every XCD
+//    reads them), waits for them to complete and increments its slab's
+//    arrival counter; the workgroup that arrives last reads the partials with
 //    device-coherent loads, adds them in slice order, applies the
 //    reference's combine and resets the counter. No workgroup waits for
 //    another, the summation order is fixed, and no L2 write-back or
-//    invalidate (a cost of ~100 us per launch here) is needed.
+//    invalidate (a cost of ~100 us per launch here) is needed; the hand-off
+//    costs three device-wide round trips, less than streaming a weight
+//    through a tenth of the CUs would.
 #include "gemm_common.h"
 
 namespace sn {
@@ -31,10 +44,27 @@ namespace {
 using gemm::f32x4;
 
 constexpr int kThreads = 256;
-constexpr int kColumns = 256;      // per workgroup: 64 lanes x 4
-constexpr int kRowsPerWave = 16;   // loads in flight per lane
-constexpr int kSlice = 4 * kRowsPerWave;
 constexpr int kMaxRows = 16;
+// Slabs (times batches) from which K is never split: one per CU. Below
+// that, reads need more CUs than slabs: an MI355X CU sustains only about
+// 16 GB/s of loads (its outstanding misses over the memory latency), so a
+// 768-wide weight streamed by 12 slabs would take 4x longer than its split
+// hand-off costs.
+constexpr int kUnsplitSlabs = 256;
+// Workgroups a split plan aims for. Each slice adds a partial sum to write
+// and read back, so fewer than one per CU: measured on the c4 layer weights,
+// 128 (M <= 4) and 192 (M = 16) beat both 48 and 512.
+constexpr int kSplitTargetFewRows = 128;
+constexpr int kSplitTargetManyRows = 192;
+
+// Loads in flight per lane: 16 for one or two rows of x, fewer as the x
+// values and accumulators of more rows need the registers (two waves per
+// SIMD throughout).
+template <int MT>
+constexpr int loads_for() { return MT <= 2 ? 16 : MT <= 8 ? 8 : 4; }
+// Rows of W one pass covers: 4 waves x loads x rows per wave load.
+template <int MT, int LPR>
+constexpr int pass_rows() { return 4 * loads_for<MT>() * (64 / LPR); }
 
 struct GemvArgs {
     const float* x;
@@ -44,91 +74,183 @@ struct GemvArgs {
     uint32_t* counters;
     int64_t m, n, k;
     int64_t stride_x, stride_w, stride_y;
+    int64_t k_per_split;
     int32_t column_blocks;
     int32_t splits;
     int32_t accumulate;
     float scale;
 };
 
-template <int MT>
+// MT: rows of x the instantiation holds; LPR: lanes per row piece (the slab
+// is 4 * LPR columns wide).
+template <int MT, int LPR>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs args) {
-    __shared__ __attribute__((aligned(16))) float x_slice[kSlice][MT];  // [row][m]: a row's MT multipliers together
-    __shared__ f32x4 partial[MT][64];
+    constexpr int kLoads = loads_for<MT>();
+    constexpr int kRowsPerLoad = 64 / LPR;
+    constexpr int kColumns = 4 * LPR;
+    constexpr int kPassRows = pass_rows<MT, LPR>();
+    __shared__ __attribute__((aligned(16))) float x_pass[2][kPassRows][MT];  // [row][m]
+    __shared__ f32x4 partial[4][MT][LPR];
     __shared__ int arrived_last;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
+    const int row_lane = lane / LPR;  // which row of a wave load
+    const int col_lane = lane % LPR;
     const int split = blockIdx.y;
     const int64_t batch = blockIdx.z;
     const int64_t n0 = int64_t(blockIdx.x) * kColumns;
-    const int64_t k_begin = int64_t(split) * kSlice;
-    const int slice = int(min(int64_t(kSlice), args.k - k_begin));
+    const int64_t k_begin = int64_t(split) * args.k_per_split;
+    const int64_t k_end = min(args.k, k_begin + args.k_per_split);
+    const int passes = int((k_end - k_begin + kPassRows - 1) / kPassRows);
 
     const float* x = args.x + batch * args.stride_x;
     const float* w = args.w + batch * args.stride_w;
+    const bool col_ok = n0 + 4 * col_lane < args.n;
+    const int32_t lane_offset = col_ok ? int32_t((int64_t(row_lane) * args.n + 4 * col_lane) * 4) : gemm::kOutOfRange;
+    // Rows of a pass are dealt to the waves in groups of kRowsPerLoad:
+    // load u of wave v reads rows (4u + v) * kRowsPerLoad + row_lane, so a
+    // short slice still spreads over all four waves. Wave-uniform: this
+    // wave's first row and the byte distance between a lane's loads.
+    const int32_t wave_row = __builtin_amdgcn_readfirstlane(wave) * kRowsPerLoad;
+    const int32_t wave_offset = int32_t(int64_t(wave_row) * args.n * 4);
+    const int32_t load_stride = int32_t(int64_t(4 * kRowsPerLoad) * args.n * 4);
 
-    // W first: one descriptor per workgroup (scalar registers), the lane's
-    // row and column as its byte offset; rows past the slice read 0.
-    const bool col_ok = n0 + 4 * lane < args.n;
-    const __amdgpu_buffer_rsrc_t rsrc = gemm::buffer_of(w + k_begin * args.n + n0);
-    f32x4 rows[kRowsPerWave];
+    // Loads of one pass: one descriptor per pass and a scalar offset per
+    // load; rows past the slice read 0 (only the last pass of a slice can
+    // have any).
+    auto load_pass = [&](int64_t k0, f32x4 (&rows)[kLoads]) {
+        const __amdgpu_buffer_rsrc_t rsrc = gemm::buffer_of(w + k0 * args.n + n0);
+        const bool full = k0 + kPassRows <= k_end;
 #pragma unroll
-    for (int u = 0; u < kRowsPerWave; ++u) {
-        const int r = wave * kRowsPerWave + u;
-        const bool ok = col_ok && r < slice;
-        rows[u] = gemm::buffer_load4(rsrc, ok ? int32_t((int64_t(r) * args.n + 4 * lane) * 4) : gemm::kOutOfRange);
-    }
-    for (int e = tid; e < MT * kSlice; e += kThreads) {
-        const int kk = e / MT;
-        const int m = e % MT;
-        x_slice[kk][m] = (m < args.m && kk < slice) ? x[m * args.k + k_begin + kk] : 0.f;
-    }
-    __syncthreads();
+        for (int u = 0; u < kLoads; ++u) {
+            const int32_t voffset =
+                full || k0 + 4 * kRowsPerLoad * u + wave_row + row_lane < k_end ? lane_offset : gemm::kOutOfRange;
+            rows[u] = __builtin_bit_cast(
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, voffset, u * load_stride + wave_offset, 0));
+        }
+    };
+    // x values of a pass: each thread loads kXPerThread of them into
+    // registers (issued before that pass's W loads, so that waiting for them
+    // never waits for W) and later writes them to the pass's LDS buffer.
+    // Branch-free buffer loads: values past the slice or past M read 0.
+    constexpr int kXPerThread = kPassRows * MT / kThreads;
+    static_assert(kPassRows * MT % kThreads == 0, "x of a pass is whole rounds of the workgroup");
+    const __amdgpu_buffer_rsrc_t x_rsrc = gemm::buffer_of(x);
+    auto load_x = [&](int64_t k0, float (&xs)[kXPerThread]) {
+#pragma unroll
+        for (int i = 0; i < kXPerThread; ++i) {
+            const int e = tid + i * kThreads;
+            const int r = e / MT;
+            const int m = e % MT;
+            const bool ok = m < args.m && k0 + r < k_end;
+            xs[i] = gemm::buffer_load1(x_rsrc, ok ? int32_t((m * args.k + k0 + r) * 4) : gemm::kOutOfRange);
+        }
+    };
+    auto store_x = [&](const float (&xs)[kXPerThread], int buf) {
+#pragma unroll
+        for (int i = 0; i < kXPerThread; ++i) {
+            const int e = tid + i * kThreads;
+            x_pass[buf][e / MT][e % MT] = xs[i];
+        }
+    };
 
     f32x4 acc[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int u = 0; u < kRowsPerWave; ++u) {
-        const float* xr = x_slice[wave * kRowsPerWave + u];
-#pragma unroll
-        for (int m = 0; m < MT; ++m) acc[m] += xr[m] * rows[u];
-    }
 
-    // Wave-ordered sum of the four waves' partials.
-    for (int turn = 0; turn < 4; ++turn) {
-        if (wave == turn) {
-#pragma unroll
-            for (int m = 0; m < MT; ++m) partial[m][lane] = turn == 0 ? acc[m] : partial[m][lane] + acc[m];
-        }
+    // One pass: start the next pass's x and W loads, then (after the barrier
+    // that publishes this pass's x and retires the other x buffer) multiply
+    // this pass, x values read one load ahead, and stage the next pass's x.
+    auto pass = [&](int p, const f32x4 (&cur)[kLoads], f32x4 (&next)[kLoads]) {
+        const int64_t k0 = k_begin + int64_t(p) * kPassRows;
+        // Unconditional: past the last pass every load is out of range and
+        // fetches nothing. (Skipping them on a branch would make the compiler
+        // assume, where the paths join, that this pass's W loads are the most
+        // recent, and wait for the next pass's loads before multiplying.)
+        float xs[kXPerThread];
+        load_x(k0 + kPassRows, xs);
+        load_pass(k0 + kPassRows, next);
         __syncthreads();
+        const float* xr = x_pass[p & 1][wave_row + row_lane];
+        float xv[MT], xn[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) xv[m] = xr[m];
+#pragma unroll
+        for (int u = 0; u < kLoads; ++u) {
+            if (u + 1 < kLoads) {
+#pragma unroll
+                for (int m = 0; m < MT; ++m) xn[m] = xr[(u + 1) * 4 * kRowsPerLoad * MT + m];
+            }
+#pragma unroll
+            for (int m = 0; m < MT; ++m) acc[m] += xv[m] * cur[u];
+#pragma unroll
+            for (int m = 0; m < MT; ++m) xv[m] = xn[m];
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        store_x(xs, (p + 1) & 1);
+    };
+
+    f32x4 ra[kLoads], rb[kLoads];
+    {
+        float xs[kXPerThread];
+        load_x(k_begin, xs);
+        load_pass(k_begin, ra);
+        store_x(xs, 0);
+    }
+    for (int p = 0; p < passes; p += 2) {
+        pass(p, ra, rb);
+        if (p + 1 < passes) pass(p + 1, rb, ra);
     }
 
-    const int64_t per_matrix = args.m * args.n;
-    if (args.splits == 1) {
-        for (int e = tid; e < MT * 64; e += kThreads) {
-            const int m = e / 64;
-            const int64_t c = n0 + 4 * (e % 64);
-            if (m >= args.m || c >= args.n) continue;
-            float* dst = args.y + batch * args.stride_y + m * args.n + c;
-            const f32x4 sum = partial[m][e % 64];
+    // The row lanes of a wave hold the same columns: add them (xor LPR, 2 LPR,
+    // .. 32), then the waves in order through LDS.
 #pragma unroll
-            for (int j = 0; j < 4; ++j) gemm::write_output(dst + j, sum[j], args.scale, args.accumulate != 0);
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float v = acc[m][j];
+#pragma unroll
+            for (int step = LPR; step < 64; step *= 2) v += __shfl_xor(v, step);
+            acc[m][j] = v;
+        }
+    if (row_lane == 0) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m) partial[wave][m][col_lane] = acc[m];
+    }
+    __syncthreads();
+
+    // One thread per (m, column group): the wave-ordered sum of the slab.
+    const int om = tid / LPR;
+    const int oc = tid % LPR;
+    const bool owner = tid < MT * LPR;
+    f32x4 slab_sum = {0.f, 0.f, 0.f, 0.f};
+    if (owner) {
+        slab_sum = partial[0][om][oc];
+#pragma unroll
+        for (int v = 1; v < 4; ++v) slab_sum += partial[v][om][oc];
+    }
+    const int64_t out_col = n0 + 4 * oc;
+    const bool out_ok = owner && om < args.m && out_col < args.n;
+
+    if (args.splits == 1) {
+        if (out_ok) {
+            float* dst = args.y + batch * args.stride_y + om * args.n + out_col;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) gemm::write_output(dst + j, slab_sum[j], args.scale, args.accumulate != 0);
         }
         return;
     }
 
-    // Partial sums of this slice, written device-coherently; offsets from
-    // the column block's origin in this slice's workspace matrix.
-    const __amdgpu_buffer_rsrc_t mine = gemm::buffer_of(args.ws + (batch * args.splits + split) * per_matrix + n0);
-    for (int e = tid; e < MT * 64; e += kThreads) {
-        const int m = e / 64;
-        const int l = e % 64;
-        const bool inside = m < args.m && n0 + 4 * l < args.n;
-        gemm::buffer_store4_coherent(mine, inside ? int32_t((m * args.n + 4 * l) * 4) : gemm::kOutOfRange,
-                                     partial[m][l]);
-    }
+    // Partial sums of this slice, written device-coherently; offsets from the
+    // slab's origin in this slice's workspace matrix.
+    const int64_t per_matrix = args.m * args.n;
+    const __amdgpu_buffer_rsrc_t mine =
+        gemm::buffer_of(args.ws + (batch * args.splits + split) * per_matrix + n0);
+    if (owner)
+        gemm::buffer_store4_coherent(mine, out_ok ? int32_t((om * args.n + 4 * oc) * 4) : gemm::kOutOfRange,
+                                     slab_sum);
     __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are complete device-wide
     __syncthreads();
     uint32_t* counter = args.counters + batch * args.column_blocks + blockIdx.x;
@@ -140,17 +262,13 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs args) {
 
     // Last to arrive: every slice's partials are complete; add them in slice
     // order (device-coherent loads) and apply the combine.
-    const __amdgpu_buffer_rsrc_t all = gemm::buffer_of(args.ws + batch * args.splits * per_matrix + n0);
-    for (int e = tid; e < MT * 64; e += kThreads) {
-        const int m = e / 64;
-        const int l = e % 64;
-        const int64_t c = n0 + 4 * l;
-        if (m >= args.m || c >= args.n) continue;
+    if (out_ok) {
+        const __amdgpu_buffer_rsrc_t all = gemm::buffer_of(args.ws + batch * args.splits * per_matrix + n0);
         f32x4 sum = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 8
         for (int s = 0; s < args.splits; ++s)
-            sum += gemm::buffer_load4_coherent(all, int32_t((s * per_matrix + m * args.n + 4 * l) * 4));
-        float* dst = args.y + batch * args.stride_y + m * args.n + c;
+            sum += gemm::buffer_load4_coherent(all, int32_t((s * per_matrix + om * args.n + 4 * oc) * 4));
+        float* dst = args.y + batch * args.stride_y + om * args.n + out_col;
 #pragma unroll
         for (int j = 0; j < 4; ++j) gemm::write_output(dst + j, sum[j], args.scale, args.accumulate != 0);
     }
@@ -158,18 +276,39 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs args) {
 }
 
 struct GemvPlan {
+    int lanes_per_row;  // lanes per 256-byte row piece: 64-column slabs
     int column_blocks;
     int splits;
+    int64_t k_per_split;
+    int64_t pass_rows;
 };
+
+template <int LPR>
+int64_t pass_rows_for(int64_t m) {
+    return m <= 2 ? pass_rows<2, LPR>() : m <= 8 ? pass_rows<8, LPR>() : pass_rows<16, LPR>();
+}
 
 GemvPlan gemv_plan(const Problem& p) {
     GemvPlan plan;
-    plan.column_blocks = int((p.n + kColumns - 1) / kColumns);
-    plan.splits = int((p.k + kSlice - 1) / kSlice);
+    plan.lanes_per_row = 16;
+    plan.pass_rows = pass_rows_for<16>(p.m);
+    plan.column_blocks = int((p.n + 63) / 64);
+    const int64_t slabs = int64_t(plan.column_blocks) * p.batch;
+    int64_t rows_per_split = std::max<int64_t>(p.k, 1);
+    if (slabs < kUnsplitSlabs) {
+        // Enough slices for about `target` workgroups, each a whole
+        // number of wave row groups (4 waves x 4 rows).
+        const int64_t groups = (std::max<int64_t>(p.k, 1) + 15) / 16;
+        const int64_t target = p.m <= 4 ? kSplitTargetFewRows : kSplitTargetManyRows;
+        const int64_t want = std::min<int64_t>(groups, (target + slabs - 1) / slabs);
+        rows_per_split = 16 * ((groups + want - 1) / want);
+    }
+    plan.k_per_split = rows_per_split;
+    plan.splits = int((std::max<int64_t>(p.k, 1) + rows_per_split - 1) / rows_per_split);
     return plan;
 }
 
-template <int MT>
+template <int MT, int LPR>
 hipError_t launch_rows(const Problem& p, const Env& env, const GemvPlan& plan, hipStream_t stream) {
     GemvArgs args;
     args.x = p.a;
@@ -183,13 +322,23 @@ hipError_t launch_rows(const Problem& p, const Env& env, const GemvPlan& plan, h
     args.stride_x = p.stride_a;
     args.stride_w = p.stride_b;
     args.stride_y = p.stride_c;
+    args.k_per_split = plan.k_per_split;
     args.column_blocks = plan.column_blocks;
     args.splits = plan.splits;
     args.accumulate = p.accumulate ? 1 : 0;
     args.scale = p.scale;
-    hipLaunchKernelGGL(gemv_kernel<MT>, dim3(plan.column_blocks, plan.splits, unsigned(p.batch)), dim3(kThreads), 0,
-                       stream, args);
+    hipLaunchKernelGGL((gemv_kernel<MT, LPR>), dim3(plan.column_blocks, plan.splits, unsigned(p.batch)),
+                       dim3(kThreads), 0, stream, args);
     return hipGetLastError();
+}
+
+template <int LPR>
+hipError_t launch_width(const Problem& p, const Env& env, const GemvPlan& plan, hipStream_t stream) {
+    if (p.m == 1) return launch_rows<1, LPR>(p, env, plan, stream);
+    if (p.m <= 2) return launch_rows<2, LPR>(p, env, plan, stream);
+    if (p.m <= 4) return launch_rows<4, LPR>(p, env, plan, stream);
+    if (p.m <= 8) return launch_rows<8, LPR>(p, env, plan, stream);
+    return launch_rows<16, LPR>(p, env, plan, stream);
 }
 
 }  // namespace
@@ -197,13 +346,14 @@ hipError_t launch_rows(const Problem& p, const Env& env, const GemvPlan& plan, h
 bool gemv_applies(const Problem& p, const Env& env) {
     // Row-major x (K-contiguous) and row-major W (N-contiguous), aligned for
     // 16-byte loads; no mask; few rows; grid dimensions, counters and the
-    // split-K workspace large enough.
+    // split-K workspace large enough; a pass's offsets within 31 bits.
     if (!(p.m >= 1 && p.m <= kMaxRows && p.k >= 1 && p.mask == SN_MASK_NONE && p.a_k_contiguous &&
           !p.b_k_contiguous && p.lda == p.k && p.ldb == p.n && p.n % 4 == 0 && p.stride_b % 4 == 0 &&
-          gemm::aligned16(p.b) && p.batch <= 65535 &&
-          (int64_t(kSlice) * p.n + kColumns) * 4 < gemm::kMaxBufferOffset))
+          gemm::aligned16(p.b) && p.batch <= 65535 && p.n < (int64_t(1) << 30)))
         return false;
     const GemvPlan plan = gemv_plan(p);
+    if ((plan.pass_rows * p.n + 64) * 4 >= gemm::kMaxBufferOffset) return false;
+    if (p.m * p.k * 4 >= gemm::kMaxBufferOffset) return false;  // x's offsets
     if (plan.splits == 1) return true;
     // Workspace offsets of one batch's partials must fit the 31-bit range.
     if (int64_t(plan.splits) * p.m * p.n * 4 >= gemm::kMaxBufferOffset) return false;
@@ -215,11 +365,7 @@ bool gemv_applies(const Problem& p, const Env& env) {
 hipError_t launch_gemv(const Problem& p, const Env& env, hipStream_t stream) {
     if (!gemv_applies(p, env)) return hipErrorNotSupported;
     const GemvPlan plan = gemv_plan(p);
-    if (p.m == 1) return launch_rows<1>(p, env, plan, stream);
-    if (p.m <= 2) return launch_rows<2>(p, env, plan, stream);
-    if (p.m <= 4) return launch_rows<4>(p, env, plan, stream);
-    if (p.m <= 8) return launch_rows<8>(p, env, plan, stream);
-    return launch_rows<16>(p, env, plan, stream);
+    return launch_width<16>(p, env, plan, stream);
 }
 
 }  // namespace sn
