@@ -293,6 +293,13 @@ def measure_decode(gpu: Gpu, events: HipEvents, pool_bytes: int = 640 << 20, rep
     Then one token's sequence (12 blocks x 4 products + head, distinct weights, M = 1)."""
     result = {"per_shape_gbs": {}, "method": "HIP-graph replay, fp32 weights rotated through a "
               f"{pool_bytes >> 20} MB pool (> 256 MB MALL); bytes = 4(KN + MK + MN)"}
+    # Practical read roofline: a plain streaming read (sn_read_sum) of 2 GiB.
+    src, sums = gpu.zeros(Shape(1 << 29, 1)), gpu.zeros(Shape(8192, 1))
+    gpu.read_sum(src, sums)
+    ms = timed(events, gpu.stream, lambda: gpu.read_sum(src, sums), 5)
+    result["stream_read_gbs"] = round((1 << 31) / (ms * 1e-3) / 1e9, 1)
+    src.free()
+    sums.free()
     for m in (1, 4, 16):
         for name, k, n in DECODE_SHAPES:
             copies = max(2, -(-pool_bytes // (4 * k * n)))
@@ -321,6 +328,9 @@ def measure_decode(gpu: Gpu, events: HipEvents, pool_bytes: int = 640 << 20, rep
     graph.launch()
     ms = timed(events, gpu.stream, graph.launch, 5)
     graph.close()
+    head = result["per_shape_gbs"][f"M=1 head {DECODE_SHAPES[4][1]}x{DECODE_SHAPES[4][2]}"]
+    result["head_m1_frac_hbm_peak"] = round(head / PEAK_HBM_GBS, 4)
+    result["head_m1_frac_stream_read"] = round(head / result["stream_read_gbs"], 4)
     result["token_sequence"] = {"products": len(layers), "mb_per_token": round(token_bytes / 1e6, 1),
                                 "us_per_token": round(ms * 1e3, 1),
                                 "gbs": round(token_bytes / (ms * 1e-3) / 1e9, 1)}

@@ -31,6 +31,14 @@ int sn_fill_normal(void *stream, float *device, size_t count, uint64_t seed, uin
  * error code. */
 int sn_copy_device(void *stream, float *dst, const float *src, size_t count);
 
+/* Enqueues on `stream` a streaming read of `count` floats at `src` (16-byte
+ * aligned, count a multiple of 4) by `sums_count` workgroups (1..65535),
+ * each writing the sum of its grid-stride share to sums[workgroup]. Measures
+ * the practical HBM read bandwidth that read-bound kernels are compared
+ * with. Returns 0, -1 for a null buffer, -7 for a misaligned buffer or bad
+ * count, or a HIP error code. */
+int sn_read_sum(void *stream, const float *src, size_t count, float *sums, size_t sums_count);
+
 #ifdef __cplusplus
 }
 #endif

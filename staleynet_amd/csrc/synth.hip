@@ -49,7 +49,47 @@ __global__ __launch_bounds__(256) void copy_kernel(float4* __restrict__ dst, con
         dst[i] = src[i];
 }
 
+// Streaming read: each workgroup sums its grid-stride share of `src` (eight
+// non-temporal 16-byte loads in flight per lane) and writes one float. The
+// practical HBM read bandwidth that read-bound kernels are compared with.
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(256) void read_sum_kernel(const f32x4_t* __restrict__ src, uint64_t vectors,
+                                                       float* __restrict__ sums) {
+    __shared__ float partial[256];
+    const uint64_t stride = uint64_t(gridDim.x) * blockDim.x;
+    uint64_t i = blockIdx.x * uint64_t(blockDim.x) + threadIdx.x;
+    float s = 0.f;
+    for (; i + 7 * stride < vectors; i += 8 * stride) {
+        f32x4_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = __builtin_nontemporal_load(src + i + u * stride);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += (v[u][0] + v[u][1]) + (v[u][2] + v[u][3]);
+    }
+    for (; i < vectors; i += stride) {
+        const f32x4_t v = __builtin_nontemporal_load(src + i);
+        s += (v[0] + v[1]) + (v[2] + v[3]);
+    }
+    partial[threadIdx.x] = s;
+    __syncthreads();
+    for (int half = 128; half > 0; half /= 2) {
+        if (int(threadIdx.x) < half) partial[threadIdx.x] += partial[threadIdx.x + half];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) sums[blockIdx.x] = partial[0];
+}
+
 }  // namespace
+
+extern "C" int sn_read_sum(void* stream, const float* src, size_t count, float* sums, size_t sums_count) {
+    if (count == 0) return 0;
+    if (src == nullptr || sums == nullptr) return -1;
+    if (count % 4 != 0 || reinterpret_cast<uintptr_t>(src) % 16 != 0 || sums_count == 0 || sums_count > 65535)
+        return -7;
+    hipLaunchKernelGGL(read_sum_kernel, dim3(unsigned(sums_count)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       reinterpret_cast<const f32x4_t*>(src), uint64_t(count / 4), sums);
+    return int(hipGetLastError());
+}
 
 extern "C" int sn_copy_device(void* stream, float* dst, const float* src, size_t count) {
     if (count == 0) return 0;

@@ -238,10 +238,11 @@ def _library() -> ctypes.CDLL:
         lib.sn_fill_normal.argtypes = [ctypes.c_void_p, ctypes.c_void_p, size, ctypes.c_uint64, ctypes.c_uint64,
                                        ctypes.c_float, ctypes.c_float]
         lib.sn_copy_device.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, size]
+        lib.sn_read_sum.argtypes = [ctypes.c_void_p, ctypes.c_void_p, size, ctypes.c_void_p, size]
         for name in ("sn_context_create", "sn_context_create_with_workspace", "sn_context_destroy",
                      "sn_context_bind", "sn_context_set_kernel", "sn_context_get_kernel", "sn_synchronize",
                      "sn_alloc_zeroed", "sn_free", "sn_upload", "sn_download", "sn_copy_from_host", "sn_fill_zero",
-                     "sn_matmul_validate", "sn_matmul", "sn_fill_normal", "sn_copy_device"):
+                     "sn_matmul_validate", "sn_matmul", "sn_fill_normal", "sn_copy_device", "sn_read_sum"):
             getattr(lib, name).restype = ctypes.c_int
         _lib = lib
     return _lib
@@ -409,6 +410,13 @@ class Gpu:
         rc = _library().sn_copy_device(ctypes.c_void_p(self.stream), ctypes.c_void_p(dst.pointer),
                                        ctypes.c_void_p(src.pointer), len(src))
         self._check(rc, "copy_device")
+
+    def read_sum(self, src: Tensor, sums: Tensor) -> None:
+        """Streaming read of ``src`` by ``len(sums)`` workgroups, each writing its share's sum
+        (include/staleynet_synth.h): the practical HBM read-bandwidth probe."""
+        rc = _library().sn_read_sum(ctypes.c_void_p(self.stream), ctypes.c_void_p(src.pointer), len(src),
+                                    ctypes.c_void_p(sums.pointer), len(sums))
+        self._check(rc, "read_sum")
 
     def matmul(self, spec: MatmulSpec, left: Tensor, right: Tensor, output: Tensor) -> None:
         """``Gpu::matmul``: enqueue ``output = scale·op(left)·op(right) (+ output)``."""
