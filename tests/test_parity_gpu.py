@@ -224,6 +224,36 @@ def test_causal_output_mask(gpu, offset, accumulate):
         assert np.all(masked == 0.0)
 
 
+@pytest.mark.parametrize("h", [64, 100, 4])
+@pytest.mark.parametrize("mask,accumulate", [(None, False), (0, False), (37, True)])
+def test_short_inner_products_over_many_heads(gpu, h, mask, accumulate):
+    # Q.K^T-shaped NT products with K in one to four 32-deep steps (h = 100: a
+    # partial last step) over 160 heads of 260 x 260 (ragged edge tiles next
+    # to the interior tiles' fast epilogue), dense or causal, overwrite or
+    # accumulate.
+    t, count = 260, 160
+    spec = MatmulSpec.new(t, t, h).right_transposed().batched(BatchStrides(count, t * h, t * h, t * t)).scaled(0.7)
+    if accumulate:
+        spec = spec.accumulate()
+    q = oracle.random_values(count * t * h, 31)
+    k = oracle.random_values(count * t * h, 32)
+    initial = oracle.random_values(count * t * t, 33)
+    dense = initial.copy()
+    oracle.matmul_parallel(to_product(spec), q, k, dense)
+    if mask is None:
+        check(dense, run_gpu(gpu, spec, q, k, initial), 1e-5, f"h={h}")
+        return
+    actual = run_gpu(gpu, spec.causal_output(mask), q, k, initial).reshape(count, t, t)
+    dense = dense.reshape(count, t, t)
+    visible = np.broadcast_to(causal_visible(t, t, mask), dense.shape)
+    check(dense[visible], actual[visible], 1e-5, f"h={h} offset={mask}")
+    masked = actual[~visible]
+    if accumulate:
+        assert np.array_equal(masked, initial.reshape(count, t, t)[~visible])
+    else:
+        assert np.all(masked == 0.0)
+
+
 @pytest.mark.parametrize("offset", [0, 45])
 @pytest.mark.parametrize("transposed", [False, True])
 def test_causal_left_mask(gpu, offset, transposed):
