@@ -439,10 +439,17 @@ __device__ __forceinline__ void write_tile(const Args& args, const f32x16 (&acc)
         // branches. The general path below costs ~20 instructions per element,
         // which at K = 64 outweighed the tile's MFMAs.
         const bool interior = m0 + T::BM <= args.m && n0 + T::BN <= args.n;
-        const bool any_masked = !partial && output_causal && n0 + T::BN - 1 > m0 + args.query_offset;
-        if (interior && !any_masked && (partial || !accumulate)) {
-            // Split-K partials are raw sums: scale 1, which is exact.
+        if (interior && (partial || !accumulate)) {
+            // Split-K partials are raw sums: scale 1, which is exact. Tiles
+            // that cross the causal diagonal write 0 where masked (a compare
+            // and a select per element, still no branch).
             const float scale = partial ? 1.f : args.scale;
+            const bool any_masked = !partial && output_causal && n0 + T::BN - 1 > m0 + args.query_offset;
+            // col - row - offset of the lane's element at block (0, 0), r = 0.
+            // (Clamped to 32 bits: beyond +-2^30 every element is on the same side.)
+            const int64_t diagonal64 = n0 + wave_n * T::WTN + col_in_block - (m0 + wave_m * T::WTM + 4 * half) -
+                                       args.query_offset;
+            const int diagonal = int(max(min(diagonal64, int64_t(1) << 30), -(int64_t(1) << 30)));
 #pragma unroll
             for (int j = 0; j < T::FN; ++j) {
                 const int32_t column_offset =
@@ -451,8 +458,10 @@ __device__ __forceinline__ void write_tile(const Args& args, const f32x16 (&acc)
                 for (int i = 0; i < T::FM; ++i)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
-                        const int32_t row_offset = int32_t((32 * i + 8 * (r / 4) + (r % 4)) * args.n * 4);
-                        const float value = scale * acc[i][j][r];
+                        const int row = 32 * i + 8 * (r / 4) + (r % 4);
+                        const int32_t row_offset = int32_t(row * args.n * 4);
+                        float value = scale * acc[i][j][r];
+                        if (any_masked) value = diagonal + 32 * j - row > 0 ? 0.f : value;
                         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, value), rsrc, column_offset,
                                                               row_offset, 0);
                     }
@@ -503,9 +512,25 @@ __device__ __forceinline__ void write_tile(const Args& args, const f32x16 (&acc)
     }
 }
 
-// Writes zeros over a tile whose outputs are all causally masked.
+// Writes zeros over a tile whose outputs are all causally masked: 16-byte
+// stores (one vector offset per lane, rows in scalar offsets) for an interior
+// tile of a 16-byte-aligned output, element stores otherwise.
 template <class T>
 __device__ __forceinline__ void zero_tile(const Args& args, float* c_batch, int64_t m0, int64_t n0, int tid) {
+    const bool interior = m0 + T::BM <= args.m && n0 + T::BN <= args.n;
+    const bool vectors = (args.n & 3) == 0 && (reinterpret_cast<uintptr_t>(c_batch) & 15) == 0;
+    if (interior && vectors) {
+        constexpr int kPerRow = T::BN / 4;                // 16-byte groups per tile row
+        constexpr int kRowsPerRound = T::THREADS / kPerRow;
+        const __amdgpu_buffer_rsrc_t rsrc = buffer_of(c_batch + m0 * args.n + n0);
+        const int32_t lane_offset = int32_t(((tid / kPerRow) * args.n + 4 * (tid % kPerRow)) * 4);
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+        for (int q = 0; q < T::BM / kRowsPerRound; ++q)
+            __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, rsrc, lane_offset,
+                                                   int32_t(q * kRowsPerRound * args.n * 4), 0);
+        return;
+    }
     for (int e = tid; e < T::BM * T::BN; e += T::THREADS) {
         const int64_t r = m0 + e / T::BN;
         const int64_t col = n0 + e % T::BN;
