@@ -389,7 +389,7 @@ def _cpu_model() -> str:
 # ---- rocprofv3 summaries ----------------------------------------------------------------
 
 # The roofline kernel: the direct-to-LDS fp32 MFMA kernel, 128x128 tile, A K-contiguous, B N-contiguous.
-NN_KERNEL_KEY = "gemm_f32_dma_kernel<sn::gemm::Tile<128, 128, 32, 2, 2>, true, false>"
+NN_KERNEL_KEY = "gemm_f32_dma_kernel<sn::gemm::(anonymous namespace)::DmaConfig<sn::gemm::Tile<128, 128, 32, 2, 2>, 2>, true, false>"
 COPY_KERNEL_KEY = "copy_kernel("
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "gemm_f32_nn_111M_hbm_traffic.txt")
 
@@ -540,7 +540,7 @@ def main() -> int:
     nn_flops_per_launch = nn["flops"] / nn["launches"]
     nn_ms_per_launch = nn["ms"] / nn["launches"]
     achieved = nn_flops_per_launch / (nn_ms_per_launch * 1e-3) / 1e12
-    roofline = {"kernel": "gemm_f32_dma_kernel<Tile<128,128,32,2,2>, A K-contiguous, B N-contiguous> "
+    roofline = {"kernel": "gemm_f32_dma_kernel<DmaConfig<Tile<128,128,32,2,2>, 2 stages>, A K-contiguous, B N-contiguous> "
                           "(every forward NN product of the set)",
                 "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "traffic": load_traffic(),

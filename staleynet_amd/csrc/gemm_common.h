@@ -65,20 +65,23 @@ __device__ __forceinline__ void buffer_store4_coherent(__amdgpu_buffer_rsrc_t rs
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, value), rsrc, offset, 0, kDeviceCoherent);
 }
 
-// f32 -> bf16, round to nearest, ties to even (IEEE 754 roundTiesToEven on
-// the 16 dropped bits); NaN stays a (quiet) NaN.
-__device__ __forceinline__ uint32_t bf16_bits(float value) {
-    const uint32_t bits = __builtin_bit_cast(uint32_t, value);
-    if ((bits & 0x7FFFFFFFu) > 0x7F800000u) return (bits >> 16) | 0x40u;
-    const uint32_t lsb = (bits >> 16) & 1u;
-    return (bits + 0x7FFFu + lsb) >> 16;
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two floats -> two bf16 in one 32-bit word (element 0 in the low half):
+// gfx950's v_cvt_pk_bf16_f32, which rounds by the MODE register's f32
+// rounding mode (round to nearest, ties to even, by default) and keeps NaN a
+// quiet NaN. One instruction per pair instead of a shift/add/compare
+// sequence per element.
+__device__ __forceinline__ uint32_t pack2_bf16(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
 }
 
 // Four floats as four bf16 packed into 8 bytes, element 0 in the low half.
 __device__ __forceinline__ u32x2 pack_bf16(f32x4 x) {
     u32x2 packed;
-    packed[0] = bf16_bits(x[0]) | (bf16_bits(x[1]) << 16);
-    packed[1] = bf16_bits(x[2]) | (bf16_bits(x[3]) << 16);
+    packed[0] = pack2_bf16(x[0], x[1]);
+    packed[1] = pack2_bf16(x[2], x[3]);
     return packed;
 }
 
@@ -625,6 +628,11 @@ Args make_args(const Problem& p, const Env& env, const Plan& plan) {
 // (aligned operands) and its launcher.
 bool dma_applies(const Problem& p);
 hipError_t launch_gemm_f32_dma(const Problem& p, const Env& env, hipStream_t stream);
+// The bf16 variant of the direct-to-LDS kernel: whether it serves `p`, its
+// launcher and the split-K workspace it uses.
+bool bf16_dma_applies(const Problem& p);
+hipError_t launch_gemm_bf16_dma(const Problem& p, const Env& env, hipStream_t stream);
+size_t bf16_dma_workspace_bytes(const Problem& p, const Env& env);
 
 // Adds the split-K partial sums in split order and applies the combine
 // (defined in gemm_mfma.hip).

@@ -1,4 +1,5 @@
-// fp32 matrix-core GEMM fed by direct global -> LDS loads.
+// fp32 matrix-core GEMM fed by direct global -> LDS loads, and its
+// bf16-input / fp32-accumulate variant.
 //
 // Same contract, tiles, grid schedule, masks, split-K and epilogue as the
 // kernel in gemm_mfma.hip (which remains the path for operands that are not
@@ -37,16 +38,25 @@ namespace gemm {
 namespace {
 
 typedef __attribute__((address_space(3))) void* lds_void;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+
+// Eight floats rounded to bf16 (four v_cvt_pk_bf16_f32).
+__device__ __forceinline__ bf16x8 to_bf16x8(const float (&v)[8]) {
+    const f32x8 x = {v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]};
+    return __builtin_convertvector(x, bf16x8);
+}
 
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, const void* lds, int32_t offset) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void)lds, 16, offset, 0, 0, 0);
 }
 
 // K-contiguous operand: ROWS rows of 32 k per stage, ROWS / 8 load
-// instructions of 8 rows each, ROWS / 32 per wave.
-template <int ROWS>
+// instructions of 8 rows each, shared out over the WAVES waves.
+template <int ROWS, int WAVES>
 struct OperandK {
-    static constexpr int PER_WAVE = ROWS / 32;
+    static constexpr int PER_WAVE = ROWS / (8 * WAVES);
+    static_assert(ROWS % (8 * WAVES) == 0, "whole load instructions per wave");
     int32_t offset[PER_WAVE];  // byte offset from the tile origin, row part
     int32_t group_k[PER_WAVE]; // the k-group (times 4) this lane fetches
 
@@ -89,10 +99,12 @@ struct OperandK {
 };
 
 // Row-contiguous operand: 32 k rows of ROWS contiguous values per stage,
-// ROWS / 8 load instructions of 256 values (64 lanes x 4), ROWS / 32 per wave.
-template <int ROWS>
+// ROWS / 8 load instructions of 256 values (64 lanes x 4), shared out over
+// the WAVES waves.
+template <int ROWS, int WAVES>
 struct OperandR {
-    static constexpr int PER_WAVE = ROWS / 32;
+    static constexpr int PER_WAVE = ROWS / (8 * WAVES);
+    static_assert(ROWS % (8 * WAVES) == 0 && ROWS <= 256, "whole load instructions per wave");
     static constexpr int LANES_PER_K = ROWS / 4;   // lanes covering one k row
     static constexpr int K_PER_LOAD = 64 / LANES_PER_K;
     int32_t offset[PER_WAVE];
@@ -129,17 +141,25 @@ struct OperandR {
     }
 };
 
-template <bool K_CONTIGUOUS, int ROWS>
-using OperandFor = typename std::conditional<K_CONTIGUOUS, OperandK<ROWS>, OperandR<ROWS>>::type;
+template <bool K_CONTIGUOUS, int ROWS, int WAVES>
+using OperandFor =
+    typename std::conditional<K_CONTIGUOUS, OperandK<ROWS, WAVES>, OperandR<ROWS, WAVES>>::type;
 
 // Multiplies one staged K-step: two 16-deep chunks. Chunk 0's fragments
 // are read first; then `prefetch` starts the next K-step's loads into the
 // other stage, and those loads and chunk 1's fragment reads are interleaved
-// one per MFMA with chunk 0's MFMAs, so that the wave issues them in the
-// MFMAs' shadow instead of stalling on them (left alone, the scheduler
-// issues each LDS read just before its first MFMA and waits on it there).
-template <class T, bool A_K, bool B_K, class Prefetch>
-__device__ __forceinline__ void multiply_stage(const OperandFor<A_K, T::BM>& oa, const OperandFor<B_K, T::BN>& ob,
+// with chunk 0's MFMAs, so that the wave issues them in the MFMAs' shadow
+// instead of stalling on them (left alone, the scheduler issues each LDS
+// read just before its first MFMA and waits on it there).
+//
+// fp32: eight v_mfma_f32_32x32x2_f32 per block and chunk, lane half h
+// feeding k = 8h + s to MFMA s. bf16: the same eight fp32 values per lane
+// are rounded to bf16 (v_cvt_pk_bf16_f32, nearest-even) and feed one
+// v_mfma_f32_32x32x16_bf16, whose lane half h holds k = 8h .. 8h+7: the
+// same k pairing of A and B, one instruction per block and chunk.
+template <class T, bool A_K, bool B_K, bool BF16, class Prefetch>
+__device__ __forceinline__ void multiply_stage(const OperandFor<A_K, T::BM, T::THREADS / 64>& oa,
+                                               const OperandFor<B_K, T::BN, T::THREADS / 64>& ob,
                                                const f32x4* sa, const f32x4* sb, f32x16 (&acc)[T::FM][T::FN],
                                                int lane, int wave_m, int wave_n, Prefetch&& prefetch) {
     static_assert(T::BK == 32, "two 16-deep chunks per stage");
@@ -153,34 +173,66 @@ __device__ __forceinline__ void multiply_stage(const OperandFor<A_K, T::BM>& oa,
         for (int j = 0; j < T::FN; ++j) ob.fragment(sb, wave_n * T::WTN + 32 * j + row, c, half, bv[c][j]);
     };
     auto multiply = [&](int c) {
+        if constexpr (BF16) {
+            bf16x8 a8[T::FM], b8[T::FN];
 #pragma unroll
-        for (int s = 0; s < 8; ++s)
+            for (int i = 0; i < T::FM; ++i) a8[i] = to_bf16x8(av[c][i]);
+#pragma unroll
+            for (int j = 0; j < T::FN; ++j) b8[j] = to_bf16x8(bv[c][j]);
 #pragma unroll
             for (int i = 0; i < T::FM; ++i)
 #pragma unroll
                 for (int j = 0; j < T::FN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[c][i][s], bv[c][j][s], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a8[i], b8[j], acc[i][j], 0, 0, 0);
+        } else {
+#pragma unroll
+            for (int s = 0; s < 8; ++s)
+#pragma unroll
+                for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < T::FN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[c][i][s], bv[c][j][s], acc[i][j], 0, 0, 0);
+        }
     };
     constexpr int DS = T::FM * (A_K ? 2 : 4) + T::FN * (B_K ? 2 : 4);
-    constexpr int VM = T::BM / 32 + T::BN / 32;
-    constexpr int MF = 8 * T::FM * T::FN;
+    constexpr int VM = (T::BM + T::BN) / (8 * (T::THREADS / 64));
     read(0);
     __builtin_amdgcn_sched_barrier(0);
     prefetch();
     read(1);
     multiply(0);
     multiply(1);
+    if constexpr (BF16) {
+        // FM * FN MFMAs per chunk: chunk 0's conversions, then its MFMAs
+        // with the loads and chunk 1's reads spread over them, then chunk
+        // 1's conversions and MFMAs.
+        constexpr int MF = T::FM * T::FN;
+        constexpr int CVT = 4 * (T::FM + T::FN);
+        constexpr int VM_PER = (VM + MF - 1) / MF;
+        constexpr int DS_PER = (DS + MF - 1) / MF;
+        __builtin_amdgcn_sched_group_barrier(0x002, CVT, 0);
 #pragma unroll
-    for (int x = 0; x < VM; ++x) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-    }
+        for (int x = 0; x < MF; ++x) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x020, VM_PER, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, DS_PER, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x002, CVT, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, MF, 0);
+    } else {
+        constexpr int MF = 8 * T::FM * T::FN;
 #pragma unroll
-    for (int x = 0; x < DS; ++x) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        for (int x = 0; x < VM; ++x) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        }
+#pragma unroll
+        for (int x = 0; x < DS; ++x) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 2 * MF - VM - DS, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 2 * MF - VM - DS, 0);
 }
 
 // Causal-left tiles on the diagonal: zeroes the staged A values of the
@@ -201,26 +253,60 @@ __device__ __forceinline__ void mask_stage(f32x4* sa, int64_t m0, int64_t k0, in
     }
 }
 
-// Waves per SIMD that the two LDS stages allow (160 KB of LDS per CU).
-template <class T>
+// Waves per SIMD that STAGES LDS stages allow (160 KB of LDS per CU).
+template <class T, int STAGES>
 constexpr int dma_waves_per_eu() {
-    return (160 * 1024 / ((T::BM + T::BN) * T::BK * 4 * 2)) * (T::THREADS / 64) / 4;
+    return (160 * 1024 / ((T::BM + T::BN) * T::BK * 4 * STAGES)) * (T::THREADS / 64) / 4;
 }
 
+// Waits until at most PENDING of this wave's vector-memory instructions are
+// outstanding (vmcnt; expcnt and lgkmcnt left at their maxima; gfx9
+// encoding: vmcnt bits 3:0 and 15:14).
+template <int PENDING>
 __device__ __forceinline__ void wait_loads() {
-    // vmcnt(0), expcnt and lgkmcnt left at their maxima (gfx9 encoding).
-    __builtin_amdgcn_s_waitcnt(0x0F70);
+    static_assert(PENDING >= 0 && PENDING < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (PENDING & 15) | ((PENDING >> 4) << 14));
 }
 
-template <class T, bool A_K, bool B_K>
-// LDS (two stages) already caps a CU at two 128x128 workgroups (two waves
-// per SIMD): let the register allocator use that budget instead of
-// squeezing for occupancy it cannot reach.
-__global__ __launch_bounds__(T::THREADS) __attribute__((amdgpu_waves_per_eu(1, dma_waves_per_eu<T>())))
-void gemm_f32_dma_kernel(Args args) {
+// Workgroup barrier for the stage hand-off. __syncthreads() fences every
+// address space, and the compiler implements the fence by waiting for all of
+// the wave's outstanding vector-memory loads, including the prefetches of
+// later stages that are meant to stay in flight (an LDS-only fence does the
+// same, since the direct-to-LDS loads are LDS writes). Here the stage's own
+// loads are waited for explicitly (wait_loads), this wave's LDS writes
+// (mask_stage) by lgkmcnt(0), and the empty asm statements keep the
+// compiler from moving memory accesses across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt left at their maxima
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// One output tile (the whole of both kernels below); BF16 selects the
+// matrix instruction fed from the fp32 LDS stages.
+//
+// STAGES LDS stages: loads run STAGES - 1 K-steps ahead of the MFMAs. At
+// each step a wave waits until only the later stages' loads are still in
+// flight (a wave's loads complete in order), the barrier makes every wave's
+// loads of this stage visible and retires every read of the stage that the
+// next prefetch overwrites, and the prefetch is issued during the multiply.
+// Every step prefetches, unconditionally: loads past the tile's K range are
+// out of bounds (no memory traffic, zeros), which keeps each step's load
+// count, and so the wait count, fixed. The loop is unrolled by STAGES so
+// that every LDS access names a statically known stage array; the compiler
+// then never waits on loads into the other stages before its LDS reads.
+template <class T, int STAGES, bool A_K, bool B_K, bool BF16>
+__device__ __forceinline__ void dma_tile(const Args& args) {
+    static_assert(STAGES >= 2 && STAGES <= 4, "two to four LDS stages");
+    constexpr int WAVES = T::THREADS / 64;
     constexpr int A_SLOTS = T::BM * T::BK / 4;
     constexpr int B_SLOTS = T::BN * T::BK / 4;
     __shared__ f32x4 a0[A_SLOTS], b0[B_SLOTS], a1[A_SLOTS], b1[B_SLOTS];
+    __shared__ f32x4 a2[STAGES > 2 ? A_SLOTS : 1], b2[STAGES > 2 ? B_SLOTS : 1];
+    __shared__ f32x4 a3[STAGES > 3 ? A_SLOTS : 1], b3[STAGES > 3 ? B_SLOTS : 1];
+    f32x4* const stage_a[4] = {a0, a1, a2, a3};
+    f32x4* const stage_b[4] = {b0, b1, b2, b3};
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -259,8 +345,8 @@ void gemm_f32_dma_kernel(Args args) {
     const float* a = args.a + batch * args.stride_a + (A_K ? m0 * args.lda : m0);
     const float* b = args.b + batch * args.stride_b + (B_K ? n0 * args.ldb : n0);
 
-    OperandFor<A_K, T::BM> oa;
-    OperandFor<B_K, T::BN> ob;
+    OperandFor<A_K, T::BM, WAVES> oa;
+    OperandFor<B_K, T::BN, WAVES> ob;
     oa.init(args.lda, m0, args.m, lane, wave);
     ob.init(args.ldb, n0, args.n, lane, wave);
 
@@ -272,48 +358,63 @@ void gemm_f32_dma_kernel(Args args) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
+    // Loads stop at the tile's K end: a partial last step, and prefetches
+    // past the last step, read zeros.
     auto issue = [&](const f32x4* sa, const f32x4* sb, int64_t k0) {
-        if constexpr (A_K) oa.issue(sa, a, k0, args.k, wave);
-        else oa.issue(sa, a, args.lda, k0, args.k, wave);
-        if constexpr (B_K) ob.issue(sb, b, k0, args.k, wave);
-        else ob.issue(sb, b, args.ldb, k0, args.k, wave);
+        if constexpr (A_K) oa.issue(sa, a, k0, k_end, wave);
+        else oa.issue(sa, a, args.lda, k0, k_end, wave);
+        if constexpr (B_K) ob.issue(sb, b, k0, k_end, wave);
+        else ob.issue(sb, b, args.ldb, k0, k_end, wave);
     };
-    // One K-step: wait for this stage's loads (every wave's, via the
-    // barrier, which also retires every read of the other stage), start the
-    // next step's loads into the other stage, multiply this one.
-    auto step_on = [&](f32x4* sa, f32x4* sb, const f32x4* na, const f32x4* nb, int64_t k0, bool more) {
-        wait_loads();
-        __syncthreads();
+    // One K-step on stage S (static): wait for this stage's loads, start
+    // the loads STAGES - 1 steps ahead into the stage read last step,
+    // multiply this stage.
+    constexpr int LOADS_PER_STEP = (T::BM + T::BN) / (8 * WAVES);
+    auto step_on = [&](auto stage, int64_t k0) {
+        constexpr int S = decltype(stage)::value;
+        constexpr int P = (S + STAGES - 1) % STAGES;
+        wait_loads<LOADS_PER_STEP * (STAGES - 2)>();
+        lds_barrier();
         // Causal-left: A values past the diagonal are zeroed in LDS on the
         // K-steps that reach it (A K-contiguous: keys past the tile's first
         // query; A transposed: queries before the tile's last key).
         if (left_causal && (A_K ? k0 + T::BK - 1 > m0 + args.query_offset : k0 + args.query_offset < row_last)) {
-            mask_stage<T, A_K>(sa, m0, k0, args.query_offset, tid);
-            __syncthreads();
+            mask_stage<T, A_K>(stage_a[S], m0, k0, args.query_offset, tid);
+            lds_barrier();
         }
-        multiply_stage<T, A_K, B_K>(oa, ob, sa, sb, acc, lane, wave_m, wave_n, [&] {
-            if (more) issue(na, nb, k0 + T::BK);
+        multiply_stage<T, A_K, B_K, BF16>(oa, ob, stage_a[S], stage_b[S], acc, lane, wave_m, wave_n, [&] {
+            issue(stage_a[P], stage_b[P], k0 + (STAGES - 1) * T::BK);
         });
     };
 
     const int steps = k_end > k_begin ? int((k_end - k_begin + T::BK - 1) / T::BK) : 0;
     if (steps > 0) {
-        issue(a0, b0, k_begin);
-        // Pairs of steps that both prefetch (branch-free bodies), then the
-        // last one or two steps.
+#pragma unroll
+        for (int s = 0; s < STAGES - 1; ++s) issue(stage_a[s], stage_b[s], k_begin + s * T::BK);
+        // Whole rounds of STAGES steps, then the remaining steps, which
+        // start again at stage 0.
+        using I0 = std::integral_constant<int, 0>;
+        using I1 = std::integral_constant<int, 1>;
+        using I2 = std::integral_constant<int, 2>;
+        using I3 = std::integral_constant<int, 3>;
         int step = 0;
-        for (; step + 2 < steps; step += 2) {
+        for (; step + STAGES <= steps; step += STAGES) {
             const int64_t k0 = k_begin + int64_t(step) * T::BK;
-            step_on(a0, b0, a1, b1, k0, true);
-            step_on(a1, b1, a0, b0, k0 + T::BK, true);
+            step_on(I0{}, k0);
+            step_on(I1{}, k0 + T::BK);
+            if constexpr (STAGES > 2) step_on(I2{}, k0 + 2 * T::BK);
+            if constexpr (STAGES > 3) step_on(I3{}, k0 + 3 * T::BK);
         }
+        const int left = steps - step;
         const int64_t k0 = k_begin + int64_t(step) * T::BK;
-        if (steps - step == 2) {
-            step_on(a0, b0, a1, b1, k0, true);
-            step_on(a1, b1, a0, b0, k0 + T::BK, false);
-        } else {
-            step_on(a0, b0, a1, b1, k0, false);
-        }
+        if (left > 0) step_on(I0{}, k0);
+        if constexpr (STAGES > 2)
+            if (left > 1) step_on(I1{}, k0 + T::BK);
+        if constexpr (STAGES > 3)
+            if (left > 2) step_on(I2{}, k0 + 2 * T::BK);
+        // The prefetches past the last step are still writing (zeros) into
+        // LDS: let them land before the workgroup can end.
+        wait_loads<0>();
     }
 
     const bool partial = args.splits > 1;
@@ -321,8 +422,36 @@ void gemm_f32_dma_kernel(Args args) {
     write_tile<T, true>(args, acc, out, m0, n0, wave_m, wave_n, lane, partial);
 }
 
-template <class T, bool A_K, bool B_K>
+// A tile shape with its number of LDS stages.
+template <class T_, int STAGES_>
+struct DmaConfig {
+    using T = T_;
+    static constexpr int STAGES = STAGES_;
+};
+
+// LDS (the stages) already caps a CU's workgroups: let the register
+// allocator use that budget instead of squeezing for occupancy it cannot
+// reach.
+template <class C, bool A_K, bool B_K>
+__global__ __launch_bounds__(C::T::THREADS)
+__attribute__((amdgpu_waves_per_eu(1, dma_waves_per_eu<typename C::T, C::STAGES>())))
+void gemm_f32_dma_kernel(Args args) {
+    dma_tile<typename C::T, C::STAGES, A_K, B_K, false>(args);
+}
+
+// bf16-input / fp32-accumulate variant (SN_PRECISION_BF16): the same loads,
+// LDS stages, schedule and epilogue; each lane rounds its fp32 fragments to
+// bf16 just before the matrix instruction.
+template <class C, bool A_K, bool B_K>
+__global__ __launch_bounds__(C::T::THREADS)
+__attribute__((amdgpu_waves_per_eu(1, dma_waves_per_eu<typename C::T, C::STAGES>())))
+void gemm_bf16_dma_kernel(Args args) {
+    dma_tile<typename C::T, C::STAGES, A_K, B_K, true>(args);
+}
+
+template <class C, bool A_K, bool B_K, bool BF16>
 hipError_t launch_dma_tiles(const Problem& p, const Env& env, hipStream_t stream) {
+    using T = typename C::T;
     const Plan plan = plan_for<T>(p, env);
     Args args = make_args<T>(p, env, plan);
     const int64_t per_batch = int64_t(plan.tiles_m) * plan.tiles_n * plan.splits;
@@ -331,8 +460,12 @@ hipError_t launch_dma_tiles(const Problem& p, const Env& env, hipStream_t stream
     for (int64_t first = 0; first < p.batch; first += chunk) {
         const int64_t count = std::min<int64_t>(chunk, p.batch - first);
         args.batch_base = first;
-        hipLaunchKernelGGL((gemm_f32_dma_kernel<T, A_K, B_K>), dim3(unsigned(count * per_batch)), dim3(T::THREADS),
-                           0, stream, args);
+        if constexpr (BF16)
+            hipLaunchKernelGGL((gemm_bf16_dma_kernel<C, A_K, B_K>), dim3(unsigned(count * per_batch)),
+                               dim3(T::THREADS), 0, stream, args);
+        else
+            hipLaunchKernelGGL((gemm_f32_dma_kernel<C, A_K, B_K>), dim3(unsigned(count * per_batch)),
+                               dim3(T::THREADS), 0, stream, args);
         hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
     }
@@ -340,16 +473,33 @@ hipError_t launch_dma_tiles(const Problem& p, const Env& env, hipStream_t stream
     return hipSuccess;
 }
 
-template <class T>
+template <class C, bool BF16>
 hipError_t launch_dma_layout(const Problem& p, const Env& env, hipStream_t stream) {
-    if (p.a_k_contiguous && p.b_k_contiguous) return launch_dma_tiles<T, true, true>(p, env, stream);
-    if (p.a_k_contiguous) return launch_dma_tiles<T, true, false>(p, env, stream);
-    if (p.b_k_contiguous) return launch_dma_tiles<T, false, true>(p, env, stream);
-    return launch_dma_tiles<T, false, false>(p, env, stream);
+    if (p.a_k_contiguous && p.b_k_contiguous) return launch_dma_tiles<C, true, true, BF16>(p, env, stream);
+    if (p.a_k_contiguous) return launch_dma_tiles<C, true, false, BF16>(p, env, stream);
+    if (p.b_k_contiguous) return launch_dma_tiles<C, false, true, BF16>(p, env, stream);
+    return launch_dma_tiles<C, false, false, BF16>(p, env, stream);
 }
 
-using DmaSquare = Tile<128, 128, 32, 2, 2>;
-using DmaNarrow = Tile<128, 64, 32, 4, 1>;
+using DmaSquare = DmaConfig<Tile<128, 128, 32, 2, 2>, 2>;
+using DmaNarrow = DmaConfig<Tile<128, 64, 32, 4, 1>, 2>;
+
+// bf16 tiles. With fp32 operands in HBM the bf16 products are bound by the
+// operand bytes each CU pulls from L2 per FLOP, so wide outputs take a
+// 128x256 tile (8 waves of 64x64, three 48 KB stages, one workgroup per
+// CU: 43 FLOP per loaded byte instead of 32). Outputs narrower than 2048
+// columns have too few such tiles to fill the CUs and keep 128x128.
+// Measured on the 111.5M set: 128x256 is 7-23 % faster at N >= 2304 and
+// up to 40 % slower at N = 768.
+using Bf16Square = DmaConfig<Tile<128, 128, 32, 2, 2>, 2>;
+using Bf16Wide = DmaConfig<Tile<128, 256, 32, 2, 4>, 3>;
+using Bf16Narrow = DmaNarrow;
+constexpr int64_t kBf16WideColumns = 2048;
+
+template <class C>
+bool config_applies(const Problem& p) {
+    return buffers_ok<typename C::T>(p);
+}
 
 }  // namespace
 
@@ -357,12 +507,31 @@ using DmaNarrow = Tile<128, 64, 32, 4, 1>;
 // batch strides, and every per-lane offset of one K-step within the buffer
 // offset range (the same conditions as the buffer-load path of gemm_mfma.hip).
 bool dma_applies(const Problem& p) {
-    return p.n <= 64 ? buffers_ok<DmaNarrow>(p) : buffers_ok<DmaSquare>(p);
+    return p.n <= 64 ? config_applies<DmaNarrow>(p) : config_applies<DmaSquare>(p);
+}
+
+bool bf16_dma_applies(const Problem& p) {
+    if (p.n <= 64) return config_applies<Bf16Narrow>(p);
+    if (p.n >= kBf16WideColumns) return config_applies<Bf16Wide>(p);
+    return config_applies<Bf16Square>(p);
 }
 
 hipError_t launch_gemm_f32_dma(const Problem& p, const Env& env, hipStream_t stream) {
-    if (p.n <= 64) return launch_dma_layout<DmaNarrow>(p, env, stream);
-    return launch_dma_layout<DmaSquare>(p, env, stream);
+    if (p.n <= 64) return launch_dma_layout<DmaNarrow, false>(p, env, stream);
+    return launch_dma_layout<DmaSquare, false>(p, env, stream);
+}
+
+hipError_t launch_gemm_bf16_dma(const Problem& p, const Env& env, hipStream_t stream) {
+    if (p.n <= 64) return launch_dma_layout<Bf16Narrow, true>(p, env, stream);
+    if (p.n >= kBf16WideColumns) return launch_dma_layout<Bf16Wide, true>(p, env, stream);
+    return launch_dma_layout<Bf16Square, true>(p, env, stream);
+}
+
+size_t bf16_dma_workspace_bytes(const Problem& p, const Env& env) {
+    const Plan plan = p.n <= 64                    ? plan_for<Bf16Narrow::T>(p, env)
+                      : p.n >= kBf16WideColumns ? plan_for<Bf16Wide::T>(p, env)
+                                                : plan_for<Bf16Square::T>(p, env);
+    return plan.splits > 1 ? size_t(plan.splits) * size_t(p.m) * size_t(p.n) * sizeof(float) : 0;
 }
 
 }  // namespace gemm
