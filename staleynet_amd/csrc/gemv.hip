@@ -10,9 +10,10 @@
 // Design (one launch). Reads, not arithmetic, set the time, and an MI355X CU
 // sustains only about 16 GB/s of loads (its outstanding misses over the
 // memory latency), so the first rule is to keep every CU streaming:
-//  * A workgroup of 4 waves owns a slab of 64 columns; a lane owns 4
+//  * A workgroup of 4 waves (8 on the matrix-core path) owns a slab of 64
+//    columns; a lane owns 4
 //    consecutive columns, 16 lanes read one 256-byte row piece and one wave
-//    load covers 4 rows. A pass is 16 (8, 4 for more rows of x) 16-byte
+//    load covers 4 rows. A pass is 16 (8 for 3-4 rows of x) 16-byte
 //    loads in flight per lane, rows dealt to the waves in groups of 4; the
 //    next pass's loads are issued before the current one is multiplied (two
 //    register sets, loads issued unconditionally so that the compiler's
@@ -21,8 +22,12 @@
 //    and read as broadcasts. A pass's x loads are issued before its W loads:
 //    load counters complete in order, so writing x to LDS then never waits
 //    for W.
-//  * Partial sums of a wave's row lanes are added with cross-lane moves, then
-//    the 4 waves' in wave order through LDS: a fixed order.
+//  * Up to 4 rows of x: FMAs on the VALU, then the partial sums of a wave's
+//    row lanes are added with cross-lane moves. 5 to 16 rows: each wave load
+//    of W (4 rows x 64 columns) feeds four v_mfma_f32_16x16x4f32, one per
+//    column of a lane's 4, with x's 4 rows as the A operand; the matrix core
+//    sums the 4 rows. Then the waves' partial sums are added in wave order
+//    through LDS: a fixed order.
 //  * With a slab per CU or more (the 16-codebook head: 256 slabs), each slab
 //    streams the whole of K. Narrower weights (768 to 3072 columns: 12 to 48
 //    slabs) split K into slices of whole 16-row groups, for 128-192
@@ -43,7 +48,11 @@ namespace {
 
 using gemm::f32x4;
 
-constexpr int kThreads = 256;
+// Waves per workgroup: 4 on the VALU paths (one per SIMD), 8 on the
+// matrix-core path, whose MFMAs (a quarter of a pass's time at 16 rows) then
+// run on one wave of a SIMD while the other waits for its loads.
+template <int MT>
+constexpr int waves_for();
 constexpr int kMaxRows = 16;
 // Cache policy of the W loads: non-temporal (each weight byte is read once
 // per launch). A streaming-read probe on MI355X reaches 6.5 TB/s with it and
@@ -61,14 +70,23 @@ constexpr int kUnsplitSlabs = 256;
 constexpr int kSplitTargetFewRows = 128;
 constexpr int kSplitTargetManyRows = 192;
 
-// Loads in flight per lane: 16 for one or two rows of x, fewer as the x
-// values and accumulators of more rows need the registers (two waves per
-// SIMD throughout).
+// Rows of x from which the products go to the matrix cores: 16 output rows
+// cost one v_mfma_f32_16x16x4f32 per 4 rows x 16 columns of W, where the
+// VALU would spend 16 FMAs per W value and hold 16 accumulators per column.
 template <int MT>
-constexpr int loads_for() { return MT <= 2 ? 16 : MT <= 8 ? 8 : 4; }
-// Rows of W one pass covers: 4 waves x loads x rows per wave load.
+constexpr bool uses_mfma() { return MT >= 8; }
+
+// Loads in flight per lane: 16 for one or two rows of x and on the matrix
+// cores (whose accumulators are 16 registers per lane for any MT), 8 for
+// four rows, whose x values and accumulators need the registers (two waves
+// per SIMD throughout).
+template <int MT>
+constexpr int loads_for() { return MT <= 2 ? 16 : 8; }
+template <int MT>
+constexpr int waves_for() { return uses_mfma<MT>() ? 8 : 4; }
+// Rows of W one pass covers: waves x loads x rows per wave load.
 template <int MT, int LPR>
-constexpr int pass_rows() { return 4 * loads_for<MT>() * (64 / LPR); }
+constexpr int pass_rows() { return waves_for<MT>() * loads_for<MT>() * (64 / LPR); }
 
 struct GemvArgs {
     const float* x;
@@ -88,13 +106,15 @@ struct GemvArgs {
 // MT: rows of x the instantiation holds; LPR: lanes per row piece (the slab
 // is 4 * LPR columns wide).
 template <int MT, int LPR>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs args) {
+__global__ __launch_bounds__(64 * waves_for<MT>()) void gemv_kernel(GemvArgs args) {
+    constexpr int kWaves = waves_for<MT>();
+    constexpr int kThreads = 64 * kWaves;
     constexpr int kLoads = loads_for<MT>();
     constexpr int kRowsPerLoad = 64 / LPR;
     constexpr int kColumns = 4 * LPR;
     constexpr int kPassRows = pass_rows<MT, LPR>();
     __shared__ __attribute__((aligned(16))) float x_pass[2][kPassRows][MT];  // [row][m]
-    __shared__ f32x4 partial[4][MT][LPR];
+    __shared__ f32x4 partial[kWaves][MT][LPR];
     __shared__ int arrived_last;
 
     const int tid = threadIdx.x;
@@ -114,12 +134,12 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs args) {
     const bool col_ok = n0 + 4 * col_lane < args.n;
     const int32_t lane_offset = col_ok ? int32_t((int64_t(row_lane) * args.n + 4 * col_lane) * 4) : gemm::kOutOfRange;
     // Rows of a pass are dealt to the waves in groups of kRowsPerLoad:
-    // load u of wave v reads rows (4u + v) * kRowsPerLoad + row_lane, so a
+    // load u of wave v reads rows (kWaves u + v) * kRowsPerLoad + row_lane, so a
     // short slice still spreads over all four waves. Wave-uniform: this
     // wave's first row and the byte distance between a lane's loads.
     const int32_t wave_row = __builtin_amdgcn_readfirstlane(wave) * kRowsPerLoad;
     const int32_t wave_offset = int32_t(int64_t(wave_row) * args.n * 4);
-    const int32_t load_stride = int32_t(int64_t(4 * kRowsPerLoad) * args.n * 4);
+    const int32_t load_stride = int32_t(int64_t(kWaves * kRowsPerLoad) * args.n * 4);
 
     // Loads of one pass: one descriptor per pass and a scalar offset per
     // load; rows past the slice read 0 (only the last pass of a slice can
@@ -130,7 +150,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs args) {
 #pragma unroll
         for (int u = 0; u < kLoads; ++u) {
             const int32_t voffset =
-                full || k0 + 4 * kRowsPerLoad * u + wave_row + row_lane < k_end ? lane_offset : gemm::kOutOfRange;
+                full || k0 + kWaves * kRowsPerLoad * u + wave_row + row_lane < k_end ? lane_offset : gemm::kOutOfRange;
             rows[u] = __builtin_bit_cast(
                 f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, voffset, u * load_stride + wave_offset, kNontemporal));
         }
@@ -160,9 +180,14 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs args) {
         }
     };
 
-    f32x4 acc[MT];
+    f32x4 acc[uses_mfma<MT>() ? 1 : MT];
 #pragma unroll
-    for (int m = 0; m < MT; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int m = 0; m < (uses_mfma<MT>() ? 1 : MT); ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // Matrix-core accumulators: macc[c][r] = row 4 * (lane / 16) + r, column
+    // n0 + 4 * (lane % 16) + c of this wave's partial sum.
+    f32x4 macc[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) macc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     // One pass: start the next pass's x and W loads, then (after the barrier
     // that publishes this pass's x and retires the other x buffer) multiply
@@ -178,20 +203,38 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs args) {
         load_pass(k0 + kPassRows, next);
         __syncthreads();
         const float* xr = x_pass[p & 1][wave_row + row_lane];
-        float xv[MT], xn[MT];
+        if constexpr (uses_mfma<MT>()) {
+            // Load u holds W rows r .. r + 3 (r its first row, lane / 16 =
+            // row_lane picks one) and 64 columns, 4 per lane. For component
+            // c, lane l supplies B[k = l / 16][j = l % 16] = W[r + k][n0 +
+            // 4j + c]; the A operand is x[m = l % 16][r + l / 16] (0 past
+            // MT). One MFMA per component adds those 4 rows into the 16 x 16
+            // block of columns n0 + 4j + c.
+            float xa[kLoads];
 #pragma unroll
-        for (int m = 0; m < MT; ++m) xv[m] = xr[m];
+            for (int u = 0; u < kLoads; ++u)
+                xa[u] = (lane & 15) < MT ? xr[u * kWaves * kRowsPerLoad * MT + (lane & 15)] : 0.f;
 #pragma unroll
-        for (int u = 0; u < kLoads; ++u) {
-            if (u + 1 < kLoads) {
+            for (int u = 0; u < kLoads; ++u)
 #pragma unroll
-                for (int m = 0; m < MT; ++m) xn[m] = xr[(u + 1) * 4 * kRowsPerLoad * MT + m];
+                for (int c = 0; c < 4; ++c)
+                    macc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[u], cur[u][c], macc[c], 0, 0, 0);
+        } else {
+            float xv[MT], xn[MT];
+#pragma unroll
+            for (int m = 0; m < MT; ++m) xv[m] = xr[m];
+#pragma unroll
+            for (int u = 0; u < kLoads; ++u) {
+                if (u + 1 < kLoads) {
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) xn[m] = xr[(u + 1) * kWaves * kRowsPerLoad * MT + m];
+                }
+#pragma unroll
+                for (int m = 0; m < MT; ++m) acc[m] += xv[m] * cur[u];
+#pragma unroll
+                for (int m = 0; m < MT; ++m) xv[m] = xn[m];
+                __builtin_amdgcn_sched_barrier(0);
             }
-#pragma unroll
-            for (int m = 0; m < MT; ++m) acc[m] += xv[m] * cur[u];
-#pragma unroll
-            for (int m = 0; m < MT; ++m) xv[m] = xn[m];
-            __builtin_amdgcn_sched_barrier(0);
         }
         store_x(xs, (p + 1) & 1);
     };
@@ -208,20 +251,31 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs args) {
         if (p + 1 < passes) pass(p + 1, rb, ra);
     }
 
-    // The row lanes of a wave hold the same columns: add them (xor LPR, 2 LPR,
-    // .. 32), then the waves in order through LDS.
+    if constexpr (uses_mfma<MT>()) {
+        // Lane l holds rows 4 (l / 16) .. +3 of columns 4 (l % 16) .. +3
+        // (col_lane = l % 16, as LPR = 16 here).
+        static_assert(LPR == 16, "16 lanes per 64-column row piece");
 #pragma unroll
-    for (int m = 0; m < MT; ++m)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            float v = acc[m][j];
-#pragma unroll
-            for (int step = LPR; step < 64; step *= 2) v += __shfl_xor(v, step);
-            acc[m][j] = v;
+        for (int r = 0; r < 4; ++r) {
+            const int m = 4 * row_lane + r;
+            if (m < MT) partial[wave][m][col_lane] = f32x4{macc[0][r], macc[1][r], macc[2][r], macc[3][r]};
         }
-    if (row_lane == 0) {
+    } else {
+        // The row lanes of a wave hold the same columns: add them (xor LPR,
+        // 2 LPR, .. 32), then the waves in order through LDS.
 #pragma unroll
-        for (int m = 0; m < MT; ++m) partial[wave][m][col_lane] = acc[m];
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float v = acc[m][j];
+#pragma unroll
+                for (int step = LPR; step < 64; step *= 2) v += __shfl_xor(v, step);
+                acc[m][j] = v;
+            }
+        if (row_lane == 0) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m) partial[wave][m][col_lane] = acc[m];
+        }
     }
     __syncthreads();
 
@@ -233,7 +287,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs args) {
     if (owner) {
         slab_sum = partial[0][om][oc];
 #pragma unroll
-        for (int v = 1; v < 4; ++v) slab_sum += partial[v][om][oc];
+        for (int v = 1; v < kWaves; ++v) slab_sum += partial[v][om][oc];
     }
     const int64_t out_col = n0 + 4 * oc;
     const bool out_ok = owner && om < args.m && out_col < args.n;
@@ -287,9 +341,11 @@ struct GemvPlan {
     int64_t pass_rows;
 };
 
+// Rows of a pass for the instantiation launch_width picks for m rows.
 template <int LPR>
 int64_t pass_rows_for(int64_t m) {
-    return m <= 2 ? pass_rows<2, LPR>() : m <= 8 ? pass_rows<8, LPR>() : pass_rows<16, LPR>();
+    return m <= 2 ? pass_rows<2, LPR>() : m <= 4 ? pass_rows<4, LPR>() : m <= 8 ? pass_rows<8, LPR>()
+                                                                               : pass_rows<16, LPR>();
 }
 
 GemvPlan gemv_plan(const Problem& p) {
@@ -301,7 +357,8 @@ GemvPlan gemv_plan(const Problem& p) {
     int64_t rows_per_split = std::max<int64_t>(p.k, 1);
     if (slabs < kUnsplitSlabs) {
         // Enough slices for about `target` workgroups, each a whole
-        // number of wave row groups (4 waves x 4 rows).
+        // number of 16-row groups (4 waves x 4 rows; on the 8-wave path a
+        // slice's last group may leave waves idle).
         const int64_t groups = (std::max<int64_t>(p.k, 1) + 15) / 16;
         const int64_t target = p.m <= 4 ? kSplitTargetFewRows : kSplitTargetManyRows;
         const int64_t want = std::min<int64_t>(groups, (target + slabs - 1) / slabs);
@@ -332,7 +389,7 @@ hipError_t launch_rows(const Problem& p, const Env& env, const GemvPlan& plan, h
     args.accumulate = p.accumulate ? 1 : 0;
     args.scale = p.scale;
     hipLaunchKernelGGL((gemv_kernel<MT, LPR>), dim3(plan.column_blocks, plan.splits, unsigned(p.batch)),
-                       dim3(kThreads), 0, stream, args);
+                       dim3(64 * waves_for<MT>()), 0, stream, args);
     return hipGetLastError();
 }
 
