@@ -299,7 +299,25 @@ def measure_decode(gpu: Gpu, events: HipEvents, pool_bytes: int = 640 << 20, rep
     ms = timed(events, gpu.stream, lambda: gpu.read_sum(src, sums), 5)
     result["stream_read_gbs"] = round((1 << 31) / (ms * 1e-3) / 1e9, 1)
     src.free()
+    # The same streaming read, one launch per head-sized (50.3 MB) buffer rotated through the
+    # pool and replayed from a HIP graph: the practical ceiling of a single launch that reads
+    # the head's weight once (launch, ramp-up and drain included). Best of 3 grid sizes.
+    head_k, head_n = DECODE_SHAPES[4][1], DECODE_SHAPES[4][2]
+    copies = max(2, -(-pool_bytes // (4 * head_k * head_n)))
+    pool = [gpu.zeros(Shape(head_k, head_n)) for _ in range(copies)]
+    best = 0.0
+    for blocks in (1024, 2048, 4096):
+        part = gpu.zeros(Shape(blocks, 1))
+        graph = HipGraph(gpu.stream, lambda: [gpu.read_sum(w, part) for w in pool])
+        graph.launch()
+        ms = timed(events, gpu.stream, graph.launch, repeats) / copies
+        graph.close()
+        part.free()
+        best = max(best, 4 * head_k * head_n / (ms * 1e-3) / 1e9)
+    for w in pool:
+        w.free()
     sums.free()
+    result["stream_read_head_size_gbs"] = round(best, 1)
     for m in (1, 4, 16):
         for name, k, n in DECODE_SHAPES:
             copies = max(2, -(-pool_bytes // (4 * k * n)))
@@ -331,6 +349,7 @@ def measure_decode(gpu: Gpu, events: HipEvents, pool_bytes: int = 640 << 20, rep
     head = result["per_shape_gbs"][f"M=1 head {DECODE_SHAPES[4][1]}x{DECODE_SHAPES[4][2]}"]
     result["head_m1_frac_hbm_peak"] = round(head / PEAK_HBM_GBS, 4)
     result["head_m1_frac_stream_read"] = round(head / result["stream_read_gbs"], 4)
+    result["head_m1_frac_stream_read_head_size"] = round(head / result["stream_read_head_size_gbs"], 4)
     result["token_sequence"] = {"products": len(layers), "mb_per_token": round(token_bytes / 1e6, 1),
                                 "us_per_token": round(ms * 1e3, 1),
                                 "gbs": round(token_bytes / (ms * 1e-3) / 1e9, 1)}
