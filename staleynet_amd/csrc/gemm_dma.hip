@@ -22,12 +22,13 @@
 //      Row-contiguous operand (B in NN/TN, A in TN/TT): the natural [k][row]
 //      layout, one k row of the tile per 512 bytes. A fragment is eight
 //      ds_read_b32 (consecutive rows across lanes: conflict-free).
-//  * Two LDS stages (32 KB each for 128x128), double-buffered: after one
-//    barrier per K-step the next step's loads are issued into the other
-//    stage and the current one is multiplied while they fly. The loop is
-//    unrolled by two so that each half reads one statically known stage
-//    array, which keeps the compiler from waiting on the in-flight loads
-//    into the other stage before its LDS reads.
+//  * Two or more LDS stages (32 KB each for 128x128), all in flight: a
+//    stage is reloaded, STAGES steps ahead, as soon as every wave has read
+//    it. The one barrier per K-step sits between its two 16-deep chunks, so
+//    each chunk's fragments are read from LDS while the previous chunk is
+//    multiplied and the matrix cores never wait on an LDS read.
+//  * bf16 variant: the same fp32 stages; each lane rounds its fragments to
+//    bf16 in registers and issues one 32x32x16 bf16 MFMA per block and chunk.
 //
 // Within a 16-deep chunk, lane half h feeds k = 8h + s to MFMA s on both
 // operands (the same pairing as gemm_mfma.hip).
@@ -145,93 +146,68 @@ template <bool K_CONTIGUOUS, int ROWS, int WAVES>
 using OperandFor =
     typename std::conditional<K_CONTIGUOUS, OperandK<ROWS, WAVES>, OperandR<ROWS, WAVES>>::type;
 
-// Multiplies one staged K-step: two 16-deep chunks. Chunk 0's fragments
-// are read first; then `prefetch` starts the next K-step's loads into the
-// other stage, and those loads and chunk 1's fragment reads are interleaved
-// with chunk 0's MFMAs, so that the wave issues them in the MFMAs' shadow
-// instead of stalling on them (left alone, the scheduler issues each LDS
-// read just before its first MFMA and waits on it there).
-//
-// fp32: eight v_mfma_f32_32x32x2_f32 per block and chunk, lane half h
-// feeding k = 8h + s to MFMA s. bf16: the same eight fp32 values per lane
-// are rounded to bf16 (v_cvt_pk_bf16_f32, nearest-even) and feed one
-// v_mfma_f32_32x32x16_bf16, whose lane half h holds k = 8h .. 8h+7: the
-// same k pairing of A and B, one instruction per block and chunk.
-template <class T, bool A_K, bool B_K, bool BF16, class Prefetch>
-__device__ __forceinline__ void multiply_stage(const OperandFor<A_K, T::BM, T::THREADS / 64>& oa,
-                                               const OperandFor<B_K, T::BN, T::THREADS / 64>& ob,
-                                               const f32x4* sa, const f32x4* sb, f32x16 (&acc)[T::FM][T::FN],
-                                               int lane, int wave_m, int wave_n, Prefetch&& prefetch) {
-    static_assert(T::BK == 32, "two 16-deep chunks per stage");
+// One 16-deep chunk of a wave's fragments: FM A and FN B fragments, 8 values
+// per lane (k = 16 c + 8 h + s for lane half h, s = 0..7).
+template <class T>
+struct Chunk {
+    float a[T::FM][8];
+    float b[T::FN][8];
+};
+
+template <class T, bool A_K, bool B_K>
+__device__ __forceinline__ void read_chunk(const OperandFor<A_K, T::BM, T::THREADS / 64>& oa,
+                                           const OperandFor<B_K, T::BN, T::THREADS / 64>& ob, const f32x4* sa,
+                                           const f32x4* sb, int c, Chunk<T>& f, int lane, int wave_m, int wave_n) {
     const int row = lane & 31;
     const int half = lane >> 5;
-    float av[2][T::FM][8], bv[2][T::FN][8];
-    auto read = [&](int c) {
 #pragma unroll
-        for (int i = 0; i < T::FM; ++i) oa.fragment(sa, wave_m * T::WTM + 32 * i + row, c, half, av[c][i]);
+    for (int i = 0; i < T::FM; ++i) oa.fragment(sa, wave_m * T::WTM + 32 * i + row, c, half, f.a[i]);
 #pragma unroll
-        for (int j = 0; j < T::FN; ++j) ob.fragment(sb, wave_n * T::WTN + 32 * j + row, c, half, bv[c][j]);
-    };
-    auto multiply = [&](int c) {
-        if constexpr (BF16) {
-            bf16x8 a8[T::FM], b8[T::FN];
+    for (int j = 0; j < T::FN; ++j) ob.fragment(sb, wave_n * T::WTN + 32 * j + row, c, half, f.b[j]);
+}
+
+// fp32: eight v_mfma_f32_32x32x2_f32 per block, lane half h feeding k = 8h + s
+// to MFMA s. bf16: the same eight fp32 values per lane are rounded to bf16
+// (v_cvt_pk_bf16_f32, nearest-even) and feed one v_mfma_f32_32x32x16_bf16,
+// whose lane half h holds k = 8h .. 8h+7: the same pairing of A and B.
+template <class T, bool BF16>
+__device__ __forceinline__ void multiply_chunk(const Chunk<T>& f, f32x16 (&acc)[T::FM][T::FN]) {
+    if constexpr (BF16) {
+        bf16x8 a8[T::FM], b8[T::FN];
 #pragma unroll
-            for (int i = 0; i < T::FM; ++i) a8[i] = to_bf16x8(av[c][i]);
+        for (int i = 0; i < T::FM; ++i) a8[i] = to_bf16x8(f.a[i]);
 #pragma unroll
-            for (int j = 0; j < T::FN; ++j) b8[j] = to_bf16x8(bv[c][j]);
+        for (int j = 0; j < T::FN; ++j) b8[j] = to_bf16x8(f.b[j]);
+#pragma unroll
+        for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+            for (int j = 0; j < T::FN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a8[i], b8[j], acc[i][j], 0, 0, 0);
+    } else {
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
 #pragma unroll
             for (int i = 0; i < T::FM; ++i)
 #pragma unroll
                 for (int j = 0; j < T::FN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a8[i], b8[j], acc[i][j], 0, 0, 0);
-        } else {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[i][s], f.b[j][s], acc[i][j], 0, 0, 0);
+    }
+}
+
+// Orders one half-step for the scheduler: the chunk's conversions (bf16),
+// then its MFMAs with the VM loads and DS fragment reads issued in their
+// shadow, spread evenly (left alone, the scheduler issues each LDS read
+// just before its first use and waits on it there).
+template <class T, bool BF16, int VM, int DS>
+__device__ __forceinline__ void interleave() {
+    constexpr int MF = (BF16 ? 1 : 8) * T::FM * T::FN;
+    if constexpr (BF16) __builtin_amdgcn_sched_group_barrier(0x002, 4 * (T::FM + T::FN), 0);
 #pragma unroll
-            for (int s = 0; s < 8; ++s)
-#pragma unroll
-                for (int i = 0; i < T::FM; ++i)
-#pragma unroll
-                    for (int j = 0; j < T::FN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[c][i][s], bv[c][j][s], acc[i][j], 0, 0, 0);
-        }
-    };
-    constexpr int DS = T::FM * (A_K ? 2 : 4) + T::FN * (B_K ? 2 : 4);
-    constexpr int VM = (T::BM + T::BN) / (8 * (T::THREADS / 64));
-    read(0);
-    __builtin_amdgcn_sched_barrier(0);
-    prefetch();
-    read(1);
-    multiply(0);
-    multiply(1);
-    if constexpr (BF16) {
-        // FM * FN MFMAs per chunk: chunk 0's conversions, then its MFMAs
-        // with the loads and chunk 1's reads spread over them, then chunk
-        // 1's conversions and MFMAs.
-        constexpr int MF = T::FM * T::FN;
-        constexpr int CVT = 4 * (T::FM + T::FN);
-        constexpr int VM_PER = (VM + MF - 1) / MF;
-        constexpr int DS_PER = (DS + MF - 1) / MF;
-        __builtin_amdgcn_sched_group_barrier(0x002, CVT, 0);
-#pragma unroll
-        for (int x = 0; x < MF; ++x) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x020, VM_PER, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, DS_PER, 0);
-        }
-        __builtin_amdgcn_sched_group_barrier(0x002, CVT, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, MF, 0);
-    } else {
-        constexpr int MF = 8 * T::FM * T::FN;
-#pragma unroll
-        for (int x = 0; x < VM; ++x) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-        }
-#pragma unroll
-        for (int x = 0; x < DS; ++x) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-        __builtin_amdgcn_sched_group_barrier(0x008, 2 * MF - VM - DS, 0);
+    for (int x = 0; x < MF; ++x) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if constexpr (VM > 0)
+            if (x * ((VM + MF - 1) / MF) < VM) __builtin_amdgcn_sched_group_barrier(0x020, (VM + MF - 1) / MF, 0);
+        if (x * ((DS + MF - 1) / MF) < DS) __builtin_amdgcn_sched_group_barrier(0x100, (DS + MF - 1) / MF, 0);
     }
 }
 
@@ -286,16 +262,16 @@ __device__ __forceinline__ void lds_barrier() {
 // One output tile (the whole of both kernels below); BF16 selects the
 // matrix instruction fed from the fp32 LDS stages.
 //
-// STAGES LDS stages: loads run STAGES - 1 K-steps ahead of the MFMAs. At
-// each step a wave waits until only the later stages' loads are still in
-// flight (a wave's loads complete in order), the barrier makes every wave's
-// loads of this stage visible and retires every read of the stage that the
-// next prefetch overwrites, and the prefetch is issued during the multiply.
-// Every step prefetches, unconditionally: loads past the tile's K range are
-// out of bounds (no memory traffic, zeros), which keeps each step's load
-// count, and so the wait count, fixed. The loop is unrolled by STAGES so
-// that every LDS access names a statically known stage array; the compiler
-// then never waits on loads into the other stages before its LDS reads.
+// STAGES LDS stages, all loading from the start: a stage is reloaded for
+// the step STAGES ahead as soon as every wave has read it. One barrier per
+// K-step, between its two 16-deep chunks (see the step halves below). At
+// the barrier a wave waits until only the later stages' loads are still in
+// flight (a wave's loads complete in order). Every step issues its loads
+// unconditionally: loads past the tile's K range are out of bounds (no
+// memory traffic, zeros), which keeps each step's load count, and so the
+// wait count, fixed. The loop is unrolled by STAGES so that every LDS
+// access names a statically known stage array; the compiler then never
+// waits on loads into the other stages before its LDS reads.
 template <class T, int STAGES, bool A_K, bool B_K, bool BF16>
 __device__ __forceinline__ void dma_tile(const Args& args) {
     static_assert(STAGES >= 2 && STAGES <= 4, "two to four LDS stages");
@@ -358,62 +334,139 @@ __device__ __forceinline__ void dma_tile(const Args& args) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    // Loads stop at the tile's K end: a partial last step, and prefetches
-    // past the last step, read zeros.
+    // Loads stop at the tile's K end: a partial last step, and loads past
+    // the last step, read zeros.
     auto issue = [&](const f32x4* sa, const f32x4* sb, int64_t k0) {
         if constexpr (A_K) oa.issue(sa, a, k0, k_end, wave);
         else oa.issue(sa, a, args.lda, k0, k_end, wave);
         if constexpr (B_K) ob.issue(sb, b, k0, k_end, wave);
         else ob.issue(sb, b, args.ldb, k0, k_end, wave);
     };
-    // One K-step on stage S (static): wait for this stage's loads, start
-    // the loads STAGES - 1 steps ahead into the stage read last step,
-    // multiply this stage.
-    constexpr int LOADS_PER_STEP = (T::BM + T::BN) / (8 * WAVES);
-    auto step_on = [&](auto stage, int64_t k0) {
-        constexpr int S = decltype(stage)::value;
-        constexpr int P = (S + STAGES - 1) % STAGES;
-        wait_loads<LOADS_PER_STEP * (STAGES - 2)>();
-        lds_barrier();
-        // Causal-left: A values past the diagonal are zeroed in LDS on the
-        // K-steps that reach it (A K-contiguous: keys past the tile's first
-        // query; A transposed: queries before the tile's last key).
+    // Causal-left: A values past the diagonal are zeroed in LDS on the
+    // K-steps that reach it (A K-contiguous: keys past the tile's first
+    // query; A transposed: queries before the tile's last key).
+    auto mask_if_needed = [&](f32x4* sa, int64_t k0) {
         if (left_causal && (A_K ? k0 + T::BK - 1 > m0 + args.query_offset : k0 + args.query_offset < row_last)) {
-            mask_stage<T, A_K>(stage_a[S], m0, k0, args.query_offset, tid);
+            mask_stage<T, A_K>(sa, m0, k0, args.query_offset, tid);
             lds_barrier();
         }
-        multiply_stage<T, A_K, B_K, BF16>(oa, ob, stage_a[S], stage_b[S], acc, lane, wave_m, wave_n, [&] {
-            issue(stage_a[P], stage_b[P], k0 + (STAGES - 1) * T::BK);
-        });
+    };
+    constexpr int LOADS_PER_STEP = (T::BM + T::BN) / (8 * WAVES);
+    constexpr int DS = T::FM * (A_K ? 2 : 4) + T::FN * (B_K ? 2 : 4);
+    Chunk<T> f0, f1;
+    // A K-step on stage S is two halves around one barrier. Entered with
+    // the stage's chunk 0 in f0, the first half reads chunk 1 into f1 while
+    // chunk 0 is multiplied. Then `sync` waits for the next step's loads
+    // (the later steps' stay in flight) and barriers: every wave's loads of
+    // the next stage have landed and every wave has read all of stage S.
+    // The second half starts the loads STAGES steps ahead into stage S and
+    // reads the next stage's chunk 0 into f0 while chunk 1 is multiplied.
+    // No LDS read is waited for with the matrix cores idle.
+    auto first_half = [&](auto stage) {
+        constexpr int S = decltype(stage)::value;
+        __builtin_amdgcn_sched_barrier(0);
+        read_chunk<T, A_K, B_K>(oa, ob, stage_a[S], stage_b[S], 1, f1, lane, wave_m, wave_n);
+        multiply_chunk<T, BF16>(f0, acc);
+        interleave<T, BF16, 0, DS>();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto sync = [&] {
+        wait_loads<LOADS_PER_STEP * (STAGES - 2)>();
+        lds_barrier();
+    };
+    auto second_half = [&](auto stage, int64_t k0) {
+        constexpr int S = decltype(stage)::value;
+        constexpr int N = (S + 1) % STAGES;
+        mask_if_needed(stage_a[N], k0 + T::BK);
+        __builtin_amdgcn_sched_barrier(0);
+        issue(stage_a[S], stage_b[S], k0 + STAGES * T::BK);
+        read_chunk<T, A_K, B_K>(oa, ob, stage_a[N], stage_b[N], 0, f0, lane, wave_m, wave_n);
+        multiply_chunk<T, BF16>(f1, acc);
+        interleave<T, BF16, LOADS_PER_STEP, DS>();
+        __builtin_amdgcn_sched_barrier(0);
     };
 
     const int steps = k_end > k_begin ? int((k_end - k_begin + T::BK - 1) / T::BK) : 0;
     if (steps > 0) {
-#pragma unroll
-        for (int s = 0; s < STAGES - 1; ++s) issue(stage_a[s], stage_b[s], k_begin + s * T::BK);
-        // Whole rounds of STAGES steps, then the remaining steps, which
-        // start again at stage 0.
         using I0 = std::integral_constant<int, 0>;
         using I1 = std::integral_constant<int, 1>;
         using I2 = std::integral_constant<int, 2>;
         using I3 = std::integral_constant<int, 3>;
+        // Every stage starts loading; step 0's chunk 0 is read and its
+        // first half run. The loop then runs from barrier to barrier (second
+        // half of step s, first half of step s + 1), so that the loads in
+        // flight where it closes are the same on every iteration (none with
+        // two stages): the compiler then tracks which stage each LDS read
+        // may depend on instead of waiting for every load.
+#pragma unroll
+        for (int s = 0; s < STAGES; ++s) issue(stage_a[s], stage_b[s], k_begin + s * T::BK);
+        wait_loads<LOADS_PER_STEP * (STAGES - 1)>();
+        lds_barrier();
+        mask_if_needed(stage_a[0], k_begin);
+        read_chunk<T, A_K, B_K>(oa, ob, stage_a[0], stage_b[0], 0, f0, lane, wave_m, wave_n);
+        first_half(I0{});
+        sync();
+        // Steps 0 .. steps - 2 close here in whole rounds of STAGES, then
+        // the rest; the last step's second half ends the tile.
         int step = 0;
-        for (; step + STAGES <= steps; step += STAGES) {
+        for (; step + STAGES < steps; step += STAGES) {
             const int64_t k0 = k_begin + int64_t(step) * T::BK;
-            step_on(I0{}, k0);
-            step_on(I1{}, k0 + T::BK);
-            if constexpr (STAGES > 2) step_on(I2{}, k0 + 2 * T::BK);
-            if constexpr (STAGES > 3) step_on(I3{}, k0 + 3 * T::BK);
+            second_half(I0{}, k0);
+            first_half(I1{});
+            sync();
+            if constexpr (STAGES == 2) {
+                second_half(I1{}, k0 + T::BK);
+                first_half(I0{});
+                sync();
+            } else {
+                second_half(I1{}, k0 + T::BK);
+                first_half(I2{});
+                sync();
+                if constexpr (STAGES == 3) {
+                    second_half(I2{}, k0 + 2 * T::BK);
+                    first_half(I0{});
+                    sync();
+                } else {
+                    second_half(I2{}, k0 + 2 * T::BK);
+                    first_half(I3{});
+                    sync();
+                    second_half(I3{}, k0 + 3 * T::BK);
+                    first_half(I0{});
+                    sync();
+                }
+            }
         }
-        const int left = steps - step;
+        // 0 .. STAGES - 1 more steps close, starting at stage 0; then the
+        // last step, on stage `left`.
+        const int left = steps - 1 - step;
         const int64_t k0 = k_begin + int64_t(step) * T::BK;
-        if (left > 0) step_on(I0{}, k0);
+        if (left > 0) {
+            second_half(I0{}, k0);
+            first_half(std::integral_constant<int, 1 % STAGES>{});
+            sync();
+        }
         if constexpr (STAGES > 2)
-            if (left > 1) step_on(I1{}, k0 + T::BK);
+            if (left > 1) {
+                second_half(I1{}, k0 + T::BK);
+                first_half(std::integral_constant<int, 2 % STAGES>{});
+                sync();
+            }
         if constexpr (STAGES > 3)
-            if (left > 2) step_on(I2{}, k0 + 2 * T::BK);
-        // The prefetches past the last step are still writing (zeros) into
-        // LDS: let them land before the workgroup can end.
+            if (left > 2) {
+                second_half(I2{}, k0 + 2 * T::BK);
+                first_half(std::integral_constant<int, 3 % STAGES>{});
+                sync();
+            }
+        const int64_t k_last = k0 + int64_t(left) * T::BK;
+        if (left == 0) second_half(I0{}, k_last);
+        if constexpr (STAGES > 1)
+            if (left == 1) second_half(std::integral_constant<int, 1 % STAGES>{}, k_last);
+        if constexpr (STAGES > 2)
+            if (left == 2) second_half(std::integral_constant<int, 2 % STAGES>{}, k_last);
+        if constexpr (STAGES > 3)
+            if (left == 3) second_half(std::integral_constant<int, 3 % STAGES>{}, k_last);
+        // The loads issued past the last step are still writing (zeros)
+        // into LDS: let them land before the workgroup can end.
         wait_loads<0>();
     }
 
@@ -429,12 +482,13 @@ struct DmaConfig {
     static constexpr int STAGES = STAGES_;
 };
 
-// LDS (the stages) already caps a CU's workgroups: let the register
-// allocator use that budget instead of squeezing for occupancy it cannot
-// reach.
+// LDS (the stages) caps a CU's workgroups; registers are held to the same
+// number of waves per SIMD (two for every tile here: 256 registers a lane),
+// so that the register file never lowers it further.
 template <class C, bool A_K, bool B_K>
 __global__ __launch_bounds__(C::T::THREADS)
-__attribute__((amdgpu_waves_per_eu(1, dma_waves_per_eu<typename C::T, C::STAGES>())))
+__attribute__((amdgpu_waves_per_eu(dma_waves_per_eu<typename C::T, C::STAGES>(),
+                                   dma_waves_per_eu<typename C::T, C::STAGES>())))
 void gemm_f32_dma_kernel(Args args) {
     dma_tile<typename C::T, C::STAGES, A_K, B_K, false>(args);
 }
@@ -444,7 +498,8 @@ void gemm_f32_dma_kernel(Args args) {
 // bf16 just before the matrix instruction.
 template <class C, bool A_K, bool B_K>
 __global__ __launch_bounds__(C::T::THREADS)
-__attribute__((amdgpu_waves_per_eu(1, dma_waves_per_eu<typename C::T, C::STAGES>())))
+__attribute__((amdgpu_waves_per_eu(dma_waves_per_eu<typename C::T, C::STAGES>(),
+                                   dma_waves_per_eu<typename C::T, C::STAGES>())))
 void gemm_bf16_dma_kernel(Args args) {
     dma_tile<typename C::T, C::STAGES, A_K, B_K, true>(args);
 }
