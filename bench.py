@@ -526,6 +526,9 @@ def main() -> int:
                         help="print a kernel table from a rocprofv3 --stats run and exit (no GPU)")
     parser.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                         help="print the NN kernel's HBM traffic from two --pmc runs and exit (no GPU)")
+    parser.add_argument("--one-product", nargs=2, metavar=("LAYOUT", "PRECISION"),
+                        help="run only config 2's qkv product (NN, TN or NT; f32 or bf16) 1 + 5 times and exit: "
+                             "the workload of the per-kernel counter profiles")
     args = parser.parse_args()
 
     if args.summarize_trace:
@@ -542,6 +545,20 @@ def main() -> int:
 
     gpu = Gpu(0)
     events = HipEvents()
+    if args.one_product:
+        layout, precision = args.one_product
+        m, d = MODEL_111M["tokens"], MODEL_111M["width"]
+        buf = LinearBuffers(gpu, m, d, 3 * d, 0)
+        spec = dict(linear_products(m, d, 3 * d))[layout]
+        if precision == "bf16":
+            spec = spec.with_precision(Precision.Bf16)
+        left, right, out = buf.operands(layout)
+        ms = timed(events, gpu.stream, lambda: gpu.matmul(spec, left, right, out), 1)
+        ms = timed(events, gpu.stream, lambda: gpu.matmul(spec, left, right, out), 5)
+        print(json.dumps({"product": f"{layout} {spec.rows}x{spec.cols}x{spec.inner}", "precision": precision,
+                          "ms": round(ms, 4), "tflops": round(spec.flops() / (ms * 1e-3) / 1e12, 1)}))
+        gpu.close()
+        return 0
     if args.copy_calibration_mib:
         src = gpu.zeros(Shape(args.copy_calibration_mib << 18, 1))
         dst = gpu.zeros(Shape(args.copy_calibration_mib << 18, 1))
@@ -603,7 +620,8 @@ def main() -> int:
                           "frac_bf16_peak": round(bf16_tflops / PEAK_BF16_TFLOPS, 4),
                           "roofline_min_peak_or_ai_x_hbm": round(attainable, 1),
                           "frac_roofline": round(bf16_tflops / attainable, 4), "per_layout": bf16_layout,
-                          "inputs": "fp32 in HBM, rounded to bf16 (nearest-even) in LDS; fp32 accumulation"}
+                          "inputs": "fp32 in HBM and LDS, rounded to bf16 (nearest-even) per fragment in registers; "
+                                    "fp32 accumulation"}
         result["attention"] = measure_attention(gpu, events)
         result["decode"] = measure_decode(gpu, events)
 
