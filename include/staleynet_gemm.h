@@ -67,6 +67,11 @@ extern "C" {
 /* The context's split-K workspace cannot hold the partial sums this product
  * needs (only possible with a workspace smaller than the default). */
 #define SN_ERR_WORKSPACE (-10)
+/* A bias or column-sum vector whose length is not the matrix's column count:
+ * "add_row_bias: bias length must equal output columns" and
+ * "accumulate_column_sums: sums length must equal input columns"
+ * (ops/elementwise.rs:33, :46). */
+#define SN_ERR_LENGTH_MISMATCH (-11)
 
 /* ---- enums (carried as uint32_t in structs) ------------------------------ */
 /* Storage (ops/matmul.rs:15-22). */
@@ -187,6 +192,41 @@ int sn_matmul_validate(const sn_matmul_spec *spec, size_t left_len, size_t right
  * loops do. */
 int sn_matmul(sn_context *context, const sn_matmul_spec *spec, const float *left, size_t left_len,
               const float *right, size_t right_len, float *output, size_t output_len);
+
+/* ---- the Linear layer's bias kernels on either side of the GEMM ----------- */
+/* `Gpu::add_row_bias` (ops/elementwise.rs:30-41; kernel kernels/elementwise.rs:
+ * 62-68), called by Linear::forward after its product (layers/linear.rs:47):
+ * output[r, c] += bias[c] over the [rows, cols] row-major output, one f32 add
+ * per element (bit-identical to the reference). bias_len must equal cols
+ * (SN_ERR_LENGTH_MISMATCH); bias must not overlap the output
+ * (SN_ERR_ALIASING). Asynchronous on the context's stream. */
+int sn_add_row_bias(sn_context *context, float *output, size_t rows, size_t cols, const float *bias,
+                    size_t bias_len);
+
+/* `Gpu::accumulate_column_sums` (ops/elementwise.rs:43-58; kernel
+ * kernels/elementwise.rs:78-93), called by Linear::backward for the bias
+ * gradient (layers/linear.rs:59): sums[c] += sum over r of input[r, c] for
+ * the [rows, cols] row-major input. The reference sums each column in row
+ * order with one thread per column; here a workgroup owns 64 columns and a
+ * slice of rows, slices are added in a fixed order and the result is the same
+ * on every run (not bit-identical to the row-order sum; within the fp32
+ * tolerance of it). sums_len must equal cols (SN_ERR_LENGTH_MISMATCH).
+ * Uses the context's split-K workspace for the per-slice sums. */
+int sn_accumulate_column_sums(sn_context *context, const float *input, size_t rows, size_t cols, float *sums,
+                              size_t sums_len);
+
+/* Linear::forward's two calls (layers/linear.rs:46-47), `Gpu::matmul`
+ * followed by `Gpu::add_row_bias` on its output, in one pass: the bias is
+ * added in the product's epilogue, after the reference's combine and rounded
+ * separately, so the result is the same as the two calls'. For a batched spec
+ * the bias is added to every output matrix, which must not share memory
+ * (batch_output >= rows * cols, else SN_ERR_UNSUPPORTED). bias_len must equal
+ * spec->cols (SN_ERR_LENGTH_MISMATCH).
+ * Saves the separate read and write of the output; a masked spec is run as
+ * the two calls. */
+int sn_matmul_bias(sn_context *context, const sn_matmul_spec *spec, const float *left, size_t left_len,
+                   const float *right, size_t right_len, const float *bias, size_t bias_len, float *output,
+                   size_t output_len);
 
 /* A short English description of a status code (never null). */
 const char *sn_status_string(int status);

@@ -27,11 +27,21 @@
  *   oracle_relative_error    crates/staleynet-cuda/tests/kernels_match_reference.rs:41-52
  *   oracle_causal_softmax    crates/staleynet-cuda/src/reference.rs:100-119
  *   oracle_softmax_backward  crates/staleynet-cuda/src/reference.rs:121-137
+ *   oracle_add_row_bias      crates/staleynet-cuda/src/kernels/elementwise.rs:62-68
+ *                            (output[r, c] += bias[c], one f32 add each)
+ *   oracle_accumulate_column_sums
+ *                            crates/staleynet-cuda/src/kernels/elementwise.rs:78-93
+ *                            (per column: f32 sum from 0 over the rows in
+ *                            order, then sums[c] += sum)
+ *   oracle_column_sums_f64   the same sums in f64 (error reporting only)
  *
  * Parity pins (tests/test_oracle.py): the reference's known-answer tests
  * (reference.rs:177-232, 267-306), an order-sensitive case whose f32 result
  * differs from the exact one, integer-valued inputs whose products are exact,
- * transpose/broadcast/scale/accumulate invariants, and an f64 error bound.
+ * transpose/broadcast/scale/accumulate invariants, and an f64 error bound;
+ * for the bias functions, the reference's own elementwise test
+ * (tests/kernels_match_reference.rs:125-170) restated, exact integer cases,
+ * an order-sensitive column and an f64 bound.
  */
 #include <math.h>
 #include <stddef.h>
@@ -164,4 +174,29 @@ void oracle_softmax_backward(const float *probabilities, float *grad, size_t row
         for (size_t c = 0; c < cols; ++c) projection = projection + g[c] * p[c];
         for (size_t c = 0; c < cols; ++c) g[c] = p[c] * (g[c] - projection);
     }
+}
+
+/* output[r, c] += bias[c] over a [rows, cols] row-major matrix. */
+void oracle_add_row_bias(float *output, size_t rows, size_t cols, const float *bias) {
+    for (size_t r = 0; r < rows; ++r)
+        for (size_t c = 0; c < cols; ++c) output[r * cols + c] = output[r * cols + c] + bias[c];
+}
+
+/* sums[c] += (f32 sum of input[0, c], input[1, c], ... in row order). The
+ * reference runs one thread per column; walking the rows in memory order and
+ * keeping one running sum per column performs the same additions in the same
+ * order. `scratch` holds `cols` floats. */
+void oracle_accumulate_column_sums(const float *input, size_t rows, size_t cols, float *sums, float *scratch) {
+    for (size_t c = 0; c < cols; ++c) scratch[c] = 0.0f;
+    for (size_t r = 0; r < rows; ++r)
+        for (size_t c = 0; c < cols; ++c) scratch[c] = scratch[c] + input[r * cols + c];
+    for (size_t c = 0; c < cols; ++c) sums[c] = sums[c] + scratch[c];
+}
+
+/* The column sums (plus the initial sums) in f64. */
+void oracle_column_sums_f64(const float *input, size_t rows, size_t cols, const float *initial, double *out) {
+    for (size_t c = 0; c < cols; ++c) out[c] = 0.0;
+    for (size_t r = 0; r < rows; ++r)
+        for (size_t c = 0; c < cols; ++c) out[c] += (double)input[r * cols + c];
+    for (size_t c = 0; c < cols; ++c) out[c] += (double)initial[c];
 }

@@ -52,6 +52,12 @@ def load() -> ctypes.CDLL:
         lib.oracle_causal_softmax.restype = None
         lib.oracle_softmax_backward.argtypes = [_f32p, _f32p, _size, _size]
         lib.oracle_softmax_backward.restype = None
+        lib.oracle_add_row_bias.argtypes = [_f32p, _size, _size, _f32p]
+        lib.oracle_add_row_bias.restype = None
+        lib.oracle_accumulate_column_sums.argtypes = [_f32p, _size, _size, _f32p, _f32p]
+        lib.oracle_accumulate_column_sums.restype = None
+        lib.oracle_column_sums_f64.argtypes = [_f32p, _size, _size, _f32p, _f64p]
+        lib.oracle_column_sums_f64.restype = None
         _lib = lib
     return _lib
 
@@ -147,6 +153,28 @@ def softmax_backward(probabilities: np.ndarray, grad: np.ndarray, cols: int) -> 
     """``reference::softmax_backward`` in place on ``grad`` (reference.rs:122-137)."""
     assert probabilities.size == grad.size and grad.size % cols == 0
     load().oracle_softmax_backward(_f32(probabilities), _f32(grad), grad.size // cols, cols)
+
+
+def add_row_bias(output: np.ndarray, cols: int, bias: np.ndarray) -> None:
+    """``output[r, c] += bias[c]`` in place on ``[rows, cols]`` (kernels/elementwise.rs:62-68)."""
+    assert output.size % cols == 0 and bias.size == cols
+    load().oracle_add_row_bias(_f32(output), output.size // cols, cols, _f32(bias))
+
+
+def accumulate_column_sums(values: np.ndarray, cols: int, sums: np.ndarray) -> None:
+    """``sums[c] += Σ_r values[r, c]``, each column summed in row order in f32
+    (kernels/elementwise.rs:78-93); ``sums`` is updated in place."""
+    assert values.size % cols == 0 and sums.size == cols
+    scratch = np.empty(cols, np.float32)
+    load().oracle_accumulate_column_sums(_f32(values), values.size // cols, cols, _f32(sums), _f32(scratch))
+
+
+def column_sums_f64(values: np.ndarray, cols: int, initial: np.ndarray) -> np.ndarray:
+    """``initial + Σ_r values[r, :]`` in f64 (an error yardstick, not the parity target)."""
+    assert values.size % cols == 0 and initial.size == cols
+    out = np.empty(cols, np.float64)
+    load().oracle_column_sums_f64(_f32(values), values.size // cols, cols, _f32(initial), out.ctypes.data_as(_f64p))
+    return out
 
 
 def _workers(workers):

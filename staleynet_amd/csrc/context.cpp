@@ -287,8 +287,16 @@ int sn_matmul_validate(const sn_matmul_spec* spec, size_t left_len, size_t right
     return SN_OK;
 }
 
-int sn_matmul(sn_context* ctx, const sn_matmul_spec* spec, const float* left, size_t left_len, const float* right,
-              size_t right_len, float* output, size_t output_len) {
+}  // extern "C"
+
+namespace {
+
+// sn_matmul and sn_matmul_bias: validation, then the product with `bias`
+// (null: none) added in its epilogue, or, for a masked spec, after it by the
+// bias kernel.
+int matmul_with_bias(sn_context* ctx, const sn_matmul_spec* spec, const float* left, size_t left_len,
+                     const float* right, size_t right_len, const float* bias, size_t bias_len, float* output,
+                     size_t output_len) {
     if (ctx == nullptr) return SN_ERR_NULL_ARGUMENT;
     int rc = sn_matmul_validate(spec, left_len, right_len, output_len);
     if (rc != SN_OK) return rc;
@@ -299,6 +307,7 @@ int sn_matmul(sn_context* ctx, const sn_matmul_spec* spec, const float* left, si
         return SN_ERR_NULL_ARGUMENT;
     if (overlaps(output, need.output, left, need.left) || overlaps(output, need.output, right, need.right))
         return SN_ERR_ALIASING;
+    if (bias != nullptr && overlaps(output, need.output, bias, bias_len)) return SN_ERR_ALIASING;
     if (spec->rows == 0 || spec->cols == 0) return SN_OK;
 
     sn::Problem p;
@@ -324,6 +333,10 @@ int sn_matmul(sn_context* ctx, const sn_matmul_spec* spec, const float* left, si
     p.accumulate = spec->write == SN_ACCUMULATE;
     p.mask = spec->mask;
     p.query_offset = int64_t(spec->query_offset);
+    // A masked product takes its bias afterwards (the kernels fuse it only
+    // into unmasked epilogues).
+    const bool bias_after = bias != nullptr && p.mask != SN_MASK_NONE;
+    p.bias = bias_after ? nullptr : bias;
 
     uint32_t kernel = ctx->kernel;
     if (spec->precision == SN_PRECISION_F32 && kernel == SN_KERNEL_MFMA_BF16) kernel = SN_KERNEL_MFMA_F32;
@@ -331,11 +344,74 @@ int sn_matmul(sn_context* ctx, const sn_matmul_spec* spec, const float* left, si
 
     hipError_t err = hipSetDevice(ctx->device);
     if (err != hipSuccess) return status(err);
-    if (kernel == SN_KERNEL_SIMPLE) return status(sn::launch_gemm_simple(p, ctx->stream));
     const bool bf16 = kernel == SN_KERNEL_MFMA_BF16;
-    if (!bf16 && sn::gemv_applies(p, ctx->env)) return status(sn::launch_gemv(p, ctx->env, ctx->stream));
-    if (sn::gemm_workspace_bytes(p, bf16, ctx->env) > ctx->env.workspace_bytes) return SN_ERR_WORKSPACE;
-    return status(bf16 ? sn::launch_gemm_bf16(p, ctx->env, ctx->stream) : sn::launch_gemm_f32(p, ctx->env, ctx->stream));
+    if (kernel == SN_KERNEL_SIMPLE) {
+        err = sn::launch_gemm_simple(p, ctx->stream);
+    } else if (!bf16 && sn::gemv_applies(p, ctx->env)) {
+        err = sn::launch_gemv(p, ctx->env, ctx->stream);
+    } else {
+        if (sn::gemm_workspace_bytes(p, bf16, ctx->env) > ctx->env.workspace_bytes) return SN_ERR_WORKSPACE;
+        err = bf16 ? sn::launch_gemm_bf16(p, ctx->env, ctx->stream) : sn::launch_gemm_f32(p, ctx->env, ctx->stream);
+    }
+    if (err == hipSuccess && bias_after)
+        err = sn::launch_add_row_bias(output, p.m, p.n, p.batch, p.stride_c, bias, ctx->stream);
+    return status(err);
+}
+
+}  // namespace
+
+extern "C" {
+
+int sn_matmul(sn_context* ctx, const sn_matmul_spec* spec, const float* left, size_t left_len, const float* right,
+              size_t right_len, float* output, size_t output_len) {
+    return matmul_with_bias(ctx, spec, left, left_len, right, right_len, nullptr, 0, output, output_len);
+}
+
+int sn_matmul_bias(sn_context* ctx, const sn_matmul_spec* spec, const float* left, size_t left_len,
+                   const float* right, size_t right_len, const float* bias, size_t bias_len, float* output,
+                   size_t output_len) {
+    const int rc = sn_matmul_validate(spec, left_len, right_len, output_len);
+    if (rc != SN_OK) return rc;
+    if (bias_len != spec->cols) return SN_ERR_LENGTH_MISMATCH;
+    // Output matrices that share memory (a batch stride below one matrix)
+    // would take the bias more than once.
+    if (spec->batch_count > 1 && spec->batch_output < spec->rows * spec->cols) return SN_ERR_UNSUPPORTED;
+    if (ctx == nullptr || (bias == nullptr && bias_len > 0)) return SN_ERR_NULL_ARGUMENT;
+    return matmul_with_bias(ctx, spec, left, left_len, right, right_len, bias, bias_len, output, output_len);
+}
+
+int sn_add_row_bias(sn_context* ctx, float* output, size_t rows, size_t cols, const float* bias, size_t bias_len) {
+    if (bias_len != cols) return SN_ERR_LENGTH_MISMATCH;
+    if (ctx == nullptr) return SN_ERR_NULL_ARGUMENT;
+    size_t elements;
+    if (mul_overflows(rows, cols, &elements) || elements >= (size_t(1) << 60)) return SN_ERR_OVERFLOW;
+    if (elements == 0) return SN_OK;
+    if (output == nullptr || bias == nullptr) return SN_ERR_NULL_ARGUMENT;
+    if (overlaps(output, elements, bias, bias_len)) return SN_ERR_ALIASING;
+    hipError_t err = hipSetDevice(ctx->device);
+    if (err == hipSuccess)
+        err = sn::launch_add_row_bias(output, int64_t(rows), int64_t(cols), 1, int64_t(elements), bias, ctx->stream);
+    return status(err);
+}
+
+int sn_accumulate_column_sums(sn_context* ctx, const float* input, size_t rows, size_t cols, float* sums,
+                              size_t sums_len) {
+    if (sums_len != cols) return SN_ERR_LENGTH_MISMATCH;
+    if (ctx == nullptr) return SN_ERR_NULL_ARGUMENT;
+    size_t elements;
+    if (mul_overflows(rows, cols, &elements) || elements >= (size_t(1) << 60) || cols >= kMaxDimension ||
+        rows >= kMaxDimension)
+        return SN_ERR_OVERFLOW;
+    if (cols == 0) return SN_OK;
+    if (sums == nullptr || (elements > 0 && input == nullptr)) return SN_ERR_NULL_ARGUMENT;
+    if (elements == 0) return SN_OK;  // every column sums to 0: sums unchanged
+    if (overlaps(sums, sums_len, input, elements)) return SN_ERR_ALIASING;
+    if (sn::column_sums_workspace_bytes(int64_t(rows), int64_t(cols), ctx->env) > ctx->env.workspace_bytes)
+        return SN_ERR_WORKSPACE;
+    hipError_t err = hipSetDevice(ctx->device);
+    if (err == hipSuccess)
+        err = sn::launch_column_sums(input, int64_t(rows), int64_t(cols), sums, ctx->env, ctx->stream);
+    return status(err);
 }
 
 const char* sn_status_string(int code) {
@@ -362,6 +438,8 @@ const char* sn_status_string(int code) {
             return "no GPU at the requested ordinal";
         case SN_ERR_WORKSPACE:
             return "matmul: split-K workspace too small";
+        case SN_ERR_LENGTH_MISMATCH:
+            return "bias or sums length must equal the matrix's columns";
         default:
             break;
     }

@@ -101,6 +101,7 @@ struct Args {
     int32_t accumulate;
     int32_t mask;
     float scale;
+    const float* bias;  // null, or one value per column added after the combine
 };
 
 template <int BM_, int BN_, int BK_, int WAVES_M_, int WAVES_N_>
@@ -415,11 +416,15 @@ inline int64_t batches_per_launch(int64_t per_batch, int threads, int64_t batch)
 }
 
 // The reference's combine (kernels/matmul.rs:166-168), the product and the
-// sum rounded separately as the reference rounds them.
-__device__ __forceinline__ void write_output(float* dst, float sum, float scale, bool accumulate) {
+// sum rounded separately as the reference rounds them; then, when fused,
+// Linear's bias (kernels/elementwise.rs:62-68) as one more rounded add.
+__device__ __forceinline__ void write_output(float* dst, float sum, float scale, bool accumulate,
+                                             const float* bias = nullptr, int64_t col = 0) {
 #pragma clang fp contract(off)
     const float scaled = scale * sum;
-    *dst = accumulate ? *dst + scaled : scaled;
+    float value = accumulate ? *dst + scaled : scaled;
+    if (bias != nullptr) value = value + bias[col];
+    *dst = value;
 }
 
 // Writes a wave's accumulators: 32x32 blocks, element r of a block at row
@@ -448,6 +453,12 @@ __device__ __forceinline__ void write_tile(const Args& args, const f32x16 (&acc)
             // and a select per element, still no branch).
             const float scale = partial ? 1.f : args.scale;
             const bool any_masked = !partial && output_causal && n0 + T::BN - 1 > m0 + args.query_offset;
+            // Fused bias (never with a mask): one value per lane and column block.
+            const bool add_bias = !partial && args.bias != nullptr;
+            float bias_value[T::FN];
+#pragma unroll
+            for (int j = 0; j < T::FN; ++j)
+                bias_value[j] = add_bias ? args.bias[n0 + wave_n * T::WTN + 32 * j + col_in_block] : 0.f;
             // col - row - offset of the lane's element at block (0, 0), r = 0.
             // (Clamped to 32 bits: beyond +-2^30 every element is on the same side.)
             const int64_t diagonal64 = n0 + wave_n * T::WTN + col_in_block - (m0 + wave_m * T::WTM + 4 * half) -
@@ -465,6 +476,7 @@ __device__ __forceinline__ void write_tile(const Args& args, const f32x16 (&acc)
                         const int32_t row_offset = int32_t(row * args.n * 4);
                         float value = scale * acc[i][j][r];
                         if (any_masked) value = diagonal + 32 * j - row > 0 ? 0.f : value;
+                        if (add_bias) value = value + bias_value[j];
                         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, value), rsrc, column_offset,
                                                               row_offset, 0);
                     }
@@ -489,7 +501,9 @@ __device__ __forceinline__ void write_tile(const Args& args, const f32x16 (&acc)
                     } else {
 #pragma clang fp contract(off)
                         const float scaled = args.scale * sum;
-                        buffer_store1(rsrc, offset, accumulate ? buffer_load1(rsrc, offset) + scaled : scaled);
+                        float value = accumulate ? buffer_load1(rsrc, offset) + scaled : scaled;
+                        if (args.bias != nullptr && inside) value = value + args.bias[n0 + col];
+                        buffer_store1(rsrc, offset, value);
                     }
                 }
     } else {
@@ -508,7 +522,7 @@ __device__ __forceinline__ void write_tile(const Args& args, const f32x16 (&acc)
                         } else if (output_causal && col > row + args.query_offset) {
                             if (!accumulate) *dst = 0.f;
                         } else {
-                            write_output(dst, acc[i][j][r], args.scale, accumulate);
+                            write_output(dst, acc[i][j][r], args.scale, accumulate, args.bias, col);
                         }
                     }
                 }
@@ -621,6 +635,7 @@ Args make_args(const Problem& p, const Env& env, const Plan& plan) {
     args.accumulate = p.accumulate ? 1 : 0;
     args.mask = int(p.mask);
     args.scale = p.scale;
+    args.bias = p.bias;
     return args;
 }
 

@@ -25,6 +25,10 @@ struct Problem {
     bool accumulate = false;
     uint32_t mask = 0;           // SN_MASK_*
     int64_t query_offset = 0;
+    // Linear's bias, fused: output[.., r, c] += bias[c] after the combine,
+    // rounded separately. Only for unmasked products (the C entry point runs
+    // a masked one as the product and then the bias kernel).
+    const float* bias = nullptr;
 };
 
 // What a launch may use beyond its operands: the context's split-K scratch,
@@ -49,5 +53,15 @@ bool gemv_applies(const Problem& p, const Env& env);
 
 // Bytes of split-K workspace launch_gemm_* would use for `p` (0 = none).
 size_t gemm_workspace_bytes(const Problem& p, bool bf16, const Env& env);
+
+// Linear's bias kernels (bias.hip). add_row_bias: out[b][r][c] += bias[c]
+// for `batch` [rows, cols] matrices `stride` floats apart. column_sums:
+// sums[c] += column c's sum over the [rows, cols] input, per-slice sums in
+// the workspace (column_sums_workspace_bytes of it).
+hipError_t launch_add_row_bias(float* out, int64_t rows, int64_t cols, int64_t batch, int64_t stride,
+                               const float* bias, hipStream_t stream);
+hipError_t launch_column_sums(const float* in, int64_t rows, int64_t cols, float* sums, const Env& env,
+                              hipStream_t stream);
+size_t column_sums_workspace_bytes(int64_t rows, int64_t cols, const Env& env);
 
 }  // namespace sn

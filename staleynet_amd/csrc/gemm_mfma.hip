@@ -176,7 +176,8 @@ __global__ __launch_bounds__(T::THREADS) void gemm_f32_kernel(Args args) {
 // the reference's combine.
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, float* c, int64_t m,
                                                             int64_t n, int64_t batches, int splits,
-                                                            int64_t stride_c, float scale, int accumulate) {
+                                                            int64_t stride_c, float scale, int accumulate,
+                                                            const float* __restrict__ bias) {
     const int64_t per_matrix = m * n;
     const int64_t total = per_matrix * batches;
     for (int64_t idx = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; idx < total;
@@ -188,15 +189,16 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
         float sum = 0.f;
 #pragma unroll 8
         for (int s = 0; s < splits; ++s) sum = sum + src[s * per_matrix];
-        write_output(c + bat * stride_c + e, sum, scale, accumulate != 0);
+        write_output(c + bat * stride_c + e, sum, scale, accumulate != 0, bias, e % n);
     }
 }
 
 // The same for 16-byte-aligned outputs with M*N a multiple of 4: four
 // consecutive outputs per thread, 16-byte loads, 8 splits in flight.
 __global__ __launch_bounds__(256) void splitk_reduce4_kernel(const f32x4* __restrict__ ws, float* c,
-                                                             int64_t per_matrix, int64_t batches, int splits,
-                                                             int64_t stride_c, float scale, int accumulate) {
+                                                             int64_t per_matrix, int64_t n, int64_t batches,
+                                                             int splits, int64_t stride_c, float scale,
+                                                             int accumulate, const float* __restrict__ bias) {
     const int64_t per_matrix4 = per_matrix / 4;
     const int64_t total = per_matrix4 * batches;
     for (int64_t idx = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; idx < total;
@@ -210,7 +212,7 @@ __global__ __launch_bounds__(256) void splitk_reduce4_kernel(const f32x4* __rest
         for (int s = 0; s < splits; ++s) sum = sum + src[s * per_matrix4];
         float* dst = c + bat * stride_c + 4 * e4;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) write_output(dst + j, sum[j], scale, accumulate != 0);
+        for (int j = 0; j < 4; ++j) write_output(dst + j, sum[j], scale, accumulate != 0, bias, (4 * e4 + j) % n);
     }
 }
 
@@ -259,13 +261,13 @@ hipError_t launch_splitk_reduce(const Problem& p, const Env& env, int splits, hi
     if ((p.m * p.n) % 4 == 0 && p.stride_c % 4 == 0 && aligned16(p.c)) {
         const int64_t grid = std::min<int64_t>((total / 4 + 255) / 256, int64_t(env.cu_count) * 16);
         hipLaunchKernelGGL(splitk_reduce4_kernel, dim3(unsigned(grid)), dim3(256), 0, stream,
-                           reinterpret_cast<const f32x4*>(env.workspace), p.c, p.m * p.n, p.batch, splits, p.stride_c,
-                           p.scale, p.accumulate ? 1 : 0);
+                           reinterpret_cast<const f32x4*>(env.workspace), p.c, p.m * p.n, p.n, p.batch, splits,
+                           p.stride_c, p.scale, p.accumulate ? 1 : 0, p.bias);
         return hipGetLastError();
     }
     const int64_t grid = std::min<int64_t>((total + 255) / 256, int64_t(env.cu_count) * 16);
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3(unsigned(grid)), dim3(256), 0, stream, env.workspace, p.c, p.m,
-                       p.n, p.batch, splits, p.stride_c, p.scale, p.accumulate ? 1 : 0);
+                       p.n, p.batch, splits, p.stride_c, p.scale, p.accumulate ? 1 : 0, p.bias);
     return hipGetLastError();
 }
 

@@ -18,6 +18,7 @@ struct SimpleArgs {
     int64_t m, n, k, lda, ldb, stride_a, stride_b, stride_c, batch_base, query_offset;
     int32_t a_k_contiguous, b_k_contiguous, accumulate, mask;
     float scale;
+    const float* bias;
 };
 
 __global__ __launch_bounds__(256) void gemm_simple_kernel(SimpleArgs p) {
@@ -47,14 +48,17 @@ __global__ __launch_bounds__(256) void gemm_simple_kernel(SimpleArgs p) {
         sum = sum + product;
     }
     const float scaled = p.scale * sum;
-    *dst = p.accumulate ? *dst + scaled : scaled;
+    float value = p.accumulate ? *dst + scaled : scaled;
+    if (p.bias != nullptr) value = value + p.bias[col];
+    *dst = value;
 }
 
 }  // namespace
 
 hipError_t launch_gemm_simple(const Problem& p, hipStream_t stream) {
     SimpleArgs args{p.a, p.b, p.c, p.m, p.n, p.k, p.lda, p.ldb, p.stride_a, p.stride_b, p.stride_c, 0,
-                    p.query_offset, p.a_k_contiguous, p.b_k_contiguous, p.accumulate, int32_t(p.mask), p.scale};
+                    p.query_offset, p.a_k_contiguous, p.b_k_contiguous, p.accumulate, int32_t(p.mask), p.scale,
+                    p.bias};
     if ((p.m + 15) / 16 > 65535 || (p.n + 15) / 16 * 16 >= (int64_t(1) << 32)) return hipErrorInvalidConfiguration;
     const dim3 grid(unsigned((p.n + 15) / 16), unsigned((p.m + 15) / 16), 1);
     for (int64_t first = 0; first < p.batch; first += 65535) {

@@ -101,6 +101,7 @@ struct GemvArgs {
     int32_t splits;
     int32_t accumulate;
     float scale;
+    const float* bias;  // null, or Linear's bias added after the combine
 };
 
 // MT: rows of x the instantiation holds; LPR: lanes per row piece (the slab
@@ -296,7 +297,8 @@ __global__ __launch_bounds__(64 * waves_for<MT>()) void gemv_kernel(GemvArgs arg
         if (out_ok) {
             float* dst = args.y + batch * args.stride_y + om * args.n + out_col;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) gemm::write_output(dst + j, slab_sum[j], args.scale, args.accumulate != 0);
+            for (int j = 0; j < 4; ++j)
+                gemm::write_output(dst + j, slab_sum[j], args.scale, args.accumulate != 0, args.bias, out_col + j);
         }
         return;
     }
@@ -328,7 +330,8 @@ __global__ __launch_bounds__(64 * waves_for<MT>()) void gemv_kernel(GemvArgs arg
             sum += gemm::buffer_load4_coherent(all, int32_t((s * per_matrix + om * args.n + 4 * oc) * 4));
         float* dst = args.y + batch * args.stride_y + om * args.n + out_col;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) gemm::write_output(dst + j, sum[j], args.scale, args.accumulate != 0);
+        for (int j = 0; j < 4; ++j)
+            gemm::write_output(dst + j, sum[j], args.scale, args.accumulate != 0, args.bias, out_col + j);
     }
     if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -388,6 +391,7 @@ hipError_t launch_rows(const Problem& p, const Env& env, const GemvPlan& plan, h
     args.splits = plan.splits;
     args.accumulate = p.accumulate ? 1 : 0;
     args.scale = p.scale;
+    args.bias = p.bias;
     hipLaunchKernelGGL((gemv_kernel<MT, LPR>), dim3(plan.column_blocks, plan.splits, unsigned(p.batch)),
                        dim3(64 * waves_for<MT>()), 0, stream, args);
     return hipGetLastError();

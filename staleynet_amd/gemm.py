@@ -44,9 +44,11 @@ SN_ERR_UNSUPPORTED = -7
 SN_ERR_ALIASING = -8
 SN_ERR_NO_DEVICE = -9
 SN_ERR_WORKSPACE = -10
+SN_ERR_LENGTH_MISMATCH = -11
 
 _VALIDATION_CODES = {SN_ERR_LEFT_TOO_SMALL, SN_ERR_RIGHT_TOO_SMALL, SN_ERR_OUTPUT_TOO_SMALL, SN_ERR_EMPTY_BATCH,
-                     SN_ERR_OVERFLOW, SN_ERR_UNSUPPORTED, SN_ERR_ALIASING, SN_ERR_NULL_ARGUMENT}
+                     SN_ERR_OVERFLOW, SN_ERR_UNSUPPORTED, SN_ERR_ALIASING, SN_ERR_NULL_ARGUMENT,
+                     SN_ERR_LENGTH_MISMATCH}
 
 
 class Storage(enum.IntEnum):
@@ -239,10 +241,15 @@ def _library() -> ctypes.CDLL:
                                        ctypes.c_float, ctypes.c_float]
         lib.sn_copy_device.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, size]
         lib.sn_read_sum.argtypes = [ctypes.c_void_p, ctypes.c_void_p, size, ctypes.c_void_p, size]
+        lib.sn_add_row_bias.argtypes = [ctx, ctypes.c_void_p, size, size, ctypes.c_void_p, size]
+        lib.sn_accumulate_column_sums.argtypes = [ctx, ctypes.c_void_p, size, size, ctypes.c_void_p, size]
+        lib.sn_matmul_bias.argtypes = [ctx, ctypes.POINTER(CMatmulSpec), ctypes.c_void_p, size, ctypes.c_void_p,
+                                       size, ctypes.c_void_p, size, ctypes.c_void_p, size]
         for name in ("sn_context_create", "sn_context_create_with_workspace", "sn_context_destroy",
                      "sn_context_bind", "sn_context_set_kernel", "sn_context_get_kernel", "sn_synchronize",
                      "sn_alloc_zeroed", "sn_free", "sn_upload", "sn_download", "sn_copy_from_host", "sn_fill_zero",
-                     "sn_matmul_validate", "sn_matmul", "sn_fill_normal", "sn_copy_device", "sn_read_sum"):
+                     "sn_matmul_validate", "sn_matmul", "sn_fill_normal", "sn_copy_device", "sn_read_sum",
+                     "sn_add_row_bias", "sn_accumulate_column_sums", "sn_matmul_bias"):
             getattr(lib, name).restype = ctypes.c_int
         _lib = lib
     return _lib
@@ -421,6 +428,33 @@ class Gpu:
     def matmul(self, spec: MatmulSpec, left: Tensor, right: Tensor, output: Tensor) -> None:
         """``Gpu::matmul``: enqueue ``output = scale·op(left)·op(right) (+ output)``."""
         self.matmul_raw(spec, left.pointer, len(left), right.pointer, len(right), output.pointer, len(output))
+
+    def matmul_bias(self, spec: MatmulSpec, left: Tensor, right: Tensor, bias: Tensor, output: Tensor) -> None:
+        """``Linear::forward``'s ``matmul`` then ``add_row_bias`` (linear.rs:46-47) in one pass
+        (``sn_matmul_bias``): the bias is added in the product's epilogue, rounded as the two calls round."""
+        c = spec.to_c()
+        rc = _library().sn_matmul_bias(self._ctx, ctypes.byref(c), ctypes.c_void_p(left.pointer), len(left),
+                                       ctypes.c_void_p(right.pointer), len(right), ctypes.c_void_p(bias.pointer),
+                                       len(bias), ctypes.c_void_p(output.pointer), len(output))
+        if rc in _VALIDATION_CODES:
+            raise MatmulPanic(rc)
+        self._check(rc, "matmul_bias")
+
+    def add_row_bias(self, output: Tensor, bias: Tensor) -> None:
+        """``Gpu::add_row_bias`` (ops/elementwise.rs:30-41): ``output[r, c] += bias[c]``."""
+        rc = _library().sn_add_row_bias(self._ctx, ctypes.c_void_p(output.pointer), output.shape().rows,
+                                        output.shape().cols, ctypes.c_void_p(bias.pointer), len(bias))
+        if rc == SN_ERR_LENGTH_MISMATCH:
+            raise AssertionError("add_row_bias: bias length must equal output columns")
+        self._check(rc, "add_row_bias")
+
+    def accumulate_column_sums(self, input: Tensor, sums: Tensor) -> None:
+        """``Gpu::accumulate_column_sums`` (ops/elementwise.rs:43-58): ``sums += Σ_rows input``."""
+        rc = _library().sn_accumulate_column_sums(self._ctx, ctypes.c_void_p(input.pointer), input.shape().rows,
+                                                  input.shape().cols, ctypes.c_void_p(sums.pointer), len(sums))
+        if rc == SN_ERR_LENGTH_MISMATCH:
+            raise AssertionError("accumulate_column_sums: sums length must equal input columns")
+        self._check(rc, "accumulate_column_sums")
 
     def matmul_raw(self, spec: MatmulSpec, left: int, left_len: int, right: int, right_len: int, output: int,
                    output_len: int) -> None:

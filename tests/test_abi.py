@@ -104,11 +104,31 @@ def test_null_spec_and_null_context_are_errors_not_crashes():
     assert lib.sn_context_destroy(None) == gemm.SN_OK
 
 
+def test_bias_entry_points_check_lengths_before_touching_the_device():
+    # ops/elementwise.rs:33 and :46 assert the vector length against the column count.
+    lib = gemm.library()
+    assert lib.sn_add_row_bias(None, None, 4, 5, None, 4) == gemm.SN_ERR_LENGTH_MISMATCH
+    assert lib.sn_add_row_bias(None, None, 4, 5, None, 5) == gemm.SN_ERR_NULL_ARGUMENT
+    assert lib.sn_accumulate_column_sums(None, None, 4, 5, None, 6) == gemm.SN_ERR_LENGTH_MISMATCH
+    assert lib.sn_accumulate_column_sums(None, None, 4, 5, None, 5) == gemm.SN_ERR_NULL_ARGUMENT
+    spec = MatmulSpec.new(4, 5, 3).to_c()
+    assert lib.sn_matmul_bias(None, ctypes.byref(spec), None, 12, None, 15, None, 4, None, 20) == \
+        gemm.SN_ERR_LENGTH_MISMATCH
+    assert lib.sn_matmul_bias(None, ctypes.byref(spec), None, 11, None, 15, None, 5, None, 20) == \
+        gemm.SN_ERR_LEFT_TOO_SMALL
+    assert lib.sn_matmul_bias(None, ctypes.byref(spec), None, 12, None, 15, None, 5, None, 20) == \
+        gemm.SN_ERR_NULL_ARGUMENT
+    shared = MatmulSpec.new(4, 5, 3).batched(gemm.BatchStrides(2, 12, 15, 0)).to_c()
+    assert lib.sn_matmul_bias(None, ctypes.byref(shared), None, 24, None, 30, None, 5, None, 20) == \
+        gemm.SN_ERR_UNSUPPORTED
+    assert gemm.status_string(gemm.SN_ERR_LENGTH_MISMATCH) == "bias or sums length must equal the matrix's columns"
+
+
 def test_status_strings_carry_the_reference_panic_messages():
     assert gemm.status_string(gemm.SN_ERR_LEFT_TOO_SMALL) == "matmul: left operand too small"
     assert gemm.status_string(gemm.SN_ERR_RIGHT_TOO_SMALL) == "matmul: right operand too small"
     assert gemm.status_string(gemm.SN_ERR_OUTPUT_TOO_SMALL) == "matmul: output too small"
-    for code in range(-10, 1):
+    for code in range(-11, 1):
         assert gemm.status_string(code)
 
 

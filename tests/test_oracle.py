@@ -226,3 +226,64 @@ def test_parallel_drivers_are_bit_identical_to_the_serial_loop():
     bi, ri, ci = np.meshgrid(np.arange(count), np.arange(rows), np.arange(cols), indexing="ij")
     picked = oracle.matmul_elements_parallel(p, a, b, bi.ravel(), ri.ravel(), ci.ravel(), c, workers=7)
     assert np.array_equal(serial, picked)
+
+
+# ---- Linear's bias kernels (kernels/elementwise.rs:62-93) -------------------
+
+def test_reference_elementwise_test_for_bias_and_column_sums():
+    # kernels_match_reference.rs:125-170 on its own inputs: shape 9 x 50, LCG seeds 7 (input), 9 (bias).
+    # The expected column sums there are bias[c] + the f32 sum of the column in row order
+    # (`.sum::<f32>()` folds left from 0), written here as an explicit f32 loop.
+    rows, cols = 9, 50
+    values = oracle.random_values(rows * cols, 7)
+    bias = oracle.random_values(cols, 9)
+    expected = np.empty(cols, np.float32)
+    for c in range(cols):
+        total = np.float32(0.0)
+        for r in range(rows):
+            total = np.float32(total + values[r * cols + c])
+        expected[c] = np.float32(bias[c] + total)
+    sums = bias.copy()
+    oracle.accumulate_column_sums(values, cols, sums)
+    assert np.array_equal(sums, expected)
+    # add_row_bias: output[i] + bias[i % cols], one f32 add per element.
+    out = values.copy()
+    oracle.add_row_bias(out, cols, bias)
+    assert np.array_equal(out, (values + np.tile(bias, rows)).astype(np.float32))
+
+
+def test_column_sums_are_sequential_in_rows_with_f32_rounding():
+    # Column 0: 2^24, 1, 1, -2^24 -> sequential f32 gives 0 (each 2^24 + 1 rounds back to 2^24);
+    # a pairwise or reversed sum would give 2. Column 1: 1, 2^24, -2^24, 1 -> sequential 1.
+    big = 2.0 ** 24
+    values = np.array([[big, 1.0], [1.0, big], [1.0, -big], [-big, 1.0]], np.float32).ravel()
+    sums = np.array([0.5, 0.0], np.float32)
+    oracle.accumulate_column_sums(values, 2, sums)
+    assert sums.tolist() == [0.5, 1.0]
+
+
+def test_bias_and_column_sums_are_exact_on_integers():
+    rng = np.random.default_rng(3)
+    rows, cols = 37, 19
+    values = rng.integers(-50, 50, rows * cols).astype(np.float32)
+    bias = rng.integers(-9, 9, cols).astype(np.float32)
+    sums = rng.integers(-9, 9, cols).astype(np.float32)
+    expected = sums.astype(np.int64) + values.reshape(rows, cols).astype(np.int64).sum(axis=0)
+    oracle.accumulate_column_sums(values, cols, sums)
+    assert np.array_equal(sums.astype(np.int64), expected)
+    out = values.copy()
+    oracle.add_row_bias(out, cols, bias)
+    assert np.array_equal(out.reshape(rows, cols).astype(np.int64),
+                          values.reshape(rows, cols).astype(np.int64) + bias.astype(np.int64))
+
+
+def test_column_sums_error_against_f64_is_within_the_sequential_bound():
+    rows, cols = 4096, 7
+    values = oracle.random_values(rows * cols, 21)
+    initial = np.zeros(cols, np.float32)
+    sums = initial.copy()
+    oracle.accumulate_column_sums(values, cols, sums)
+    truth = oracle.column_sums_f64(values, cols, initial)
+    bound = rows * 2.0 ** -24 * np.abs(values.reshape(rows, cols).astype(np.float64)).sum(axis=0)
+    assert np.all(np.abs(sums - truth) <= bound)
+    assert np.max(np.abs(sums - truth)) > 0
