@@ -21,7 +21,9 @@ The printed JSON line is the driver's contract plus:
 - ``attention``: config 3's six causal attention products, 192 heads x T = 2048 x h = 64;
 - ``decode``: config 4's M in {1, 4, 16} products against the 111.5M weights, replayed
   from a HIP graph over a weight pool larger than the 256 MB Infinity Cache, and one
-  decode token's 49 products in sequence.
+  decode token's 49 products in sequence;
+- ``linear_bias``: config 2's Linear forward as the reference calls it (matmul, then
+  add_row_bias) against the fused sn_matmul_bias, and the bias-gradient column sums.
 """
 from __future__ import annotations
 
@@ -356,6 +358,43 @@ def measure_decode(gpu: Gpu, events: HipEvents, pool_bytes: int = 640 << 20, rep
     return result
 
 
+# ---- Linear's bias kernels (SURVEY next row: the steps either side of NN and TN) ---------
+
+def measure_linear(gpu: Gpu, events: HipEvents, buffers, repeats: int = 5):
+    """Config 2's Linear layers (block 0's four and the head): the forward as the reference
+    calls it (matmul, then add_row_bias; linear.rs:46-47) against the fused sn_matmul_bias, and
+    the bias gradient (accumulate_column_sums, linear.rs:59), with the bias kernels' HBM rates
+    (add_row_bias: 8 bytes per output element; column sums: 4 bytes per input element)."""
+    layers = [b for b, (label, _, _) in zip(buffers, training_set()) if label.startswith("b0.") or label == "head"]
+    names = ["qkv", "out", "up", "down", "head"]
+    result = {}
+    for name, buf in zip(names, layers):
+        m, n = buf.y.shape().rows, buf.y.shape().cols
+        k = buf.x.shape().cols
+        bias = gpu.zeros(Shape.vector(n))
+        gpu.fill_normal(bias, SEED, 4000, 0.0, 0.02)
+        sums = gpu.zeros(Shape.vector(n))
+        spec = MatmulSpec.new(m, n, k)
+        gpu.matmul(spec, buf.x, buf.w, buf.y)  # warm-up of each call
+        gpu.add_row_bias(buf.y, bias)
+        gpu.matmul_bias(spec, buf.x, buf.w, bias, buf.y)
+        gpu.accumulate_column_sums(buf.dy, sums)
+        separate = timed(events, gpu.stream, lambda: (gpu.matmul(spec, buf.x, buf.w, buf.y),
+                                                       gpu.add_row_bias(buf.y, bias)), repeats)
+        fused = timed(events, gpu.stream, lambda: gpu.matmul_bias(spec, buf.x, buf.w, bias, buf.y), repeats)
+        bias_ms = timed(events, gpu.stream, lambda: gpu.add_row_bias(buf.y, bias), repeats)
+        sums_ms = timed(events, gpu.stream, lambda: gpu.accumulate_column_sums(buf.dy, sums), repeats)
+        result[f"{name} {m}x{n}x{k}"] = {
+            "forward_separate_ms": round(separate, 4), "forward_fused_ms": round(fused, 4),
+            "fused_saving_pct": round(100 * (1 - fused / separate), 1),
+            "add_row_bias_gbs": round(8 * m * n / (bias_ms * 1e-3) / 1e9, 1),
+            "column_sums_ms": round(sums_ms, 4),
+            "column_sums_gbs": round(4 * m * n / (sums_ms * 1e-3) / 1e9, 1)}
+        bias.free()
+        sums.free()
+    return result
+
+
 # ---- CPU baseline -----------------------------------------------------------------------
 
 def cpu_baseline(gpu: Gpu, calls, budget_s: float):
@@ -622,6 +661,7 @@ def main() -> int:
                           "frac_roofline": round(bf16_tflops / attainable, 4), "per_layout": bf16_layout,
                           "inputs": "fp32 in HBM and LDS, rounded to bf16 (nearest-even) per fragment in registers; "
                                     "fp32 accumulation"}
+        result["linear_bias"] = measure_linear(gpu, events, _buffers)
         result["attention"] = measure_attention(gpu, events)
         result["decode"] = measure_decode(gpu, events)
 

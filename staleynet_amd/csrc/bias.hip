@@ -12,12 +12,13 @@
 //    The reference gives each column one thread that walks all rows in
 //    order (at M = 32768: 2304 threads reading one float each per step, a
 //    small fraction of the machine). Here the work is split two ways: a
-//    workgroup owns 256 columns (a lane 4, one 16-byte load per row) and a
-//    slice of rows, its 4 waves take every 4th row of the slice, and the
-//    waves' sums are added in wave order through LDS; a second kernel adds
-//    the slices' sums in slice order and adds the result to `sums`. The
-//    order is fixed, so every run gives the same bits; it differs from the
-//    reference's row-order sum only in rounding (the tests bound the gap).
+//    workgroup owns 64 columns (a lane 4, one 16-byte load per row) and a
+//    slice of rows, which its 4 row lanes x 4 waves take in turn; the lanes'
+//    and then the waves' sums are added in a fixed order, and a second
+//    kernel adds the slices' sums (eight accumulators, in slice order) and
+//    adds the result to `sums`. The order is fixed, so every run gives the
+//    same bits; it differs from the reference's row-order sum only in
+//    rounding (the tests bound the gap).
 //    HBM-bound: 4 bytes per element read once.
 #include <hip/hip_runtime.h>
 
@@ -59,22 +60,28 @@ __global__ __launch_bounds__(kThreads) void add_row_bias_kernel(float* __restric
     }
 }
 
-// Columns per workgroup and rows a wave loads before it adds (loads in
-// flight per lane).
-constexpr int kColumns = 4 * 64;
+// Column sums: a workgroup owns 64 columns and a slice of rows. A lane owns 4
+// columns (16 lanes cover a 256-byte row piece) and one of 4 row lanes, so a
+// wave load covers 4 rows x 64 columns and the workgroup's 4 waves take 16
+// consecutive rows per round; kUnroll rounds of loads are in flight before
+// they are added.
+constexpr int kColumns = 64;
 constexpr int kUnroll = 8;
 
-// Sum of columns [c0, c0 + 256) over rows [r0, r1) of the input: lane l owns
-// columns c0 + 4l .. +3, wave w rows r0 + w, r0 + w + 4, ... Writes the
-// slice's sums to partial[slice][c] (columns past `cols` are not written).
+// Sum of columns [c0, c0 + 64) over rows [r0, r1): each lane sums its rows in
+// order, the 4 row lanes of a wave are added (xor 16, then 32), then the 4
+// waves in wave order through LDS. Writes partial[slice][c] (columns past
+// `cols` are not written).
 template <bool VECTOR>
 __global__ __launch_bounds__(kThreads) void column_slice_sums_kernel(const float* __restrict__ in, int64_t rows,
                                                                      int64_t cols, int64_t rows_per_slice,
                                                                      float* __restrict__ partial) {
-    __shared__ f32x4 wave_sums[kThreads / 64][64];
+    __shared__ f32x4 wave_sums[kThreads / 64][16];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int64_t c = int64_t(blockIdx.x) * kColumns + 4 * lane;
+    const int col_lane = lane & 15;
+    const int row_lane = lane >> 4;
+    const int64_t c = int64_t(blockIdx.x) * kColumns + 4 * col_lane;
     const int64_t slice = blockIdx.y;
     const int64_t r0 = slice * rows_per_slice;
     const int64_t r1 = std::min<int64_t>(rows, r0 + rows_per_slice);
@@ -92,21 +99,26 @@ __global__ __launch_bounds__(kThreads) void column_slice_sums_kernel(const float
             return v;
         }
     };
-    int64_t r = r0 + wave;
-    for (; r + 4 * (kUnroll - 1) < r1; r += 4 * kUnroll) {
+    int64_t r = r0 + 4 * wave + row_lane;
+    for (; r + 16 * (kUnroll - 1) < r1; r += 16 * kUnroll) {
         f32x4 v[kUnroll];
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) v[u] = load(r + 4 * u);
+        for (int u = 0; u < kUnroll; ++u) v[u] = load(r + 16 * u);
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) sum = sum + v[u];
     }
-    for (; r < r1; r += 4) sum = sum + load(r);
-    wave_sums[wave][lane] = sum;
-    __syncthreads();
-    if (wave == 0) {
-        f32x4 total = wave_sums[0][lane];
+    for (; r < r1; r += 16) sum = sum + load(r);
 #pragma unroll
-        for (int w = 1; w < kThreads / 64; ++w) total = total + wave_sums[w][lane];
+    for (int j = 0; j < 4; ++j) {
+        sum[j] = sum[j] + __shfl_xor(sum[j], 16);
+        sum[j] = sum[j] + __shfl_xor(sum[j], 32);
+    }
+    if (row_lane == 0) wave_sums[wave][col_lane] = sum;
+    __syncthreads();
+    if (threadIdx.x < 16) {
+        f32x4 total = wave_sums[0][threadIdx.x];
+#pragma unroll
+        for (int w = 1; w < kThreads / 64; ++w) total = total + wave_sums[w][threadIdx.x];
         float* dst = partial + slice * cols + c;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -114,25 +126,40 @@ __global__ __launch_bounds__(kThreads) void column_slice_sums_kernel(const float
     }
 }
 
-// sums[c] += (partial[0][c] + partial[1][c] + ...), slices in order.
+// sums[c] += the slices' sums: slice s goes to accumulator s % 8 (so eight
+// loads are in flight), the accumulators are added in order, then the
+// total is added to sums[c]. A fixed order.
 __global__ __launch_bounds__(kThreads) void column_sums_finish_kernel(const float* __restrict__ partial,
                                                                       int64_t slices, int64_t cols,
                                                                       float* __restrict__ sums) {
     const int64_t c = blockIdx.x * int64_t(kThreads) + threadIdx.x;
     if (c >= cols) return;
-    float total = 0.f;
-    for (int64_t s = 0; s < slices; ++s) total = total + partial[s * cols + c];
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    int64_t s = 0;
+    for (; s + 8 <= slices; s += 8) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = partial[(s + j) * cols + c];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = acc[j] + v[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        if (s + j < slices) acc[j] = acc[j] + partial[(s + j) * cols + c];
+    float total = acc[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) total = total + acc[j];
     sums[c] = sums[c] + total;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Slices of rows for about 4 workgroups per CU (each a few hundred rows or
-// more), capped by the workspace.
+// Slices of rows for about 2 workgroups per CU, each at least 256 rows,
+// capped by the workspace.
 int64_t slices_for(int64_t rows, int64_t cols, const Env& env) {
     const int64_t column_blocks = (cols + kColumns - 1) / kColumns;
-    int64_t slices = std::max<int64_t>(1, (int64_t(env.cu_count) * 4 + column_blocks - 1) / column_blocks);
-    slices = std::min<int64_t>(slices, std::max<int64_t>(1, rows / 64));
+    int64_t slices = std::max<int64_t>(1, (int64_t(env.cu_count) * 2 + column_blocks - 1) / column_blocks);
+    slices = std::min<int64_t>(slices, std::max<int64_t>(1, rows / 256));
     const int64_t fit = int64_t(env.workspace_bytes / (sizeof(float) * size_t(std::max<int64_t>(cols, 1))));
     return std::max<int64_t>(1, std::min<int64_t>({slices, fit, 65535}));
 }

@@ -8,6 +8,9 @@
 //   Gpu (new, bind, synchronize, zeros, upload,
 //        download, copy_from_host, fill_zero)      crates/staleynet-cuda/src/device.rs:129-208
 //   Gpu::matmul                                    crates/staleynet-cuda/src/ops/matmul.rs:144-171
+//   Gpu::add_row_bias, Gpu::accumulate_column_sums crates/staleynet-cuda/src/ops/elementwise.rs:30-58
+//   Gpu::matmul_bias (matmul + add_row_bias fused; no reference counterpart: the two calls of
+//                     Linear::forward, crates/staleynet-model/src/layers/linear.rs:46-47)
 //   Shape, Tensor                                  crates/staleynet-cuda/src/device.rs:210-275
 // The reference panics on undersized operands; here that is a thrown
 // staleynet_cuda::Panic carrying the same message. Driver errors (the
@@ -243,6 +246,32 @@ class Gpu {
         const sn_matmul_spec c = spec.to_ffi();
         check(sn_matmul(context_, &c, left.data(), left.len(), right.data(), right.len(), output.data(),
                         output.len()));
+    }
+
+    // `Gpu::add_row_bias`: output[r, c] += bias[c].
+    void add_row_bias(Tensor& output, const Tensor& bias) const {
+        const int rc = sn_add_row_bias(context_, output.data(), output.shape().rows, output.shape().cols, bias.data(),
+                                       bias.len());
+        if (rc == SN_ERR_LENGTH_MISMATCH) throw Panic(rc, "add_row_bias: bias length must equal output columns");
+        check(rc);
+    }
+
+    // `Gpu::accumulate_column_sums`: sums += the column sums of input.
+    void accumulate_column_sums(const Tensor& input, Tensor& sums) const {
+        const int rc = sn_accumulate_column_sums(context_, input.data(), input.shape().rows, input.shape().cols,
+                                                 sums.data(), sums.len());
+        if (rc == SN_ERR_LENGTH_MISMATCH)
+            throw Panic(rc, "accumulate_column_sums: sums length must equal input columns");
+        check(rc);
+    }
+
+    // `matmul` then `add_row_bias` on its output, in one pass (sn_matmul_bias).
+    void matmul_bias(const MatmulSpec& spec, const Tensor& left, const Tensor& right, const Tensor& bias,
+                     Tensor& output) const {
+        check(sn_context_set_kernel(context_, abi_kernel(matmul_kernel)));
+        const sn_matmul_spec c = spec.to_ffi();
+        check(sn_matmul_bias(context_, &c, left.data(), left.len(), right.data(), right.len(), bias.data(),
+                             bias.len(), output.data(), output.len()));
     }
 
     sn_context* raw() const { return context_; }

@@ -21,6 +21,8 @@ void oracle_matmul(size_t rows, size_t cols, size_t inner, int left_t, int right
                    const float* right, float* output);
 void oracle_random_values(size_t count, uint64_t seed, float* out);
 float oracle_relative_error(const float* expected, const float* actual, size_t n);
+void oracle_add_row_bias(float* output, size_t rows, size_t cols, const float* bias);
+void oracle_accumulate_column_sums(const float* input, size_t rows, size_t cols, float* sums, float* scratch);
 }
 
 using namespace staleynet_cuda;
@@ -103,6 +105,59 @@ int main() {
     if (!panicked) {
         ++failures;
         std::printf("FAIL undersized left operand did not panic\n");
+    }
+
+    // The bias half of `elementwise_ops_match_reference` (kernels_match_reference.rs:125-170):
+    // shape 9 x 50, LCG seeds 7 (input) and 9 (bias); add_row_bias is exact, the column sums
+    // within the tolerance. Then Linear::forward fused (matmul_bias) against matmul +
+    // add_row_bias: the same bits.
+    {
+        const size_t rows = 9, cols = 50;
+        const std::vector<float> input = random_values(rows * cols, 7);
+        const std::vector<float> bias = random_values(cols, 9);
+        std::vector<float> expected = input;
+        oracle_add_row_bias(expected.data(), rows, cols, bias.data());
+        Tensor combined = gpu.upload(Shape::new_(rows, cols), input);
+        const Tensor bias_tensor = gpu.upload(Shape::vector(cols), bias);
+        gpu.add_row_bias(combined, bias_tensor);
+        ++cases;
+        if (gpu.download(combined) != expected) {
+            ++failures;
+            std::printf("FAIL add_row_bias differs from the reference's per-element add\n");
+        }
+        std::vector<float> sums_expected = bias, scratch(cols);
+        oracle_accumulate_column_sums(input.data(), rows, cols, sums_expected.data(), scratch.data());
+        Tensor sums = gpu.upload(Shape::vector(cols), bias);
+        gpu.accumulate_column_sums(gpu.upload(Shape::new_(rows, cols), input), sums);
+        ++cases;
+        if (!(relative_error(sums_expected, gpu.download(sums)) < tolerance(MatmulKernel::Blocked))) {
+            ++failures;
+            std::printf("FAIL accumulate_column_sums\n");
+        }
+        gpu.matmul_kernel = MatmulKernel::Blocked;
+        const std::vector<float> x = random_values(130 * 100, 1), w = random_values(100 * cols, 2);
+        const Tensor xt = gpu.upload(Shape::new_(130, 100), x), wt = gpu.upload(Shape::new_(100, cols), w);
+        Tensor fused = gpu.zeros(Shape::new_(130, cols)), separate = gpu.zeros(Shape::new_(130, cols));
+        gpu.matmul_bias(MatmulSpec::new_(130, cols, 100), xt, wt, bias_tensor, fused);
+        gpu.matmul(MatmulSpec::new_(130, cols, 100), xt, wt, separate);
+        gpu.add_row_bias(separate, bias_tensor);
+        ++cases;
+        if (gpu.download(fused) != gpu.download(separate)) {
+            ++failures;
+            std::printf("FAIL matmul_bias differs from matmul + add_row_bias\n");
+        }
+        bool length_panic = false;
+        try {
+            Tensor out = gpu.zeros(Shape::new_(rows, cols));
+            gpu.add_row_bias(out, gpu.zeros(Shape::vector(cols - 1)));
+        } catch (const Panic& panic) {
+            length_panic = std::string(panic.what()) == "add_row_bias: bias length must equal output columns";
+        }
+        ++cases;
+        if (!length_panic) {
+            ++failures;
+            std::printf("FAIL short bias did not panic\n");
+        }
     }
 
     std::printf("%d of %d cases passed\n", cases - failures + (panicked ? 1 : 0), cases + 1);
