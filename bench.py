@@ -275,6 +275,21 @@ def measure_attention(gpu: Gpu, events: HipEvents, repeats: int = 3):
     result["all_six"] = {"dense_ms": round(total["dense"], 3), "causal_ms": round(total["causal"], 3),
                          "causal_tflops_on_visible_work": round(6 * causal_flops / (total["causal"] * 1e-3) / 1e12, 1),
                          "dense_tflops": round(6 * dense_flops / (total["dense"] * 1e-3) / 1e12, 1)}
+    # The row-wise kernels between the products (attention.rs:210, :249), on the same 192 x 2048 x
+    # 2048 matrices: causal_softmax reads each visible score and writes every element (4 bytes
+    # each); softmax_backward reads P and dP and writes dS (12 bytes per element).
+    visible = heads * t * (t + 1) // 2
+    gpu.copy_device(p, s_out)
+    softmax_ms = timed(events, gpu.stream, lambda: gpu.causal_softmax(s_out, t, 0.125, 0), repeats)
+    gpu.causal_softmax(p, t, 0.125, 0)
+    backward_ms = timed(events, gpu.stream, lambda: gpu.softmax_backward(p, dp_out), repeats)
+    result["row_kernels"] = {
+        "causal_softmax_ms": round(softmax_ms, 3),
+        "causal_softmax_gbs": round(4 * (visible + heads * t * t) / (softmax_ms * 1e-3) / 1e9, 1),
+        "softmax_backward_ms": round(backward_ms, 3),
+        "softmax_backward_gbs": round(12 * heads * t * t / (backward_ms * 1e-3) / 1e9, 1)}
+    result["step_ms"] = {"products_causal": round(total["causal"], 3),
+                         "with_softmax_and_backward": round(total["causal"] + softmax_ms + backward_ms, 3)}
     return result
 
 

@@ -72,6 +72,10 @@ extern "C" {
  * "accumulate_column_sums: sums length must equal input columns"
  * (ops/elementwise.rs:33, :46). */
 #define SN_ERR_LENGTH_MISMATCH (-11)
+/* A row-wise kernel's shapes disagree: "causal_softmax: rows must be a
+ * multiple of queries" (ops/attention.rs:59) or "softmax_backward: shape
+ * mismatch" (ops/attention.rs:79). */
+#define SN_ERR_SHAPE (-12)
 
 /* ---- enums (carried as uint32_t in structs) ------------------------------ */
 /* Storage (ops/matmul.rs:15-22). */
@@ -227,6 +231,24 @@ int sn_accumulate_column_sums(sn_context *context, const float *input, size_t ro
 int sn_matmul_bias(sn_context *context, const sn_matmul_spec *spec, const float *left, size_t left_len,
                    const float *right, size_t right_len, const float *bias, size_t bias_len, float *output,
                    size_t output_len);
+
+/* ---- the row-wise kernels between the attention products ------------------ */
+/* `Gpu::causal_softmax` (ops/attention.rs:56-74; kernel kernels/attention.rs:
+ * 140-183), in place on the [rows, keys] scores, called between S = Q K^T and
+ * O = P V (layers/attention.rs:210): row r of each block of `queries` rows
+ * sees keys 0 ..= (r mod queries) + query_offset, which become
+ * exp(s * scale - max) / sum over the visible keys; the other keys become 0.
+ * rows must be a multiple of queries (SN_ERR_SHAPE). Summation order differs
+ * from the reference's, so results are within the fp32 tolerance. */
+int sn_causal_softmax(sn_context *context, float *scores, size_t rows, size_t keys, size_t queries, float scale,
+                      size_t query_offset);
+
+/* `Gpu::softmax_backward` (ops/attention.rs:76-92; kernel kernels/attention.rs:
+ * 185-207), in place on the gradient (layers/attention.rs:249):
+ * grad <- p * (grad - sum(grad * p)) per row. The two shapes must be equal
+ * (SN_ERR_SHAPE); grad must not overlap probabilities (SN_ERR_ALIASING). */
+int sn_softmax_backward(sn_context *context, const float *probabilities, size_t probability_rows,
+                        size_t probability_cols, float *grad, size_t grad_rows, size_t grad_cols);
 
 /* A short English description of a status code (never null). */
 const char *sn_status_string(int status);

@@ -394,6 +394,40 @@ int sn_add_row_bias(sn_context* ctx, float* output, size_t rows, size_t cols, co
     return status(err);
 }
 
+int sn_causal_softmax(sn_context* ctx, float* scores, size_t rows, size_t keys, size_t queries, float scale,
+                      size_t query_offset) {
+    if (queries == 0 || rows % queries != 0) return SN_ERR_SHAPE;
+    if (ctx == nullptr) return SN_ERR_NULL_ARGUMENT;
+    size_t elements;
+    if (mul_overflows(rows, keys, &elements) || elements >= (size_t(1) << 60) || rows >= (size_t(1) << 33) ||
+        query_offset >= (size_t(1) << 62))
+        return SN_ERR_OVERFLOW;
+    if (elements == 0) return SN_OK;
+    if (scores == nullptr) return SN_ERR_NULL_ARGUMENT;
+    hipError_t err = hipSetDevice(ctx->device);
+    if (err == hipSuccess)
+        err = sn::launch_causal_softmax(scores, int64_t(rows), int64_t(queries), int64_t(keys), scale,
+                                        int64_t(query_offset), ctx->stream);
+    return status(err);
+}
+
+int sn_softmax_backward(sn_context* ctx, const float* probabilities, size_t probability_rows,
+                        size_t probability_cols, float* grad, size_t grad_rows, size_t grad_cols) {
+    if (probability_rows != grad_rows || probability_cols != grad_cols) return SN_ERR_SHAPE;
+    if (ctx == nullptr) return SN_ERR_NULL_ARGUMENT;
+    size_t elements;
+    if (mul_overflows(grad_rows, grad_cols, &elements) || elements >= (size_t(1) << 60) ||
+        grad_rows >= (size_t(1) << 33))
+        return SN_ERR_OVERFLOW;
+    if (elements == 0) return SN_OK;
+    if (probabilities == nullptr || grad == nullptr) return SN_ERR_NULL_ARGUMENT;
+    if (overlaps(grad, elements, probabilities, elements)) return SN_ERR_ALIASING;
+    hipError_t err = hipSetDevice(ctx->device);
+    if (err == hipSuccess)
+        err = sn::launch_softmax_backward(probabilities, grad, int64_t(grad_rows), int64_t(grad_cols), ctx->stream);
+    return status(err);
+}
+
 int sn_accumulate_column_sums(sn_context* ctx, const float* input, size_t rows, size_t cols, float* sums,
                               size_t sums_len) {
     if (sums_len != cols) return SN_ERR_LENGTH_MISMATCH;
@@ -440,6 +474,8 @@ const char* sn_status_string(int code) {
             return "matmul: split-K workspace too small";
         case SN_ERR_LENGTH_MISMATCH:
             return "bias or sums length must equal the matrix's columns";
+        case SN_ERR_SHAPE:
+            return "row-wise kernel: rows must be a multiple of queries, or the shapes differ";
         default:
             break;
     }

@@ -64,4 +64,10 @@ hipError_t launch_column_sums(const float* in, int64_t rows, int64_t cols, float
                               hipStream_t stream);
 size_t column_sums_workspace_bytes(int64_t rows, int64_t cols, const Env& env);
 
+// The row-wise kernels between the attention products (softmax.hip).
+hipError_t launch_causal_softmax(float* scores, int64_t rows, int64_t queries, int64_t keys, float scale,
+                                 int64_t query_offset, hipStream_t stream);
+hipError_t launch_softmax_backward(const float* probabilities, float* grad, int64_t rows, int64_t cols,
+                                   hipStream_t stream);
+
 }  // namespace sn

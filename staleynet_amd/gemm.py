@@ -45,6 +45,7 @@ SN_ERR_ALIASING = -8
 SN_ERR_NO_DEVICE = -9
 SN_ERR_WORKSPACE = -10
 SN_ERR_LENGTH_MISMATCH = -11
+SN_ERR_SHAPE = -12
 
 _VALIDATION_CODES = {SN_ERR_LEFT_TOO_SMALL, SN_ERR_RIGHT_TOO_SMALL, SN_ERR_OUTPUT_TOO_SMALL, SN_ERR_EMPTY_BATCH,
                      SN_ERR_OVERFLOW, SN_ERR_UNSUPPORTED, SN_ERR_ALIASING, SN_ERR_NULL_ARGUMENT,
@@ -245,11 +246,14 @@ def _library() -> ctypes.CDLL:
         lib.sn_accumulate_column_sums.argtypes = [ctx, ctypes.c_void_p, size, size, ctypes.c_void_p, size]
         lib.sn_matmul_bias.argtypes = [ctx, ctypes.POINTER(CMatmulSpec), ctypes.c_void_p, size, ctypes.c_void_p,
                                        size, ctypes.c_void_p, size, ctypes.c_void_p, size]
+        lib.sn_causal_softmax.argtypes = [ctx, ctypes.c_void_p, size, size, size, ctypes.c_float, size]
+        lib.sn_softmax_backward.argtypes = [ctx, ctypes.c_void_p, size, size, ctypes.c_void_p, size, size]
         for name in ("sn_context_create", "sn_context_create_with_workspace", "sn_context_destroy",
                      "sn_context_bind", "sn_context_set_kernel", "sn_context_get_kernel", "sn_synchronize",
                      "sn_alloc_zeroed", "sn_free", "sn_upload", "sn_download", "sn_copy_from_host", "sn_fill_zero",
                      "sn_matmul_validate", "sn_matmul", "sn_fill_normal", "sn_copy_device", "sn_read_sum",
-                     "sn_add_row_bias", "sn_accumulate_column_sums", "sn_matmul_bias"):
+                     "sn_add_row_bias", "sn_accumulate_column_sums", "sn_matmul_bias", "sn_causal_softmax",
+                     "sn_softmax_backward"):
             getattr(lib, name).restype = ctypes.c_int
         _lib = lib
     return _lib
@@ -455,6 +459,23 @@ class Gpu:
         if rc == SN_ERR_LENGTH_MISMATCH:
             raise AssertionError("accumulate_column_sums: sums length must equal input columns")
         self._check(rc, "accumulate_column_sums")
+
+    def causal_softmax(self, scores: Tensor, queries: int, scale: float, query_offset: int) -> None:
+        """``Gpu::causal_softmax`` (ops/attention.rs:56-74), in place on ``[rows, keys]`` scores."""
+        rc = _library().sn_causal_softmax(self._ctx, ctypes.c_void_p(scores.pointer), scores.shape().rows,
+                                          scores.shape().cols, queries, scale, query_offset)
+        if rc == SN_ERR_SHAPE:
+            raise AssertionError("causal_softmax: rows must be a multiple of queries")
+        self._check(rc, "causal_softmax")
+
+    def softmax_backward(self, probabilities: Tensor, grad: Tensor) -> None:
+        """``Gpu::softmax_backward`` (ops/attention.rs:76-92), in place on ``grad``."""
+        p, g = probabilities.shape(), grad.shape()
+        rc = _library().sn_softmax_backward(self._ctx, ctypes.c_void_p(probabilities.pointer), p.rows, p.cols,
+                                            ctypes.c_void_p(grad.pointer), g.rows, g.cols)
+        if rc == SN_ERR_SHAPE:
+            raise AssertionError("softmax_backward: shape mismatch")
+        self._check(rc, "softmax_backward")
 
     def matmul_raw(self, spec: MatmulSpec, left: int, left_len: int, right: int, right_len: int, output: int,
                    output_len: int) -> None:

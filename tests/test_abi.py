@@ -124,11 +124,21 @@ def test_bias_entry_points_check_lengths_before_touching_the_device():
     assert gemm.status_string(gemm.SN_ERR_LENGTH_MISMATCH) == "bias or sums length must equal the matrix's columns"
 
 
+def test_row_wise_kernels_check_shapes_before_touching_the_device():
+    # ops/attention.rs:59 (rows % queries) and :79 (equal shapes) are asserts in the reference.
+    lib = gemm.library()
+    assert lib.sn_causal_softmax(None, None, 10, 8, 3, 1.0, 0) == gemm.SN_ERR_SHAPE
+    assert lib.sn_causal_softmax(None, None, 10, 8, 0, 1.0, 0) == gemm.SN_ERR_SHAPE
+    assert lib.sn_causal_softmax(None, None, 10, 8, 5, 1.0, 0) == gemm.SN_ERR_NULL_ARGUMENT
+    assert lib.sn_softmax_backward(None, None, 4, 5, None, 4, 6) == gemm.SN_ERR_SHAPE
+    assert lib.sn_softmax_backward(None, None, 4, 5, None, 4, 5) == gemm.SN_ERR_NULL_ARGUMENT
+
+
 def test_status_strings_carry_the_reference_panic_messages():
     assert gemm.status_string(gemm.SN_ERR_LEFT_TOO_SMALL) == "matmul: left operand too small"
     assert gemm.status_string(gemm.SN_ERR_RIGHT_TOO_SMALL) == "matmul: right operand too small"
     assert gemm.status_string(gemm.SN_ERR_OUTPUT_TOO_SMALL) == "matmul: output too small"
-    for code in range(-11, 1):
+    for code in range(-12, 1):
         assert gemm.status_string(code)
 
 
