@@ -23,7 +23,8 @@ The printed JSON line is the driver's contract plus:
   from a HIP graph over a weight pool larger than the 256 MB Infinity Cache, and one
   decode token's 49 products in sequence;
 - ``linear_bias``: config 2's Linear forward as the reference calls it (matmul, then
-  add_row_bias) against the fused sn_matmul_bias, and the bias-gradient column sums.
+  add_row_bias) against the fused sn_matmul_bias, and the bias-gradient column sums;
+- ``head_cross_entropy``: the head's 16 per-codebook cross-entropy calls at config 2.
 """
 from __future__ import annotations
 
@@ -410,6 +411,32 @@ def measure_linear(gpu: Gpu, events: HipEvents, buffers, repeats: int = 5):
     return result
 
 
+def measure_loss(gpu: Gpu, events: HipEvents, buffers, repeats: int = 3):
+    """The head product's consumer at config 2 (training.rs:208-239): softmax cross-entropy and its
+    gradient for each of the 16 codebooks over the [32768, 16 x 1024] logits, one call per codebook
+    as the reference makes them. HBM rate on 8 bytes per logit (read the logits, write the gradient)."""
+    from staleynet_amd.gemm import CrossEntropyHead
+    head = buffers[-1]
+    rows, cols = head.y.shape().rows, head.y.shape().cols
+    codebooks, size = 16, cols // 16
+    rng = np.random.default_rng(SEED)
+    targets = gpu.upload_tokens(rng.integers(0, size, rows * codebooks).astype(np.uint32))
+    losses, grad = gpu.zeros(Shape.vector(rows)), gpu.zeros(Shape(rows, cols))
+    heads = [CrossEntropyHead(c * size, size, codebooks, c, 1.0 / (rows * codebooks)) for c in range(codebooks)]
+
+    def all_codebooks():
+        for h in heads:
+            gpu.cross_entropy(head.y, targets, h, losses, grad)
+
+    all_codebooks()
+    ms = timed(events, gpu.stream, all_codebooks, repeats)
+    grad.free()
+    losses.free()
+    targets.free()
+    return {"codebooks": codebooks, "shape": f"{rows}x{cols}", "ms_all_codebooks": round(ms, 3),
+            "gbs": round(8 * rows * cols / (ms * 1e-3) / 1e9, 1)}
+
+
 # ---- CPU baseline -----------------------------------------------------------------------
 
 def cpu_baseline(gpu: Gpu, calls, budget_s: float):
@@ -677,6 +704,7 @@ def main() -> int:
                           "inputs": "fp32 in HBM and LDS, rounded to bf16 (nearest-even) per fragment in registers; "
                                     "fp32 accumulation"}
         result["linear_bias"] = measure_linear(gpu, events, _buffers)
+        result["head_cross_entropy"] = measure_loss(gpu, events, _buffers)
         result["attention"] = measure_attention(gpu, events)
         result["decode"] = measure_decode(gpu, events)
 

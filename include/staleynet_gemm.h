@@ -250,6 +250,40 @@ int sn_causal_softmax(sn_context *context, float *scores, size_t rows, size_t ke
 int sn_softmax_backward(sn_context *context, const float *probabilities, size_t probability_rows,
                         size_t probability_cols, float *grad, size_t grad_rows, size_t grad_cols);
 
+/* ---- the head's consumer: per-codebook softmax cross-entropy ------------- */
+/* An empty target slot (crates/staleynet-cuda/src/kernels/mod.rs:46). */
+#define SN_EMPTY_TOKEN 0xFFFFFFFFu
+
+/* `CrossEntropyHead` (crates/staleynet-cuda/src/ops/loss.rs:14-30): which
+ * columns of a logits row and which target of a target row one classifier
+ * owns. */
+typedef struct sn_cross_entropy_head {
+    size_t column_offset;
+    size_t classes;
+    size_t target_stride;
+    size_t target_offset;
+    float grad_scale;
+} sn_cross_entropy_head;
+
+/* `Gpu::cross_entropy` (ops/loss.rs:34-71; kernel kernels/loss.rs:54-97),
+ * called once per codebook on the head's logits (training.rs:208-239): for
+ * each row, loss = log_partition - logit[target] and, in the head's columns
+ * of logits_grad, (softmax - onehot) * grad_scale; an empty target gives 0
+ * and 0, a target outside the head a NaN loss. The reference's asserts
+ * become SN_ERR_SHAPE (gradient shape differs from the logits' "cross_entropy:
+ * gradient shape"; head past the row "cross_entropy: head exceeds logits") and
+ * SN_ERR_LENGTH_MISMATCH ("cross_entropy: losses too small", "cross_entropy:
+ * too few targets"). targets are device memory (sn_upload_tokens). */
+int sn_cross_entropy(sn_context *context, const float *logits, size_t rows, size_t cols, const uint32_t *targets,
+                     size_t targets_len, const sn_cross_entropy_head *head, float *losses, size_t losses_len,
+                     float *logits_grad, size_t grad_rows, size_t grad_cols);
+
+/* Token id buffers in device memory (`Gpu::upload_tokens`, `download_tokens`,
+ * device.rs:194-208). */
+int sn_upload_tokens(sn_context *context, const uint32_t *host, size_t count, uint32_t **out);
+int sn_download_tokens(sn_context *context, const uint32_t *device, size_t count, uint32_t *host);
+int sn_free_tokens(sn_context *context, uint32_t *buffer);
+
 /* A short English description of a status code (never null). */
 const char *sn_status_string(int status);
 

@@ -34,6 +34,12 @@
  *                            (per column: f32 sum from 0 over the rows in
  *                            order, then sums[c] += sum)
  *   oracle_column_sums_f64   the same sums in f64 (error reporting only)
+ *   oracle_cross_entropy     crates/staleynet-cuda/src/reference.rs:139-166
+ *                            (per row of one head: max, log-partition from
+ *                            the f32 sum of exp(logit - max) in class order,
+ *                            loss = log_partition - logit[target], gradient
+ *                            (exp(logit - log_partition) - onehot) * scale;
+ *                            empty targets (0xFFFFFFFF) give 0 and 0)
  *
  * Parity pins (tests/test_oracle.py): the reference's known-answer tests
  * (reference.rs:177-232, 267-306), an order-sensitive case whose f32 result
@@ -41,7 +47,8 @@
  * transpose/broadcast/scale/accumulate invariants, and an f64 error bound;
  * for the bias functions, the reference's own elementwise test
  * (tests/kernels_match_reference.rs:125-170) restated, exact integer cases,
- * an order-sensitive column and an f64 bound.
+ * an order-sensitive column and an f64 bound; for cross-entropy, the
+ * reference's three known-answer tests (reference.rs:308-366).
  */
 #include <math.h>
 #include <stddef.h>
@@ -199,4 +206,34 @@ void oracle_column_sums_f64(const float *input, size_t rows, size_t cols, const 
     for (size_t r = 0; r < rows; ++r)
         for (size_t c = 0; c < cols; ++c) out[c] += (double)input[r * cols + c];
     for (size_t c = 0; c < cols; ++c) out[c] += (double)initial[c];
+}
+
+/* Cross-entropy of one classifier head over `rows` rows of [rows, cols]
+ * logits: its classes are columns column_offset .. +classes, its target is
+ * targets[row * target_stride + target_offset]. Writes losses[row] and the
+ * head's columns of grad; other columns of grad are left alone. */
+void oracle_cross_entropy(const float *logits, const uint32_t *targets, size_t rows, size_t cols,
+                          size_t column_offset, size_t classes, size_t target_stride, size_t target_offset,
+                          float grad_scale, float *losses, float *grad) {
+    for (size_t row = 0; row < rows; ++row) {
+        const float *z = logits + row * cols + column_offset;
+        float *g = grad + row * cols + column_offset;
+        const uint32_t target = targets[row * target_stride + target_offset];
+        if (target == 0xFFFFFFFFu) {
+            losses[row] = 0.0f;
+            for (size_t c = 0; c < classes; ++c) g[c] = 0.0f;
+            continue;
+        }
+        float maximum = -INFINITY;
+        for (size_t c = 0; c < classes; ++c) maximum = fmaxf(maximum, z[c]);
+        float total = 0.0f;
+        for (size_t c = 0; c < classes; ++c) total = total + expf(z[c] - maximum);
+        const float log_partition = maximum + logf(total);
+        losses[row] = log_partition - z[target];
+        for (size_t c = 0; c < classes; ++c) {
+            const float one_hot = c == target ? 1.0f : 0.0f;
+            const float probability = expf(z[c] - log_partition);
+            g[c] = (probability - one_hot) * grad_scale;
+        }
+    }
 }

@@ -58,6 +58,9 @@ def load() -> ctypes.CDLL:
         lib.oracle_accumulate_column_sums.restype = None
         lib.oracle_column_sums_f64.argtypes = [_f32p, _size, _size, _f32p, _f64p]
         lib.oracle_column_sums_f64.restype = None
+        lib.oracle_cross_entropy.argtypes = [_f32p, ctypes.POINTER(ctypes.c_uint32), _size, _size, _size, _size,
+                                             _size, _size, ctypes.c_float, _f32p, _f32p]
+        lib.oracle_cross_entropy.restype = None
         _lib = lib
     return _lib
 
@@ -175,6 +178,32 @@ def column_sums_f64(values: np.ndarray, cols: int, initial: np.ndarray) -> np.nd
     out = np.empty(cols, np.float64)
     load().oracle_column_sums_f64(_f32(values), values.size // cols, cols, _f32(initial), out.ctypes.data_as(_f64p))
     return out
+
+
+EMPTY_TOKEN = 0xFFFFFFFF  # crates/staleynet-cuda/src/kernels/mod.rs:46
+
+
+@dataclass(frozen=True)
+class CrossEntropyHead:
+    """``CrossEntropyHead`` (crates/staleynet-cuda/src/ops/loss.rs:14-30)."""
+
+    column_offset: int
+    classes: int
+    target_stride: int
+    target_offset: int
+    grad_scale: float
+
+
+def cross_entropy(logits: np.ndarray, targets: np.ndarray, cols: int, head: CrossEntropyHead,
+                  losses: np.ndarray, grad: np.ndarray) -> None:
+    """``reference::cross_entropy`` (reference.rs:139-166): ``losses`` and the head's columns of
+    ``grad`` are written in place."""
+    targets = np.ascontiguousarray(targets, np.uint32)
+    rows = losses.size
+    assert logits.size == grad.size == rows * cols and targets.size >= rows * head.target_stride
+    load().oracle_cross_entropy(_f32(logits), targets.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), rows, cols,
+                                head.column_offset, head.classes, head.target_stride, head.target_offset,
+                                head.grad_scale, _f32(losses), _f32(grad))
 
 
 def _workers(workers):

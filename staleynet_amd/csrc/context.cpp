@@ -394,6 +394,56 @@ int sn_add_row_bias(sn_context* ctx, float* output, size_t rows, size_t cols, co
     return status(err);
 }
 
+int sn_cross_entropy(sn_context* ctx, const float* logits, size_t rows, size_t cols, const uint32_t* targets,
+                     size_t targets_len, const sn_cross_entropy_head* head, float* losses, size_t losses_len,
+                     float* logits_grad, size_t grad_rows, size_t grad_cols) {
+    if (head == nullptr) return SN_ERR_NULL_ARGUMENT;
+    if (grad_rows != rows || grad_cols != cols) return SN_ERR_SHAPE;
+    if (head->column_offset > cols || head->classes > cols - head->column_offset) return SN_ERR_SHAPE;
+    if (losses_len < rows) return SN_ERR_LENGTH_MISMATCH;
+    size_t elements, target_span;
+    if (mul_overflows(rows, cols, &elements) || elements >= (size_t(1) << 60) || rows >= (size_t(1) << 33) ||
+        mul_overflows(rows, head->target_stride, &target_span))
+        return SN_ERR_OVERFLOW;
+    // Every row's target slot must exist: (rows - 1) * stride + offset < len.
+    if (rows > 0 && (targets_len < target_span || head->target_offset >= targets_len ||
+                     (rows - 1) * head->target_stride > targets_len - 1 - head->target_offset))
+        return SN_ERR_LENGTH_MISMATCH;
+    if (ctx == nullptr) return SN_ERR_NULL_ARGUMENT;
+    if (rows == 0) return SN_OK;
+    if (logits == nullptr || targets == nullptr || losses == nullptr || logits_grad == nullptr)
+        return SN_ERR_NULL_ARGUMENT;
+    if (overlaps(logits_grad, elements, logits, elements) || overlaps(losses, rows, logits, elements) ||
+        overlaps(losses, rows, logits_grad, elements))
+        return SN_ERR_ALIASING;
+    sn::CrossEntropyArgs args;
+    args.logits = logits;
+    args.targets = targets;
+    args.losses = losses;
+    args.grad = logits_grad;
+    args.rows = int64_t(rows);
+    args.cols = int64_t(cols);
+    args.column_offset = int64_t(head->column_offset);
+    args.classes = int64_t(head->classes);
+    args.target_stride = int64_t(head->target_stride);
+    args.target_offset = int64_t(head->target_offset);
+    args.grad_scale = head->grad_scale;
+    hipError_t err = hipSetDevice(ctx->device);
+    if (err == hipSuccess) err = sn::launch_cross_entropy(args, ctx->stream);
+    return status(err);
+}
+
+int sn_upload_tokens(sn_context* ctx, const uint32_t* host, size_t count, uint32_t** out) {
+    static_assert(sizeof(uint32_t) == sizeof(float), "token ids travel as 4-byte words");
+    return sn_upload(ctx, reinterpret_cast<const float*>(host), count, reinterpret_cast<float**>(out));
+}
+
+int sn_download_tokens(sn_context* ctx, const uint32_t* device, size_t count, uint32_t* host) {
+    return sn_download(ctx, reinterpret_cast<const float*>(device), count, reinterpret_cast<float*>(host));
+}
+
+int sn_free_tokens(sn_context* ctx, uint32_t* buffer) { return sn_free(ctx, reinterpret_cast<float*>(buffer)); }
+
 int sn_causal_softmax(sn_context* ctx, float* scores, size_t rows, size_t keys, size_t queries, float scale,
                       size_t query_offset) {
     if (queries == 0 || rows % queries != 0) return SN_ERR_SHAPE;

@@ -70,4 +70,16 @@ hipError_t launch_causal_softmax(float* scores, int64_t rows, int64_t queries, i
 hipError_t launch_softmax_backward(const float* probabilities, float* grad, int64_t rows, int64_t cols,
                                    hipStream_t stream);
 
+// One classifier head's softmax cross-entropy and gradient (loss.hip).
+struct CrossEntropyArgs {
+    const float* logits;
+    const uint32_t* targets;
+    float* losses;
+    float* grad;
+    int64_t rows, cols;
+    int64_t column_offset, classes, target_stride, target_offset;
+    float grad_scale;
+};
+hipError_t launch_cross_entropy(const CrossEntropyArgs& args, hipStream_t stream);
+
 }  // namespace sn

@@ -185,6 +185,49 @@ class CMatmulSpec(ctypes.Structure):
                 ("precision", ctypes.c_uint32), ("query_offset", ctypes.c_size_t)]
 
 
+EMPTY_TOKEN = 0xFFFFFFFF  # crates/staleynet-cuda/src/kernels/mod.rs:46
+
+
+@dataclass(frozen=True)
+class CrossEntropyHead:
+    """``CrossEntropyHead`` (crates/staleynet-cuda/src/ops/loss.rs:14-30)."""
+
+    column_offset: int
+    classes: int
+    target_stride: int
+    target_offset: int
+    grad_scale: float
+
+
+class CCrossEntropyHead(ctypes.Structure):
+    _fields_ = [("column_offset", ctypes.c_size_t), ("classes", ctypes.c_size_t),
+                ("target_stride", ctypes.c_size_t), ("target_offset", ctypes.c_size_t),
+                ("grad_scale", ctypes.c_float)]
+
+
+class TokenBuffer:
+    """Token ids (u32) in device memory (``TokenBuffer``, device.rs:35-36)."""
+
+    def __init__(self, gpu: "Gpu", pointer: int, count: int):
+        self._gpu = gpu
+        self.pointer = pointer
+        self._count = count
+
+    def __len__(self) -> int:
+        return self._count
+
+    def free(self) -> None:
+        if self.pointer:
+            _library().sn_free_tokens(self._gpu._ctx, ctypes.c_void_p(self.pointer))
+            self.pointer = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
 class GpuError(RuntimeError):
     """A failed call into the library; ``status`` is the C status code."""
 
@@ -247,13 +290,21 @@ def _library() -> ctypes.CDLL:
         lib.sn_matmul_bias.argtypes = [ctx, ctypes.POINTER(CMatmulSpec), ctypes.c_void_p, size, ctypes.c_void_p,
                                        size, ctypes.c_void_p, size, ctypes.c_void_p, size]
         lib.sn_causal_softmax.argtypes = [ctx, ctypes.c_void_p, size, size, size, ctypes.c_float, size]
+        lib.sn_cross_entropy.argtypes = [ctx, ctypes.c_void_p, size, size, ctypes.c_void_p, size,
+                                         ctypes.POINTER(CCrossEntropyHead), ctypes.c_void_p, size, ctypes.c_void_p,
+                                         size, size]
+        lib.sn_upload_tokens.argtypes = [ctx, ctypes.POINTER(ctypes.c_uint32), size,
+                                         ctypes.POINTER(ctypes.c_void_p)]
+        lib.sn_download_tokens.argtypes = [ctx, ctypes.c_void_p, size, ctypes.POINTER(ctypes.c_uint32)]
+        lib.sn_free_tokens.argtypes = [ctx, ctypes.c_void_p]
         lib.sn_softmax_backward.argtypes = [ctx, ctypes.c_void_p, size, size, ctypes.c_void_p, size, size]
         for name in ("sn_context_create", "sn_context_create_with_workspace", "sn_context_destroy",
                      "sn_context_bind", "sn_context_set_kernel", "sn_context_get_kernel", "sn_synchronize",
                      "sn_alloc_zeroed", "sn_free", "sn_upload", "sn_download", "sn_copy_from_host", "sn_fill_zero",
                      "sn_matmul_validate", "sn_matmul", "sn_fill_normal", "sn_copy_device", "sn_read_sum",
                      "sn_add_row_bias", "sn_accumulate_column_sums", "sn_matmul_bias", "sn_causal_softmax",
-                     "sn_softmax_backward"):
+                     "sn_softmax_backward", "sn_cross_entropy", "sn_upload_tokens", "sn_download_tokens",
+                     "sn_free_tokens"):
             getattr(lib, name).restype = ctypes.c_int
         _lib = lib
     return _lib
@@ -476,6 +527,38 @@ class Gpu:
         if rc == SN_ERR_SHAPE:
             raise AssertionError("softmax_backward: shape mismatch")
         self._check(rc, "softmax_backward")
+
+    def upload_tokens(self, tokens) -> TokenBuffer:
+        """``Gpu::upload_tokens`` (device.rs:194-197)."""
+        host = np.ascontiguousarray(tokens, dtype=np.uint32).ravel()
+        out = ctypes.c_void_p()
+        self._check(_library().sn_upload_tokens(self._ctx, host.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
+                                                host.size, ctypes.byref(out)), "upload_tokens")
+        return TokenBuffer(self, out.value or 0, host.size)
+
+    def download_tokens(self, tokens: TokenBuffer) -> np.ndarray:
+        host = np.empty(len(tokens), np.uint32)
+        self._check(_library().sn_download_tokens(self._ctx, ctypes.c_void_p(tokens.pointer), host.size,
+                                                  host.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32))),
+                    "download_tokens")
+        return host
+
+    def cross_entropy(self, logits: Tensor, targets: TokenBuffer, head: CrossEntropyHead, losses: Tensor,
+                      logits_grad: Tensor) -> None:
+        """``Gpu::cross_entropy`` (ops/loss.rs:34-71): losses and the head's columns of the gradient."""
+        shape = logits.shape()
+        assert logits_grad.shape() == shape, "cross_entropy: gradient shape"
+        assert head.column_offset + head.classes <= shape.cols, "cross_entropy: head exceeds logits"
+        assert len(losses) >= shape.rows, "cross_entropy: losses too small"
+        assert len(targets) >= shape.rows * head.target_stride, "cross_entropy: too few targets"
+        c = CCrossEntropyHead(head.column_offset, head.classes, head.target_stride, head.target_offset,
+                              head.grad_scale)
+        rc = _library().sn_cross_entropy(self._ctx, ctypes.c_void_p(logits.pointer), shape.rows, shape.cols,
+                                         ctypes.c_void_p(targets.pointer), len(targets), ctypes.byref(c),
+                                         ctypes.c_void_p(losses.pointer), len(losses),
+                                         ctypes.c_void_p(logits_grad.pointer), logits_grad.shape().rows,
+                                         logits_grad.shape().cols)
+        self._check(rc, "cross_entropy")
 
     def matmul_raw(self, spec: MatmulSpec, left: int, left_len: int, right: int, right_len: int, output: int,
                    output_len: int) -> None:

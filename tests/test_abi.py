@@ -134,6 +134,20 @@ def test_row_wise_kernels_check_shapes_before_touching_the_device():
     assert lib.sn_softmax_backward(None, None, 4, 5, None, 4, 5) == gemm.SN_ERR_NULL_ARGUMENT
 
 
+def test_cross_entropy_checks_before_touching_the_device():
+    # ops/loss.rs:44-47: gradient shape, head inside the row, losses and targets long enough.
+    lib = gemm.library()
+    head = gemm.CCrossEntropyHead(10, 37, 2, 1, 0.25)
+    args = lambda rows, targets, losses, grows, gcols: (None, None, rows, 50, None, targets, ctypes.byref(head),  # noqa
+                                                        None, losses, None, grows, gcols)
+    assert lib.sn_cross_entropy(*args(13, 26, 13, 13, 49)) == gemm.SN_ERR_SHAPE
+    assert lib.sn_cross_entropy(None, None, 13, 46, None, 26, ctypes.byref(head), None, 13, None, 13, 46) == \
+        gemm.SN_ERR_SHAPE
+    assert lib.sn_cross_entropy(*args(13, 26, 12, 13, 50)) == gemm.SN_ERR_LENGTH_MISMATCH
+    assert lib.sn_cross_entropy(*args(13, 25, 13, 13, 50)) == gemm.SN_ERR_LENGTH_MISMATCH
+    assert lib.sn_cross_entropy(*args(13, 26, 13, 13, 50)) == gemm.SN_ERR_NULL_ARGUMENT
+
+
 def test_status_strings_carry_the_reference_panic_messages():
     assert gemm.status_string(gemm.SN_ERR_LEFT_TOO_SMALL) == "matmul: left operand too small"
     assert gemm.status_string(gemm.SN_ERR_RIGHT_TOO_SMALL) == "matmul: right operand too small"

@@ -287,3 +287,57 @@ def test_column_sums_error_against_f64_is_within_the_sequential_bound():
     bound = rows * 2.0 ** -24 * np.abs(values.reshape(rows, cols).astype(np.float64)).sum(axis=0)
     assert np.all(np.abs(sums - truth) <= bound)
     assert np.max(np.abs(sums - truth)) > 0
+
+
+# ---- cross-entropy (reference.rs:139-166), its known-answer tests (:308-366) --
+
+def _ce(logits, targets, cols, head, losses_init, grad_init):
+    logits = np.asarray(logits, np.float32)
+    losses = np.asarray(losses_init, np.float32).copy()
+    grad = np.asarray(grad_init, np.float32).copy()
+    oracle.cross_entropy(logits, np.asarray(targets, np.uint32), cols, head, losses, grad)
+    return losses, grad
+
+
+def test_cross_entropy_writes_losses_and_gradients_for_the_target_head():
+    head = oracle.CrossEntropyHead(column_offset=0, classes=3, target_stride=1, target_offset=0, grad_scale=1.0)
+    losses, grad = _ce([1, 2, 3, 0, 0, 0, 0, 0], [2, 0], 4, head, [0, 0], [7.0] * 8)
+    assert losses == pytest.approx([0.407606, 1.098612], abs=1e-5)
+    assert grad[:3] == pytest.approx([0.09003, 0.24473, -0.33476], abs=1e-4)
+    assert grad[3] == 7.0 and grad[7] == 7.0
+    assert grad[4:7] == pytest.approx([-0.666667, 0.333333, 0.333333], abs=1e-5)
+
+
+def test_cross_entropy_skips_empty_targets():
+    head = oracle.CrossEntropyHead(column_offset=0, classes=3, target_stride=1, target_offset=0, grad_scale=1.0)
+    losses, grad = _ce([1, 2, 3, 0, 0, 0, 0, 0], [oracle.EMPTY_TOKEN, 0], 4, head, [9, 9], [7.0] * 8)
+    assert losses[0] == 0.0 and grad[:3].tolist() == [0.0, 0.0, 0.0] and grad[3] == 7.0
+    assert losses[1] > 0 and grad[4] < 0 < grad[5] and grad[6] > 0
+
+
+def test_cross_entropy_honours_head_offsets_and_gradient_scale():
+    head = oracle.CrossEntropyHead(column_offset=2, classes=2, target_stride=2, target_offset=1, grad_scale=0.5)
+    losses, grad = _ce([1, 2, 3, 4, 5, 1, 2, 3, 4, 5], [0, 1, 0, 0], 5, head, [0, 0], [7.0] * 10)
+    assert grad[0:2].tolist() == [7.0, 7.0] and grad[4] == 7.0 and grad[5:7].tolist() == [7.0, 7.0]
+    assert grad[9] == 7.0 and np.all(losses > 0) and np.all(np.isfinite(grad[[2, 3, 7, 8]]))
+    # beyond the reference's checks: row 0's target is class 1 (logits 3, 4), row 1's class 0 (3, 4)
+    lp = 4 + np.log1p(np.exp(-1.0))
+    assert losses == pytest.approx([lp - 4, lp - 3], rel=1e-6)
+    assert grad[[2, 3]] == pytest.approx([0.5 * np.exp(3 - lp), 0.5 * (np.exp(4 - lp) - 1)], rel=1e-5)
+
+
+def test_cross_entropy_gradient_rows_sum_to_zero_and_match_f64():
+    rng = np.random.default_rng(5)
+    rows, cols = 64, 48
+    head = oracle.CrossEntropyHead(column_offset=8, classes=33, target_stride=3, target_offset=2, grad_scale=0.25)
+    logits = rng.normal(0, 3, rows * cols).astype(np.float32)
+    targets = rng.integers(0, 33, rows * 3).astype(np.uint32)
+    losses, grad = _ce(logits, targets, cols, head, np.zeros(rows), np.zeros(rows * cols))
+    z = logits.reshape(rows, cols)[:, 8:41].astype(np.float64)
+    t = targets.reshape(rows, 3)[:, 2]
+    lse = np.log(np.exp(z - z.max(1, keepdims=True)).sum(1)) + z.max(1)
+    assert losses == pytest.approx(lse - z[np.arange(rows), t], abs=2e-5)
+    g = grad.reshape(rows, cols)[:, 8:41]
+    assert np.abs(g.sum(1)).max() < 1e-6
+    expected = (np.exp(z - lse[:, None]) - np.eye(33)[t]) * 0.25
+    assert np.abs(g - expected).max() < 1e-6
