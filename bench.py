@@ -108,8 +108,10 @@ class HipGraph:
 
 
 def timed(events: HipEvents, stream: int, body, repeats: int) -> float:
-    """Milliseconds per repeat of `body`, events on `stream` around all repeats."""
+    """Milliseconds per repeat of `body`, events on `stream` around all repeats, after one
+    untimed call (first launches of a kernel pay one-time loading costs)."""
     start, end = events.create(), events.create()
+    body()
     events.device_synchronize()
     events.record(start, stream)
     for _ in range(repeats):
@@ -289,8 +291,23 @@ def measure_attention(gpu: Gpu, events: HipEvents, repeats: int = 3):
         "causal_softmax_gbs": round(4 * (visible + heads * t * t) / (softmax_ms * 1e-3) / 1e9, 1),
         "softmax_backward_ms": round(backward_ms, 3),
         "softmax_backward_gbs": round(12 * heads * t * t / (backward_ms * 1e-3) / 1e9, 1)}
+    # The head permutes around them (attention.rs:56-95): Q, K and V split out of the packed
+    # [16 x 2048, 3 x 768] QKV projection into head-major [192 x 2048, 64], and the context merged
+    # back into [16 x 2048, 768]; 8 bytes per moved element.
+    from staleynet_amd.gemm import HeadLayout
+    packed = gpu.zeros(Shape(16 * t, 3 * 12 * h))
+    gpu.fill_normal(packed, SEED, 950)
+    layouts = [HeadLayout.dense(16, t, 12, h, 3 * 12 * h, part * 12 * h) for part in range(3)]
+    split_ms = timed(events, gpu.stream, lambda: [gpu.split_heads(packed, dst, lay)
+                                                  for dst, lay in zip((q, k, v), layouts)], repeats)
+    merge_ms = timed(events, gpu.stream, lambda: gpu.merge_heads(o, packed, layouts[0]), repeats)
+    moved = heads * t * h
+    result["row_kernels"].update({
+        "split_qkv_ms": round(split_ms, 3), "split_qkv_gbs": round(3 * 8 * moved / (split_ms * 1e-3) / 1e9, 1),
+        "merge_ms": round(merge_ms, 3), "merge_gbs": round(8 * moved / (merge_ms * 1e-3) / 1e9, 1)})
+    packed.free()
     result["step_ms"] = {"products_causal": round(total["causal"], 3),
-                         "with_softmax_and_backward": round(total["causal"] + softmax_ms + backward_ms, 3)}
+                         "with_row_kernels": round(total["causal"] + softmax_ms + backward_ms + split_ms + merge_ms, 3)}
     return result
 
 

@@ -250,6 +250,34 @@ int sn_causal_softmax(sn_context *context, float *scores, size_t rows, size_t ke
 int sn_softmax_backward(sn_context *context, const float *probabilities, size_t probability_rows,
                         size_t probability_cols, float *grad, size_t grad_rows, size_t grad_cols);
 
+/* `HeadLayout` (kernels/attention.rs:19-43): where a group of attention heads
+ * lives in the packed [batch * time, width] layout (head h of a row at columns
+ * column_offset + h * head_dim ..) and in the head-major [batch, heads,
+ * time_capacity, head_dim] layout (time steps written or read from
+ * time_offset on, which appends to a key/value cache). */
+typedef struct sn_head_layout {
+    size_t batch;
+    size_t time;
+    size_t heads;
+    size_t head_dim;
+    size_t width;
+    size_t column_offset;
+    size_t time_capacity;
+    size_t time_offset;
+} sn_head_layout;
+
+/* `Gpu::split_heads` / `Gpu::merge_heads` (ops/attention.rs:20-52; kernels
+ * kernels/attention.rs:113-138): packed columns -> head-major, and back (the
+ * other packed columns are left alone). Bit-exact copies. The reference's
+ * checks (ops/attention.rs:11-18) become SN_ERR_SHAPE ("HeadLayout: time range
+ * exceeds capacity"; here also heads that run past a packed row) and
+ * SN_ERR_LENGTH_MISMATCH ("HeadLayout: packed tensor too small", "HeadLayout:
+ * head-major tensor too small"). */
+int sn_split_heads(sn_context *context, const float *packed, size_t packed_len, float *head_major,
+                   size_t head_major_len, const sn_head_layout *layout);
+int sn_merge_heads(sn_context *context, const float *head_major, size_t head_major_len, float *packed,
+                   size_t packed_len, const sn_head_layout *layout);
+
 /* ---- the head's consumer: per-codebook softmax cross-entropy ------------- */
 /* An empty target slot (crates/staleynet-cuda/src/kernels/mod.rs:46). */
 #define SN_EMPTY_TOKEN 0xFFFFFFFFu

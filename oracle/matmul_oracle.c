@@ -34,6 +34,10 @@
  *                            (per column: f32 sum from 0 over the rows in
  *                            order, then sums[c] += sum)
  *   oracle_column_sums_f64   the same sums in f64 (error reporting only)
+ *   oracle_split_heads, oracle_merge_heads
+ *                            crates/staleynet-cuda/src/kernels/attention.rs:
+ *                            77-138 (HeadLayout::element, packed_index,
+ *                            head_major_index; one copy per moved element)
  *   oracle_cross_entropy     crates/staleynet-cuda/src/reference.rs:139-166
  *                            (per row of one head: max, log-partition from
  *                            the f32 sum of exp(logit - max) in class order,
@@ -236,4 +240,38 @@ void oracle_cross_entropy(const float *logits, const uint32_t *targets, size_t r
             g[c] = (probability - one_hot) * grad_scale;
         }
     }
+}
+
+/* HeadLayout (kernels/attention.rs:19-43): batch, time, heads, head_dim,
+ * width, column_offset, time_capacity, time_offset. Element (b, h, t, d) is
+ * packed[(b * time + t) * width + column_offset + h * head_dim + d] and
+ * head_major[((b * heads + h) * time_capacity + time_offset + t) * head_dim + d]. */
+static inline void head_indices(const size_t *layout, size_t b, size_t h, size_t t, size_t d, size_t *packed,
+                                size_t *head_major) {
+    const size_t time = layout[1], heads = layout[2], head_dim = layout[3], width = layout[4];
+    const size_t column_offset = layout[5], capacity = layout[6], offset = layout[7];
+    *packed = (b * time + t) * width + column_offset + h * head_dim + d;
+    *head_major = ((b * heads + h) * capacity + offset + t) * head_dim + d;
+}
+
+void oracle_split_heads(const float *packed, float *head_major, const size_t *layout) {
+    for (size_t b = 0; b < layout[0]; ++b)
+        for (size_t h = 0; h < layout[2]; ++h)
+            for (size_t t = 0; t < layout[1]; ++t)
+                for (size_t d = 0; d < layout[3]; ++d) {
+                    size_t p, m;
+                    head_indices(layout, b, h, t, d, &p, &m);
+                    head_major[m] = packed[p];
+                }
+}
+
+void oracle_merge_heads(const float *head_major, float *packed, const size_t *layout) {
+    for (size_t b = 0; b < layout[0]; ++b)
+        for (size_t h = 0; h < layout[2]; ++h)
+            for (size_t t = 0; t < layout[1]; ++t)
+                for (size_t d = 0; d < layout[3]; ++d) {
+                    size_t p, m;
+                    head_indices(layout, b, h, t, d, &p, &m);
+                    packed[p] = head_major[m];
+                }
 }

@@ -58,6 +58,10 @@ def load() -> ctypes.CDLL:
         lib.oracle_accumulate_column_sums.restype = None
         lib.oracle_column_sums_f64.argtypes = [_f32p, _size, _size, _f32p, _f64p]
         lib.oracle_column_sums_f64.restype = None
+        lib.oracle_split_heads.argtypes = [_f32p, _f32p, ctypes.POINTER(_size)]
+        lib.oracle_split_heads.restype = None
+        lib.oracle_merge_heads.argtypes = [_f32p, _f32p, ctypes.POINTER(_size)]
+        lib.oracle_merge_heads.restype = None
         lib.oracle_cross_entropy.argtypes = [_f32p, ctypes.POINTER(ctypes.c_uint32), _size, _size, _size, _size,
                                              _size, _size, ctypes.c_float, _f32p, _f32p]
         lib.oracle_cross_entropy.restype = None
@@ -178,6 +182,34 @@ def column_sums_f64(values: np.ndarray, cols: int, initial: np.ndarray) -> np.nd
     out = np.empty(cols, np.float64)
     load().oracle_column_sums_f64(_f32(values), values.size // cols, cols, _f32(initial), out.ctypes.data_as(_f64p))
     return out
+
+
+@dataclass(frozen=True)
+class HeadLayout:
+    """``HeadLayout`` (crates/staleynet-cuda/src/kernels/attention.rs:19-43)."""
+
+    batch: int
+    time: int
+    heads: int
+    head_dim: int
+    width: int
+    column_offset: int
+    time_capacity: int
+    time_offset: int
+
+    def _c(self):
+        return (_size * 8)(self.batch, self.time, self.heads, self.head_dim, self.width, self.column_offset,
+                           self.time_capacity, self.time_offset)
+
+
+def split_heads(packed: np.ndarray, head_major: np.ndarray, layout: HeadLayout) -> None:
+    """Packed columns -> head-major (kernels/attention.rs:113-121), in place on ``head_major``."""
+    load().oracle_split_heads(_f32(packed), _f32(head_major), layout._c())
+
+
+def merge_heads(head_major: np.ndarray, packed: np.ndarray, layout: HeadLayout) -> None:
+    """Head-major -> packed columns (kernels/attention.rs:130-138), in place on ``packed``."""
+    load().oracle_merge_heads(_f32(head_major), _f32(packed), layout._c())
 
 
 EMPTY_TOKEN = 0xFFFFFFFF  # crates/staleynet-cuda/src/kernels/mod.rs:46

@@ -394,6 +394,60 @@ int sn_add_row_bias(sn_context* ctx, float* output, size_t rows, size_t cols, co
     return status(err);
 }
 
+}  // extern "C"
+
+namespace {
+
+// sn_split_heads / sn_merge_heads: the reference's checks, then the copy.
+int permute_heads(sn_context* ctx, bool split, const float* src, size_t src_len, float* dst, size_t dst_len,
+                  const sn_head_layout* layout) {
+    if (layout == nullptr) return SN_ERR_NULL_ARGUMENT;
+    const sn_head_layout& l = *layout;
+    const size_t limit = size_t(1) << 40;
+    if (l.batch >= limit || l.time >= limit || l.heads >= limit || l.head_dim >= limit || l.width >= limit ||
+        l.column_offset >= limit || l.time_capacity >= limit || l.time_offset >= limit)
+        return SN_ERR_OVERFLOW;
+    if (l.time_offset + l.time > l.time_capacity) return SN_ERR_SHAPE;
+    size_t head_columns;
+    if (mul_overflows(l.heads, l.head_dim, &head_columns)) return SN_ERR_OVERFLOW;
+    if (l.column_offset + head_columns > l.width) return SN_ERR_SHAPE;
+    // batch * time * width, batch * heads * time_capacity * head_dim and the moved count.
+    size_t rows, packed_need, matrices, per_matrix, major_need, per_moved, moved;
+    if (mul_overflows(l.batch, l.time, &rows) || mul_overflows(rows, l.width, &packed_need) ||
+        mul_overflows(l.batch, l.heads, &matrices) || mul_overflows(l.time_capacity, l.head_dim, &per_matrix) ||
+        mul_overflows(matrices, per_matrix, &major_need) || mul_overflows(l.time, l.head_dim, &per_moved) ||
+        mul_overflows(matrices, per_moved, &moved))
+        return SN_ERR_OVERFLOW;
+    if (packed_need >= (size_t(1) << 60) || major_need >= (size_t(1) << 60)) return SN_ERR_OVERFLOW;
+    const size_t packed_len = split ? src_len : dst_len;
+    const size_t major_len = split ? dst_len : src_len;
+    if (packed_len < packed_need || major_len < major_need) return SN_ERR_LENGTH_MISMATCH;
+    if (ctx == nullptr) return SN_ERR_NULL_ARGUMENT;
+    if (moved == 0) return SN_OK;
+    if (src == nullptr || dst == nullptr) return SN_ERR_NULL_ARGUMENT;
+    if (overlaps(dst, split ? major_need : packed_need, src, split ? packed_need : major_need)) return SN_ERR_ALIASING;
+    const sn::HeadLayoutArgs args{int64_t(l.batch),     int64_t(l.time),  int64_t(l.heads),
+                                  int64_t(l.head_dim),  int64_t(l.width), int64_t(l.column_offset),
+                                  int64_t(l.time_capacity), int64_t(l.time_offset)};
+    hipError_t err = hipSetDevice(ctx->device);
+    if (err == hipSuccess) err = sn::launch_permute_heads(split, src, dst, args, ctx->stream);
+    return status(err);
+}
+
+}  // namespace
+
+extern "C" {
+
+int sn_split_heads(sn_context* ctx, const float* packed, size_t packed_len, float* head_major, size_t head_major_len,
+                   const sn_head_layout* layout) {
+    return permute_heads(ctx, true, packed, packed_len, head_major, head_major_len, layout);
+}
+
+int sn_merge_heads(sn_context* ctx, const float* head_major, size_t head_major_len, float* packed, size_t packed_len,
+                   const sn_head_layout* layout) {
+    return permute_heads(ctx, false, head_major, head_major_len, packed, packed_len, layout);
+}
+
 int sn_cross_entropy(sn_context* ctx, const float* logits, size_t rows, size_t cols, const uint32_t* targets,
                      size_t targets_len, const sn_cross_entropy_head* head, float* losses, size_t losses_len,
                      float* logits_grad, size_t grad_rows, size_t grad_cols) {

@@ -70,6 +70,13 @@ hipError_t launch_causal_softmax(float* scores, int64_t rows, int64_t queries, i
 hipError_t launch_softmax_backward(const float* probabilities, float* grad, int64_t rows, int64_t cols,
                                    hipStream_t stream);
 
+// The attention head permutes (heads.hip): split = packed -> head-major.
+struct HeadLayoutArgs {
+    int64_t batch, time, heads, head_dim, width, column_offset, time_capacity, time_offset;
+};
+hipError_t launch_permute_heads(bool split, const float* src, float* dst, const HeadLayoutArgs& layout,
+                                hipStream_t stream);
+
 // One classifier head's softmax cross-entropy and gradient (loss.hip).
 struct CrossEntropyArgs {
     const float* logits;

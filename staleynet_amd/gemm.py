@@ -205,6 +205,36 @@ class CCrossEntropyHead(ctypes.Structure):
                 ("grad_scale", ctypes.c_float)]
 
 
+@dataclass(frozen=True)
+class HeadLayout:
+    """``HeadLayout`` (crates/staleynet-cuda/src/kernels/attention.rs:19-75)."""
+
+    batch: int
+    time: int
+    heads: int
+    head_dim: int
+    width: int
+    column_offset: int
+    time_capacity: int
+    time_offset: int
+
+    @staticmethod
+    def dense(batch: int, time: int, heads: int, head_dim: int, width: int, column_offset: int) -> "HeadLayout":
+        return HeadLayout(batch, time, heads, head_dim, width, column_offset, time, 0)
+
+    def in_cache(self, capacity: int, offset: int) -> "HeadLayout":
+        return replace(self, time_capacity=capacity, time_offset=offset)
+
+    def to_c(self) -> "CHeadLayout":
+        return CHeadLayout(self.batch, self.time, self.heads, self.head_dim, self.width, self.column_offset,
+                           self.time_capacity, self.time_offset)
+
+
+class CHeadLayout(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_size_t) for name in ("batch", "time", "heads", "head_dim", "width", "column_offset",
+                                                     "time_capacity", "time_offset")]
+
+
 class TokenBuffer:
     """Token ids (u32) in device memory (``TokenBuffer``, device.rs:35-36)."""
 
@@ -297,6 +327,10 @@ def _library() -> ctypes.CDLL:
                                          ctypes.POINTER(ctypes.c_void_p)]
         lib.sn_download_tokens.argtypes = [ctx, ctypes.c_void_p, size, ctypes.POINTER(ctypes.c_uint32)]
         lib.sn_free_tokens.argtypes = [ctx, ctypes.c_void_p]
+        lib.sn_split_heads.argtypes = [ctx, ctypes.c_void_p, size, ctypes.c_void_p, size,
+                                       ctypes.POINTER(CHeadLayout)]
+        lib.sn_merge_heads.argtypes = [ctx, ctypes.c_void_p, size, ctypes.c_void_p, size,
+                                       ctypes.POINTER(CHeadLayout)]
         lib.sn_softmax_backward.argtypes = [ctx, ctypes.c_void_p, size, size, ctypes.c_void_p, size, size]
         for name in ("sn_context_create", "sn_context_create_with_workspace", "sn_context_destroy",
                      "sn_context_bind", "sn_context_set_kernel", "sn_context_get_kernel", "sn_synchronize",
@@ -304,7 +338,7 @@ def _library() -> ctypes.CDLL:
                      "sn_matmul_validate", "sn_matmul", "sn_fill_normal", "sn_copy_device", "sn_read_sum",
                      "sn_add_row_bias", "sn_accumulate_column_sums", "sn_matmul_bias", "sn_causal_softmax",
                      "sn_softmax_backward", "sn_cross_entropy", "sn_upload_tokens", "sn_download_tokens",
-                     "sn_free_tokens"):
+                     "sn_free_tokens", "sn_split_heads", "sn_merge_heads"):
             getattr(lib, name).restype = ctypes.c_int
         _lib = lib
     return _lib
@@ -527,6 +561,24 @@ class Gpu:
         if rc == SN_ERR_SHAPE:
             raise AssertionError("softmax_backward: shape mismatch")
         self._check(rc, "softmax_backward")
+
+    def _permute_heads(self, fn, src: Tensor, dst: Tensor, layout: HeadLayout, packed: Tensor,
+                       head_major: Tensor) -> None:
+        assert layout.time_offset + layout.time <= layout.time_capacity, "HeadLayout: time range exceeds capacity"
+        assert len(packed) >= layout.batch * layout.time * layout.width, "HeadLayout: packed tensor too small"
+        assert len(head_major) >= layout.batch * layout.heads * layout.time_capacity * layout.head_dim, \
+            "HeadLayout: head-major tensor too small"
+        c = layout.to_c()
+        self._check(fn(self._ctx, ctypes.c_void_p(src.pointer), len(src), ctypes.c_void_p(dst.pointer), len(dst),
+                       ctypes.byref(c)), "permute heads")
+
+    def split_heads(self, packed: Tensor, head_major: Tensor, layout: HeadLayout) -> None:
+        """``Gpu::split_heads`` (ops/attention.rs:20-35): packed columns -> head-major."""
+        self._permute_heads(_library().sn_split_heads, packed, head_major, layout, packed, head_major)
+
+    def merge_heads(self, head_major: Tensor, packed: Tensor, layout: HeadLayout) -> None:
+        """``Gpu::merge_heads`` (ops/attention.rs:37-52): head-major -> packed columns."""
+        self._permute_heads(_library().sn_merge_heads, head_major, packed, layout, packed, head_major)
 
     def upload_tokens(self, tokens) -> TokenBuffer:
         """``Gpu::upload_tokens`` (device.rs:194-197)."""

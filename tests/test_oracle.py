@@ -341,3 +341,38 @@ def test_cross_entropy_gradient_rows_sum_to_zero_and_match_f64():
     assert np.abs(g.sum(1)).max() < 1e-6
     expected = (np.exp(z - lse[:, None]) - np.eye(33)[t]) * 0.25
     assert np.abs(g - expected).max() < 1e-6
+
+
+# ---- head permutes (kernels/attention.rs:77-138) ------------------------------
+
+def test_split_and_merge_heads_follow_the_reference_layout_formula():
+    # kernels_match_reference.rs:196-233: dense(2, 5, 3, 4, 3*12+2, 13).in_cache(9, 2), LCG seed 12.
+    layout = oracle.HeadLayout(batch=2, time=5, heads=3, head_dim=4, width=3 * 12 + 2, column_offset=13,
+                               time_capacity=9, time_offset=2)
+    packed = oracle.random_values(layout.batch * layout.time * layout.width, 12)
+    head_major = np.zeros(layout.batch * layout.heads * layout.time_capacity * layout.head_dim, np.float32)
+    oracle.split_heads(packed, head_major, layout)
+    for b in range(2):
+        for h in range(3):
+            for t in range(5):
+                for d in range(4):
+                    source = (b * 5 + t) * layout.width + 13 + h * 4 + d
+                    target = ((b * 3 + h) * 9 + 2 + t) * 4 + d
+                    assert head_major[target] == packed[source]
+    merged = np.zeros_like(packed)
+    oracle.merge_heads(head_major, merged, layout)
+    columns = np.arange(packed.size) % layout.width
+    inside = (columns >= 13) & (columns < 13 + 3 * 4)
+    assert np.array_equal(merged, np.where(inside, packed, 0.0).astype(np.float32))
+
+
+def test_split_heads_is_numpys_reshape_and_transpose():
+    batch, time, heads, head_dim = 3, 7, 4, 8
+    width = 3 * heads * head_dim
+    packed = np.arange(batch * time * width, dtype=np.float32)
+    for offset in (0, heads * head_dim, 2 * heads * head_dim):
+        layout = oracle.HeadLayout(batch, time, heads, head_dim, width, offset, time, 0)
+        head_major = np.zeros(batch * heads * time * head_dim, np.float32)
+        oracle.split_heads(packed, head_major, layout)
+        expected = packed.reshape(batch, time, 3, heads, head_dim)[:, :, offset // (heads * head_dim)]
+        assert np.array_equal(head_major.reshape(batch, heads, time, head_dim), expected.transpose(0, 2, 1, 3))
