@@ -291,7 +291,7 @@ def measure_attention(gpu: Gpu, events: HipEvents, repeats: int = 3):
         "causal_softmax_gbs": round(4 * (visible + heads * t * t) / (softmax_ms * 1e-3) / 1e9, 1),
         "softmax_backward_ms": round(backward_ms, 3),
         "softmax_backward_gbs": round(12 * heads * t * t / (backward_ms * 1e-3) / 1e9, 1)}
-    # The head permutes around them (attention.rs:56-95): Q, K and V split out of the packed
+    # The head permutes around them (layers/attention.rs:202-214): Q, K and V split out of the packed
     # [16 x 2048, 3 x 768] QKV projection into head-major [192 x 2048, 64], and the context merged
     # back into [16 x 2048, 768]; 8 bytes per moved element.
     from staleynet_amd.gemm import HeadLayout

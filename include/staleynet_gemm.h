@@ -267,7 +267,7 @@ typedef struct sn_head_layout {
 } sn_head_layout;
 
 /* `Gpu::split_heads` / `Gpu::merge_heads` (ops/attention.rs:20-52; kernels
- * kernels/attention.rs:113-138): packed columns -> head-major, and back (the
+ * at kernels/attention.rs:113-138): packed columns -> head-major, and back (the
  * other packed columns are left alone). Bit-exact copies. The reference's
  * checks (ops/attention.rs:11-18) become SN_ERR_SHAPE ("HeadLayout: time range
  * exceeds capacity"; here also heads that run past a packed row) and

@@ -1,6 +1,6 @@
 // The attention head permutes on either side of the attention products
-// (kernels/attention.rs:77-138, called at layers/attention.rs:56-95, :288-297
-// and after the value product): split_heads copies each head's columns of
+// (kernels/attention.rs:77-138, called at layers/attention.rs:202-214, :237,
+// :262-264 and :289-317): split_heads copies each head's columns of
 // the packed [batch * time, width] activations (from column_offset, e.g.
 // the Q, K or V part of the fused QKV projection) into the head-major
 // [batch, heads, time_capacity, head_dim] layout from time step time_offset

@@ -1,7 +1,7 @@
 """GPU parity of the attention head permutes (``sn_split_heads`` / ``sn_merge_heads``,
 ``Gpu::split_heads`` / ``merge_heads``, ops/attention.rs:20-52): bit-exact against the oracle's
 restatement of kernels/attention.rs:77-138. The reference's own GPU test
-(tests/kernels_match_reference.rs:196-233) comes first, on its inputs; then config 3's QKV
+(tests/kernels_match_reference.rs:199-231) comes first, on its inputs; then config 3's QKV
 split and merge, a cache append, the scalar (unaligned) path and the layout checks.
 """
 import numpy as np

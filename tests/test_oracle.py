@@ -346,7 +346,7 @@ def test_cross_entropy_gradient_rows_sum_to_zero_and_match_f64():
 # ---- head permutes (kernels/attention.rs:77-138) ------------------------------
 
 def test_split_and_merge_heads_follow_the_reference_layout_formula():
-    # kernels_match_reference.rs:196-233: dense(2, 5, 3, 4, 3*12+2, 13).in_cache(9, 2), LCG seed 12.
+    # kernels_match_reference.rs:199-231: dense(2, 5, 3, 4, 3*12+2, 13).in_cache(9, 2), LCG seed 12.
     layout = oracle.HeadLayout(batch=2, time=5, heads=3, head_dim=4, width=3 * 12 + 2, column_offset=13,
                                time_capacity=9, time_offset=2)
     packed = oracle.random_values(layout.batch * layout.time * layout.width, 12)
