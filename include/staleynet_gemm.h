@@ -146,10 +146,12 @@ typedef struct sn_context sn_context;
 sn_matmul_spec sn_matmul_spec_new(size_t rows, size_t cols, size_t inner);
 
 /* `Gpu::new(ordinal)` (device.rs:148-155): selects the device, creates one
- * stream and a split-K workspace of the default size (256 MiB; every
- * product of the reference's model configurations fits in it). */
+ * stream and a workspace of the default size (1.5 GiB: split-K partial
+ * sums, and the bf16 products' operands staged as bf16; every product of
+ * the reference's model configurations fits in it). */
 int sn_context_create(int ordinal, sn_context **out);
-/* The same with an explicit workspace size in bytes (0 disables split-K). */
+/* The same with an explicit workspace size in bytes (0 disables split-K and
+ * bf16 staging; a product that does not fit takes a path that needs less). */
 int sn_context_create_with_workspace(int ordinal, size_t workspace_bytes, sn_context **out);
 int sn_context_destroy(sn_context *context);
 /* `Gpu::bind_to_current_thread` (device.rs:157-161): makes the context's

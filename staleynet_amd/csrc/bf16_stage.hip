@@ -1,0 +1,155 @@
+// Operand staging for the bf16 products: an fp32 operand rounded to bf16
+// (v_cvt_pk_bf16_f32, nearest-even: the rounding the bf16 kernels apply as
+// they read their fp32 stages) and laid out K-contiguous,
+// dst[batch][row][0 .. kp) with kp = K rounded up to 8 and zeros past K, so
+// that the product's matrix cores read 8 consecutive k of a row as one
+// 16-byte slot whatever the operand's stored layout.
+//
+//  * K-contiguous source (element (r, k) at src[r * ld + k]): a thread
+//    converts 8 consecutive k of a row (two 16-byte loads, one 16-byte
+//    store).
+//  * Row-contiguous source (element (r, k) at src[k * ld + r]): 64 x 64
+//    tiles transposed through LDS. Loads read 64 consecutive rows of each k
+//    (16 bytes a lane); 8 consecutive lanes then write one row's 64 k (128
+//    bytes). The LDS pitch of 65 floats keeps both sides conflict-free.
+//
+// HBM-bound: 4 bytes read and 2 written per element.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "gemm_internal.h"
+
+namespace sn {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kThreads = 256;
+constexpr int kTile = 64;
+constexpr int kPitch = kTile + 1;
+
+__device__ __forceinline__ bf16x8 round8(const float (&v)[8]) {
+    const f32x8 x = {v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]};
+    return __builtin_convertvector(x, bf16x8);
+}
+
+// VECTOR: rows start 16-byte aligned (ld % 4 == 0, aligned base), so whole
+// groups inside K load as two float4.
+template <bool VECTOR>
+__global__ __launch_bounds__(kThreads) void stage_rows_kernel(const float* __restrict__ src, int64_t ld,
+                                                              int64_t rows, int64_t k, int64_t kp,
+                                                              int64_t src_stride, uint16_t* __restrict__ dst) {
+    const int64_t groups = kp / 8;
+    const int64_t g = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (g >= rows * groups) return;
+    const int64_t batch = blockIdx.y;
+    const int64_t r = g / groups;
+    const int64_t k0 = (g - r * groups) * 8;
+    const float* row = src + batch * src_stride + r * ld;
+    float v[8];
+    if (VECTOR && k0 + 8 <= k) {
+        const f32x4 lo = *reinterpret_cast<const f32x4*>(row + k0);
+        const f32x4 hi = *reinterpret_cast<const f32x4*>(row + k0 + 4);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            v[s] = lo[s];
+            v[4 + s] = hi[s];
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < 8; ++s) v[s] = k0 + s < k ? row[k0 + s] : 0.f;
+    }
+    *reinterpret_cast<bf16x8*>(dst + (batch * rows + r) * kp + k0) = round8(v);
+}
+
+template <bool VECTOR>
+__global__ __launch_bounds__(kThreads) void stage_transposed_kernel(const float* __restrict__ src, int64_t ld,
+                                                                    int64_t rows, int64_t k, int64_t kp,
+                                                                    int64_t src_stride,
+                                                                    uint16_t* __restrict__ dst) {
+    __shared__ float tile[kTile * kPitch];  // [k][row]
+    const int tid = threadIdx.x;
+    const int64_t k_base = int64_t(blockIdx.x) * kTile;
+    const int64_t r_base = int64_t(blockIdx.y) * kTile;
+    const int64_t batch = blockIdx.z;
+    const float* s = src + batch * src_stride;
+
+    // Loads: thread t covers rows 4 (t % 16) .. +3 of k rows t / 16 + 16 i.
+    const int c4 = 4 * (tid % 16);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int kk = tid / 16 + 16 * i;
+        const int64_t kg = k_base + kk;
+        const int64_t r = r_base + c4;
+        float v[4] = {0.f, 0.f, 0.f, 0.f};
+        if (kg < k) {
+            const float* p = s + kg * ld + r;
+            if (VECTOR && r + 4 <= rows) {
+                const f32x4 x = *reinterpret_cast<const f32x4*>(p);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[j] = x[j];
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[j] = r + j < rows ? p[j] : 0.f;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) tile[kk * kPitch + c4 + j] = v[j];
+    }
+    __syncthreads();
+
+    // Stores: 8 lanes per row, lane l of a group writing k 8 (l % 8) .. +7.
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int e = tid + kThreads * i;
+        const int kgrp = e % 8;
+        const int rr = e / 8;
+        const int64_t r = r_base + rr;
+        const int64_t k0 = k_base + 8 * kgrp;
+        if (r < rows && k0 < kp) {
+            float v[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) v[t] = tile[(8 * kgrp + t) * kPitch + rr];
+            *reinterpret_cast<bf16x8*>(dst + (batch * rows + r) * kp + k0) = round8(v);
+        }
+    }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+hipError_t launch_stage_bf16(const float* src, bool k_contiguous, int64_t ld, int64_t rows, int64_t k, int64_t kp,
+                             int64_t batch, int64_t src_stride, uint16_t* dst, hipStream_t stream) {
+    if (rows == 0 || kp == 0 || batch == 0) return hipSuccess;
+    if (batch > 65535 || kp % 8 != 0 || kp < k) return hipErrorInvalidValue;
+    const bool vector = ld % 4 == 0 && src_stride % 4 == 0 && aligned16(src);
+    if (k_contiguous) {
+        const int64_t work = rows * (kp / 8);
+        if ((work + kThreads - 1) / kThreads > 0x7FFFFFFF) return hipErrorInvalidValue;
+        const dim3 grid(unsigned((work + kThreads - 1) / kThreads), unsigned(batch));
+        if (vector)
+            hipLaunchKernelGGL(stage_rows_kernel<true>, grid, dim3(kThreads), 0, stream, src, ld, rows, k, kp,
+                               src_stride, dst);
+        else
+            hipLaunchKernelGGL(stage_rows_kernel<false>, grid, dim3(kThreads), 0, stream, src, ld, rows, k, kp,
+                               src_stride, dst);
+    } else {
+        const int64_t tiles_k = (kp + kTile - 1) / kTile;
+        const int64_t tiles_r = (rows + kTile - 1) / kTile;
+        if (tiles_r > 65535) return hipErrorInvalidValue;
+        const dim3 grid{unsigned(tiles_k), unsigned(tiles_r), unsigned(batch)};
+        if (vector)
+            hipLaunchKernelGGL(stage_transposed_kernel<true>, grid, dim3(kThreads), 0, stream, src, ld, rows, k, kp,
+                               src_stride, dst);
+        else
+            hipLaunchKernelGGL(stage_transposed_kernel<false>, grid, dim3(kThreads), 0, stream, src, ld, rows, k,
+                               kp, src_stride, dst);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace sn

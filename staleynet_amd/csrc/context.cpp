@@ -22,7 +22,7 @@ struct sn_context {
 
 namespace {
 
-constexpr size_t kDefaultWorkspaceBytes = size_t(256) << 20;
+constexpr size_t kDefaultWorkspaceBytes = size_t(1536) << 20;
 constexpr size_t kCounterCount = 16384;
 // Dimensions above this would overflow the kernels' 32-bit tile counters.
 constexpr size_t kMaxDimension = size_t(1) << 31;

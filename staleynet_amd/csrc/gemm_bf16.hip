@@ -173,6 +173,7 @@ using TileNarrow = Tile<256, 64, 32, 4, 1>;
 }  // namespace
 
 size_t bf16_workspace_bytes(const Problem& p, const Env& env) {
+    if (bf16_staged_applies(p, env)) return bf16_staged_workspace_bytes(p, env);
     if (bf16_dma_applies(p)) return bf16_dma_workspace_bytes(p, env);
     const Plan plan = p.n <= 64 ? plan_for<TileNarrow>(p, env) : plan_for<TileSquare>(p, env);
     return plan.splits > 1 ? size_t(plan.splits) * size_t(p.m) * size_t(p.n) * sizeof(float) : 0;
@@ -181,6 +182,7 @@ size_t bf16_workspace_bytes(const Problem& p, const Env& env) {
 }  // namespace gemm
 
 hipError_t launch_gemm_bf16(const Problem& p, const Env& env, hipStream_t stream) {
+    if (gemm::bf16_staged_applies(p, env)) return gemm::launch_gemm_bf16_staged(p, env, stream);
     if (gemm::bf16_dma_applies(p)) return gemm::launch_gemm_bf16_dma(p, env, stream);
     if (p.n <= 64) return gemm::dispatch_layout_bf16<gemm::TileNarrow>(p, env, stream);
     return gemm::dispatch_layout_bf16<gemm::TileSquare>(p, env, stream);

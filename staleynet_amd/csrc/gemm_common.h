@@ -648,6 +648,12 @@ hipError_t launch_gemm_f32_dma(const Problem& p, const Env& env, hipStream_t str
 bool bf16_dma_applies(const Problem& p);
 hipError_t launch_gemm_bf16_dma(const Problem& p, const Env& env, hipStream_t stream);
 size_t bf16_dma_workspace_bytes(const Problem& p, const Env& env);
+// bf16 with both operands first staged as bf16 in the workspace (gemm_dma.hip):
+// whether it serves `p` (unmasked, aligned, staged operands fit), its
+// launcher and the workspace it uses (staged operands and partial sums).
+bool bf16_staged_applies(const Problem& p, const Env& env);
+hipError_t launch_gemm_bf16_staged(const Problem& p, const Env& env, hipStream_t stream);
+size_t bf16_staged_workspace_bytes(const Problem& p, const Env& env);
 
 // Adds the split-K partial sums in split order and applies the combine
 // (defined in gemm_mfma.hip).

@@ -166,13 +166,46 @@ __device__ __forceinline__ void read_chunk(const OperandFor<A_K, T::BM, T::THREA
     for (int j = 0; j < T::FN; ++j) ob.fragment(sb, wave_n * T::WTN + 32 * j + row, c, half, f.b[j]);
 }
 
-// fp32: eight v_mfma_f32_32x32x2_f32 per block, lane half h feeding k = 8h + s
-// to MFMA s. bf16: the same eight fp32 values per lane are rounded to bf16
-// (v_cvt_pk_bf16_f32, nearest-even) and feed one v_mfma_f32_32x32x16_bf16,
-// whose lane half h holds k = 8h .. 8h+7: the same pairing of A and B.
-template <class T, bool BF16>
+// How the LDS stages feed the matrix cores.
+//  kFeedF32: fp32 stages, eight v_mfma_f32_32x32x2_f32 per block, lane half
+//    h feeding k = 8h + s to MFMA s.
+//  kFeedRound: fp32 stages; the same eight values per lane are rounded to
+//    bf16 (v_cvt_pk_bf16_f32, nearest-even) and feed one
+//    v_mfma_f32_32x32x16_bf16, whose lane half h holds k = 8h .. 8h+7.
+//  kFeedBf16: bf16 stages (operands converted before the product, both
+//    K-contiguous). A stage row is the same 128 bytes, now 64 k, and the
+//    kernel counts k in pairs; a lane's 8 words of a chunk are 16 bf16, k =
+//    32c + 16h + (0..15), which feed two v_mfma_f32_32x32x16_bf16 (the
+//    first 8 and the last 8).
+// In every mode A and B are paired on the same k.
+constexpr int kFeedF32 = 0;
+constexpr int kFeedRound = 1;
+constexpr int kFeedBf16 = 2;
+
+template <class T, int FEED>
 __device__ __forceinline__ void multiply_chunk(const Chunk<T>& f, f32x16 (&acc)[T::FM][T::FN]) {
-    if constexpr (BF16) {
+    if constexpr (FEED == kFeedBf16) {
+        bf16x8 a8[T::FM][2], b8[T::FN][2];
+#pragma unroll
+        for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+                a8[i][q] = __builtin_bit_cast(
+                    bf16x8, f32x4{f.a[i][4 * q], f.a[i][4 * q + 1], f.a[i][4 * q + 2], f.a[i][4 * q + 3]});
+#pragma unroll
+        for (int j = 0; j < T::FN; ++j)
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+                b8[j][q] = __builtin_bit_cast(
+                    bf16x8, f32x4{f.b[j][4 * q], f.b[j][4 * q + 1], f.b[j][4 * q + 2], f.b[j][4 * q + 3]});
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+            for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+                for (int j = 0; j < T::FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a8[i][q], b8[j][q], acc[i][j], 0, 0, 0);
+    } else if constexpr (FEED == kFeedRound) {
         bf16x8 a8[T::FM], b8[T::FN];
 #pragma unroll
         for (int i = 0; i < T::FM; ++i) a8[i] = to_bf16x8(f.a[i]);
@@ -198,10 +231,10 @@ __device__ __forceinline__ void multiply_chunk(const Chunk<T>& f, f32x16 (&acc)[
 // then its MFMAs with the VM loads and DS fragment reads issued in their
 // shadow, spread evenly (left alone, the scheduler issues each LDS read
 // just before its first use and waits on it there).
-template <class T, bool BF16, int VM, int DS>
+template <class T, int FEED, int VM, int DS>
 __device__ __forceinline__ void interleave() {
-    constexpr int MF = (BF16 ? 1 : 8) * T::FM * T::FN;
-    if constexpr (BF16) __builtin_amdgcn_sched_group_barrier(0x002, 4 * (T::FM + T::FN), 0);
+    constexpr int MF = (FEED == kFeedF32 ? 8 : FEED == kFeedBf16 ? 2 : 1) * T::FM * T::FN;
+    if constexpr (FEED == kFeedRound) __builtin_amdgcn_sched_group_barrier(0x002, 4 * (T::FM + T::FN), 0);
 #pragma unroll
     for (int x = 0; x < MF; ++x) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -259,8 +292,8 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("" ::: "memory");
 }
 
-// One output tile (the whole of both kernels below); BF16 selects the
-// matrix instruction fed from the fp32 LDS stages.
+// One output tile (the whole of the kernels below); FEED selects what the
+// stages hold and the matrix instruction they feed.
 //
 // STAGES LDS stages, all loading from the start: a stage is reloaded for
 // the step STAGES ahead as soon as every wave has read it. One barrier per
@@ -272,7 +305,7 @@ __device__ __forceinline__ void lds_barrier() {
 // wait count, fixed. The loop is unrolled by STAGES so that every LDS
 // access names a statically known stage array; the compiler then never
 // waits on loads into the other stages before its LDS reads.
-template <class T, int STAGES, bool A_K, bool B_K, bool BF16>
+template <class T, int STAGES, bool A_K, bool B_K, int FEED>
 __device__ __forceinline__ void dma_tile(const Args& args) {
     static_assert(STAGES >= 2 && STAGES <= 4, "two to four LDS stages");
     constexpr int WAVES = T::THREADS / 64;
@@ -366,8 +399,8 @@ __device__ __forceinline__ void dma_tile(const Args& args) {
         constexpr int S = decltype(stage)::value;
         __builtin_amdgcn_sched_barrier(0);
         read_chunk<T, A_K, B_K>(oa, ob, stage_a[S], stage_b[S], 1, f1, lane, wave_m, wave_n);
-        multiply_chunk<T, BF16>(f0, acc);
-        interleave<T, BF16, 0, DS>();
+        multiply_chunk<T, FEED>(f0, acc);
+        interleave<T, FEED, 0, DS>();
         __builtin_amdgcn_sched_barrier(0);
     };
     auto sync = [&] {
@@ -381,8 +414,8 @@ __device__ __forceinline__ void dma_tile(const Args& args) {
         __builtin_amdgcn_sched_barrier(0);
         issue(stage_a[S], stage_b[S], k0 + STAGES * T::BK);
         read_chunk<T, A_K, B_K>(oa, ob, stage_a[N], stage_b[N], 0, f0, lane, wave_m, wave_n);
-        multiply_chunk<T, BF16>(f1, acc);
-        interleave<T, BF16, LOADS_PER_STEP, DS>();
+        multiply_chunk<T, FEED>(f1, acc);
+        interleave<T, FEED, LOADS_PER_STEP, DS>();
         __builtin_amdgcn_sched_barrier(0);
     };
 
@@ -490,7 +523,7 @@ __global__ __launch_bounds__(C::T::THREADS)
 __attribute__((amdgpu_waves_per_eu(dma_waves_per_eu<typename C::T, C::STAGES>(),
                                    dma_waves_per_eu<typename C::T, C::STAGES>())))
 void gemm_f32_dma_kernel(Args args) {
-    dma_tile<typename C::T, C::STAGES, A_K, B_K, false>(args);
+    dma_tile<typename C::T, C::STAGES, A_K, B_K, kFeedF32>(args);
 }
 
 // bf16-input / fp32-accumulate variant (SN_PRECISION_BF16): the same loads,
@@ -501,10 +534,21 @@ __global__ __launch_bounds__(C::T::THREADS)
 __attribute__((amdgpu_waves_per_eu(dma_waves_per_eu<typename C::T, C::STAGES>(),
                                    dma_waves_per_eu<typename C::T, C::STAGES>())))
 void gemm_bf16_dma_kernel(Args args) {
-    dma_tile<typename C::T, C::STAGES, A_K, B_K, true>(args);
+    dma_tile<typename C::T, C::STAGES, A_K, B_K, kFeedRound>(args);
 }
 
-template <class C, bool A_K, bool B_K, bool BF16>
+// bf16 operands staged ahead of the product (both K-contiguous, k counted in
+// pairs of bf16): the same loads, stages, schedule and epilogue, half the
+// LDS bytes per FLOP.
+template <class C>
+__global__ __launch_bounds__(C::T::THREADS)
+__attribute__((amdgpu_waves_per_eu(dma_waves_per_eu<typename C::T, C::STAGES>(),
+                                   dma_waves_per_eu<typename C::T, C::STAGES>())))
+void gemm_bf16_staged_kernel(Args args) {
+    dma_tile<typename C::T, C::STAGES, true, true, kFeedBf16>(args);
+}
+
+template <class C, bool A_K, bool B_K, int FEED>
 hipError_t launch_dma_tiles(const Problem& p, const Env& env, hipStream_t stream) {
     using T = typename C::T;
     const Plan plan = plan_for<T>(p, env);
@@ -515,7 +559,10 @@ hipError_t launch_dma_tiles(const Problem& p, const Env& env, hipStream_t stream
     for (int64_t first = 0; first < p.batch; first += chunk) {
         const int64_t count = std::min<int64_t>(chunk, p.batch - first);
         args.batch_base = first;
-        if constexpr (BF16)
+        if constexpr (FEED == kFeedBf16)
+            hipLaunchKernelGGL((gemm_bf16_staged_kernel<C>), dim3(unsigned(count * per_batch)), dim3(T::THREADS), 0,
+                               stream, args);
+        else if constexpr (FEED == kFeedRound)
             hipLaunchKernelGGL((gemm_bf16_dma_kernel<C, A_K, B_K>), dim3(unsigned(count * per_batch)),
                                dim3(T::THREADS), 0, stream, args);
         else
@@ -528,12 +575,12 @@ hipError_t launch_dma_tiles(const Problem& p, const Env& env, hipStream_t stream
     return hipSuccess;
 }
 
-template <class C, bool BF16>
+template <class C, int FEED>
 hipError_t launch_dma_layout(const Problem& p, const Env& env, hipStream_t stream) {
-    if (p.a_k_contiguous && p.b_k_contiguous) return launch_dma_tiles<C, true, true, BF16>(p, env, stream);
-    if (p.a_k_contiguous) return launch_dma_tiles<C, true, false, BF16>(p, env, stream);
-    if (p.b_k_contiguous) return launch_dma_tiles<C, false, true, BF16>(p, env, stream);
-    return launch_dma_tiles<C, false, false, BF16>(p, env, stream);
+    if (p.a_k_contiguous && p.b_k_contiguous) return launch_dma_tiles<C, true, true, FEED>(p, env, stream);
+    if (p.a_k_contiguous) return launch_dma_tiles<C, true, false, FEED>(p, env, stream);
+    if (p.b_k_contiguous) return launch_dma_tiles<C, false, true, FEED>(p, env, stream);
+    return launch_dma_tiles<C, false, false, FEED>(p, env, stream);
 }
 
 using DmaSquare = DmaConfig<Tile<128, 128, 32, 2, 2>, 2>;
@@ -572,14 +619,113 @@ bool bf16_dma_applies(const Problem& p) {
 }
 
 hipError_t launch_gemm_f32_dma(const Problem& p, const Env& env, hipStream_t stream) {
-    if (p.n <= 64) return launch_dma_layout<DmaNarrow, false>(p, env, stream);
-    return launch_dma_layout<DmaSquare, false>(p, env, stream);
+    if (p.n <= 64) return launch_dma_layout<DmaNarrow, kFeedF32>(p, env, stream);
+    return launch_dma_layout<DmaSquare, kFeedF32>(p, env, stream);
 }
 
 hipError_t launch_gemm_bf16_dma(const Problem& p, const Env& env, hipStream_t stream) {
-    if (p.n <= 64) return launch_dma_layout<Bf16Narrow, true>(p, env, stream);
-    if (p.n >= kBf16WideColumns) return launch_dma_layout<Bf16Wide, true>(p, env, stream);
-    return launch_dma_layout<Bf16Square, true>(p, env, stream);
+    if (p.n <= 64) return launch_dma_layout<Bf16Narrow, kFeedRound>(p, env, stream);
+    if (p.n >= kBf16WideColumns) return launch_dma_layout<Bf16Wide, kFeedRound>(p, env, stream);
+    return launch_dma_layout<Bf16Square, kFeedRound>(p, env, stream);
+}
+
+// ---- bf16 operands staged in the workspace -------------------------------
+
+namespace {
+
+// Where the staged operands go: A as [batch][m][kp] bf16 and B as
+// [batch][n][kp], each from the workspace's start in 256-byte units; the
+// product's split-K partial sums follow them.
+struct Staging {
+    int64_t kp = 0;          // K rounded up to 8 bf16 (one 16-byte slot)
+    int64_t batches_a = 1;   // 1 when A is shared by every batch (stride 0)
+    int64_t batches_b = 1;
+    size_t a_bytes = 0, b_bytes = 0;
+};
+
+size_t round256(size_t bytes) { return (bytes + 255) / 256 * 256; }
+
+Staging staging_for(const Problem& p) {
+    Staging st;
+    st.kp = (p.k + 7) / 8 * 8;
+    st.batches_a = p.stride_a == 0 ? 1 : p.batch;
+    st.batches_b = p.stride_b == 0 ? 1 : p.batch;
+    st.a_bytes = round256(size_t(st.batches_a) * size_t(p.m) * size_t(st.kp) * 2);
+    st.b_bytes = round256(size_t(st.batches_b) * size_t(p.n) * size_t(st.kp) * 2);
+    return st;
+}
+
+// The product on the staged operands, k counted in pairs of bf16.
+Problem staged_problem(const Problem& p, const Staging& st, const Env& env) {
+    Problem q = p;
+    const char* base = reinterpret_cast<const char*>(env.workspace);
+    q.a = reinterpret_cast<const float*>(base);
+    q.b = reinterpret_cast<const float*>(base + st.a_bytes);
+    q.k = st.kp / 2;
+    q.a_k_contiguous = true;
+    q.b_k_contiguous = true;
+    q.lda = st.kp / 2;
+    q.ldb = st.kp / 2;
+    q.stride_a = st.batches_a == 1 ? 0 : p.m * st.kp / 2;
+    q.stride_b = st.batches_b == 1 ? 0 : p.n * st.kp / 2;
+    return q;
+}
+
+// The workspace left for split-K partials after the staged operands.
+Env staged_env(const Env& env, const Staging& st) {
+    Env e = env;
+    const size_t used = st.a_bytes + st.b_bytes;
+    e.workspace = reinterpret_cast<float*>(reinterpret_cast<char*>(env.workspace) + used);
+    e.workspace_bytes = env.workspace_bytes - used;
+    return e;
+}
+
+using Bf16StagedSquare = DmaConfig<Tile<128, 128, 32, 2, 2>, 2>;
+using Bf16StagedWide = DmaConfig<Tile<128, 256, 32, 2, 4>, 3>;
+
+template <class F>
+hipError_t with_staged_config(const Problem& q, F&& f) {
+    if (q.n >= kBf16WideColumns) return f(Bf16StagedWide{});
+    return f(Bf16StagedSquare{});
+}
+
+}  // namespace
+
+bool bf16_staged_applies(const Problem& p, const Env& env) {
+    // Unmasked (the masked products keep their in-stage masking), operands
+    // that the direct-to-LDS loads could read, n above the narrow tile, and
+    // room for both staged operands.
+    if (p.mask != SN_MASK_NONE || p.n <= 64 || p.k < 1 || env.workspace == nullptr || !bf16_dma_applies(p))
+        return false;
+    if (p.batch > 65535) return false;
+    const Staging st = staging_for(p);
+    if (st.a_bytes + st.b_bytes > env.workspace_bytes) return false;
+    const Problem q = staged_problem(p, st, env);
+    return with_staged_config(q, [&](auto c) { return config_applies<decltype(c)>(q) ? hipSuccess : hipErrorNotSupported; }) ==
+           hipSuccess;
+}
+
+hipError_t launch_gemm_bf16_staged(const Problem& p, const Env& env, hipStream_t stream) {
+    const Staging st = staging_for(p);
+    const Problem q = staged_problem(p, st, env);
+    uint16_t* a16 = reinterpret_cast<uint16_t*>(const_cast<float*>(q.a));
+    uint16_t* b16 = reinterpret_cast<uint16_t*>(const_cast<float*>(q.b));
+    hipError_t err = launch_stage_bf16(p.a, p.a_k_contiguous, p.lda, p.m, p.k, st.kp, st.batches_a, p.stride_a, a16,
+                                       stream);
+    if (err == hipSuccess)
+        err = launch_stage_bf16(p.b, p.b_k_contiguous, p.ldb, p.n, p.k, st.kp, st.batches_b, p.stride_b, b16, stream);
+    if (err != hipSuccess) return err;
+    const Env rest = staged_env(env, st);
+    return with_staged_config(q, [&](auto c) { return launch_dma_tiles<decltype(c), true, true, kFeedBf16>(q, rest, stream); });
+}
+
+size_t bf16_staged_workspace_bytes(const Problem& p, const Env& env) {
+    const Staging st = staging_for(p);
+    const Problem q = staged_problem(p, st, env);
+    const Env rest = staged_env(env, st);
+    const Plan plan = q.n >= kBf16WideColumns ? plan_for<Bf16StagedWide::T>(q, rest) : plan_for<Bf16StagedSquare::T>(q, rest);
+    const size_t partials = plan.splits > 1 ? size_t(plan.splits) * size_t(p.m) * size_t(p.n) * sizeof(float) : 0;
+    return st.a_bytes + st.b_bytes + partials;
 }
 
 size_t bf16_dma_workspace_bytes(const Problem& p, const Env& env) {

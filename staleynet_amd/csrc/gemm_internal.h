@@ -51,7 +51,15 @@ hipError_t launch_gemm_simple(const Problem& p, hipStream_t stream);
 hipError_t launch_gemv(const Problem& p, const Env& env, hipStream_t stream);
 bool gemv_applies(const Problem& p, const Env& env);
 
-// Bytes of split-K workspace launch_gemm_* would use for `p` (0 = none).
+// Rounds an fp32 operand to bf16 (nearest-even) into dst[batch][rows][kp],
+// K-contiguous, zeros for k in [k, kp) (bf16_stage.hip). Element (r, k) of
+// the source is src[r * ld + k] when k_contiguous, else src[k * ld + r];
+// batches are src_stride floats apart. kp must be a multiple of 8 and >= k.
+hipError_t launch_stage_bf16(const float* src, bool k_contiguous, int64_t ld, int64_t rows, int64_t k, int64_t kp,
+                             int64_t batch, int64_t src_stride, uint16_t* dst, hipStream_t stream);
+
+// Bytes of workspace launch_gemm_* would use for `p` (0 = none): split-K
+// partial sums, and for bf16 the staged operands.
 size_t gemm_workspace_bytes(const Problem& p, bool bf16, const Env& env);
 
 // Linear's bias kernels (bias.hip). add_row_bias: out[b][r][c] += bias[c]

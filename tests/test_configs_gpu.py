@@ -222,7 +222,7 @@ def test_cached_decode_attention_matches_the_oracle(gpu, cached):
 
 # ---- bf16-input variant at config 2 ----------------------------------------------------------
 
-@pytest.mark.parametrize("layer", ["qkv", "down"])
+@pytest.mark.parametrize("layer", ["qkv", "down", "head"])
 def test_bf16_products_within_the_stated_tolerance(gpu, layer):
     """bf16 inputs with fp32 accumulation against the fp32 oracle: max relative
     error below 2e-2 (the variant's stated tolerance)."""

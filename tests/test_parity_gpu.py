@@ -298,7 +298,8 @@ def test_bf16_is_exact_on_bf16_representable_integers(gpu, variant):
     assert np.array_equal(expected, actual)
 
 
-def test_bf16_inputs_round_to_nearest_even(gpu):
+@pytest.mark.parametrize("k", [16, 128])  # 16: the narrow tile; 128: operands staged as bf16 first
+def test_bf16_inputs_round_to_nearest_even(gpu, k):
     # A times the identity returns A rounded to bf16 (7 stored mantissa bits).
     # Expected values follow from IEEE roundTiesToEven by hand:
     u = 2.0 ** -7  # bf16 ulp in [1, 2)
@@ -315,7 +316,6 @@ def test_bf16_inputs_round_to_nearest_even(gpu):
         (2.0 ** -100 * 1.5, 2.0 ** -100 * 1.5),    # exact, small exponent
         (0.0, 0.0),
     ]
-    k = 16
     a = np.zeros((len(cases), k), np.float32)
     a[:, 0] = [c[0] for c in cases]
     eye = np.eye(k, dtype=np.float32)
@@ -323,6 +323,64 @@ def test_bf16_inputs_round_to_nearest_even(gpu):
     out = run_gpu(gpu, spec, a.ravel(), eye.ravel(), np.zeros(len(cases) * k, np.float32), MatmulKernel.MfmaBf16)
     got = out.reshape(len(cases), k)[:, 0]
     assert got.tolist() == [np.float32(c[1]) for c in cases]
+
+
+# Unmasked aligned bf16 products with more than 64 columns first round both operands to
+# bf16, K-contiguous, in the context's workspace (zeros pad K to a multiple of 8), then
+# multiply; exact integer inputs pin every layout, padding, batch and shared-operand case.
+@pytest.mark.parametrize("variant,rows,cols,inner", [
+    ("TN", 96, 160, 203),    # both operands transposed while staged, K padded to 208
+    ("TT", 68, 132, 36),     # A transposed, B K-contiguous
+    ("NT", 100, 72, 1000),   # both K-contiguous
+    ("NN", 260, 2052, 96),   # the 128x256 tile, partial tiles on both edges
+])
+def test_bf16_staged_operands_are_exact_on_integers(gpu, variant, rows, cols, inner):
+    rng = np.random.default_rng(rows + cols + inner)
+    left = rng.integers(-16, 17, size=rows * inner).astype(np.float32)
+    right = rng.integers(-16, 17, size=inner * cols).astype(np.float32)
+    spec = MatmulSpec.new(rows, cols, inner).scaled(0.5)
+    if variant[0] == "T":
+        spec = spec.left_transposed()
+    if variant[1] == "T":
+        spec = spec.right_transposed()
+    initial = rng.integers(-8, 9, size=rows * cols).astype(np.float32)
+    expected = expected_for(spec.accumulate(), left, right, initial)
+    actual = run_gpu(gpu, spec.accumulate(), left, right, initial, MatmulKernel.MfmaBf16)
+    assert np.array_equal(expected, actual)
+
+
+@pytest.mark.parametrize("shared", ["none", "left", "right"])
+def test_bf16_staged_batches_and_shared_operands(gpu, shared):
+    batches, rows, cols, inner = 3, 72, 136, 64
+    rng = np.random.default_rng(5)
+    left_stride = 0 if shared == "left" else rows * inner
+    right_stride = 0 if shared == "right" else inner * cols
+    left = rng.integers(-16, 17, size=max(left_stride, rows * inner) * (1 if shared == "left" else batches))
+    right = rng.integers(-16, 17, size=max(right_stride, inner * cols) * (1 if shared == "right" else batches))
+    spec = MatmulSpec.new(rows, cols, inner).right_transposed().batched(
+        BatchStrides(batches, left_stride, right_stride, rows * cols))
+    initial = np.zeros(batches * rows * cols, np.float32)
+    expected = expected_for(spec, left.astype(np.float32), right.astype(np.float32), initial)
+    actual = run_gpu(gpu, spec, left.astype(np.float32), right.astype(np.float32), initial, MatmulKernel.MfmaBf16)
+    assert np.array_equal(expected, actual)
+
+
+def test_bf16_without_room_to_stage_takes_the_fp32_staged_kernel():
+    # A context whose workspace cannot hold the staged operands multiplies from fp32 stages
+    # (rounding each fragment): the same exact result.
+    from staleynet_amd.gemm import Gpu
+    small = Gpu(0, workspace_bytes=4096)
+    try:
+        rows, cols, inner = 128, 256, 512
+        rng = np.random.default_rng(8)
+        left = rng.integers(-16, 17, size=rows * inner).astype(np.float32)
+        right = rng.integers(-16, 17, size=inner * cols).astype(np.float32)
+        spec = MatmulSpec.new(rows, cols, inner)
+        initial = np.zeros(rows * cols, np.float32)
+        actual = run_gpu(small, spec, left, right, initial, MatmulKernel.MfmaBf16)
+        assert np.array_equal(expected_for(spec, left, right, initial), actual)
+    finally:
+        small.close()
 
 
 # ---- decode-shaped products (few rows, row-major weight) ------------------------------
