@@ -581,33 +581,72 @@ struct Plan {
     int64_t k_per_split;
 };
 
-// Products whose output tiles cannot fill every CU twice over (the
-// K = 32768 weight gradients: 36 to 768 tiles of 128x128) split K instead,
-// into enough BK-aligned slices of at least 8 steps for about eight
-// workgroups per CU, as far as the workspace allows. Measured on the
-// c2 weight gradients, eight per CU beats three (+2 to +8 %) and matches
-// twelve; more slices only add partial sums to write and add.
+// How a kernel instantiation occupies the device, for the split-K choice:
+// workgroups resident per CU (LDS-limited), the FLOP rate one CU sustains
+// on it, and the k values one K-step index counts (2 when the operands are
+// bf16 pairs).
+struct SplitCost {
+    int workgroups_per_cu = 2;
+    double flops_per_cu = 522e9;  // fp32 matrix cores at about 85 % of 157.3 TFLOP/s / 256 CUs
+    int k_per_index = 1;
+};
+
+// Products whose output tiles cannot fill every CU four times over (the
+// K = 32768 weight gradients: 36 to 768 tiles of 128x128) split K into
+// BK-aligned slices of at least 8 steps, as far as the workspace allows. The
+// count is the cheapest under a model of the launch, measured on c2's
+// weight gradients:
+//  * workgroups are dealt evenly over the CUs; the busiest CU runs
+//    ceil(tiles x slices / CUs) of them, workgroups_per_cu at a time, and
+//    a last, partly filled group runs faster than a full one (about 0.7 of
+//    its time when it is one of two);
+//  * a workgroup costs its K-steps plus about 3 steps of start-up and
+//    epilogue;
+//  * the partial sums cost 8 bytes per slice and output (written, then
+//    read by the reduce) at about 6 TB/s.
+// Counts just past a whole number of groups leave a few workgroups running
+// alone at the end; the former rule (about eight workgroups per CU) hit
+// that on four of the five c2 weight gradients.
 template <class T>
-Plan plan_for(const Problem& p, const Env& env) {
+Plan plan_for(const Problem& p, const Env& env, const SplitCost& cost = SplitCost{}) {
     Plan plan;
     plan.tiles_m = int((p.m + T::BM - 1) / T::BM);
     plan.tiles_n = int((p.n + T::BN - 1) / T::BN);
     plan.splits = 1;
     plan.k_per_split = std::max<int64_t>(p.k, 1);
     const int64_t tiles = int64_t(plan.tiles_m) * plan.tiles_n * p.batch;
-    const int64_t threshold = int64_t(env.cu_count) * 4;
-    const int64_t target = int64_t(env.cu_count) * 8;
+    const int64_t cus = std::max(env.cu_count, 1);
+    const int64_t threshold = cus * 4;
     const int64_t k_steps = (p.k + T::BK - 1) / T::BK;
-    if (p.mask == SN_MASK_NONE && tiles < threshold && k_steps >= 16 && p.batch == 1) {
-        int64_t splits = std::min<int64_t>((target + tiles - 1) / tiles, k_steps / 8);
-        const int64_t per_split_bytes = p.m * p.n * int64_t(sizeof(float));
-        if (per_split_bytes > 0) splits = std::min<int64_t>(splits, int64_t(env.workspace_bytes) / per_split_bytes);
-        if (splits >= 2) {
-            const int64_t steps_per_split = (k_steps + splits - 1) / splits;
+    if (p.mask != SN_MASK_NONE || tiles >= threshold || k_steps < 16 || p.batch != 1) return plan;
+    int64_t max_splits = k_steps / 8;
+    const int64_t per_split_bytes = p.m * p.n * int64_t(sizeof(float));
+    if (per_split_bytes > 0) max_splits = std::min<int64_t>(max_splits, int64_t(env.workspace_bytes) / per_split_bytes);
+    if (max_splits < 2) return plan;
+    // One K-step of a full group of workgroups, and the partial-sum bytes
+    // the reduce moves in that time.
+    const int group = std::max(cost.workgroups_per_cu, 1);
+    const double step_seconds = 2.0 * T::BM * T::BN * T::BK * cost.k_per_index * group / cost.flops_per_cu;
+    const double reduce_bytes_per_step = 6e12 * step_seconds;
+    auto time_of = [&](int64_t steps_per_split, int64_t splits) {
+        const int64_t per_cu = (tiles * splits + cus - 1) / cus;
+        const int64_t full = per_cu / group, rest = per_cu % group;
+        const double groups = double(full) + (rest ? 1.0 - 0.3 * double(group - rest) / double(group - 1 > 0 ? group - 1 : 1) : 0.0);
+        const double reduce = splits > 1 ? double(splits) * double(per_split_bytes) * 2.0 / reduce_bytes_per_step : 0.0;
+        return groups * double(steps_per_split + 3) + reduce;
+    };
+    double best = time_of(k_steps, 1);
+    for (int64_t want = 2; want <= max_splits; ++want) {
+        const int64_t steps_per_split = (k_steps + want - 1) / want;
+        const int64_t splits = (k_steps + steps_per_split - 1) / steps_per_split;
+        const double t = time_of(steps_per_split, splits);
+        if (t < best) {
+            best = t;
             plan.k_per_split = steps_per_split * T::BK;
-            plan.splits = int((p.k + plan.k_per_split - 1) / plan.k_per_split);
+            plan.splits = int(splits);
         }
     }
+    if (plan.splits > 1) plan.splits = int((p.k + plan.k_per_split - 1) / plan.k_per_split);
     return plan;
 }
 
@@ -643,6 +682,7 @@ Args make_args(const Problem& p, const Env& env, const Plan& plan) {
 // (aligned operands) and its launcher.
 bool dma_applies(const Problem& p);
 hipError_t launch_gemm_f32_dma(const Problem& p, const Env& env, hipStream_t stream);
+size_t f32_dma_workspace_bytes(const Problem& p, const Env& env);
 // The bf16 variant of the direct-to-LDS kernel: whether it serves `p`, its
 // launcher and the split-K workspace it uses.
 bool bf16_dma_applies(const Problem& p);

@@ -548,10 +548,24 @@ void gemm_bf16_staged_kernel(Args args) {
     dma_tile<typename C::T, C::STAGES, true, true, kFeedBf16>(args);
 }
 
+// The split-K model's view of an instantiation: workgroups per CU from its
+// LDS stages, and the rate one CU sustains on it (measured: fp32 at about
+// 85 % of the matrix-core peak; bf16 from fp32 stages about 20 %, from bf16
+// stages about 30 % of 2.5 PFLOP/s over 256 CUs).
+template <class C, int FEED>
+SplitCost split_cost() {
+    using T = typename C::T;
+    SplitCost cost;
+    cost.workgroups_per_cu = std::max(1, 160 * 1024 / ((T::BM + T::BN) * T::BK * 4 * C::STAGES));
+    cost.flops_per_cu = FEED == kFeedF32 ? 522e9 : FEED == kFeedRound ? 1.95e12 : 2.9e12;
+    cost.k_per_index = FEED == kFeedBf16 ? 2 : 1;
+    return cost;
+}
+
 template <class C, bool A_K, bool B_K, int FEED>
 hipError_t launch_dma_tiles(const Problem& p, const Env& env, hipStream_t stream) {
     using T = typename C::T;
-    const Plan plan = plan_for<T>(p, env);
+    const Plan plan = plan_for<T>(p, env, split_cost<C, FEED>());
     Args args = make_args<T>(p, env, plan);
     const int64_t per_batch = int64_t(plan.tiles_m) * plan.tiles_n * plan.splits;
     const int64_t chunk = batches_per_launch(per_batch, T::THREADS, p.batch);
@@ -723,15 +737,23 @@ size_t bf16_staged_workspace_bytes(const Problem& p, const Env& env) {
     const Staging st = staging_for(p);
     const Problem q = staged_problem(p, st, env);
     const Env rest = staged_env(env, st);
-    const Plan plan = q.n >= kBf16WideColumns ? plan_for<Bf16StagedWide::T>(q, rest) : plan_for<Bf16StagedSquare::T>(q, rest);
+    const Plan plan = q.n >= kBf16WideColumns
+                          ? plan_for<Bf16StagedWide::T>(q, rest, split_cost<Bf16StagedWide, kFeedBf16>())
+                          : plan_for<Bf16StagedSquare::T>(q, rest, split_cost<Bf16StagedSquare, kFeedBf16>());
     const size_t partials = plan.splits > 1 ? size_t(plan.splits) * size_t(p.m) * size_t(p.n) * sizeof(float) : 0;
     return st.a_bytes + st.b_bytes + partials;
 }
 
+size_t f32_dma_workspace_bytes(const Problem& p, const Env& env) {
+    const Plan plan = p.n <= 64 ? plan_for<DmaNarrow::T>(p, env, split_cost<DmaNarrow, kFeedF32>())
+                                : plan_for<DmaSquare::T>(p, env, split_cost<DmaSquare, kFeedF32>());
+    return plan.splits > 1 ? size_t(plan.splits) * size_t(p.m) * size_t(p.n) * sizeof(float) : 0;
+}
+
 size_t bf16_dma_workspace_bytes(const Problem& p, const Env& env) {
-    const Plan plan = p.n <= 64                    ? plan_for<Bf16Narrow::T>(p, env)
-                      : p.n >= kBf16WideColumns ? plan_for<Bf16Wide::T>(p, env)
-                                                : plan_for<Bf16Square::T>(p, env);
+    const Plan plan = p.n <= 64 ? plan_for<Bf16Narrow::T>(p, env, split_cost<Bf16Narrow, kFeedRound>())
+                      : p.n >= kBf16WideColumns ? plan_for<Bf16Wide::T>(p, env, split_cost<Bf16Wide, kFeedRound>())
+                                                : plan_for<Bf16Square::T>(p, env, split_cost<Bf16Square, kFeedRound>());
     return plan.splits > 1 ? size_t(plan.splits) * size_t(p.m) * size_t(p.n) * sizeof(float) : 0;
 }
 

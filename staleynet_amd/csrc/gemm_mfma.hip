@@ -272,6 +272,7 @@ hipError_t launch_splitk_reduce(const Problem& p, const Env& env, int splits, hi
 }
 
 size_t f32_workspace_bytes(const Problem& p, const Env& env) {
+    if (dma_applies(p)) return f32_dma_workspace_bytes(p, env);
     const Plan plan = use_narrow(p) ? plan_for<TileNarrow>(p, env) : plan_for<TileSquare>(p, env);
     return plan.splits > 1 ? size_t(plan.splits) * size_t(p.m) * size_t(p.n) * sizeof(float) : 0;
 }
