@@ -308,6 +308,18 @@ def measure_attention(gpu: Gpu, events: HipEvents, repeats: int = 3):
     packed.free()
     result["step_ms"] = {"products_causal": round(total["causal"], 3),
                          "with_row_kernels": round(total["causal"] + softmax_ms + backward_ms + split_ms + merge_ms, 3)}
+    # The fused forward (sn_causal_attention) against the three calls it replaces (scores
+    # product, causal_softmax, mix product): O only, and O with the probabilities the backward
+    # reads. FLOPs on the visible (query, key) pairs: two products of 2 h per pair.
+    unfused_ms = (result["products"]["scores Q.K^T"]["causal_ms"] + softmax_ms
+                  + result["products"]["mix P.V"]["causal_ms"])
+    fused_ms = timed(events, gpu.stream, lambda: gpu.causal_attention(q, k, v, o, heads, t, t, h, 0.125), repeats)
+    fused_p_ms = timed(events, gpu.stream, lambda: gpu.causal_attention(q, k, v, o, heads, t, t, h, 0.125,
+                                                                        probabilities=p), repeats)
+    result["fused_forward"] = {
+        "three_calls_ms": round(unfused_ms, 3), "fused_ms": round(fused_ms, 3),
+        "fused_with_probabilities_ms": round(fused_p_ms, 3),
+        "fused_tflops_on_visible_work": round(2 * causal_flops / (fused_ms * 1e-3) / 1e12, 1)}
     return result
 
 

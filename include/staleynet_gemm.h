@@ -280,6 +280,42 @@ int sn_split_heads(sn_context *context, const float *packed, size_t packed_len, 
 int sn_merge_heads(sn_context *context, const float *head_major, size_t head_major_len, float *packed,
                    size_t packed_len, const sn_head_layout *layout);
 
+/* ---- fused causal attention forward --------------------------------------- */
+/* Where the attention matrices are: `heads` (batch x heads) matrices; Q
+ * [heads][queries][head_dim] with q_stride floats between heads, K and V
+ * [heads][keys][head_dim] with kv_stride between heads (a key/value cache
+ * of capacity `keys`), rows head_dim floats apart; query q of a head sees
+ * keys 0 ..= q + query_offset. */
+typedef struct sn_attention_shape {
+    size_t heads;
+    size_t queries;
+    size_t keys;
+    size_t head_dim;
+    size_t q_stride;
+    size_t kv_stride;
+    size_t query_offset;
+    float scale;
+} sn_attention_shape;
+
+/* Fused causal attention forward. It has no counterpart in the reference's
+ * Gpu API: it computes in one launch what CausalSelfAttention::forward
+ * (crates/staleynet-model/src/layers/attention.rs:206-213) computes with
+ * three calls, the scores product (MatmulSpec::new(queries, keys, h)
+ * .right_transposed(), batched over the heads), Gpu::causal_softmax(scores,
+ * queries, scale, query_offset) and the mix product (MatmulSpec::new(
+ * queries, h, keys)), without writing the scores. out: O [heads][queries]
+ * [head_dim]. probabilities (may be null): the [heads][queries][keys]
+ * matrix causal_softmax leaves, 0 past the diagonal, for the backward.
+ * head_dim 32, 64 or 128 and 16-byte aligned buffers and strides
+ * (SN_ERR_UNSUPPORTED; strides may overlap heads, 0 shares one K and V);
+ * keys >= 1 (SN_ERR_SHAPE); buffers too small for the shape
+ * (SN_ERR_LENGTH_MISMATCH);
+ * out or probabilities overlapping an input or each other (SN_ERR_ALIASING).
+ * Within the fp32 tolerance of the three calls. */
+int sn_causal_attention(sn_context *context, const sn_attention_shape *shape, const float *q, size_t q_len,
+                        const float *k, size_t k_len, const float *v, size_t v_len, float *out, size_t out_len,
+                        float *probabilities, size_t probabilities_len);
+
 /* ---- the head's consumer: per-codebook softmax cross-entropy ------------- */
 /* An empty target slot (crates/staleynet-cuda/src/kernels/mod.rs:46). */
 #define SN_EMPTY_TOKEN 0xFFFFFFFFu

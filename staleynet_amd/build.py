@@ -19,7 +19,8 @@ LIBRARY = os.path.join(PACKAGE_DIR, "libstaleynet_gemm.so")
 INCLUDE = os.path.join(REPO_ROOT, "include")
 
 SOURCES = ["context.cpp", "gemm_mfma.hip", "gemm_dma.hip", "gemm_bf16.hip", "gemm_simple.hip", "gemv.hip", "bias.hip",
-           "softmax.hip", "loss.hip", "heads.hip", "bf16_stage.hip", "synth.hip"]
+           "softmax.hip", "loss.hip", "heads.hip", "attention.hip", "bf16_stage.hip",
+           "synth.hip"]
 
 # Packed-fp32 instructions are switched off: some of their forms have given
 # wrong results on these machines, and the kernels here never need them.

@@ -1,0 +1,431 @@
+// Fused causal attention forward: O = causal_softmax(scale * Q K^T) V per
+// head, without writing the [queries, keys] score matrix. The reference
+// computes it as three calls (layers/attention.rs:206-213): the scores
+// product (MatmulSpec::new(T, T, h).right_transposed(), batched over the
+// heads), causal_softmax (kernels/attention.rs:140-183) and the mix product
+// (MatmulSpec::new(T, h, T)); the probabilities it keeps for the backward
+// are written here on request, so the backward (attention.rs:220-267) can
+// run unchanged.
+//
+// Layout: Q [heads][queries][h] and K, V [heads][keys][h] (head-major, rows
+// q_stride / kv_stride floats apart per head), O [heads][queries][h], P
+// [heads][queries][keys]. Query q of a head sees keys 0 ..= q +
+// query_offset (as causal_softmax with `queries` rows per matrix).
+//
+// Design (gfx950, fp32 matrix cores, v_mfma_f32_32x32x2f32):
+//  * A workgroup of 4 waves owns 128 queries of one head; a wave owns 32.
+//    K and V stream through LDS in blocks of 64 keys, two stages, loaded
+//    straight from memory into LDS (buffer_load ... lds); K's 16-byte chunks
+//    are XOR-swizzled by row so that fragment reads are conflict-free.
+//  * A wave computes S^T = K Q^T for 32 keys at a time (keys along the
+//    accumulator rows, its 32 queries along the columns, Q held in
+//    registers). In the 32x32 accumulator, lane l holds column l % 32, so
+//    every register of a lane belongs to the lane's query: the online
+//    softmax (running max m, running sum l, O rescaled by exp(m_old -
+//    m_new)) is per lane, with one exchange between the lane pair (l, l ^
+//    32) that share a query, and the probabilities are already laid out as
+//    the B operand of O^T += V^T P^T: no trip through LDS.
+//  * Element arithmetic follows causal_softmax: s * scale, minus the
+//    maximum, expf, each rounded; the sum is accumulated in a different
+//    order (per 32-key block, then rescaled), so parity is to the fp32
+//    tolerance.
+//  * P (optional) takes a second pass over K with the final m and l: p =
+//    expf(s * scale - m) / l, 0 past the diagonal, so it matches the
+//    probabilities causal_softmax leaves.
+//  * Query blocks are launched longest first across all heads (the last
+//    queries see the most keys).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <type_traits>
+
+#include "gemm_internal.h"
+
+namespace sn {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void* lds_void;
+
+constexpr int kWaves = 4;
+constexpr int kQueries = 32 * kWaves;  // per workgroup
+constexpr int kKeys = 64;              // per LDS stage
+constexpr int32_t kRecords = 0x7FFFFFFF;
+constexpr int32_t kOutOfRange = int32_t(0x80000000u);
+constexpr int32_t kRawBufferFormat = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const float* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, kRecords, kRawBufferFormat);
+}
+
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, const void* lds, int32_t offset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void)lds, 16, offset, 0, 0, 0);
+}
+
+// Waits until at most PENDING of this wave's vector-memory loads are in
+// flight (vmcnt; the other counters left at their maxima).
+template <int PENDING>
+__device__ __forceinline__ void wait_loads() {
+    static_assert(PENDING >= 0 && PENDING < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (PENDING & 15) | ((PENDING >> 4) << 14));
+}
+
+// Workgroup barrier that does not wait for loads still in flight (the
+// direct-to-LDS loads of the next stage); LDS reads are completed first.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int H>
+struct Geometry {
+    static constexpr int SLOTS = H / 4;                        // 16-byte chunks per row
+    static constexpr int SWIZZLE = SLOTS < 16 ? SLOTS - 1 : 15;  // row bits XORed into the chunk index
+    static constexpr int CHUNKS = H / 16;                      // 16-deep MFMA chunks over h
+    static constexpr int OBLOCKS = H / 32;                     // 32-row accumulator blocks of O^T
+    static constexpr int STAGE_SLOTS = kKeys * SLOTS;          // f32x4 per operand per stage
+    static constexpr int LOADS = STAGE_SLOTS / (64 * kWaves);  // load instructions per wave per operand
+    static_assert(H == 32 || H == 64 || H == 128, "head dims 32, 64, 128");
+    static_assert(STAGE_SLOTS % (64 * kWaves) == 0, "whole load instructions per wave");
+};
+
+struct AttentionArgs {
+    const float* q;
+    const float* k;
+    const float* v;
+    float* o;
+    float* p;  // null: no probabilities
+    int64_t queries, keys;
+    int64_t q_stride, kv_stride;  // floats between heads
+    int64_t query_offset;
+    int64_t heads;
+    int32_t query_blocks;
+    float scale;
+};
+
+template <int H>
+__global__ __launch_bounds__(64 * kWaves) void causal_attention_kernel(AttentionArgs args) {
+#pragma clang fp contract(off)
+    using G = Geometry<H>;
+    // Two LDS stages per operand, each its own array: every LDS access below
+    // names its stage at compile time, so the compiler's wait counts leave the
+    // other stage's loads in flight.
+    __shared__ f32x4 k_stage0[G::STAGE_SLOTS], k_stage1[G::STAGE_SLOTS];
+    __shared__ f32x4 v_stage0[G::STAGE_SLOTS], v_stage1[G::STAGE_SLOTS];
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    auto k_of = [&](auto stage) __attribute__((always_inline)) -> f32x4* {
+        if constexpr (decltype(stage)::value == 0) return k_stage0;
+        else return k_stage1;
+    };
+    auto v_of = [&](auto stage) __attribute__((always_inline)) -> f32x4* {
+        if constexpr (decltype(stage)::value == 0) return v_stage0;
+        else return v_stage1;
+    };
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 31;  // this lane's query within the wave
+    const int half = lane >> 5;
+
+    // Longest query blocks first, over all heads: the heads' last query
+    // blocks (which see the most keys), then the ones before, so that the
+    // short blocks fill in at the end.
+    const int64_t block = blockIdx.x;
+    const int64_t head = block % args.heads;
+    const int64_t query_block = args.query_blocks - 1 - block / args.heads;
+    const int64_t q_first = query_block * kQueries;
+    const int64_t q_wave = q_first + 32 * wave;
+    const int64_t q = q_wave + col;
+    // Keys this workgroup and this wave can see (exclusive ends).
+    const int64_t wg_keys = min(args.keys, min(q_first + kQueries, args.queries) - 1 + args.query_offset + 1);
+    const int64_t wave_keys = min(args.keys, q_wave + 31 + args.query_offset + 1);
+    const int stages_total = int((wg_keys + kKeys - 1) / kKeys);
+
+    const float* kh = args.k + head * args.kv_stride;
+    const float* vh = args.v + head * args.kv_stride;
+    const __amdgpu_buffer_rsrc_t k_rsrc = buffer_of(kh);
+    const __amdgpu_buffer_rsrc_t v_rsrc = buffer_of(vh);
+
+    // Q of this lane's query in registers: chunk c, MFMA s: h index 16c + 8 half + s.
+    float qreg[G::CHUNKS][8];
+    {
+        // Lanes past the last query read query 0 and keep zeros.
+        const bool ok = q < args.queries;
+        const float* qrow = args.q + head * args.q_stride + (ok ? q : 0) * H;
+#pragma unroll
+        for (int c = 0; c < G::CHUNKS; ++c) {
+            const f32x4 lo = *reinterpret_cast<const f32x4*>(qrow + 16 * c + 8 * half);
+            const f32x4 hi = *reinterpret_cast<const f32x4*>(qrow + 16 * c + 8 * half + 4);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                qreg[c][s] = ok ? lo[s] : 0.f;
+                qreg[c][4 + s] = ok ? hi[s] : 0.f;
+            }
+        }
+    }
+
+    // Stage loads: instruction u of wave w covers rows 4 (w * LOADS + u) + lane / SLOTS' groups;
+    // lane i writes LDS slot (row, i % SLOTS) of its 1 KB; for K that slot holds global chunk
+    // (slot ^ swizzle(row)), for V chunk slot.
+    auto issue = [&](auto stage, int64_t key0, bool with_v) __attribute__((always_inline)) {
+        f32x4* ks = k_of(stage);
+        f32x4* vs = v_of(stage);
+#pragma unroll
+        for (int u = 0; u < G::LOADS; ++u) {
+            const int instr = wave * G::LOADS + u;
+            const int e = 64 * instr + lane;  // f32x4 slot in the stage
+            const int row = e / G::SLOTS;
+            const int slot = e % G::SLOTS;
+            const int64_t key = key0 + row;
+            const int chunk_k = slot ^ (row & G::SWIZZLE);
+            const int32_t k_off = key < args.keys ? int32_t((key * H + 4 * chunk_k) * 4) : kOutOfRange;
+            dma16(k_rsrc, ks + 64 * instr, k_off);
+            if (with_v) {
+                const int32_t v_off = key < args.keys ? int32_t((key * H + 4 * slot) * 4) : kOutOfRange;
+                dma16(v_rsrc, vs + 64 * instr, v_off);
+            }
+        }
+    };
+
+    // S^T for 32 keys (rows sub * 32 .. +31 of the stage) against this wave's queries.
+    auto scores = [&](auto stage, int sub) __attribute__((always_inline)) {
+        const f32x4* ks = k_of(stage);
+        f32x16 acc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+        const int row = 32 * sub + col;
+        const int swz = row & G::SWIZZLE;
+#pragma unroll
+        for (int c = 0; c < G::CHUNKS; ++c) {
+            const int g = 4 * c + 2 * half;  // chunk of h = 16c + 8 half
+            const f32x4 lo = ks[row * G::SLOTS + (g ^ swz)];
+            const f32x4 hi = ks[row * G::SLOTS + ((g + 1) ^ swz)];
+            const float kv[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+            for (int s = 0; s < 8; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[s], qreg[c][s], acc, 0, 0, 0);
+        }
+        return acc;
+    };
+    // Key of accumulator register r of this lane, within the 32-key sub-block.
+    auto key_of = [&](int r) __attribute__((always_inline)) { return 4 * half + 8 * (r / 4) + (r % 4); };
+
+    // Online softmax state of this lane's query, and O^T (rows h, column q).
+    float m = -INFINITY, l = 0.f;
+    f32x16 o[G::OBLOCKS];
+#pragma unroll
+    for (int b = 0; b < G::OBLOCKS; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[b][r] = 0.f;
+
+    // Online softmax of one 32-key block (scores acc, keys sub0 ..) and its
+    // O^T += V^T P^T.
+    auto softmax_and_mix = [&](auto stage, int sub, const f32x16& acc, int64_t sub0) __attribute__((always_inline)) {
+        float x[16];
+        float block_max = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t key = sub0 + key_of(r);
+            const bool visible = key < args.keys && key <= q + args.query_offset;
+            x[r] = visible ? acc[r] * args.scale : -INFINITY;
+            block_max = fmaxf(block_max, x[r]);
+        }
+        block_max = fmaxf(block_max, __shfl_xor(block_max, 32));
+        const float m_new = fmaxf(m, block_max);
+        const float alpha = expf(m - m_new);
+        float p[16];
+        float sum = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float shifted = x[r] - m_new;
+            p[r] = x[r] == -INFINITY ? 0.f : expf(shifted);
+            sum = sum + p[r];
+        }
+        sum = sum + __shfl_xor(sum, 32);
+        l = l * alpha + sum;
+        m = m_new;
+        const float* vs = reinterpret_cast<const float*>(v_of(stage));
+#pragma unroll
+        for (int b = 0; b < G::OBLOCKS; ++b) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[b][r] = o[b][r] * alpha;
+            // O^T rows 32 b .. +31 += V^T (rows h) P^T: MFMA t pairs keys key_of(t) of the two
+            // lane halves; lane l supplies V[key_of(t)][32 b + col].
+            const float* vrow = vs + (32 * sub) * H + 32 * b + col;
+#pragma unroll
+            for (int t = 0; t < 16; ++t)
+                o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[key_of(t) * H], p[t], o[b], 0, 0, 0);
+        }
+    };
+    // Both 32-key blocks of a stage (their scores first, so that the second
+    // block's matrix work can overlap the first block's exponentials).
+    auto compute = [&](auto stage, int64_t key0) __attribute__((always_inline)) {
+        if (key0 + 32 < wave_keys) {  // wave-uniform: both blocks
+            const f32x16 s0 = scores(stage, 0);
+            const f32x16 s1 = scores(stage, 1);
+            softmax_and_mix(stage, 0, s0, key0);
+            softmax_and_mix(stage, 1, s1, key0 + 32);
+        } else if (key0 < wave_keys) {
+            const f32x16 s0 = scores(stage, 0);
+            softmax_and_mix(stage, 0, s0, key0);
+        }
+    };
+    // The stage loop runs from barrier to barrier with both stages loading
+    // at the top of every iteration (loads past the last key read zeros), so
+    // the loads in flight are the same on every pass and each stage is
+    // waited for by count: a stage's loads are done when only the other
+    // stage's are still in flight.
+    constexpr int kStageLoads = 2 * G::LOADS;
+    issue(I0{}, 0, true);
+    issue(I1{}, kKeys, true);
+    for (int st = 0; st < stages_total; st += 2) {
+        const int64_t key0 = int64_t(st) * kKeys;
+        wait_loads<kStageLoads>();
+        lds_barrier();
+        compute(I0{}, key0);
+        lds_barrier();
+        issue(I0{}, key0 + 2 * kKeys, true);
+        wait_loads<kStageLoads>();
+        lds_barrier();
+        if (st + 1 < stages_total) compute(I1{}, key0 + kKeys);
+        lds_barrier();
+        issue(I1{}, key0 + 3 * kKeys, true);
+    }
+    wait_loads<0>();  // the loads past the end land before the stages are reused
+
+    // O = O^T / l: lane l holds h rows 32 b + 4 half + 8 (r / 4) + (r % 4) of its query.
+    if (q < args.queries) {
+        float* orow = args.o + (head * args.queries + q) * H;
+#pragma unroll
+        for (int b = 0; b < G::OBLOCKS; ++b)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                f32x4 out;
+#pragma unroll
+                for (int s = 0; s < 4; ++s) out[s] = o[b][4 * g + s] / l;
+                *reinterpret_cast<f32x4*>(orow + 32 * b + 4 * half + 8 * g) = out;
+            }
+    }
+    if (args.p == nullptr) return;
+
+    // Probabilities: a second pass over K with the final m and l; 0 past the diagonal.
+    float* prow = args.p + (head * args.queries + q) * args.keys;
+    const bool row_ok = q < args.queries;
+    const bool vector_rows = (args.keys & 3) == 0;
+    auto probabilities_of = [&](auto stage, int64_t key0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) {
+            const int64_t sub0 = key0 + 32 * sub;
+            if (sub0 >= args.keys) continue;
+            f32x16 acc;
+            if (sub0 < wave_keys) {
+                acc = scores(stage, sub);
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+            }
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                float pv[4];
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const int64_t key = sub0 + key_of(4 * g + s);
+                    const bool visible = key <= q + args.query_offset;
+                    const float shifted = acc[4 * g + s] * args.scale - m;
+                    pv[s] = visible ? expf(shifted) / l : 0.f;
+                }
+                const int64_t key = sub0 + 4 * half + 8 * g;
+                if (row_ok) {
+                    if (vector_rows && key + 4 <= args.keys) {
+                        *reinterpret_cast<f32x4*>(prow + key) = f32x4{pv[0], pv[1], pv[2], pv[3]};
+                    } else {
+#pragma unroll
+                        for (int s = 0; s < 4; ++s)
+                            if (key + s < args.keys) prow[key + s] = pv[s];
+                    }
+                }
+            }
+        }
+    };
+    // The same stage loop over K alone. The probability stores are vector
+    // memory operations too: each wait also covers the stores issued since,
+    // which only makes it wait longer, never too little.
+    issue(I0{}, 0, false);
+    issue(I1{}, kKeys, false);
+    for (int st = 0; st < stages_total; st += 2) {
+        const int64_t key0 = int64_t(st) * kKeys;
+        wait_loads<G::LOADS>();
+        lds_barrier();
+        probabilities_of(I0{}, key0);
+        lds_barrier();
+        issue(I0{}, key0 + 2 * kKeys, false);
+        wait_loads<G::LOADS>();
+        lds_barrier();
+        if (st + 1 < stages_total) probabilities_of(I1{}, key0 + kKeys);
+        lds_barrier();
+        issue(I1{}, key0 + 3 * kKeys, false);
+    }
+    wait_loads<0>();
+    // Keys past every query of the workgroup: zeros, each row filled by the
+    // whole workgroup with contiguous stores.
+    const int64_t zero_from = int64_t(stages_total) * kKeys;
+    if (zero_from < args.keys) {
+        const int64_t rows = min(int64_t(kQueries), args.queries - q_first);
+        for (int64_t r = 0; r < rows; ++r) {
+            float* zrow = args.p + (head * args.queries + q_first + r) * args.keys;
+            if (vector_rows) {
+                for (int64_t e = zero_from + 4 * tid; e < args.keys; e += 4 * 64 * kWaves)
+                    *reinterpret_cast<f32x4*>(zrow + e) = f32x4{0.f, 0.f, 0.f, 0.f};
+            } else {
+                for (int64_t e = zero_from + tid; e < args.keys; e += 64 * kWaves) zrow[e] = 0.f;
+            }
+        }
+    }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+hipError_t launch_causal_attention(const CausalAttentionArgs& a, hipStream_t stream) {
+    if (a.heads == 0 || a.queries == 0) return hipSuccess;
+    AttentionArgs args;
+    args.q = a.q;
+    args.k = a.k;
+    args.v = a.v;
+    args.o = a.o;
+    args.p = a.p;
+    args.queries = a.queries;
+    args.keys = a.keys;
+    args.q_stride = a.q_stride;
+    args.kv_stride = a.kv_stride;
+    args.query_offset = a.query_offset;
+    args.heads = a.heads;
+    args.query_blocks = int32_t((a.queries + kQueries - 1) / kQueries);
+    args.scale = a.scale;
+    const dim3 grid(unsigned(a.heads * args.query_blocks));
+    switch (a.head_dim) {
+        case 32: hipLaunchKernelGGL(causal_attention_kernel<32>, grid, dim3(64 * kWaves), 0, stream, args); break;
+        case 64: hipLaunchKernelGGL(causal_attention_kernel<64>, grid, dim3(64 * kWaves), 0, stream, args); break;
+        case 128: hipLaunchKernelGGL(causal_attention_kernel<128>, grid, dim3(64 * kWaves), 0, stream, args); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+bool causal_attention_supported(const CausalAttentionArgs& a) {
+    const bool dims = a.head_dim == 32 || a.head_dim == 64 || a.head_dim == 128;
+    const bool aligned = aligned16(a.q) && aligned16(a.k) && aligned16(a.v) && aligned16(a.o) &&
+                         (a.p == nullptr || aligned16(a.p)) && a.q_stride % 4 == 0 && a.kv_stride % 4 == 0;
+    // Per-head buffer offsets (keys x h floats) within 31 bits; the grid within 32 bits.
+    const bool offsets = a.keys * a.head_dim * 4 < (int64_t(1) << 31) - 4096;
+    const int64_t query_blocks = (a.queries + kQueries - 1) / kQueries;
+    const bool grid = a.heads * query_blocks < (int64_t(1) << 31);
+    return dims && aligned && offsets && grid;
+}
+
+}  // namespace sn

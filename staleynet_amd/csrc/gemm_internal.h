@@ -51,6 +51,27 @@ hipError_t launch_gemm_simple(const Problem& p, hipStream_t stream);
 hipError_t launch_gemv(const Problem& p, const Env& env, hipStream_t stream);
 bool gemv_applies(const Problem& p, const Env& env);
 
+// Fused causal attention forward (attention.hip): O = causal_softmax(scale *
+// Q K^T) V per head, and optionally the probabilities P. Q [heads][queries]
+// [head_dim] rows q_stride floats apart per head, K and V [heads][keys]
+// [head_dim] kv_stride apart; O [heads][queries][head_dim] and P [heads]
+// [queries][keys] dense. Query q sees keys 0 ..= q + query_offset.
+struct CausalAttentionArgs {
+    const float* q = nullptr;
+    const float* k = nullptr;
+    const float* v = nullptr;
+    float* o = nullptr;
+    float* p = nullptr;
+    int64_t heads = 0, queries = 0, keys = 0, head_dim = 0;
+    int64_t q_stride = 0, kv_stride = 0;
+    int64_t query_offset = 0;
+    float scale = 1.f;
+};
+hipError_t launch_causal_attention(const CausalAttentionArgs& args, hipStream_t stream);
+// Head dims 32, 64, 128; 16-byte aligned pointers and strides; per-head
+// offsets within 31 bits.
+bool causal_attention_supported(const CausalAttentionArgs& args);
+
 // Rounds an fp32 operand to bf16 (nearest-even) into dst[batch][rows][kp],
 // K-contiguous, zeros for k in [k, kp) (bf16_stage.hip). Element (r, k) of
 // the source is src[r * ld + k] when k_contiguous, else src[k * ld + r];

@@ -205,6 +205,12 @@ class CCrossEntropyHead(ctypes.Structure):
                 ("grad_scale", ctypes.c_float)]
 
 
+class CAttentionShape(ctypes.Structure):
+    _fields_ = [("heads", ctypes.c_size_t), ("queries", ctypes.c_size_t), ("keys", ctypes.c_size_t),
+                ("head_dim", ctypes.c_size_t), ("q_stride", ctypes.c_size_t), ("kv_stride", ctypes.c_size_t),
+                ("query_offset", ctypes.c_size_t), ("scale", ctypes.c_float)]
+
+
 @dataclass(frozen=True)
 class HeadLayout:
     """``HeadLayout`` (crates/staleynet-cuda/src/kernels/attention.rs:19-75)."""
@@ -320,6 +326,9 @@ def _library() -> ctypes.CDLL:
         lib.sn_matmul_bias.argtypes = [ctx, ctypes.POINTER(CMatmulSpec), ctypes.c_void_p, size, ctypes.c_void_p,
                                        size, ctypes.c_void_p, size, ctypes.c_void_p, size]
         lib.sn_causal_softmax.argtypes = [ctx, ctypes.c_void_p, size, size, size, ctypes.c_float, size]
+        lib.sn_causal_attention.argtypes = [ctx, ctypes.POINTER(CAttentionShape), ctypes.c_void_p, size,
+                                            ctypes.c_void_p, size, ctypes.c_void_p, size, ctypes.c_void_p, size,
+                                            ctypes.c_void_p, size]
         lib.sn_cross_entropy.argtypes = [ctx, ctypes.c_void_p, size, size, ctypes.c_void_p, size,
                                          ctypes.POINTER(CCrossEntropyHead), ctypes.c_void_p, size, ctypes.c_void_p,
                                          size, size]
@@ -552,6 +561,26 @@ class Gpu:
         if rc == SN_ERR_SHAPE:
             raise AssertionError("causal_softmax: rows must be a multiple of queries")
         self._check(rc, "causal_softmax")
+
+    def causal_attention(self, q: Tensor, k: Tensor, v: Tensor, out: Tensor, heads: int, queries: int, keys: int,
+                         head_dim: int, scale: float, query_offset: int = 0, q_stride: int | None = None,
+                         kv_stride: int | None = None, probabilities: Tensor | None = None) -> None:
+        """Fused causal attention forward (``sn_causal_attention``): ``out`` = O of the three calls of
+        CausalSelfAttention::forward (layers/attention.rs:206-213) — scores, ``causal_softmax``, mix —
+        and, when given, ``probabilities`` = the softmax they leave. Strides default to dense heads."""
+        shape = CAttentionShape(heads, queries, keys, head_dim,
+                                queries * head_dim if q_stride is None else q_stride,
+                                keys * head_dim if kv_stride is None else kv_stride, query_offset, scale)
+        p_pointer, p_len = (None, 0) if probabilities is None else (probabilities.pointer, len(probabilities))
+        rc = _library().sn_causal_attention(self._ctx, ctypes.byref(shape), ctypes.c_void_p(q.pointer), len(q),
+                                            ctypes.c_void_p(k.pointer), len(k), ctypes.c_void_p(v.pointer), len(v),
+                                            ctypes.c_void_p(out.pointer), len(out), ctypes.c_void_p(p_pointer),
+                                            p_len)
+        if rc == SN_ERR_SHAPE:
+            raise AssertionError("causal_attention: no keys")
+        if rc == SN_ERR_LENGTH_MISMATCH:
+            raise AssertionError("causal_attention: a buffer is too small for the shape")
+        self._check(rc, "causal_attention")
 
     def softmax_backward(self, probabilities: Tensor, grad: Tensor) -> None:
         """``Gpu::softmax_backward`` (ops/attention.rs:76-92), in place on ``grad``."""

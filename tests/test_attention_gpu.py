@@ -1,0 +1,117 @@
+"""GPU parity of the fused causal attention forward (``sn_causal_attention``) against the oracle's
+restatement of the three calls it replaces in CausalSelfAttention::forward
+(crates/staleynet-model/src/layers/attention.rs:206-213): the scores product
+(``MatmulSpec::new(T, keys, h).right_transposed()`` batched over the heads, reference.rs:19-38),
+``causal_softmax`` (reference.rs:100-119) and the mix product (``MatmulSpec::new(T, h, keys)``).
+O and the probabilities are compared at the reference's fp32 tolerance. Cases: ragged query
+blocks and key counts, query offsets (a cached prefix), one-query decode against a partly written
+cache, head dims 32 / 64 / 128, K and V shared by every head, config 3's size, determinism, and the
+entry point's checks.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle
+from staleynet_amd.gemm import Shape
+
+pytestmark = pytest.mark.gpu
+
+TOLERANCE = 1e-5  # kernels_match_reference.rs:12
+
+
+def reference(q, k, v, heads, queries, keys, h, scale, offset, q_stride, kv_stride):
+    scores = np.zeros(heads * queries * keys, np.float32)
+    oracle.matmul_parallel(oracle.Product(queries, keys, h, False, True, heads, q_stride, kv_stride, queries * keys,
+                                          1.0, False), q, k, scores)
+    oracle.causal_softmax(scores, queries, keys, scale, offset)
+    out = np.zeros(heads * queries * h, np.float32)
+    oracle.matmul_parallel(oracle.Product(queries, h, keys, False, False, heads, queries * keys, kv_stride,
+                                          queries * h, 1.0, False), scores, v, out)
+    return out, scores
+
+
+def run(gpu, heads, queries, keys, h, scale, offset, q_stride=None, kv_stride=None, seed=0, with_p=True):
+    q_stride = queries * h if q_stride is None else q_stride
+    kv_stride = keys * h if kv_stride is None else kv_stride
+    q_len = (heads - 1) * q_stride + queries * h
+    kv_len = (heads - 1) * kv_stride + keys * h
+    rng = np.random.default_rng(seed)
+    q = rng.normal(0, 1, q_len).astype(np.float32)
+    k = rng.normal(0, 1, kv_len).astype(np.float32)
+    v = rng.normal(0, 1, kv_len).astype(np.float32)
+    Q, K, V = (gpu.upload(Shape.vector(len(x)), x) for x in (q, k, v))
+    out = gpu.upload(Shape.vector(heads * queries * h), np.full(heads * queries * h, np.nan, np.float32))
+    probabilities = None
+    if with_p:
+        probabilities = gpu.upload(Shape.vector(heads * queries * keys),
+                                   np.full(heads * queries * keys, np.nan, np.float32))
+    gpu.causal_attention(Q, K, V, out, heads, queries, keys, h, scale, offset, q_stride, kv_stride, probabilities)
+    expected_o, expected_p = reference(q, k, v, heads, queries, keys, h, scale, offset, q_stride, kv_stride)
+    got_p = gpu.download(probabilities) if with_p else None
+    return expected_o, gpu.download(out), expected_p, got_p
+
+
+@pytest.mark.parametrize("heads,queries,keys,h,offset,scale", [
+    (2, 128, 128, 64, 0, 0.125),     # one query block, square causal
+    (3, 200, 200, 64, 0, 0.125),     # a ragged second query block, keys not a multiple of 64
+    (2, 100, 300, 64, 200, 0.125),   # a cached prefix: offset 200, more keys than queries
+    (2, 96, 96, 32, 0, 0.17),        # head dim 32 (config 0)
+    (1, 64, 130, 128, 66, 0.09),     # head dim 128
+    (2, 37, 37, 64, 0, 1.0),         # fewer queries than a wave's block
+    (1, 300, 260, 64, 0, 0.125),     # keys run out before the diagonal
+])
+def test_fused_attention_matches_the_three_calls(gpu, heads, queries, keys, h, offset, scale):
+    eo, go, ep, gp = run(gpu, heads, queries, keys, h, scale, offset, seed=queries + keys + h)
+    assert np.all(np.isfinite(go)) and np.all(np.isfinite(gp))
+    assert oracle.relative_error(eo, go) < TOLERANCE
+    assert oracle.relative_error(ep, gp) < TOLERANCE
+    # Keys past each query's horizon are exactly 0, as causal_softmax leaves them.
+    p = gp.reshape(heads, queries, keys)
+    for r in range(queries):
+        visible = min(r + offset + 1, keys)
+        assert not np.any(p[:, r, visible:])
+
+
+def test_decode_query_against_a_partly_written_cache(gpu):
+    # attention.rs:274-320: one new position per head against a 1408-step cache holding 701.
+    heads, capacity, h = 12, 1408, 64
+    eo, go, ep, gp = run(gpu, heads, 1, capacity, h, 0.125, 700, q_stride=h, kv_stride=capacity * h, seed=3)
+    assert oracle.relative_error(eo, go) < TOLERANCE
+    assert oracle.relative_error(ep, gp) < TOLERANCE
+
+
+def test_keys_and_values_shared_by_every_head(gpu):
+    eo, go, ep, gp = run(gpu, 3, 64, 64, 64, 0.125, 0, kv_stride=0, seed=4)
+    assert oracle.relative_error(eo, go) < TOLERANCE
+    assert oracle.relative_error(ep, gp) < TOLERANCE
+
+
+def test_without_probabilities_the_output_is_the_same(gpu):
+    eo, go, _, _ = run(gpu, 2, 256, 256, 64, 0.125, 0, seed=5, with_p=False)
+    assert oracle.relative_error(eo, go) < TOLERANCE
+
+
+def test_config_3_heads_at_full_size_and_determinism(gpu):
+    # Two of config 3's 192 heads: T = 2048, h = 64, scale 1/8, Q, K, V ~ N(0, 1).
+    heads, t, h = 2, 2048, 64
+    eo, go, ep, gp = run(gpu, heads, t, t, h, 0.125, 0, seed=6)
+    assert oracle.relative_error(eo, go) < TOLERANCE
+    assert oracle.relative_error(ep, gp) < TOLERANCE
+    _, go2, _, gp2 = run(gpu, heads, t, t, h, 0.125, 0, seed=6)
+    assert np.array_equal(go, go2) and np.array_equal(gp, gp2)
+
+
+def test_entry_point_checks(gpu):
+    from staleynet_amd.gemm import GpuError
+    q, k, v = (gpu.zeros(Shape.vector(2 * 64 * 64)) for _ in range(3))
+    out = gpu.zeros(Shape.vector(2 * 64 * 64))
+    with pytest.raises(AssertionError, match="no keys"):
+        gpu.causal_attention(q, k, v, out, 2, 64, 0, 64, 1.0)
+    with pytest.raises(AssertionError, match="too small"):
+        gpu.causal_attention(q, k, v, out, 2, 64, 65, 64, 1.0)
+    with pytest.raises(AssertionError, match="too small"):
+        gpu.causal_attention(q, k, v, out, 2, 64, 64, 64, 1.0, probabilities=gpu.zeros(Shape.vector(100)))
+    with pytest.raises(GpuError):  # head dim 48: unsupported
+        gpu.causal_attention(q, k, v, out, 2, 64, 64, 48, 1.0)
+    with pytest.raises(GpuError):  # the output overlapping an input
+        gpu.causal_attention(q, k, v, q, 2, 64, 64, 64, 1.0)
