@@ -12,6 +12,13 @@
 //   Gpu::matmul_bias (matmul + add_row_bias fused; no reference counterpart: the two calls of
 //                     Linear::forward, crates/staleynet-model/src/layers/linear.rs:46-47)
 //   Shape, Tensor                                  crates/staleynet-cuda/src/device.rs:210-275
+//   TokenBuffer, Gpu::upload_tokens                crates/staleynet-cuda/src/device.rs:35-36, :194-197
+//   Gpu::causal_softmax, Gpu::softmax_backward     crates/staleynet-cuda/src/ops/attention.rs:54-92
+//   HeadLayout, Gpu::split_heads / merge_heads     crates/staleynet-cuda/src/kernels/attention.rs:19-75,
+//                                                  crates/staleynet-cuda/src/ops/attention.rs:10-52
+//   CrossEntropyHead, Gpu::cross_entropy           crates/staleynet-cuda/src/ops/loss.rs:14-71
+//   Gpu::causal_attention (scores, causal_softmax and mix in one launch; no reference counterpart:
+//                     the three calls of crates/staleynet-model/src/layers/attention.rs:206-213)
 // The reference panics on undersized operands; here that is a thrown
 // staleynet_cuda::Panic carrying the same message. Driver errors (the
 // reference's Err(DriverError)) are thrown as staleynet_cuda::GpuError.
@@ -19,6 +26,7 @@
 #pragma once
 
 #include <cstddef>
+#include <cstdint>
 #include <stdexcept>
 #include <string>
 #include <utility>
@@ -193,6 +201,66 @@ class Tensor {
     Shape shape_{0, 0};
 };
 
+// Token ids (u32) in device memory; owns its buffer (move-only).
+class TokenBuffer {
+   public:
+    TokenBuffer() = default;
+    TokenBuffer(sn_context* context, uint32_t* buffer, size_t count) : context_(context), buffer_(buffer), count_(count) {}
+    TokenBuffer(const TokenBuffer&) = delete;
+    TokenBuffer& operator=(const TokenBuffer&) = delete;
+    TokenBuffer(TokenBuffer&& other) noexcept { *this = std::move(other); }
+    TokenBuffer& operator=(TokenBuffer&& other) noexcept {
+        if (this != &other) {
+            release();
+            context_ = std::exchange(other.context_, nullptr);
+            buffer_ = std::exchange(other.buffer_, nullptr);
+            count_ = std::exchange(other.count_, 0);
+        }
+        return *this;
+    }
+    ~TokenBuffer() { release(); }
+
+    size_t len() const { return count_; }
+    const uint32_t* data() const { return buffer_; }
+
+   private:
+    void release() {
+        if (buffer_ != nullptr) sn_free_tokens(context_, buffer_);
+        buffer_ = nullptr;
+    }
+    sn_context* context_ = nullptr;
+    uint32_t* buffer_ = nullptr;
+    size_t count_ = 0;
+};
+
+// Where a group of attention heads sits in the packed activations and in the
+// head-major tensor (HeadLayout, kernels/attention.rs:19-75).
+struct HeadLayout {
+    size_t batch, time, heads, head_dim, width, column_offset, time_capacity, time_offset;
+
+    static HeadLayout dense(size_t batch, size_t time, size_t heads, size_t head_dim, size_t width,
+                            size_t column_offset) {
+        return HeadLayout{batch, time, heads, head_dim, width, column_offset, time, 0};
+    }
+    HeadLayout in_cache(size_t capacity, size_t offset) const {
+        HeadLayout l = *this;
+        l.time_capacity = capacity;
+        l.time_offset = offset;
+        return l;
+    }
+    size_t element_count() const { return batch * heads * time * head_dim; }
+    sn_head_layout to_ffi() const {
+        return sn_head_layout{batch, time, heads, head_dim, width, column_offset, time_capacity, time_offset};
+    }
+};
+
+// Which columns of a logits row and which target of a target row one
+// classifier owns (CrossEntropyHead, ops/loss.rs:14-30).
+struct CrossEntropyHead {
+    size_t column_offset, classes, target_stride, target_offset;
+    float grad_scale;
+};
+
 // One device, one stream, and the kernel choice (device.rs:129-155).
 class Gpu {
    public:
@@ -274,9 +342,88 @@ class Gpu {
                              bias.len(), output.data(), output.len()));
     }
 
+    TokenBuffer upload_tokens(const std::vector<uint32_t>& tokens) const {
+        uint32_t* buffer = nullptr;
+        check(sn_upload_tokens(context_, tokens.data(), tokens.size(), &buffer));
+        return TokenBuffer(context_, buffer, tokens.size());
+    }
+
+    std::vector<uint32_t> download_tokens(const TokenBuffer& tokens) const {
+        std::vector<uint32_t> host(tokens.len());
+        check(sn_download_tokens(context_, tokens.data(), host.size(), host.data()));
+        return host;
+    }
+
+    // `Gpu::causal_softmax`: in place on [matrices · queries, keys] scores.
+    void causal_softmax(Tensor& scores, size_t queries, float scale, size_t query_offset) const {
+        const int rc = sn_causal_softmax(context_, scores.data(), scores.shape().rows, scores.shape().cols, queries,
+                                         scale, query_offset);
+        if (rc == SN_ERR_SHAPE) throw Panic(rc, "causal_softmax: rows must be a multiple of queries");
+        check(rc);
+    }
+
+    // `Gpu::softmax_backward`: grad <- p * (grad - sum(grad * p)) per row.
+    void softmax_backward(const Tensor& probabilities, Tensor& grad) const {
+        const int rc = sn_softmax_backward(context_, probabilities.data(), probabilities.shape().rows,
+                                           probabilities.shape().cols, grad.data(), grad.shape().rows,
+                                           grad.shape().cols);
+        if (rc == SN_ERR_SHAPE) throw Panic(rc, "softmax_backward: shape mismatch");
+        check(rc);
+    }
+
+    // `Gpu::split_heads`: packed columns -> head-major tensor.
+    void split_heads(const Tensor& packed, Tensor& head_major, const HeadLayout& layout) const {
+        check_layout(layout, packed, head_major);
+        const sn_head_layout l = layout.to_ffi();
+        check(sn_split_heads(context_, packed.data(), packed.len(), head_major.data(), head_major.len(), &l));
+    }
+
+    // `Gpu::merge_heads`: head-major tensor -> packed columns (the others left alone).
+    void merge_heads(const Tensor& head_major, Tensor& packed, const HeadLayout& layout) const {
+        check_layout(layout, packed, head_major);
+        const sn_head_layout l = layout.to_ffi();
+        check(sn_merge_heads(context_, head_major.data(), head_major.len(), packed.data(), packed.len(), &l));
+    }
+
+    // `Gpu::cross_entropy`: one codebook's losses and its columns of the gradient.
+    void cross_entropy(const Tensor& logits, const TokenBuffer& targets, const CrossEntropyHead& head, Tensor& losses,
+                       Tensor& logits_grad) const {
+        const Shape shape = logits.shape();
+        if (logits_grad.shape().rows != shape.rows || logits_grad.shape().cols != shape.cols)
+            throw Panic(SN_ERR_SHAPE, "cross_entropy: gradient shape");
+        if (head.column_offset + head.classes > shape.cols) throw Panic(SN_ERR_SHAPE, "cross_entropy: head exceeds logits");
+        if (losses.len() < shape.rows) throw Panic(SN_ERR_LENGTH_MISMATCH, "cross_entropy: losses too small");
+        if (targets.len() < shape.rows * head.target_stride)
+            throw Panic(SN_ERR_LENGTH_MISMATCH, "cross_entropy: too few targets");
+        const sn_cross_entropy_head h{head.column_offset, head.classes, head.target_stride, head.target_offset,
+                                      head.grad_scale};
+        check(sn_cross_entropy(context_, logits.data(), shape.rows, shape.cols, targets.data(), targets.len(), &h,
+                               losses.data(), losses.len(), logits_grad.data(), logits_grad.shape().rows,
+                               logits_grad.shape().cols));
+    }
+
+    // The scores product, causal_softmax and the mix product in one launch
+    // (sn_causal_attention); `probabilities` may be null.
+    void causal_attention(const Tensor& q, const Tensor& k, const Tensor& v, Tensor& out, const sn_attention_shape& shape,
+                          Tensor* probabilities = nullptr) const {
+        check(sn_causal_attention(context_, &shape, q.data(), q.len(), k.data(), k.len(), v.data(), v.len(),
+                                  out.data(), out.len(), probabilities ? probabilities->data() : nullptr,
+                                  probabilities ? probabilities->len() : 0));
+    }
+
     sn_context* raw() const { return context_; }
 
    private:
+    // check_layout (ops/attention.rs:11-18).
+    static void check_layout(const HeadLayout& layout, const Tensor& packed, const Tensor& head_major) {
+        if (layout.time_offset + layout.time > layout.time_capacity)
+            throw Panic(SN_ERR_SHAPE, "HeadLayout: time range exceeds capacity");
+        if (packed.len() < layout.batch * layout.time * layout.width)
+            throw Panic(SN_ERR_LENGTH_MISMATCH, "HeadLayout: packed tensor too small");
+        if (head_major.len() < layout.batch * layout.heads * layout.time_capacity * layout.head_dim)
+            throw Panic(SN_ERR_LENGTH_MISMATCH, "HeadLayout: head-major tensor too small");
+    }
+
     explicit Gpu(sn_context* context) : context_(context) {}
     sn_context* context_ = nullptr;
 };

@@ -23,6 +23,14 @@ void oracle_random_values(size_t count, uint64_t seed, float* out);
 float oracle_relative_error(const float* expected, const float* actual, size_t n);
 void oracle_add_row_bias(float* output, size_t rows, size_t cols, const float* bias);
 void oracle_accumulate_column_sums(const float* input, size_t rows, size_t cols, float* sums, float* scratch);
+void oracle_causal_softmax(float* scores, size_t total_rows, size_t queries, size_t keys, float scale,
+                           size_t query_offset);
+void oracle_softmax_backward(const float* probabilities, float* grad, size_t rows, size_t cols);
+void oracle_cross_entropy(const float* logits, const uint32_t* targets, size_t rows, size_t cols, size_t column_offset,
+                          size_t classes, size_t target_stride, size_t target_offset, float grad_scale, float* losses,
+                          float* grad);
+void oracle_split_heads(const float* packed, float* head_major, const size_t* layout);
+void oracle_merge_heads(const float* head_major, float* packed, const size_t* layout);
 }
 
 using namespace staleynet_cuda;
@@ -158,6 +166,111 @@ int main() {
             ++failures;
             std::printf("FAIL short bias did not panic\n");
         }
+    }
+
+    auto expect = [&](bool ok, const char* what) {
+        ++cases;
+        if (!ok) {
+            ++failures;
+            std::printf("FAIL %s\n", what);
+        }
+    };
+
+    // `causal_softmax_and_backward_match_reference` (kernels_match_reference.rs:172-195):
+    // 3 matrices of 5 queries x 70 keys, query offset 40, scale 0.5, LCG seeds 10 and 11.
+    {
+        const size_t matrices = 3, queries = 5, keys = 70, rows = matrices * queries;
+        const std::vector<float> scores = random_values(rows * keys, 10);
+        const std::vector<float> upstream = random_values(rows * keys, 11);
+        std::vector<float> probabilities = scores, grad = upstream;
+        oracle_causal_softmax(probabilities.data(), rows, queries, keys, 0.5f, 40);
+        oracle_softmax_backward(probabilities.data(), grad.data(), rows, keys);
+        Tensor p = gpu.upload(Shape::new_(rows, keys), scores);
+        gpu.causal_softmax(p, queries, 0.5f, 40);
+        Tensor g = gpu.upload(Shape::new_(rows, keys), upstream);
+        gpu.softmax_backward(p, g);
+        expect(relative_error(probabilities, gpu.download(p)) < tolerance(MatmulKernel::Blocked), "causal_softmax");
+        expect(relative_error(grad, gpu.download(g)) < tolerance(MatmulKernel::Blocked), "softmax_backward");
+        bool shape_panic = false;
+        try {
+            Tensor bad = gpu.zeros(Shape::new_(10, 8));
+            gpu.causal_softmax(bad, 3, 1.0f, 0);
+        } catch (const Panic& panic) {
+            shape_panic = std::string(panic.what()) == "causal_softmax: rows must be a multiple of queries";
+        }
+        expect(shape_panic, "causal_softmax shape panic");
+    }
+
+    // `split_and_merge_heads_follow_the_layout_formula` (kernels_match_reference.rs:199-231):
+    // dense(2, 5, 3, 4, 3 * 12 + 2, 13).in_cache(9, 2), LCG seed 12; bit-exact.
+    {
+        const HeadLayout layout = HeadLayout::dense(2, 5, 3, 4, 3 * 12 + 2, 13).in_cache(9, 2);
+        const std::vector<float> packed = random_values(layout.batch * layout.time * layout.width, 12);
+        const sn_head_layout l = layout.to_ffi();
+        const size_t fields[8] = {l.batch, l.time, l.heads, l.head_dim, l.width, l.column_offset, l.time_capacity,
+                                  l.time_offset};
+        std::vector<float> head_major(layout.batch * layout.heads * layout.time_capacity * layout.head_dim, 0.f);
+        oracle_split_heads(packed.data(), head_major.data(), fields);
+        std::vector<float> merged(packed.size(), 0.f);
+        oracle_merge_heads(head_major.data(), merged.data(), fields);
+        const Tensor packed_tensor = gpu.upload(Shape::new_(layout.batch * layout.time, layout.width), packed);
+        Tensor head_tensor = gpu.zeros(Shape::new_(layout.batch * layout.heads * layout.time_capacity, layout.head_dim));
+        gpu.split_heads(packed_tensor, head_tensor, layout);
+        expect(gpu.download(head_tensor) == head_major, "split_heads");
+        Tensor merged_tensor = gpu.zeros(packed_tensor.shape());
+        gpu.merge_heads(head_tensor, merged_tensor, layout);
+        expect(gpu.download(merged_tensor) == merged, "merge_heads");
+        bool range_panic = false;
+        try {
+            gpu.split_heads(packed_tensor, head_tensor, layout.in_cache(9, 5));
+        } catch (const Panic& panic) {
+            range_panic = std::string(panic.what()) == "HeadLayout: time range exceeds capacity";
+        }
+        expect(range_panic, "HeadLayout range panic");
+    }
+
+    // `cross_entropy_matches_reference` (kernels_match_reference.rs:277-298): 13 x 50 logits
+    // (LCG seed 15), the head at columns 10 .. 47 with 2 targets per row (slot 1), every 7th
+    // target empty, gradient scale 0.25.
+    {
+        const size_t rows = 13, cols = 50;
+        const CrossEntropyHead head{10, 37, 2, 1, 0.25f};
+        const std::vector<float> logits = random_values(rows * cols, 15);
+        std::vector<uint32_t> targets(rows * 2);
+        for (size_t i = 0; i < targets.size(); ++i) targets[i] = i % 7 == 0 ? SN_EMPTY_TOKEN : uint32_t(i * 5 % 37);
+        std::vector<float> losses(rows, 0.f), grad(rows * cols, 0.f);
+        oracle_cross_entropy(logits.data(), targets.data(), rows, cols, head.column_offset, head.classes,
+                             head.target_stride, head.target_offset, head.grad_scale, losses.data(), grad.data());
+        const Tensor logit_tensor = gpu.upload(Shape::new_(rows, cols), logits);
+        const TokenBuffer target_buffer = gpu.upload_tokens(targets);
+        Tensor loss_tensor = gpu.zeros(Shape::vector(rows));
+        Tensor grad_tensor = gpu.zeros(Shape::new_(rows, cols));
+        gpu.cross_entropy(logit_tensor, target_buffer, head, loss_tensor, grad_tensor);
+        expect(relative_error(losses, gpu.download(loss_tensor)) < tolerance(MatmulKernel::Blocked), "cross_entropy losses");
+        expect(relative_error(grad, gpu.download(grad_tensor)) < tolerance(MatmulKernel::Blocked), "cross_entropy grad");
+        expect(gpu.download_tokens(target_buffer) == targets, "token round trip");
+    }
+
+    // The fused attention forward against the reference's three calls (scores product,
+    // causal_softmax, mix product; layers/attention.rs:206-213): 2 heads x 70 queries x 70
+    // keys x 64, scale 0.125, LCG seeds 20-22.
+    {
+        const size_t heads = 2, t = 70, h = 64;
+        const std::vector<float> q = random_values(heads * t * h, 20), k = random_values(heads * t * h, 21),
+                                 v = random_values(heads * t * h, 22);
+        std::vector<float> scores(heads * t * t, 0.f), out(heads * t * h, 0.f);
+        reference_matmul(MatmulSpec::new_(t, t, h).right_transposed().batched(BatchStrides{heads, t * h, t * h, t * t}),
+                         q, k, scores);
+        oracle_causal_softmax(scores.data(), heads * t, t, t, 0.125f, 0);
+        reference_matmul(MatmulSpec::new_(t, h, t).batched(BatchStrides{heads, t * t, t * h, t * h}), scores, v, out);
+        const Tensor qt = gpu.upload(Shape::new_(heads * t, h), q), kt = gpu.upload(Shape::new_(heads * t, h), k),
+                     vt = gpu.upload(Shape::new_(heads * t, h), v);
+        Tensor ot = gpu.zeros(Shape::new_(heads * t, h)), pt = gpu.zeros(Shape::new_(heads * t, t));
+        const sn_attention_shape shape{heads, t, t, h, t * h, t * h, 0, 0.125f};
+        gpu.causal_attention(qt, kt, vt, ot, shape, &pt);
+        expect(relative_error(out, gpu.download(ot)) < tolerance(MatmulKernel::Blocked), "causal_attention output");
+        expect(relative_error(scores, gpu.download(pt)) < tolerance(MatmulKernel::Blocked),
+               "causal_attention probabilities");
     }
 
     std::printf("%d of %d cases passed\n", cases - failures + (panicked ? 1 : 0), cases + 1);
