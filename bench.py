@@ -316,6 +316,13 @@ def measure_attention(gpu: Gpu, events: HipEvents, repeats: int = 3):
     fused_ms = timed(events, gpu.stream, lambda: gpu.causal_attention(q, k, v, o, heads, t, t, h, 0.125), repeats)
     fused_p_ms = timed(events, gpu.stream, lambda: gpu.causal_attention(q, k, v, o, heads, t, t, h, 0.125,
                                                                         probabilities=p), repeats)
+    # The fused probability gradient against the dP product (causal mask) and softmax_backward.
+    unfused_grad_ms = result["products"]["dP = dO.V^T"]["causal_ms"] + backward_ms
+    gpu.causal_attention(q, k, v, o, heads, t, t, h, 0.125, probabilities=p)
+    fused_grad_ms = timed(events, gpu.stream, lambda: gpu.causal_attention_score_grad(do, v, o, p, ds, heads, t, t, h),
+                          repeats)
+    result["fused_score_grad"] = {"dp_and_softmax_backward_ms": round(unfused_grad_ms, 3),
+                                  "fused_ms": round(fused_grad_ms, 3)}
     result["fused_forward"] = {
         "three_calls_ms": round(unfused_ms, 3), "fused_ms": round(fused_ms, 3),
         "fused_with_probabilities_ms": round(fused_p_ms, 3),

@@ -316,6 +316,25 @@ int sn_causal_attention(sn_context *context, const sn_attention_shape *shape, co
                         const float *k, size_t k_len, const float *v, size_t v_len, float *out, size_t out_len,
                         float *probabilities, size_t probabilities_len);
 
+/* The probability gradient of that attention, fused. It has no counterpart in
+ * the reference's Gpu API: it computes in one launch what
+ * CausalSelfAttention::backward (crates/staleynet-model/src/layers/
+ * attention.rs:238-248) computes with the dP product (MatmulSpec::new(
+ * queries, keys, h).right_transposed(): dP = dO V^T, batched over the heads)
+ * and Gpu::softmax_backward(probabilities, dP), without writing dP: grad =
+ * P * (dP - D) with D per query = sum over h of dO * O (equal to the
+ * softmax's projection sum over keys of dP * P, since O = P V). d_out: dO
+ * [heads][queries][head_dim], q_stride apart per head; v as in
+ * sn_causal_attention; out: the forward's O, dense; probabilities: P as
+ * causal_softmax leaves it (0 past the diagonal); grad: dS, same layout as
+ * P, 0 past the diagonal. The same checks and codes as sn_causal_attention;
+ * grad must not overlap an input. Within the fp32 tolerance of the two
+ * calls. */
+int sn_causal_attention_score_grad(sn_context *context, const sn_attention_shape *shape, const float *d_out,
+                                   size_t d_out_len, const float *v, size_t v_len, const float *out, size_t out_len,
+                                   const float *probabilities, size_t probabilities_len, float *grad,
+                                   size_t grad_len);
+
 /* ---- the head's consumer: per-codebook softmax cross-entropy ------------- */
 /* An empty target slot (crates/staleynet-cuda/src/kernels/mod.rs:46). */
 #define SN_EMPTY_TOKEN 0xFFFFFFFFu

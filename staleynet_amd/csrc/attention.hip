@@ -387,6 +387,229 @@ __global__ __launch_bounds__(64 * kWaves) void causal_attention_kernel(Attention
     }
 }
 
+// The probability gradient of the same attention, fused: what the reference's
+// backward (layers/attention.rs:238-248) computes with the dP product
+// (MatmulSpec::new(T, T, h).right_transposed(): dP = dO V^T) and
+// softmax_backward(P, dP) (kernels/attention.rs:185-207): dS = P * (dP -
+// D) with D = sum over keys of dP * P per query, in one pass that never
+// writes dP. D is taken as sum over h of dO * O (the same quantity, since O =
+// P V), from the forward's output O. The layout is the forward's: a wave
+// computes dP^T = V dO^T for 32 keys against its 32 queries (dO in
+// registers), so lane l reads and writes its own query's row of P and dS.
+// Keys past each query's horizon get 0, as P is 0 there.
+struct ScoreGradArgs {
+    const float* d_out;   // dO [heads][queries][h]
+    const float* v;       // V [heads][keys][h], kv_stride apart
+    const float* out;     // O [heads][queries][h]
+    const float* p;       // P [heads][queries][keys]
+    float* grad;          // dS, same layout as P
+    int64_t queries, keys;
+    int64_t q_stride, kv_stride;
+    int64_t query_offset;
+    int64_t heads;
+    int32_t query_blocks;
+};
+
+// PREFETCH (rows of P 16-byte aligned: keys a multiple of 4): each stage's P
+// values are loaded with the stage, into one of two register sets, so that
+// they are waited for by count with the stage's V; otherwise they are loaded
+// where they are used.
+template <int H, bool PREFETCH>
+__global__ __launch_bounds__(64 * kWaves) void attention_score_grad_kernel(ScoreGradArgs args) {
+#pragma clang fp contract(off)
+    using G = Geometry<H>;
+    __shared__ f32x4 v_stage0[G::STAGE_SLOTS], v_stage1[G::STAGE_SLOTS];
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    auto v_of = [&](auto stage) __attribute__((always_inline)) -> f32x4* {
+        if constexpr (decltype(stage)::value == 0) return v_stage0;
+        else return v_stage1;
+    };
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 31;
+    const int half = lane >> 5;
+
+    const int64_t block = blockIdx.x;
+    const int64_t head = block % args.heads;
+    const int64_t query_block = args.query_blocks - 1 - block / args.heads;
+    const int64_t q_first = query_block * kQueries;
+    const int64_t q_wave = q_first + 32 * wave;
+    const int64_t q = q_wave + col;
+    const int64_t wg_keys = min(args.keys, min(q_first + kQueries, args.queries) - 1 + args.query_offset + 1);
+    const int64_t wave_keys = min(args.keys, q_wave + 31 + args.query_offset + 1);
+    const int stages_total = int((wg_keys + kKeys - 1) / kKeys);
+    const bool row_ok = q < args.queries;
+
+    const __amdgpu_buffer_rsrc_t v_rsrc = buffer_of(args.v + head * args.kv_stride);
+
+    // dO of this lane's query in registers (the forward's Q pattern) and D.
+    float dreg[G::CHUNKS][8];
+    float d_row;
+    {
+        const int64_t row = head * args.q_stride + (row_ok ? q : 0) * H;
+        const int64_t out_row = (head * args.queries + (row_ok ? q : 0)) * H;
+        float partial = 0.f;
+#pragma unroll
+        for (int c = 0; c < G::CHUNKS; ++c) {
+            const f32x4 lo = *reinterpret_cast<const f32x4*>(args.d_out + row + 16 * c + 8 * half);
+            const f32x4 hi = *reinterpret_cast<const f32x4*>(args.d_out + row + 16 * c + 8 * half + 4);
+            const f32x4 olo = *reinterpret_cast<const f32x4*>(args.out + out_row + 16 * c + 8 * half);
+            const f32x4 ohi = *reinterpret_cast<const f32x4*>(args.out + out_row + 16 * c + 8 * half + 4);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                dreg[c][s] = row_ok ? lo[s] : 0.f;
+                dreg[c][4 + s] = row_ok ? hi[s] : 0.f;
+                const float a = dreg[c][s] * olo[s];
+                partial = partial + a;
+            }
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const float a = dreg[c][4 + s] * ohi[s];
+                partial = partial + a;
+            }
+        }
+        d_row = partial + __shfl_xor(partial, 32);
+    }
+
+    auto issue = [&](auto stage, int64_t key0) __attribute__((always_inline)) {
+        f32x4* vs = v_of(stage);
+#pragma unroll
+        for (int u = 0; u < G::LOADS; ++u) {
+            const int instr = wave * G::LOADS + u;
+            const int e = 64 * instr + lane;
+            const int row = e / G::SLOTS;
+            const int slot = e % G::SLOTS;
+            const int64_t key = key0 + row;
+            const int chunk = slot ^ (row & G::SWIZZLE);
+            dma16(v_rsrc, vs + 64 * instr, key < args.keys ? int32_t((key * H + 4 * chunk) * 4) : kOutOfRange);
+        }
+    };
+    // dP^T for 32 keys (rows sub * 32 .. +31 of the stage) against this wave's queries.
+    auto products = [&](auto stage, int sub) __attribute__((always_inline)) {
+        const f32x4* vs = v_of(stage);
+        f32x16 acc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+        const int row = 32 * sub + col;
+        const int swz = row & G::SWIZZLE;
+#pragma unroll
+        for (int c = 0; c < G::CHUNKS; ++c) {
+            const int g = 4 * c + 2 * half;
+            const f32x4 lo = vs[row * G::SLOTS + (g ^ swz)];
+            const f32x4 hi = vs[row * G::SLOTS + ((g + 1) ^ swz)];
+            const float vv[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+            for (int s = 0; s < 8; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[s], dreg[c][s], acc, 0, 0, 0);
+        }
+        return acc;
+    };
+
+    const float* prow = args.p + (head * args.queries + q) * args.keys;
+    float* grow = args.grad + (head * args.queries + q) * args.keys;
+    const bool vector_rows = (args.keys & 3) == 0;
+    // P of a stage for the prefetching form: 2 blocks x 4 groups of 4 keys.
+    const __amdgpu_buffer_rsrc_t p_rsrc = buffer_of(args.p + head * args.queries * args.keys);
+    auto load_p = [&](int64_t key0, f32x4 (&pr)[2][4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int64_t key = key0 + 32 * sub + 4 * half + 8 * g;
+                const int32_t off = row_ok && key < args.keys ? int32_t((q * args.keys + key) * 4) : kOutOfRange;
+                pr[sub][g] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(p_rsrc, off, 0, 0));
+            }
+    };
+    auto gradients_of = [&](auto stage, int64_t key0, const f32x4 (&pr)[2][4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) {
+            const int64_t sub0 = key0 + 32 * sub;
+            if (sub0 >= args.keys) continue;
+            f32x16 acc;
+            if (sub0 < wave_keys) {
+                acc = products(stage, sub);
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+            }
+            if (!row_ok) continue;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int64_t key = sub0 + 4 * half + 8 * g;
+                float pv[4];
+                if constexpr (PREFETCH) {
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) pv[s] = pr[sub][g][s];
+                } else if (vector_rows && key + 4 <= args.keys) {
+                    const f32x4 x = *reinterpret_cast<const f32x4*>(prow + key);
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) pv[s] = x[s];
+                } else {
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) pv[s] = key + s < args.keys ? prow[key + s] : 0.f;
+                }
+                float gv[4];
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const bool visible = key + s <= q + args.query_offset;
+                    const float difference = acc[4 * g + s] - d_row;
+                    gv[s] = visible ? pv[s] * difference : 0.f;
+                }
+                if (vector_rows && key + 4 <= args.keys) {
+                    *reinterpret_cast<f32x4*>(grow + key) = f32x4{gv[0], gv[1], gv[2], gv[3]};
+                } else {
+#pragma unroll
+                    for (int s = 0; s < 4; ++s)
+                        if (key + s < args.keys) grow[key + s] = gv[s];
+                }
+            }
+        }
+    };
+    // The forward's stage loop (both stages loading at the top of every pass;
+    // loads past the last key read zeros), with each stage's P loaded beside
+    // its V in the prefetching form. The dS stores (and P loads in the other
+    // form) are vector memory operations too; a wait by count then only waits
+    // longer.
+    constexpr int kStageLoads = G::LOADS + (PREFETCH ? 8 : 0);
+    f32x4 p0[2][4], p1[2][4];
+    issue(I0{}, 0);
+    if constexpr (PREFETCH) load_p(0, p0);
+    issue(I1{}, kKeys);
+    if constexpr (PREFETCH) load_p(kKeys, p1);
+    for (int st = 0; st < stages_total; st += 2) {
+        const int64_t key0 = int64_t(st) * kKeys;
+        wait_loads<kStageLoads>();
+        lds_barrier();
+        gradients_of(I0{}, key0, p0);
+        lds_barrier();
+        issue(I0{}, key0 + 2 * kKeys);
+        if constexpr (PREFETCH) load_p(key0 + 2 * kKeys, p0);
+        wait_loads<kStageLoads>();
+        lds_barrier();
+        if (st + 1 < stages_total) gradients_of(I1{}, key0 + kKeys, p1);
+        lds_barrier();
+        issue(I1{}, key0 + 3 * kKeys);
+        if constexpr (PREFETCH) load_p(key0 + 3 * kKeys, p1);
+    }
+    wait_loads<0>();
+    // Keys past every query of the workgroup: zeros.
+    const int64_t zero_from = int64_t(stages_total) * kKeys;
+    if (zero_from < args.keys) {
+        const int64_t rows = min(int64_t(kQueries), args.queries - q_first);
+        for (int64_t r = 0; r < rows; ++r) {
+            float* zrow = args.grad + (head * args.queries + q_first + r) * args.keys;
+            if (vector_rows) {
+                for (int64_t e = zero_from + 4 * tid; e < args.keys; e += 4 * 64 * kWaves)
+                    *reinterpret_cast<f32x4*>(zrow + e) = f32x4{0.f, 0.f, 0.f, 0.f};
+            } else {
+                for (int64_t e = zero_from + tid; e < args.keys; e += 64 * kWaves) zrow[e] = 0.f;
+            }
+        }
+    }
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
@@ -422,6 +645,49 @@ bool causal_attention_supported(const CausalAttentionArgs& a) {
     const bool aligned = aligned16(a.q) && aligned16(a.k) && aligned16(a.v) && aligned16(a.o) &&
                          (a.p == nullptr || aligned16(a.p)) && a.q_stride % 4 == 0 && a.kv_stride % 4 == 0;
     // Per-head buffer offsets (keys x h floats) within 31 bits; the grid within 32 bits.
+    const bool offsets = a.keys * a.head_dim * 4 < (int64_t(1) << 31) - 4096;
+    const int64_t query_blocks = (a.queries + kQueries - 1) / kQueries;
+    const bool grid = a.heads * query_blocks < (int64_t(1) << 31);
+    return dims && aligned && offsets && grid;
+}
+
+hipError_t launch_attention_score_grad(const AttentionScoreGradArgs& a, hipStream_t stream) {
+    if (a.heads == 0 || a.queries == 0) return hipSuccess;
+    ScoreGradArgs args;
+    args.d_out = a.d_out;
+    args.v = a.v;
+    args.out = a.out;
+    args.p = a.p;
+    args.grad = a.grad;
+    args.queries = a.queries;
+    args.keys = a.keys;
+    args.q_stride = a.q_stride;
+    args.kv_stride = a.kv_stride;
+    args.query_offset = a.query_offset;
+    args.heads = a.heads;
+    args.query_blocks = int32_t((a.queries + kQueries - 1) / kQueries);
+    const dim3 grid(unsigned(a.heads * args.query_blocks));
+    // Prefetching needs 16-byte P rows and a head's P within 31-bit offsets.
+    const bool prefetch = a.keys % 4 == 0 && a.queries * a.keys * 4 < (int64_t(1) << 31) - 4096;
+    auto launch = [&](auto h, auto pf) {
+        hipLaunchKernelGGL((attention_score_grad_kernel<decltype(h)::value, decltype(pf)::value>), grid,
+                           dim3(64 * kWaves), 0, stream, args);
+    };
+    using T = std::true_type;
+    using F = std::false_type;
+    switch (a.head_dim) {
+        case 32: prefetch ? launch(std::integral_constant<int, 32>{}, T{}) : launch(std::integral_constant<int, 32>{}, F{}); break;
+        case 64: prefetch ? launch(std::integral_constant<int, 64>{}, T{}) : launch(std::integral_constant<int, 64>{}, F{}); break;
+        case 128: prefetch ? launch(std::integral_constant<int, 128>{}, T{}) : launch(std::integral_constant<int, 128>{}, F{}); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+bool attention_score_grad_supported(const AttentionScoreGradArgs& a) {
+    const bool dims = a.head_dim == 32 || a.head_dim == 64 || a.head_dim == 128;
+    const bool aligned = aligned16(a.d_out) && aligned16(a.v) && aligned16(a.out) && aligned16(a.p) &&
+                         aligned16(a.grad) && a.q_stride % 4 == 0 && a.kv_stride % 4 == 0;
     const bool offsets = a.keys * a.head_dim * 4 < (int64_t(1) << 31) - 4096;
     const int64_t query_blocks = (a.queries + kQueries - 1) / kQueries;
     const bool grid = a.heads * query_blocks < (int64_t(1) << 31);

@@ -565,6 +565,51 @@ int sn_causal_attention(sn_context* ctx, const sn_attention_shape* shape, const 
     return status(err);
 }
 
+int sn_causal_attention_score_grad(sn_context* ctx, const sn_attention_shape* shape, const float* d_out,
+                                   size_t d_out_len, const float* v, size_t v_len, const float* out, size_t out_len,
+                                   const float* probabilities, size_t probabilities_len, float* grad,
+                                   size_t grad_len) {
+    if (ctx == nullptr || shape == nullptr) return SN_ERR_NULL_ARGUMENT;
+    const sn_attention_shape& a = *shape;
+    if (a.heads == 0 || a.queries == 0) return SN_OK;
+    if (a.keys == 0) return SN_ERR_SHAPE;
+    if (a.head_dim != 32 && a.head_dim != 64 && a.head_dim != 128) return SN_ERR_UNSUPPORTED;
+    const size_t limit = size_t(1) << 60;
+    size_t q_rows, kv_rows, q_last, kv_last, o_need, head_rows, p_rows;
+    if (mul_overflows(a.queries, a.head_dim, &q_rows) || mul_overflows(a.keys, a.head_dim, &kv_rows) ||
+        mul_overflows(a.heads - 1, a.q_stride, &q_last) || mul_overflows(a.heads - 1, a.kv_stride, &kv_last) ||
+        mul_overflows(a.heads, q_rows, &o_need) || mul_overflows(a.heads, a.queries, &head_rows) ||
+        mul_overflows(head_rows, a.keys, &p_rows) || a.heads >= limit || a.queries >= limit || q_rows >= limit ||
+        kv_rows >= limit || q_last >= limit || kv_last >= limit || o_need >= limit || p_rows >= limit ||
+        a.query_offset >= (size_t(1) << 62))
+        return SN_ERR_OVERFLOW;
+    const size_t d_need = q_last + q_rows, kv_need = kv_last + kv_rows;
+    if (d_out_len < d_need || v_len < kv_need || out_len < o_need || probabilities_len < p_rows || grad_len < p_rows)
+        return SN_ERR_LENGTH_MISMATCH;
+    if (d_out == nullptr || v == nullptr || out == nullptr || probabilities == nullptr || grad == nullptr)
+        return SN_ERR_NULL_ARGUMENT;
+    if (overlaps(grad, p_rows, d_out, d_need) || overlaps(grad, p_rows, v, kv_need) ||
+        overlaps(grad, p_rows, out, o_need) || overlaps(grad, p_rows, probabilities, p_rows))
+        return SN_ERR_ALIASING;
+    sn::AttentionScoreGradArgs args;
+    args.d_out = d_out;
+    args.v = v;
+    args.out = out;
+    args.p = probabilities;
+    args.grad = grad;
+    args.heads = int64_t(a.heads);
+    args.queries = int64_t(a.queries);
+    args.keys = int64_t(a.keys);
+    args.head_dim = int64_t(a.head_dim);
+    args.q_stride = int64_t(a.heads > 1 ? a.q_stride : q_rows);
+    args.kv_stride = int64_t(a.heads > 1 ? a.kv_stride : kv_rows);
+    args.query_offset = int64_t(a.query_offset);
+    if (!sn::attention_score_grad_supported(args)) return SN_ERR_UNSUPPORTED;
+    hipError_t err = hipSetDevice(ctx->device);
+    if (err == hipSuccess) err = sn::launch_attention_score_grad(args, ctx->stream);
+    return status(err);
+}
+
 int sn_softmax_backward(sn_context* ctx, const float* probabilities, size_t probability_rows,
                         size_t probability_cols, float* grad, size_t grad_rows, size_t grad_cols) {
     if (probability_rows != grad_rows || probability_cols != grad_cols) return SN_ERR_SHAPE;

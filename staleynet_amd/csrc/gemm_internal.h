@@ -72,6 +72,24 @@ hipError_t launch_causal_attention(const CausalAttentionArgs& args, hipStream_t 
 // offsets within 31 bits.
 bool causal_attention_supported(const CausalAttentionArgs& args);
 
+// The fused probability gradient of that attention (attention.hip): grad =
+// softmax_backward(P, dO V^T) per head, with the softmax projection taken
+// as sum over h of dO * O; 0 past each query's horizon. dO and O
+// [heads][queries][head_dim] (dO rows q_stride apart per head, O dense),
+// V [heads][keys][head_dim] kv_stride apart, P and grad [heads][queries][keys].
+struct AttentionScoreGradArgs {
+    const float* d_out = nullptr;
+    const float* v = nullptr;
+    const float* out = nullptr;
+    const float* p = nullptr;
+    float* grad = nullptr;
+    int64_t heads = 0, queries = 0, keys = 0, head_dim = 0;
+    int64_t q_stride = 0, kv_stride = 0;
+    int64_t query_offset = 0;
+};
+hipError_t launch_attention_score_grad(const AttentionScoreGradArgs& args, hipStream_t stream);
+bool attention_score_grad_supported(const AttentionScoreGradArgs& args);
+
 // Rounds an fp32 operand to bf16 (nearest-even) into dst[batch][rows][kp],
 // K-contiguous, zeros for k in [k, kp) (bf16_stage.hip). Element (r, k) of
 // the source is src[r * ld + k] when k_contiguous, else src[k * ld + r];

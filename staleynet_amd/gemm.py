@@ -329,6 +329,9 @@ def _library() -> ctypes.CDLL:
         lib.sn_causal_attention.argtypes = [ctx, ctypes.POINTER(CAttentionShape), ctypes.c_void_p, size,
                                             ctypes.c_void_p, size, ctypes.c_void_p, size, ctypes.c_void_p, size,
                                             ctypes.c_void_p, size]
+        lib.sn_causal_attention_score_grad.argtypes = [ctx, ctypes.POINTER(CAttentionShape), ctypes.c_void_p, size,
+                                                       ctypes.c_void_p, size, ctypes.c_void_p, size,
+                                                       ctypes.c_void_p, size, ctypes.c_void_p, size]
         lib.sn_cross_entropy.argtypes = [ctx, ctypes.c_void_p, size, size, ctypes.c_void_p, size,
                                          ctypes.POINTER(CCrossEntropyHead), ctypes.c_void_p, size, ctypes.c_void_p,
                                          size, size]
@@ -581,6 +584,26 @@ class Gpu:
         if rc == SN_ERR_LENGTH_MISMATCH:
             raise AssertionError("causal_attention: a buffer is too small for the shape")
         self._check(rc, "causal_attention")
+
+    def causal_attention_score_grad(self, d_out: Tensor, v: Tensor, out: Tensor, probabilities: Tensor,
+                                    grad: Tensor, heads: int, queries: int, keys: int, head_dim: int,
+                                    query_offset: int = 0, q_stride: int | None = None,
+                                    kv_stride: int | None = None) -> None:
+        """Fused probability gradient (``sn_causal_attention_score_grad``): ``grad`` = what the dP
+        product and ``softmax_backward`` of CausalSelfAttention::backward (layers/attention.rs:238-248)
+        leave in ``grads.probabilities``."""
+        shape = CAttentionShape(heads, queries, keys, head_dim,
+                                queries * head_dim if q_stride is None else q_stride,
+                                keys * head_dim if kv_stride is None else kv_stride, query_offset, 1.0)
+        rc = _library().sn_causal_attention_score_grad(
+            self._ctx, ctypes.byref(shape), ctypes.c_void_p(d_out.pointer), len(d_out), ctypes.c_void_p(v.pointer),
+            len(v), ctypes.c_void_p(out.pointer), len(out), ctypes.c_void_p(probabilities.pointer),
+            len(probabilities), ctypes.c_void_p(grad.pointer), len(grad))
+        if rc == SN_ERR_SHAPE:
+            raise AssertionError("causal_attention_score_grad: no keys")
+        if rc == SN_ERR_LENGTH_MISMATCH:
+            raise AssertionError("causal_attention_score_grad: a buffer is too small for the shape")
+        self._check(rc, "causal_attention_score_grad")
 
     def softmax_backward(self, probabilities: Tensor, grad: Tensor) -> None:
         """``Gpu::softmax_backward`` (ops/attention.rs:76-92), in place on ``grad``."""

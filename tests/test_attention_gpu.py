@@ -6,7 +6,8 @@ restatement of the three calls it replaces in CausalSelfAttention::forward
 O and the probabilities are compared at the reference's fp32 tolerance. Cases: ragged query
 blocks and key counts, query offsets (a cached prefix), one-query decode against a partly written
 cache, head dims 32 / 64 / 128, K and V shared by every head, config 3's size, determinism, and the
-entry point's checks.
+entry point's checks. The same for the fused probability gradient (``sn_causal_attention_score_grad``)
+against the dP product and ``softmax_backward`` of CausalSelfAttention::backward (attention.rs:238-248).
 """
 import numpy as np
 import pytest
@@ -115,3 +116,71 @@ def test_entry_point_checks(gpu):
         gpu.causal_attention(q, k, v, out, 2, 64, 64, 48, 1.0)
     with pytest.raises(GpuError):  # the output overlapping an input
         gpu.causal_attention(q, k, v, q, 2, 64, 64, 64, 1.0)
+
+
+# ---- the fused probability gradient (sn_causal_attention_score_grad) ---------------------------
+# Against the reference's two calls in CausalSelfAttention::backward (attention.rs:238-248): the dP
+# product (MatmulSpec::new(T, keys, h).right_transposed(), reference.rs:19-38) and softmax_backward
+# (reference.rs:121-137), on the probabilities and output the oracle's forward gives.
+
+def run_score_grad(gpu, heads, queries, keys, h, scale, offset, q_stride=None, kv_stride=None, seed=0):
+    q_stride = queries * h if q_stride is None else q_stride
+    kv_stride = keys * h if kv_stride is None else kv_stride
+    q_len = (heads - 1) * q_stride + queries * h
+    kv_len = (heads - 1) * kv_stride + keys * h
+    rng = np.random.default_rng(seed)
+    q = rng.normal(0, 1, q_len).astype(np.float32)
+    k = rng.normal(0, 1, kv_len).astype(np.float32)
+    v = rng.normal(0, 1, kv_len).astype(np.float32)
+    d_out = rng.normal(0, 1, q_len).astype(np.float32)
+    out, p = reference(q, k, v, heads, queries, keys, h, scale, offset, q_stride, kv_stride)
+    expected = np.zeros(heads * queries * keys, np.float32)
+    oracle.matmul_parallel(oracle.Product(queries, keys, h, False, True, heads, q_stride, kv_stride, queries * keys,
+                                          1.0, False), d_out, v, expected)
+    oracle.softmax_backward(p, expected, keys)
+    D, V, O, P = (gpu.upload(Shape.vector(len(x)), x) for x in (d_out, v, out, p))
+    grad = gpu.upload(Shape.vector(len(p)), np.full(len(p), np.nan, np.float32))
+    gpu.causal_attention_score_grad(D, V, O, P, grad, heads, queries, keys, h, offset, q_stride, kv_stride)
+    return expected, gpu.download(grad)
+
+
+@pytest.mark.parametrize("heads,queries,keys,h,offset", [
+    (2, 128, 128, 64, 0),
+    (3, 200, 200, 64, 0),
+    (2, 100, 300, 64, 200),
+    (2, 96, 96, 32, 0),
+    (1, 64, 130, 128, 66),
+    (2, 37, 37, 64, 0),
+    (1, 300, 260, 64, 0),
+])
+def test_fused_score_grad_matches_dp_and_softmax_backward(gpu, heads, queries, keys, h, offset):
+    expected, got = run_score_grad(gpu, heads, queries, keys, h, 0.125, offset, seed=queries + keys + h + 1)
+    assert np.all(np.isfinite(got))
+    assert oracle.relative_error(expected, got) < TOLERANCE
+    g = got.reshape(heads, queries, keys)
+    for r in range(queries):
+        assert not np.any(g[:, r, min(r + offset + 1, keys):])
+
+
+def test_fused_score_grad_decode_and_shared_values(gpu):
+    expected, got = run_score_grad(gpu, 12, 1, 1408, 64, 0.125, 700, q_stride=64, kv_stride=1408 * 64, seed=7)
+    assert oracle.relative_error(expected, got) < TOLERANCE
+    expected, got = run_score_grad(gpu, 3, 64, 64, 64, 0.125, 0, kv_stride=0, seed=8)
+    assert oracle.relative_error(expected, got) < TOLERANCE
+
+
+def test_fused_score_grad_config_3_heads_and_determinism(gpu):
+    expected, got = run_score_grad(gpu, 2, 2048, 2048, 64, 0.125, 0, seed=9)
+    assert oracle.relative_error(expected, got) < TOLERANCE
+    _, again = run_score_grad(gpu, 2, 2048, 2048, 64, 0.125, 0, seed=9)
+    assert np.array_equal(got, again)
+
+
+def test_fused_score_grad_checks(gpu):
+    from staleynet_amd.gemm import GpuError
+    x = gpu.zeros(Shape.vector(2 * 64 * 64))
+    p, g = gpu.zeros(Shape.vector(2 * 64 * 64)), gpu.zeros(Shape.vector(2 * 64 * 64))
+    with pytest.raises(AssertionError, match="too small"):
+        gpu.causal_attention_score_grad(x, x, x, p, g, 2, 64, 65, 64)
+    with pytest.raises(GpuError):  # the gradient overlapping the probabilities
+        gpu.causal_attention_score_grad(x, x, x, p, p, 2, 64, 64, 64)
