@@ -19,6 +19,8 @@
 //   CrossEntropyHead, Gpu::cross_entropy           crates/staleynet-cuda/src/ops/loss.rs:14-71
 //   Gpu::causal_attention (scores, causal_softmax and mix in one launch; no reference counterpart:
 //                     the three calls of crates/staleynet-model/src/layers/attention.rs:206-213)
+//   Gpu::causal_attention_score_grad (the dP product and softmax_backward in one launch; no
+//                     reference counterpart: crates/staleynet-model/src/layers/attention.rs:238-248)
 // The reference panics on undersized operands; here that is a thrown
 // staleynet_cuda::Panic carrying the same message. Driver errors (the
 // reference's Err(DriverError)) are thrown as staleynet_cuda::GpuError.
@@ -409,6 +411,15 @@ class Gpu {
         check(sn_causal_attention(context_, &shape, q.data(), q.len(), k.data(), k.len(), v.data(), v.len(),
                                   out.data(), out.len(), probabilities ? probabilities->data() : nullptr,
                                   probabilities ? probabilities->len() : 0));
+    }
+
+    // The dP product and softmax_backward of the attention backward in one launch
+    // (sn_causal_attention_score_grad): grad = P * (dO V^T - rowsum(dO * O)).
+    void causal_attention_score_grad(const Tensor& d_out, const Tensor& v, const Tensor& out, const Tensor& probabilities,
+                                     Tensor& grad, const sn_attention_shape& shape) const {
+        check(sn_causal_attention_score_grad(context_, &shape, d_out.data(), d_out.len(), v.data(), v.len(),
+                                             out.data(), out.len(), probabilities.data(), probabilities.len(),
+                                             grad.data(), grad.len()));
     }
 
     sn_context* raw() const { return context_; }

@@ -271,6 +271,19 @@ int main() {
         expect(relative_error(out, gpu.download(ot)) < tolerance(MatmulKernel::Blocked), "causal_attention output");
         expect(relative_error(scores, gpu.download(pt)) < tolerance(MatmulKernel::Blocked),
                "causal_attention probabilities");
+
+        // The backward's dP product and softmax_backward (attention.rs:238-248) against the fused
+        // probability gradient, on the oracle's probabilities and output; dO from LCG seed 23.
+        const std::vector<float> d_out = random_values(heads * t * h, 23);
+        std::vector<float> dp(heads * t * t, 0.f);
+        reference_matmul(MatmulSpec::new_(t, t, h).right_transposed().batched(BatchStrides{heads, t * h, t * h, t * t}),
+                         d_out, v, dp);
+        oracle_softmax_backward(scores.data(), dp.data(), heads * t, t);
+        const Tensor dot = gpu.upload(Shape::new_(heads * t, h), d_out), oref = gpu.upload(Shape::new_(heads * t, h), out),
+                     pref = gpu.upload(Shape::new_(heads * t, t), scores);
+        Tensor ds = gpu.zeros(Shape::new_(heads * t, t));
+        gpu.causal_attention_score_grad(dot, vt, oref, pref, ds, shape);
+        expect(relative_error(dp, gpu.download(ds)) < tolerance(MatmulKernel::Blocked), "causal_attention_score_grad");
     }
 
     std::printf("%d of %d cases passed\n", cases - failures + (panicked ? 1 : 0), cases + 1);
