@@ -321,8 +321,14 @@ def measure_attention(gpu: Gpu, events: HipEvents, repeats: int = 3):
     gpu.causal_attention(q, k, v, o, heads, t, t, h, 0.125, probabilities=p)
     fused_grad_ms = timed(events, gpu.stream, lambda: gpu.causal_attention_score_grad(do, v, o, p, ds, heads, t, t, h),
                           repeats)
+    # ... and with the query gradient (dQ = scale dS K) accumulated in the same launch.
+    unfused_grad_q_ms = unfused_grad_ms + result["products"]["dQ = s.dS.K"]["causal_ms"]
+    fused_grad_q_ms = timed(events, gpu.stream, lambda: gpu.causal_attention_score_grad(
+        do, v, o, p, ds, heads, t, t, h, k=k, q_grad=dq, scale=0.125), repeats)
     result["fused_score_grad"] = {"dp_and_softmax_backward_ms": round(unfused_grad_ms, 3),
-                                  "fused_ms": round(fused_grad_ms, 3)}
+                                  "fused_ms": round(fused_grad_ms, 3),
+                                  "dp_softmax_backward_and_dq_ms": round(unfused_grad_q_ms, 3),
+                                  "fused_with_dq_ms": round(fused_grad_q_ms, 3)}
     result["fused_forward"] = {
         "three_calls_ms": round(unfused_ms, 3), "fused_ms": round(fused_ms, 3),
         "fused_with_probabilities_ms": round(fused_p_ms, 3),

@@ -327,13 +327,16 @@ int sn_causal_attention(sn_context *context, const sn_attention_shape *shape, co
  * [heads][queries][head_dim], q_stride apart per head; v as in
  * sn_causal_attention; out: the forward's O, dense; probabilities: P as
  * causal_softmax leaves it (0 past the diagonal); grad: dS, same layout as
- * P, 0 past the diagonal. The same checks and codes as sn_causal_attention;
- * grad must not overlap an input. Within the fp32 tolerance of the two
- * calls. */
+ * P, 0 past the diagonal. q_grad (may be null; then k may be null too): the
+ * backward's next call as well, dQ = shape->scale * dS K (attention.rs:
+ * 250-253, MatmulSpec::new(queries, h, keys).scaled(scale)), [heads]
+ * [queries][head_dim], with k laid out as v. The same checks and codes as
+ * sn_causal_attention; grad and q_grad must not overlap an input or each
+ * other. Within the fp32 tolerance of the calls it replaces. */
 int sn_causal_attention_score_grad(sn_context *context, const sn_attention_shape *shape, const float *d_out,
                                    size_t d_out_len, const float *v, size_t v_len, const float *out, size_t out_len,
                                    const float *probabilities, size_t probabilities_len, float *grad,
-                                   size_t grad_len);
+                                   size_t grad_len, const float *k, size_t k_len, float *q_grad, size_t q_grad_len);
 
 /* ---- the head's consumer: per-codebook softmax cross-entropy ------------- */
 /* An empty target slot (crates/staleynet-cuda/src/kernels/mod.rs:46). */

@@ -403,27 +403,40 @@ struct ScoreGradArgs {
     const float* out;     // O [heads][queries][h]
     const float* p;       // P [heads][queries][keys]
     float* grad;          // dS, same layout as P
+    const float* k;       // K [heads][keys][h], kv_stride apart (with q_grad)
+    float* q_grad;        // null, or dQ = scale dS K [heads][queries][h]
     int64_t queries, keys;
     int64_t q_stride, kv_stride;
     int64_t query_offset;
     int64_t heads;
     int32_t query_blocks;
+    float scale;
 };
 
 // PREFETCH (rows of P 16-byte aligned: keys a multiple of 4): each stage's P
 // values are loaded with the stage, into one of two register sets, so that
 // they are waited for by count with the stage's V; otherwise they are loaded
 // where they are used.
-template <int H, bool PREFETCH>
+// QGRAD: the query gradient of the backward's next call (attention.rs:250-253,
+// MatmulSpec::new(T, h, T).scaled(scale): dQ = scale dS K) is accumulated too.
+// Each lane's dS values are already the B operand of dQ^T += K^T dS^T (the
+// forward's O^T += V^T P^T): K is staged beside V, unswizzled.
+template <int H, bool PREFETCH, bool QGRAD>
 __global__ __launch_bounds__(64 * kWaves) void attention_score_grad_kernel(ScoreGradArgs args) {
 #pragma clang fp contract(off)
     using G = Geometry<H>;
+    constexpr int K_SLOTS = QGRAD ? G::STAGE_SLOTS : 1;
     __shared__ f32x4 v_stage0[G::STAGE_SLOTS], v_stage1[G::STAGE_SLOTS];
+    __shared__ f32x4 k_stage0[K_SLOTS], k_stage1[K_SLOTS];
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
     auto v_of = [&](auto stage) __attribute__((always_inline)) -> f32x4* {
         if constexpr (decltype(stage)::value == 0) return v_stage0;
         else return v_stage1;
+    };
+    auto k_of = [&](auto stage) __attribute__((always_inline)) -> f32x4* {
+        if constexpr (decltype(stage)::value == 0) return k_stage0;
+        else return k_stage1;
     };
 
     const int tid = threadIdx.x;
@@ -444,6 +457,7 @@ __global__ __launch_bounds__(64 * kWaves) void attention_score_grad_kernel(Score
     const bool row_ok = q < args.queries;
 
     const __amdgpu_buffer_rsrc_t v_rsrc = buffer_of(args.v + head * args.kv_stride);
+    const __amdgpu_buffer_rsrc_t k_rsrc = buffer_of(QGRAD ? args.k + head * args.kv_stride : args.v);
 
     // dO of this lane's query in registers (the forward's Q pattern) and D.
     float dreg[G::CHUNKS][8];
@@ -476,6 +490,7 @@ __global__ __launch_bounds__(64 * kWaves) void attention_score_grad_kernel(Score
 
     auto issue = [&](auto stage, int64_t key0) __attribute__((always_inline)) {
         f32x4* vs = v_of(stage);
+        f32x4* ks = k_of(stage);
 #pragma unroll
         for (int u = 0; u < G::LOADS; ++u) {
             const int instr = wave * G::LOADS + u;
@@ -485,6 +500,8 @@ __global__ __launch_bounds__(64 * kWaves) void attention_score_grad_kernel(Score
             const int64_t key = key0 + row;
             const int chunk = slot ^ (row & G::SWIZZLE);
             dma16(v_rsrc, vs + 64 * instr, key < args.keys ? int32_t((key * H + 4 * chunk) * 4) : kOutOfRange);
+            if constexpr (QGRAD)
+                dma16(k_rsrc, ks + 64 * instr, key < args.keys ? int32_t((key * H + 4 * slot) * 4) : kOutOfRange);
         }
     };
     // dP^T for 32 keys (rows sub * 32 .. +31 of the stage) against this wave's queries.
@@ -522,47 +539,75 @@ __global__ __launch_bounds__(64 * kWaves) void attention_score_grad_kernel(Score
                 pr[sub][g] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(p_rsrc, off, 0, 0));
             }
     };
+    // dQ^T (rows h, column q) when QGRAD.
+    f32x16 dq[QGRAD ? G::OBLOCKS : 1];
+#pragma unroll
+    for (int b = 0; b < (QGRAD ? G::OBLOCKS : 1); ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dq[b][r] = 0.f;
     auto gradients_of = [&](auto stage, int64_t key0, const f32x4 (&pr)[2][4]) __attribute__((always_inline)) {
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub) {
             const int64_t sub0 = key0 + 32 * sub;
-            if (sub0 >= args.keys) continue;
+            if (sub0 >= args.keys) continue;  // wave-uniform
+            const bool computed = sub0 < wave_keys;  // wave-uniform
             f32x16 acc;
-            if (sub0 < wave_keys) {
+            if (computed) {
                 acc = products(stage, sub);
             } else {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[r] = 0.f;
             }
-            if (!row_ok) continue;
+            // dS of this lane's 16 keys (0 for a lane past the last query).
+            float ds[16];
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int64_t key = sub0 + 4 * half + 8 * g;
-                float pv[4];
+                float pv[4] = {0.f, 0.f, 0.f, 0.f};
                 if constexpr (PREFETCH) {
 #pragma unroll
                     for (int s = 0; s < 4; ++s) pv[s] = pr[sub][g][s];
-                } else if (vector_rows && key + 4 <= args.keys) {
-                    const f32x4 x = *reinterpret_cast<const f32x4*>(prow + key);
+                } else if (row_ok) {
+                    if (vector_rows && key + 4 <= args.keys) {
+                        const f32x4 x = *reinterpret_cast<const f32x4*>(prow + key);
 #pragma unroll
-                    for (int s = 0; s < 4; ++s) pv[s] = x[s];
-                } else {
+                        for (int s = 0; s < 4; ++s) pv[s] = x[s];
+                    } else {
 #pragma unroll
-                    for (int s = 0; s < 4; ++s) pv[s] = key + s < args.keys ? prow[key + s] : 0.f;
+                        for (int s = 0; s < 4; ++s) pv[s] = key + s < args.keys ? prow[key + s] : 0.f;
+                    }
                 }
-                float gv[4];
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
-                    const bool visible = key + s <= q + args.query_offset;
+                    const bool visible = row_ok && key + s <= q + args.query_offset;
                     const float difference = acc[4 * g + s] - d_row;
-                    gv[s] = visible ? pv[s] * difference : 0.f;
+                    ds[4 * g + s] = visible ? pv[s] * difference : 0.f;
                 }
-                if (vector_rows && key + 4 <= args.keys) {
-                    *reinterpret_cast<f32x4*>(grow + key) = f32x4{gv[0], gv[1], gv[2], gv[3]};
-                } else {
+                if (row_ok) {
+                    if (vector_rows && key + 4 <= args.keys) {
+                        *reinterpret_cast<f32x4*>(grow + key) =
+                            f32x4{ds[4 * g], ds[4 * g + 1], ds[4 * g + 2], ds[4 * g + 3]};
+                    } else {
 #pragma unroll
-                    for (int s = 0; s < 4; ++s)
-                        if (key + s < args.keys) grow[key + s] = gv[s];
+                        for (int s = 0; s < 4; ++s)
+                            if (key + s < args.keys) grow[key + s] = ds[4 * g + s];
+                    }
+                }
+            }
+            if constexpr (QGRAD) {
+                if (computed) {
+                    // dQ^T rows 32 b .. +31 += K^T dS^T: MFMA t pairs keys key_of(t) of the two
+                    // lane halves; lane l supplies K[key_of(t)][32 b + col].
+                    const float* ks = reinterpret_cast<const float*>(k_of(stage));
+#pragma unroll
+                    for (int b = 0; b < G::OBLOCKS; ++b) {
+                        const float* krow = ks + (32 * sub) * H + 32 * b + col;
+#pragma unroll
+                        for (int t = 0; t < 16; ++t) {
+                            const int key = 4 * half + 8 * (t / 4) + (t % 4);
+                            dq[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(krow[key * H], ds[t], dq[b], 0, 0, 0);
+                        }
+                    }
                 }
             }
         }
@@ -572,7 +617,7 @@ __global__ __launch_bounds__(64 * kWaves) void attention_score_grad_kernel(Score
     // its V in the prefetching form. The dS stores (and P loads in the other
     // form) are vector memory operations too; a wait by count then only waits
     // longer.
-    constexpr int kStageLoads = G::LOADS + (PREFETCH ? 8 : 0);
+    constexpr int kStageLoads = G::LOADS * (QGRAD ? 2 : 1) + (PREFETCH ? 8 : 0);
     f32x4 p0[2][4], p1[2][4];
     issue(I0{}, 0);
     if constexpr (PREFETCH) load_p(0, p0);
@@ -594,6 +639,21 @@ __global__ __launch_bounds__(64 * kWaves) void attention_score_grad_kernel(Score
         if constexpr (PREFETCH) load_p(key0 + 3 * kKeys, p1);
     }
     wait_loads<0>();
+    if constexpr (QGRAD) {
+        // dQ = scale (dS K): lane l holds h rows 32 b + 4 half + 8 g + (0..3) of its query.
+        if (row_ok) {
+            float* qrow = args.q_grad + (head * args.queries + q) * H;
+#pragma unroll
+            for (int b = 0; b < G::OBLOCKS; ++b)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    f32x4 out;
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) out[s] = args.scale * dq[b][4 * g + s];
+                    *reinterpret_cast<f32x4*>(qrow + 32 * b + 4 * half + 8 * g) = out;
+                }
+        }
+    }
     // Keys past every query of the workgroup: zeros.
     const int64_t zero_from = int64_t(stages_total) * kKeys;
     if (zero_from < args.keys) {
@@ -659,6 +719,9 @@ hipError_t launch_attention_score_grad(const AttentionScoreGradArgs& a, hipStrea
     args.out = a.out;
     args.p = a.p;
     args.grad = a.grad;
+    args.k = a.k;
+    args.q_grad = a.q_grad;
+    args.scale = a.scale;
     args.queries = a.queries;
     args.keys = a.keys;
     args.q_stride = a.q_stride;
@@ -669,12 +732,16 @@ hipError_t launch_attention_score_grad(const AttentionScoreGradArgs& a, hipStrea
     const dim3 grid(unsigned(a.heads * args.query_blocks));
     // Prefetching needs 16-byte P rows and a head's P within 31-bit offsets.
     const bool prefetch = a.keys % 4 == 0 && a.queries * a.keys * 4 < (int64_t(1) << 31) - 4096;
-    auto launch = [&](auto h, auto pf) {
-        hipLaunchKernelGGL((attention_score_grad_kernel<decltype(h)::value, decltype(pf)::value>), grid,
-                           dim3(64 * kWaves), 0, stream, args);
+    auto launch_q = [&](auto h, auto pf, auto qg) {
+        hipLaunchKernelGGL((attention_score_grad_kernel<decltype(h)::value, decltype(pf)::value, decltype(qg)::value>),
+                           grid, dim3(64 * kWaves), 0, stream, args);
     };
     using T = std::true_type;
     using F = std::false_type;
+    auto launch = [&](auto h, auto pf) {
+        if (a.q_grad != nullptr) launch_q(h, pf, T{});
+        else launch_q(h, pf, F{});
+    };
     switch (a.head_dim) {
         case 32: prefetch ? launch(std::integral_constant<int, 32>{}, T{}) : launch(std::integral_constant<int, 32>{}, F{}); break;
         case 64: prefetch ? launch(std::integral_constant<int, 64>{}, T{}) : launch(std::integral_constant<int, 64>{}, F{}); break;
@@ -687,7 +754,8 @@ hipError_t launch_attention_score_grad(const AttentionScoreGradArgs& a, hipStrea
 bool attention_score_grad_supported(const AttentionScoreGradArgs& a) {
     const bool dims = a.head_dim == 32 || a.head_dim == 64 || a.head_dim == 128;
     const bool aligned = aligned16(a.d_out) && aligned16(a.v) && aligned16(a.out) && aligned16(a.p) &&
-                         aligned16(a.grad) && a.q_stride % 4 == 0 && a.kv_stride % 4 == 0;
+                         aligned16(a.grad) && (a.q_grad == nullptr || (aligned16(a.q_grad) && aligned16(a.k))) &&
+                         a.q_stride % 4 == 0 && a.kv_stride % 4 == 0;
     const bool offsets = a.keys * a.head_dim * 4 < (int64_t(1) << 31) - 4096;
     const int64_t query_blocks = (a.queries + kQueries - 1) / kQueries;
     const bool grid = a.heads * query_blocks < (int64_t(1) << 31);

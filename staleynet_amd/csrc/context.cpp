@@ -568,7 +568,7 @@ int sn_causal_attention(sn_context* ctx, const sn_attention_shape* shape, const 
 int sn_causal_attention_score_grad(sn_context* ctx, const sn_attention_shape* shape, const float* d_out,
                                    size_t d_out_len, const float* v, size_t v_len, const float* out, size_t out_len,
                                    const float* probabilities, size_t probabilities_len, float* grad,
-                                   size_t grad_len) {
+                                   size_t grad_len, const float* k, size_t k_len, float* q_grad, size_t q_grad_len) {
     if (ctx == nullptr || shape == nullptr) return SN_ERR_NULL_ARGUMENT;
     const sn_attention_shape& a = *shape;
     if (a.heads == 0 || a.queries == 0) return SN_OK;
@@ -584,12 +584,20 @@ int sn_causal_attention_score_grad(sn_context* ctx, const sn_attention_shape* sh
         a.query_offset >= (size_t(1) << 62))
         return SN_ERR_OVERFLOW;
     const size_t d_need = q_last + q_rows, kv_need = kv_last + kv_rows;
-    if (d_out_len < d_need || v_len < kv_need || out_len < o_need || probabilities_len < p_rows || grad_len < p_rows)
+    if (d_out_len < d_need || v_len < kv_need || out_len < o_need || probabilities_len < p_rows || grad_len < p_rows ||
+        (q_grad != nullptr && (k_len < kv_need || q_grad_len < o_need)))
         return SN_ERR_LENGTH_MISMATCH;
-    if (d_out == nullptr || v == nullptr || out == nullptr || probabilities == nullptr || grad == nullptr)
+    if (d_out == nullptr || v == nullptr || out == nullptr || probabilities == nullptr || grad == nullptr ||
+        (q_grad != nullptr && k == nullptr))
         return SN_ERR_NULL_ARGUMENT;
     if (overlaps(grad, p_rows, d_out, d_need) || overlaps(grad, p_rows, v, kv_need) ||
         overlaps(grad, p_rows, out, o_need) || overlaps(grad, p_rows, probabilities, p_rows))
+        return SN_ERR_ALIASING;
+    if (q_grad != nullptr &&
+        (overlaps(q_grad, o_need, d_out, d_need) || overlaps(q_grad, o_need, v, kv_need) ||
+         overlaps(q_grad, o_need, out, o_need) || overlaps(q_grad, o_need, probabilities, p_rows) ||
+         overlaps(q_grad, o_need, grad, p_rows) || overlaps(q_grad, o_need, k, kv_need) ||
+         overlaps(grad, p_rows, k, kv_need)))
         return SN_ERR_ALIASING;
     sn::AttentionScoreGradArgs args;
     args.d_out = d_out;
@@ -597,6 +605,9 @@ int sn_causal_attention_score_grad(sn_context* ctx, const sn_attention_shape* sh
     args.out = out;
     args.p = probabilities;
     args.grad = grad;
+    args.k = k;
+    args.q_grad = q_grad;
+    args.scale = a.scale;
     args.heads = int64_t(a.heads);
     args.queries = int64_t(a.queries);
     args.keys = int64_t(a.keys);

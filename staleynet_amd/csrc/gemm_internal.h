@@ -83,6 +83,9 @@ struct AttentionScoreGradArgs {
     const float* out = nullptr;
     const float* p = nullptr;
     float* grad = nullptr;
+    const float* k = nullptr;   // with q_grad: K, kv_stride apart like V
+    float* q_grad = nullptr;    // null, or dQ = scale grad K, [heads][queries][head_dim]
+    float scale = 1.f;
     int64_t heads = 0, queries = 0, keys = 0, head_dim = 0;
     int64_t q_stride = 0, kv_stride = 0;
     int64_t query_offset = 0;

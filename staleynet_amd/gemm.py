@@ -331,6 +331,7 @@ def _library() -> ctypes.CDLL:
                                             ctypes.c_void_p, size]
         lib.sn_causal_attention_score_grad.argtypes = [ctx, ctypes.POINTER(CAttentionShape), ctypes.c_void_p, size,
                                                        ctypes.c_void_p, size, ctypes.c_void_p, size,
+                                                       ctypes.c_void_p, size, ctypes.c_void_p, size,
                                                        ctypes.c_void_p, size, ctypes.c_void_p, size]
         lib.sn_cross_entropy.argtypes = [ctx, ctypes.c_void_p, size, size, ctypes.c_void_p, size,
                                          ctypes.POINTER(CCrossEntropyHead), ctypes.c_void_p, size, ctypes.c_void_p,
@@ -588,17 +589,22 @@ class Gpu:
     def causal_attention_score_grad(self, d_out: Tensor, v: Tensor, out: Tensor, probabilities: Tensor,
                                     grad: Tensor, heads: int, queries: int, keys: int, head_dim: int,
                                     query_offset: int = 0, q_stride: int | None = None,
-                                    kv_stride: int | None = None) -> None:
+                                    kv_stride: int | None = None, k: Tensor | None = None,
+                                    q_grad: Tensor | None = None, scale: float = 1.0) -> None:
         """Fused probability gradient (``sn_causal_attention_score_grad``): ``grad`` = what the dP
         product and ``softmax_backward`` of CausalSelfAttention::backward (layers/attention.rs:238-248)
-        leave in ``grads.probabilities``."""
+        leave in ``grads.probabilities``; with ``k`` and ``q_grad``, also the next call's
+        ``grads.queries`` = scale * grad * K (:250-253)."""
         shape = CAttentionShape(heads, queries, keys, head_dim,
                                 queries * head_dim if q_stride is None else q_stride,
-                                keys * head_dim if kv_stride is None else kv_stride, query_offset, 1.0)
+                                keys * head_dim if kv_stride is None else kv_stride, query_offset, scale)
+        k_pointer, k_len = (None, 0) if k is None else (k.pointer, len(k))
+        q_pointer, q_len = (None, 0) if q_grad is None else (q_grad.pointer, len(q_grad))
         rc = _library().sn_causal_attention_score_grad(
             self._ctx, ctypes.byref(shape), ctypes.c_void_p(d_out.pointer), len(d_out), ctypes.c_void_p(v.pointer),
             len(v), ctypes.c_void_p(out.pointer), len(out), ctypes.c_void_p(probabilities.pointer),
-            len(probabilities), ctypes.c_void_p(grad.pointer), len(grad))
+            len(probabilities), ctypes.c_void_p(grad.pointer), len(grad), ctypes.c_void_p(k_pointer), k_len,
+            ctypes.c_void_p(q_pointer), q_len)
         if rc == SN_ERR_SHAPE:
             raise AssertionError("causal_attention_score_grad: no keys")
         if rc == SN_ERR_LENGTH_MISMATCH:

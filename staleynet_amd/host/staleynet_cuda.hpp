@@ -415,11 +415,14 @@ class Gpu {
 
     // The dP product and softmax_backward of the attention backward in one launch
     // (sn_causal_attention_score_grad): grad = P * (dO V^T - rowsum(dO * O)).
+    // With k and q_grad, also the query gradient q_grad = shape.scale * grad K.
     void causal_attention_score_grad(const Tensor& d_out, const Tensor& v, const Tensor& out, const Tensor& probabilities,
-                                     Tensor& grad, const sn_attention_shape& shape) const {
+                                     Tensor& grad, const sn_attention_shape& shape, const Tensor* k = nullptr,
+                                     Tensor* q_grad = nullptr) const {
         check(sn_causal_attention_score_grad(context_, &shape, d_out.data(), d_out.len(), v.data(), v.len(),
                                              out.data(), out.len(), probabilities.data(), probabilities.len(),
-                                             grad.data(), grad.len()));
+                                             grad.data(), grad.len(), k ? k->data() : nullptr, k ? k->len() : 0,
+                                             q_grad ? q_grad->data() : nullptr, q_grad ? q_grad->len() : 0));
     }
 
     sn_context* raw() const { return context_; }

@@ -123,7 +123,8 @@ def test_entry_point_checks(gpu):
 # product (MatmulSpec::new(T, keys, h).right_transposed(), reference.rs:19-38) and softmax_backward
 # (reference.rs:121-137), on the probabilities and output the oracle's forward gives.
 
-def run_score_grad(gpu, heads, queries, keys, h, scale, offset, q_stride=None, kv_stride=None, seed=0):
+def run_score_grad(gpu, heads, queries, keys, h, scale, offset, q_stride=None, kv_stride=None, seed=0,
+                   with_q=False):
     q_stride = queries * h if q_stride is None else q_stride
     kv_stride = keys * h if kv_stride is None else kv_stride
     q_len = (heads - 1) * q_stride + queries * h
@@ -140,8 +141,18 @@ def run_score_grad(gpu, heads, queries, keys, h, scale, offset, q_stride=None, k
     oracle.softmax_backward(p, expected, keys)
     D, V, O, P = (gpu.upload(Shape.vector(len(x)), x) for x in (d_out, v, out, p))
     grad = gpu.upload(Shape.vector(len(p)), np.full(len(p), np.nan, np.float32))
-    gpu.causal_attention_score_grad(D, V, O, P, grad, heads, queries, keys, h, offset, q_stride, kv_stride)
-    return expected, gpu.download(grad)
+    if not with_q:
+        gpu.causal_attention_score_grad(D, V, O, P, grad, heads, queries, keys, h, offset, q_stride, kv_stride)
+        return expected, gpu.download(grad)
+    # The backward's next call: dQ = scale dS K (attention.rs:250-253).
+    expected_q = np.zeros(heads * queries * h, np.float32)
+    oracle.matmul_parallel(oracle.Product(queries, h, keys, False, False, heads, queries * keys, kv_stride, queries * h,
+                                          scale, False), expected, k, expected_q)
+    K = gpu.upload(Shape.vector(len(k)), k)
+    q_grad = gpu.upload(Shape.vector(len(expected_q)), np.full(len(expected_q), np.nan, np.float32))
+    gpu.causal_attention_score_grad(D, V, O, P, grad, heads, queries, keys, h, offset, q_stride, kv_stride, k=K,
+                                    q_grad=q_grad, scale=scale)
+    return expected, gpu.download(grad), expected_q, gpu.download(q_grad)
 
 
 @pytest.mark.parametrize("heads,queries,keys,h,offset", [
@@ -162,6 +173,20 @@ def test_fused_score_grad_matches_dp_and_softmax_backward(gpu, heads, queries, k
         assert not np.any(g[:, r, min(r + offset + 1, keys):])
 
 
+@pytest.mark.parametrize("heads,queries,keys,h,offset", [
+    (2, 128, 128, 64, 0),
+    (3, 200, 200, 64, 0),
+    (2, 100, 300, 64, 200),
+    (2, 96, 96, 32, 0),
+    (1, 64, 130, 128, 66),
+])
+def test_fused_query_grad_matches_the_next_product(gpu, heads, queries, keys, h, offset):
+    eg, gg, eq, gq = run_score_grad(gpu, heads, queries, keys, h, 0.125, offset, seed=queries + h + 2, with_q=True)
+    assert np.all(np.isfinite(gq))
+    assert oracle.relative_error(eg, gg) < TOLERANCE
+    assert oracle.relative_error(eq, gq) < TOLERANCE
+
+
 def test_fused_score_grad_decode_and_shared_values(gpu):
     expected, got = run_score_grad(gpu, 12, 1, 1408, 64, 0.125, 700, q_stride=64, kv_stride=1408 * 64, seed=7)
     assert oracle.relative_error(expected, got) < TOLERANCE
@@ -174,6 +199,9 @@ def test_fused_score_grad_config_3_heads_and_determinism(gpu):
     assert oracle.relative_error(expected, got) < TOLERANCE
     _, again = run_score_grad(gpu, 2, 2048, 2048, 64, 0.125, 0, seed=9)
     assert np.array_equal(got, again)
+    eg, gg, eq, gq = run_score_grad(gpu, 2, 2048, 2048, 64, 0.125, 0, seed=9, with_q=True)
+    assert np.array_equal(gg, got)
+    assert oracle.relative_error(eq, gq) < TOLERANCE
 
 
 def test_fused_score_grad_checks(gpu):
