@@ -416,6 +416,49 @@ def measure_decode(gpu: Gpu, events: HipEvents, pool_bytes: int = 640 << 20, rep
     return result
 
 
+DECODE_PMC_POOL_BYTES = 640 << 20
+DECODE_PMC_MEASURED = 8
+
+
+def _decode_pmc_launches(pool_bytes: int = DECODE_PMC_POOL_BYTES, measured: int = DECODE_PMC_MEASURED):
+    """(m, name, k, n, weight index, measured) of every decode product the counter workload
+    launches, in launch order, without a GPU: per shape one pass over a weight pool larger than
+    the 256 MB Infinity Cache, then `measured` more products on the pool's first weights, each
+    last read about pool_bytes earlier, so their reads come from HBM."""
+    for m in (1, 4, 16):
+        for name, k, n in DECODE_SHAPES:
+            copies = max(2, -(-pool_bytes // (4 * k * n)))
+            for i in range(copies):
+                yield m, name, k, n, i, False
+            for i in range(measured):
+                yield m, name, k, n, i % copies, True
+
+
+def run_decode_pmc_workload(gpu: Gpu) -> int:
+    """The decode products of _decode_pmc_launches, one plain launch each (no graph, so every
+    dispatch is its own counter sample and trace record)."""
+    launches = list(_decode_pmc_launches())
+    current, pool, x, y = None, [], None, None
+    for m, name, k, n, i, _ in launches:
+        if current != (m, name):
+            for t in pool + [x, y]:
+                if t is not None:
+                    t.free()
+            copies = max(2, -(-DECODE_PMC_POOL_BYTES // (4 * k * n)))
+            pool = [gpu.zeros(Shape(k, n)) for _ in range(copies)]
+            for j, w in enumerate(pool):
+                gpu.fill_normal(w, SEED, 1000 + j, 0.0, 0.02)
+            x, y = gpu.zeros(Shape(m, k)), gpu.zeros(Shape(m, n))
+            gpu.fill_normal(x, SEED, 999)
+            spec = MatmulSpec.new(m, n, k)
+            current = (m, name)
+        gpu.matmul(spec, x, pool[i], y)
+    gpu.synchronize()
+    for t in pool + [x, y]:
+        t.free()
+    return len(launches)
+
+
 # ---- Linear's bias kernels (SURVEY next row: the steps either side of NN and TN) ---------
 
 def measure_linear(gpu: Gpu, events: HipEvents, buffers, repeats: int = 5):
@@ -603,6 +646,64 @@ def summarize_pmc(fetch_csv: str, write_csv: str, copy_mib: int) -> str:
     return "\n".join(lines)
 
 
+GEMV_KERNEL_KEY = "gemv_kernel<"
+
+
+def _in_dispatch_order(csv_path: str, counter: str, key: str):
+    """Values of `counter` for every dispatch whose kernel name holds `key` (the GEMV's name
+    differs per row count), in dispatch order, from a counter_collection.csv."""
+    import csv
+    with open(csv_path, newline="") as f:
+        rows = sorted((r for r in csv.DictReader(f) if r["Counter_Name"] == counter and key in r["Kernel_Name"]),
+                      key=lambda r: int(r["Dispatch_Id"]))
+    return [float(r["Counter_Value"]) for r in rows]
+
+
+def _trace_durations(trace_csv: str, key: str):
+    """Durations (ns) of the dispatches whose kernel name holds `key`, in dispatch order, from a
+    rocprofv3 kernel_trace.csv."""
+    import csv
+    with open(trace_csv, newline="") as f:
+        rows = sorted((r for r in csv.DictReader(f) if key in r["Kernel_Name"]), key=lambda r: int(r["Dispatch_Id"]))
+    return [int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in rows]
+
+
+def summarize_decode_pmc(fetch_csv: str, write_csv: str, trace_csv: str, copy_mib: int) -> str:
+    """HBM bytes and GB/s of the decode GEMV per shape: FETCH_SIZE and WRITE_SIZE per dispatch
+    (copy-calibrated as in summarize_pmc) over the kernel's duration from a separate kernel-trace
+    run of the same workload; the measured dispatches of each shape only."""
+    fetch, write = _per_dispatch(fetch_csv, "FETCH_SIZE"), _per_dispatch(write_csv, "WRITE_SIZE")
+    copy_bytes = copy_mib << 20
+    pick = lambda table, key: next(v for k, v in table.items() if key in k)  # noqa: E731
+    f_factor = pick(fetch, COPY_KERNEL_KEY)[-1] * 1024 / copy_bytes
+    w_factor = pick(write, COPY_KERNEL_KEY)[-1] * 1024 / copy_bytes
+    f_gemv = _in_dispatch_order(fetch_csv, "FETCH_SIZE", GEMV_KERNEL_KEY)
+    w_gemv = _in_dispatch_order(write_csv, "WRITE_SIZE", GEMV_KERNEL_KEY)
+    durations = _trace_durations(trace_csv, GEMV_KERNEL_KEY)
+    launches = list(_decode_pmc_launches())
+    assert len(f_gemv) == len(w_gemv) == len(durations) == len(launches), \
+        (len(f_gemv), len(w_gemv), len(durations), len(launches))
+    groups = {}
+    for (m, name, k, n, _, measured), f, w, ns in zip(launches, f_gemv, w_gemv, durations):
+        if measured:
+            g = groups.setdefault((m, name, k, n), [0, 0.0, 0.0, 0.0])
+            g[0] += 1
+            g[1] += f * 1024 / f_factor
+            g[2] += w * 1024 / w_factor
+            g[3] += ns
+    lines = [f"copy kernel ({copy_mib} MiB read + {copy_mib} MiB written): factors {f_factor:.4f} (fetch), "
+             f"{w_factor:.4f} (write)", "",
+             f"{'product':>24} {'alg MB':>8} {'HBM rd MB':>10} {'HBM wr MB':>10} {'traffic/alg':>11} "
+             f"{'kernel us':>10} {'alg GB/s':>9} {'HBM GB/s':>9} {'of 8 TB/s':>9}"]
+    for (m, name, k, n), (count, rd, wr, ns) in groups.items():
+        alg = decode_bytes(m, k, n)
+        rd, wr, ns = rd / count, wr / count, ns / count
+        lines.append(f"{f'M={m} {name} {k}x{n}':>24} {alg / 1e6:>8.2f} {rd / 1e6:>10.2f} {wr / 1e6:>10.3f} "
+                     f"{(rd + wr) / alg:>11.3f} {ns / 1e3:>10.2f} {alg / ns:>9.0f} {(rd + wr) / ns:>9.0f} "
+                     f"{(rd + wr) / ns / PEAK_HBM_GBS:>9.3f}")
+    return "\n".join(lines)
+
+
 def summarize_trace(stats_csv: str, bench_json: str = "") -> str:
     """Kernel table from rocprofv3's kernel_stats.csv; with the bench line of the same run, the NN
     kernel's rocprof average beside the HIP-event mean bench.py reported."""
@@ -649,6 +750,12 @@ def main() -> int:
                         help="print a kernel table from a rocprofv3 --stats run and exit (no GPU)")
     parser.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                         help="print the NN kernel's HBM traffic from two --pmc runs and exit (no GPU)")
+    parser.add_argument("--decode-pmc", action="store_true",
+                        help="run only the decode counter workload (each config-4 product over a weight pool, "
+                             "plain launches; with --copy-calibration-mib, the calibration copy first) and exit")
+    parser.add_argument("--summarize-decode-pmc", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "KERNEL_TRACE_CSV"),
+                        help="print the decode GEMV's HBM bytes and GB/s per product from two --pmc runs and a "
+                             "kernel-trace run of --decode-pmc, and exit (no GPU)")
     parser.add_argument("--one-product", nargs=2, metavar=("LAYOUT", "PRECISION"),
                         help="run only config 2's qkv product (NN, TN or NT; f32 or bf16) 1 + 5 times and exit: "
                              "the workload of the per-kernel counter profiles")
@@ -659,6 +766,9 @@ def main() -> int:
         return 0
     if args.summarize_pmc:
         print(summarize_pmc(*args.summarize_pmc, args.copy_calibration_mib or 1024))
+        return 0
+    if args.summarize_decode_pmc:
+        print(summarize_decode_pmc(*args.summarize_decode_pmc, args.copy_calibration_mib or 1024))
         return 0
 
     if args.gpus != 1:
@@ -690,6 +800,10 @@ def main() -> int:
         gpu.synchronize()
         src.free()
         dst.free()
+    if args.decode_pmc:
+        print(json.dumps({"decode_pmc_launches": run_decode_pmc_workload(gpu)}))
+        gpu.close()
+        return 0
     calls, _buffers = build_set(gpu)
     set_flops = sum(spec.flops() for _, _, spec, _ in calls)
 
