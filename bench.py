@@ -336,6 +336,30 @@ def measure_attention(gpu: Gpu, events: HipEvents, repeats: int = 3):
     return result
 
 
+def run_one_attention(gpu: Gpu, events: HipEvents, kind: str) -> dict:
+    """Config 3's fused attention kernel alone (192 heads, T = 2048, h = 64), one warm-up and five
+    timed calls: `forward` (O only), `forward_p` (O and the probabilities), `score_grad` (dS from
+    dO, V, O, P) or `score_grad_dq` (with dQ): the workload of the attention counter profiles."""
+    heads, t, h = 16 * 12, 2048, 64
+    q, k, v, o, do, dq = (gpu.zeros(Shape(heads * t, h)) for _ in range(6))
+    p, ds = gpu.zeros(Shape(heads * t, t)), gpu.zeros(Shape(heads * t, t))
+    for i, tensor in enumerate((q, k, v, do)):
+        gpu.fill_normal(tensor, SEED, 900 + i)
+    gpu.causal_attention(q, k, v, o, heads, t, t, h, 0.125, probabilities=p)
+    calls = {
+        "forward": lambda: gpu.causal_attention(q, k, v, o, heads, t, t, h, 0.125),
+        "forward_p": lambda: gpu.causal_attention(q, k, v, o, heads, t, t, h, 0.125, probabilities=p),
+        "score_grad": lambda: gpu.causal_attention_score_grad(do, v, o, p, ds, heads, t, t, h),
+        "score_grad_dq": lambda: gpu.causal_attention_score_grad(do, v, o, p, ds, heads, t, t, h, k=k, q_grad=dq,
+                                                                 scale=0.125),
+    }
+    ms = timed(events, gpu.stream, calls[kind], 5)
+    visible = heads * t * (t + 1) // 2
+    products = {"forward": 2, "forward_p": 2, "score_grad": 1, "score_grad_dq": 2}[kind]
+    return {"attention": kind, "ms": round(ms, 4),
+            "tflops_on_visible_work": round(products * 2 * h * visible / (ms * 1e-3) / 1e12, 1)}
+
+
 # ---- config 4: decode ------------------------------------------------------------------
 
 DECODE_SHAPES = [("qkv", 768, 2304), ("out", 768, 768), ("up", 768, 3072), ("down", 3072, 768),
@@ -756,6 +780,9 @@ def main() -> int:
     parser.add_argument("--summarize-decode-pmc", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "KERNEL_TRACE_CSV"),
                         help="print the decode GEMV's HBM bytes and GB/s per product from two --pmc runs and a "
                              "kernel-trace run of --decode-pmc, and exit (no GPU)")
+    parser.add_argument("--one-attention", choices=["forward", "forward_p", "score_grad", "score_grad_dq"],
+                        help="run only config 3's fused attention kernel 1 + 5 times and exit: the workload of the "
+                             "attention counter profiles")
     parser.add_argument("--one-product", nargs=2, metavar=("LAYOUT", "PRECISION"),
                         help="run only config 2's qkv product (NN, TN or NT; f32 or bf16) 1 + 5 times and exit: "
                              "the workload of the per-kernel counter profiles")
@@ -778,6 +805,10 @@ def main() -> int:
 
     gpu = Gpu(0)
     events = HipEvents()
+    if args.one_attention:
+        print(json.dumps(run_one_attention(gpu, events, args.one_attention)))
+        gpu.close()
+        return 0
     if args.one_product:
         layout, precision = args.one_product
         m, d = MODEL_111M["tokens"], MODEL_111M["width"]

@@ -26,12 +26,14 @@
 //    32) that share a query, and the probabilities are already laid out as
 //    the B operand of O^T += V^T P^T: no trip through LDS.
 //  * Element arithmetic follows causal_softmax: s * scale, minus the
-//    maximum, expf, each rounded; the sum is accumulated in a different
-//    order (per 32-key block, then rescaled), so parity is to the fp32
-//    tolerance.
+//    maximum, each rounded, then the exponential (as 2^(d log2 e) on the
+//    transcendental unit); the sum is accumulated in a different order (per
+//    32-key block, then rescaled), so parity is to the fp32 tolerance.
+//  * Only the 32-key blocks on a wave's diagonal (or past the last key) test
+//    keys against each query's horizon; the others skip the mask.
 //  * P (optional) takes a second pass over K with the final m and l: p =
-//    expf(s * scale - m) / l, 0 past the diagonal, so it matches the
-//    probabilities causal_softmax leaves.
+//    e^(s * scale - m) * (1 / l), 0 past the diagonal, so it matches the
+//    probabilities causal_softmax leaves to the fp32 tolerance.
 //  * Query blocks are launched longest first across all heads (the last
 //    queries see the most keys).
 #include <hip/hip_runtime.h>
@@ -41,6 +43,7 @@
 #include <type_traits>
 
 #include "gemm_internal.h"
+
 
 namespace sn {
 namespace {
@@ -72,6 +75,14 @@ __device__ __forceinline__ void wait_loads() {
     __builtin_amdgcn_s_waitcnt(0x0F70 | (PENDING & 15) | ((PENDING >> 4) << 14));
 }
 
+// e^d as 2^(d log2 e) on the transcendental unit (v_exp_f32, about 1 ulp).
+// d is a difference x - m already rounded as causal_softmax rounds it, so
+// rounding d log2 e adds at most |d| 2^-24 to the exponent: a relative error
+// under 2e-6 for every probability above e^-20, whatever the logits' size.
+// d = -inf gives 0.
+constexpr float kLog2e = 1.44269504088896340736f;
+__device__ __forceinline__ float exp_of(float d) { return __builtin_amdgcn_exp2f(d * kLog2e); }
+
 // Workgroup barrier that does not wait for loads still in flight (the
 // direct-to-LDS loads of the next stage); LDS reads are completed first.
 __device__ __forceinline__ void lds_barrier() {
@@ -81,13 +92,13 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("" ::: "memory");
 }
 
-template <int H>
+template <int H, int KEYS = kKeys>
 struct Geometry {
     static constexpr int SLOTS = H / 4;                        // 16-byte chunks per row
     static constexpr int SWIZZLE = SLOTS < 16 ? SLOTS - 1 : 15;  // row bits XORed into the chunk index
     static constexpr int CHUNKS = H / 16;                      // 16-deep MFMA chunks over h
     static constexpr int OBLOCKS = H / 32;                     // 32-row accumulator blocks of O^T
-    static constexpr int STAGE_SLOTS = kKeys * SLOTS;          // f32x4 per operand per stage
+    static constexpr int STAGE_SLOTS = KEYS * SLOTS;           // f32x4 per operand per stage
     static constexpr int LOADS = STAGE_SLOTS / (64 * kWaves);  // load instructions per wave per operand
     static_assert(H == 32 || H == 64 || H == 128, "head dims 32, 64, 128");
     static_assert(STAGE_SLOTS % (64 * kWaves) == 0, "whole load instructions per wave");
@@ -107,10 +118,18 @@ struct AttentionArgs {
     float scale;
 };
 
+// Waves per SIMD the forward kernel's registers are budgeted for: as many
+// workgroups as its LDS stages allow (64 KB at h = 64: two per CU).
+constexpr int forward_waves_per_simd(int h) { return h <= 32 ? 3 : h == 64 ? 2 : 1; }
+
 template <int H>
-__global__ __launch_bounds__(64 * kWaves) void causal_attention_kernel(AttentionArgs args) {
+__global__ __launch_bounds__(64 * kWaves)
+__attribute__((amdgpu_waves_per_eu(forward_waves_per_simd(H), forward_waves_per_simd(H))))
+void causal_attention_kernel(AttentionArgs args) {
 #pragma clang fp contract(off)
-    using G = Geometry<H>;
+    constexpr int KEYS = kKeys;      // per LDS stage
+    constexpr int SUBS = KEYS / 32;  // 32-key blocks per stage
+    using G = Geometry<H, KEYS>;
     // Two LDS stages per operand, each its own array: every LDS access below
     // names its stage at compile time, so the compiler's wait counts leave the
     // other stage's loads in flight.
@@ -144,7 +163,7 @@ __global__ __launch_bounds__(64 * kWaves) void causal_attention_kernel(Attention
     // Keys this workgroup and this wave can see (exclusive ends).
     const int64_t wg_keys = min(args.keys, min(q_first + kQueries, args.queries) - 1 + args.query_offset + 1);
     const int64_t wave_keys = min(args.keys, q_wave + 31 + args.query_offset + 1);
-    const int stages_total = int((wg_keys + kKeys - 1) / kKeys);
+    const int stages_total = int((wg_keys + KEYS - 1) / KEYS);
 
     const float* kh = args.k + head * args.kv_stride;
     const float* vh = args.v + head * args.kv_stride;
@@ -222,28 +241,36 @@ __global__ __launch_bounds__(64 * kWaves) void causal_attention_kernel(Attention
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[b][r] = 0.f;
 
-    // Online softmax of one 32-key block (scores acc, keys sub0 ..) and its
-    // O^T += V^T P^T.
-    auto softmax_and_mix = [&](auto stage, int sub, const f32x16& acc, int64_t sub0) __attribute__((always_inline)) {
+    // Last key of the 32-key block from sub0 that this lane's query sees, as
+    // an offset within the block: -1 (none) .. 31 (all).
+    auto visible_limit = [&](int64_t sub0) __attribute__((always_inline)) {
+        const int64_t last = min(args.keys - 1, q + args.query_offset) - sub0;
+        return int(max(int64_t(-1), min(int64_t(31), last)));
+    };
+    // Online softmax of one 32-key block (scores acc; keys sub0 .., block sub
+    // of the stage) and its O^T += V^T P^T. MASKED is false when the wave's
+    // first query sees the whole block (so every lane's query does): no
+    // per-key test.
+    auto softmax_and_mix = [&](auto stage, auto masked, int sub, const f32x16& acc, int64_t sub0)
+                               __attribute__((always_inline)) {
+        constexpr bool MASKED = decltype(masked)::value;
         float x[16];
         float block_max = -INFINITY;
+        const int limit = MASKED ? visible_limit(sub0) : 31;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int64_t key = sub0 + key_of(r);
-            const bool visible = key < args.keys && key <= q + args.query_offset;
-            x[r] = visible ? acc[r] * args.scale : -INFINITY;
+            x[r] = acc[r] * args.scale;
+            if (MASKED) x[r] = key_of(r) <= limit ? x[r] : -INFINITY;
             block_max = fmaxf(block_max, x[r]);
         }
         block_max = fmaxf(block_max, __shfl_xor(block_max, 32));
         const float m_new = fmaxf(m, block_max);
-        const float alpha = expf(m - m_new);
-        float p[16];
+        const float alpha = exp_of(m - m_new);
         float sum = 0.f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const float shifted = x[r] - m_new;
-            p[r] = x[r] == -INFINITY ? 0.f : expf(shifted);
-            sum = sum + p[r];
+            x[r] = exp_of(x[r] - m_new);  // now the probability numerator
+            sum = sum + x[r];
         }
         sum = sum + __shfl_xor(sum, 32);
         l = l * alpha + sum;
@@ -258,20 +285,27 @@ __global__ __launch_bounds__(64 * kWaves) void causal_attention_kernel(Attention
             const float* vrow = vs + (32 * sub) * H + 32 * b + col;
 #pragma unroll
             for (int t = 0; t < 16; ++t)
-                o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[key_of(t) * H], p[t], o[b], 0, 0, 0);
+                o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[key_of(t) * H], x[t], o[b], 0, 0, 0);
         }
     };
-    // Both 32-key blocks of a stage (their scores first, so that the second
-    // block's matrix work can overlap the first block's exponentials).
+    // The stage's 32-key blocks that the wave's last query sees, one at a
+    // time (scores, softmax, mix: the fewest registers live, so that two
+    // workgroups share a CU at h = 64). A block is whole for the wave when
+    // its first query sees every key of it (wave-uniform).
+    using Masked = std::true_type;
+    using Whole = std::false_type;
+    const int64_t wave_horizon = q_wave + args.query_offset;  // last key the wave's first query sees
     auto compute = [&](auto stage, int64_t key0) __attribute__((always_inline)) {
-        if (key0 + 32 < wave_keys) {  // wave-uniform: both blocks
-            const f32x16 s0 = scores(stage, 0);
-            const f32x16 s1 = scores(stage, 1);
-            softmax_and_mix(stage, 0, s0, key0);
-            softmax_and_mix(stage, 1, s1, key0 + 32);
-        } else if (key0 < wave_keys) {
-            const f32x16 s0 = scores(stage, 0);
-            softmax_and_mix(stage, 0, s0, key0);
+#pragma unroll
+        for (int sub = 0; sub < SUBS; ++sub) {
+            const int64_t sub0 = key0 + 32 * sub;
+            if (sub0 < wave_keys) {  // wave-uniform
+                const f32x16 s = scores(stage, sub);
+                if (sub0 + 31 <= wave_horizon && sub0 + 32 <= args.keys)
+                    softmax_and_mix(stage, Whole{}, sub, s, sub0);
+                else
+                    softmax_and_mix(stage, Masked{}, sub, s, sub0);
+            }
         }
     };
     // The stage loop runs from barrier to barrier with both stages loading
@@ -281,19 +315,19 @@ __global__ __launch_bounds__(64 * kWaves) void causal_attention_kernel(Attention
     // stage's are still in flight.
     constexpr int kStageLoads = 2 * G::LOADS;
     issue(I0{}, 0, true);
-    issue(I1{}, kKeys, true);
+    issue(I1{}, KEYS, true);
     for (int st = 0; st < stages_total; st += 2) {
-        const int64_t key0 = int64_t(st) * kKeys;
+        const int64_t key0 = int64_t(st) * KEYS;
         wait_loads<kStageLoads>();
         lds_barrier();
         compute(I0{}, key0);
         lds_barrier();
-        issue(I0{}, key0 + 2 * kKeys, true);
+        issue(I0{}, key0 + 2 * KEYS, true);
         wait_loads<kStageLoads>();
         lds_barrier();
-        if (st + 1 < stages_total) compute(I1{}, key0 + kKeys);
+        if (st + 1 < stages_total) compute(I1{}, key0 + KEYS);
         lds_barrier();
-        issue(I1{}, key0 + 3 * kKeys, true);
+        issue(I1{}, key0 + 3 * KEYS, true);
     }
     wait_loads<0>();  // the loads past the end land before the stages are reused
 
@@ -316,9 +350,10 @@ __global__ __launch_bounds__(64 * kWaves) void causal_attention_kernel(Attention
     float* prow = args.p + (head * args.queries + q) * args.keys;
     const bool row_ok = q < args.queries;
     const bool vector_rows = (args.keys & 3) == 0;
+    const float inv_l = 1.f / l;
     auto probabilities_of = [&](auto stage, int64_t key0) __attribute__((always_inline)) {
 #pragma unroll
-        for (int sub = 0; sub < 2; ++sub) {
+        for (int sub = 0; sub < SUBS; ++sub) {
             const int64_t sub0 = key0 + 32 * sub;
             if (sub0 >= args.keys) continue;
             f32x16 acc;
@@ -328,15 +363,14 @@ __global__ __launch_bounds__(64 * kWaves) void causal_attention_kernel(Attention
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[r] = 0.f;
             }
+            const int limit = visible_limit(sub0);
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 float pv[4];
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
-                    const int64_t key = sub0 + key_of(4 * g + s);
-                    const bool visible = key <= q + args.query_offset;
                     const float shifted = acc[4 * g + s] * args.scale - m;
-                    pv[s] = visible ? expf(shifted) / l : 0.f;
+                    pv[s] = key_of(4 * g + s) <= limit ? exp_of(shifted) * inv_l : 0.f;
                 }
                 const int64_t key = sub0 + 4 * half + 8 * g;
                 if (row_ok) {
@@ -355,24 +389,24 @@ __global__ __launch_bounds__(64 * kWaves) void causal_attention_kernel(Attention
     // memory operations too: each wait also covers the stores issued since,
     // which only makes it wait longer, never too little.
     issue(I0{}, 0, false);
-    issue(I1{}, kKeys, false);
+    issue(I1{}, KEYS, false);
     for (int st = 0; st < stages_total; st += 2) {
-        const int64_t key0 = int64_t(st) * kKeys;
+        const int64_t key0 = int64_t(st) * KEYS;
         wait_loads<G::LOADS>();
         lds_barrier();
         probabilities_of(I0{}, key0);
         lds_barrier();
-        issue(I0{}, key0 + 2 * kKeys, false);
+        issue(I0{}, key0 + 2 * KEYS, false);
         wait_loads<G::LOADS>();
         lds_barrier();
-        if (st + 1 < stages_total) probabilities_of(I1{}, key0 + kKeys);
+        if (st + 1 < stages_total) probabilities_of(I1{}, key0 + KEYS);
         lds_barrier();
-        issue(I1{}, key0 + 3 * kKeys, false);
+        issue(I1{}, key0 + 3 * KEYS, false);
     }
     wait_loads<0>();
     // Keys past every query of the workgroup: zeros, each row filled by the
     // whole workgroup with contiguous stores.
-    const int64_t zero_from = int64_t(stages_total) * kKeys;
+    const int64_t zero_from = int64_t(stages_total) * KEYS;
     if (zero_from < args.keys) {
         const int64_t rows = min(int64_t(kQueries), args.queries - q_first);
         for (int64_t r = 0; r < rows; ++r) {
