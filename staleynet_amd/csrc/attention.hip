@@ -455,8 +455,18 @@ struct ScoreGradArgs {
 // MatmulSpec::new(T, h, T).scaled(scale): dQ = scale dS K) is accumulated too.
 // Each lane's dS values are already the B operand of dQ^T += K^T dS^T (the
 // forward's O^T += V^T P^T): K is staged beside V, unswizzled.
+// Waves per SIMD the gradient kernel's registers are budgeted for where the
+// compiler's own choice would leave one workgroup per CU although the LDS
+// stages fit two (h = 64 with K staged: 264 -> 240 registers; h = 128
+// without: 272 -> 256). A budget of three spills.
+constexpr int score_grad_waves_per_simd(int h, bool qgrad) {
+    return (h == 64 && qgrad) || (h == 128 && !qgrad) ? 2 : 1;
+}
+
 template <int H, bool PREFETCH, bool QGRAD>
-__global__ __launch_bounds__(64 * kWaves) void attention_score_grad_kernel(ScoreGradArgs args) {
+__global__ __launch_bounds__(64 * kWaves)
+__attribute__((amdgpu_waves_per_eu(score_grad_waves_per_simd(H, QGRAD), score_grad_waves_per_simd(H, QGRAD))))
+void attention_score_grad_kernel(ScoreGradArgs args) {
 #pragma clang fp contract(off)
     using G = Geometry<H>;
     constexpr int K_SLOTS = QGRAD ? G::STAGE_SLOTS : 1;
