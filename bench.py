@@ -345,7 +345,8 @@ def run_one_attention(gpu: Gpu, events: HipEvents, kind: str) -> dict:
     p, ds = gpu.zeros(Shape(heads * t, t)), gpu.zeros(Shape(heads * t, t))
     for i, tensor in enumerate((q, k, v, do)):
         gpu.fill_normal(tensor, SEED, 900 + i)
-    gpu.causal_attention(q, k, v, o, heads, t, t, h, 0.125, probabilities=p)
+    if kind.startswith("score_grad"):  # the gradient reads the forward's O and P
+        gpu.causal_attention(q, k, v, o, heads, t, t, h, 0.125, probabilities=p)
     calls = {
         "forward": lambda: gpu.causal_attention(q, k, v, o, heads, t, t, h, 0.125),
         "forward_p": lambda: gpu.causal_attention(q, k, v, o, heads, t, t, h, 0.125, probabilities=p),
@@ -728,6 +729,37 @@ def summarize_decode_pmc(fetch_csv: str, write_csv: str, trace_csv: str, copy_mi
     return "\n".join(lines)
 
 
+def summarize_counters(csv_paths) -> str:
+    """Per-kernel means over dispatches of every counter in one or more rocprofv3
+    counter_collection.csv files (one counter group per run), with the derived shares:
+    MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (4 SIMDs x SQ_BUSY_CU_CYCLES); waiting =
+    SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES; VALU per MFMA = (SQ_INSTS_VALU - SQ_INSTS_MFMA) / SQ_INSTS_MFMA."""
+    import csv
+    sums = {}
+    for path in csv_paths:
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                k = sums.setdefault(_short(r["Kernel_Name"]), {}).setdefault(r["Counter_Name"], [0.0, 0])
+                k[0] += float(r["Counter_Value"])
+                k[1] += 1
+    lines = []
+    for kernel, counters in sums.items():
+        mean = {name: total / count for name, (total, count) in counters.items()}
+        derived = []
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in mean and mean.get("SQ_BUSY_CU_CYCLES"):
+            derived.append(f"MFMA busy {mean['SQ_VALU_MFMA_BUSY_CYCLES'] / (4 * mean['SQ_BUSY_CU_CYCLES']):.3f}")
+        if "SQ_WAIT_INST_ANY" in mean and mean.get("SQ_WAVE_CYCLES"):
+            derived.append(f"waiting {mean['SQ_WAIT_INST_ANY'] / mean['SQ_WAVE_CYCLES']:.3f}")
+        if mean.get("SQ_INSTS_MFMA") and "SQ_INSTS_VALU" in mean:
+            derived.append(f"VALU per MFMA {(mean['SQ_INSTS_VALU'] - mean['SQ_INSTS_MFMA']) / mean['SQ_INSTS_MFMA']:.2f}")
+        lines.append(f"{kernel[:90]}")
+        if derived:
+            lines.append("    " + "; ".join(derived))
+        for name in sorted(mean):
+            lines.append(f"    {name:<28} {mean[name]:>16.0f}")
+    return "\n".join(lines)
+
+
 def summarize_trace(stats_csv: str, bench_json: str = "") -> str:
     """Kernel table from rocprofv3's kernel_stats.csv; with the bench line of the same run, the NN
     kernel's rocprof average beside the HIP-event mean bench.py reported."""
@@ -774,6 +806,9 @@ def main() -> int:
                         help="print a kernel table from a rocprofv3 --stats run and exit (no GPU)")
     parser.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                         help="print the NN kernel's HBM traffic from two --pmc runs and exit (no GPU)")
+    parser.add_argument("--summarize-counters", nargs="+", metavar="COUNTER_CSV",
+                        help="print per-kernel counter means (and MFMA busy, wait share) from rocprofv3 --pmc "
+                             "counter_collection.csv files and exit (no GPU)")
     parser.add_argument("--decode-pmc", action="store_true",
                         help="run only the decode counter workload (each config-4 product over a weight pool, "
                              "plain launches; with --copy-calibration-mib, the calibration copy first) and exit")
@@ -793,6 +828,9 @@ def main() -> int:
         return 0
     if args.summarize_pmc:
         print(summarize_pmc(*args.summarize_pmc, args.copy_calibration_mib or 1024))
+        return 0
+    if args.summarize_counters:
+        print(summarize_counters(args.summarize_counters))
         return 0
     if args.summarize_decode_pmc:
         print(summarize_decode_pmc(*args.summarize_decode_pmc, args.copy_calibration_mib or 1024))
