@@ -31,14 +31,14 @@ def reference(q, k, v, heads, queries, keys, h, scale, offset, q_stride, kv_stri
     return out, scores
 
 
-def run(gpu, heads, queries, keys, h, scale, offset, q_stride=None, kv_stride=None, seed=0, with_p=True):
+def run(gpu, heads, queries, keys, h, scale, offset, q_stride=None, kv_stride=None, seed=0, with_p=True, spread=1.0):
     q_stride = queries * h if q_stride is None else q_stride
     kv_stride = keys * h if kv_stride is None else kv_stride
     q_len = (heads - 1) * q_stride + queries * h
     kv_len = (heads - 1) * kv_stride + keys * h
     rng = np.random.default_rng(seed)
-    q = rng.normal(0, 1, q_len).astype(np.float32)
-    k = rng.normal(0, 1, kv_len).astype(np.float32)
+    q = rng.normal(0, spread, q_len).astype(np.float32)
+    k = rng.normal(0, spread, kv_len).astype(np.float32)
     v = rng.normal(0, 1, kv_len).astype(np.float32)
     Q, K, V = (gpu.upload(Shape.vector(len(x)), x) for x in (q, k, v))
     out = gpu.upload(Shape.vector(heads * queries * h), np.full(heads * queries * h, np.nan, np.float32))
@@ -60,6 +60,8 @@ def run(gpu, heads, queries, keys, h, scale, offset, q_stride=None, kv_stride=No
     (1, 64, 130, 128, 66, 0.09),     # head dim 128
     (2, 37, 37, 64, 0, 1.0),         # fewer queries than a wave's block
     (1, 300, 260, 64, 0, 0.125),     # keys run out before the diagonal
+    (2, 512, 512, 32, 0, 0.17),      # head dim 32 over several query blocks (three waves per SIMD)
+    (2, 384, 448, 128, 64, 0.09),    # head dim 128 over several query blocks, with an offset
 ])
 def test_fused_attention_matches_the_three_calls(gpu, heads, queries, keys, h, offset, scale):
     eo, go, ep, gp = run(gpu, heads, queries, keys, h, scale, offset, seed=queries + keys + h)
@@ -71,6 +73,18 @@ def test_fused_attention_matches_the_three_calls(gpu, heads, queries, keys, h, o
     for r in range(queries):
         visible = min(r + offset + 1, keys)
         assert not np.any(p[:, r, visible:])
+
+
+def test_large_logits(gpu):
+    # Q and K ~ N(0, 9): scaled scores with a spread of about 9 and row maxima near 30, so the
+    # differences from the maximum reach -60 or so. The exponential of a rounded difference d is
+    # taken as 2^(d log2 e); its error grows with |d| but stays within the tolerance, because the
+    # probabilities it affects are tiny.
+    eo, go, ep, gp = run(gpu, 2, 1024, 1024, 64, 0.125, 0, seed=11, spread=3.0)
+    assert np.all(np.isfinite(go)) and np.all(np.isfinite(gp))
+    assert oracle.relative_error(eo, go) < TOLERANCE
+    assert oracle.relative_error(ep, gp) < TOLERANCE
+    print(f"large logits: O {oracle.relative_error(eo, go):.2e}, P {oracle.relative_error(ep, gp):.2e}")
 
 
 def test_decode_query_against_a_partly_written_cache(gpu):
