@@ -16,7 +16,8 @@ with HIP events on the library's stream.
 The printed JSON line is the driver's contract plus:
 - ``roofline``: the forward-NN kernel, timed per launch with HIP events;
 - ``cpu_baseline``: the reference's CPU matmul restated bit-for-bit in oracle/, on one
-  host core, over a bounded row sample of every GEMM of the set, scaled to the full set;
+  host core, over a bounded row sample of every GEMM of the set, scaled to the full set
+  (``cpu_baseline_all_cores``: the same with each sample's rows split over the host's cores);
 - ``bf16``: the same set with bf16-rounded inputs and fp32 accumulation;
 - ``attention``: config 3's six causal attention products, 192 heads x T = 2048 x h = 64;
 - ``decode``: config 4's M in {1, 4, 16} products against the 111.5M weights, replayed
