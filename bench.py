@@ -432,6 +432,7 @@ def measure_decode(gpu: Gpu, events: HipEvents, pool_bytes: int = 640 << 20, rep
     graph.launch()
     ms = timed(events, gpu.stream, graph.launch, 5)
     graph.close()
+    result["attention"] = measure_decode_attention(gpu, events, repeats)
     head = result["per_shape_gbs"][f"M=1 head {DECODE_SHAPES[4][1]}x{DECODE_SHAPES[4][2]}"]
     result["head_m1_frac_hbm_peak"] = round(head / PEAK_HBM_GBS, 4)
     result["head_m1_frac_stream_read"] = round(head / result["stream_read_gbs"], 4)
@@ -440,6 +441,44 @@ def measure_decode(gpu: Gpu, events: HipEvents, pool_bytes: int = 640 << 20, rep
                                 "us_per_token": round(ms * 1e3, 1),
                                 "gbs": round(token_bytes / (ms * 1e-3) / 1e9, 1)}
     return result
+
+
+def measure_decode_attention(gpu: Gpu, events: HipEvents, repeats: int = 3):
+    """One decode step's attention per layer of the 111.5M model (attention.rs:274-320): 12 heads,
+    one new position against a 1408-position KV cache holding `cached` positions. The reference's
+    three calls (scores product against the cache, causal_softmax, mix product; causal masks from the
+    query offset) against the fused sn_causal_attention, whose few-query form splits the cached keys
+    over workgroups; each replayed 12 times from a HIP graph, microseconds per layer."""
+    heads, capacity, h = 12, 1408, 64
+    q, o = gpu.zeros(Shape(heads, h)), gpu.zeros(Shape(heads, h))
+    k, v = gpu.zeros(Shape(heads * capacity, h)), gpu.zeros(Shape(heads * capacity, h))
+    scores = gpu.zeros(Shape(heads, capacity))
+    for i, t in enumerate((q, k, v)):
+        gpu.fill_normal(t, SEED, 960 + i)
+    out = {"shape": f"{heads} heads, 1 query, cache {capacity} x {h}, fp32", "method": "HIP-graph replay x12"}
+    for cached in (701, capacity):
+        offset = cached - 1
+        fused = lambda: gpu.causal_attention(q, k, v, o, heads, 1, capacity, h, 0.125,  # noqa: E731
+                                             query_offset=offset, q_stride=h, kv_stride=capacity * h)
+        per_head = BatchStrides(heads, h, capacity * h, capacity)
+        score_spec = MatmulSpec.new(1, capacity, h).right_transposed().batched(per_head).causal_output(offset)
+        mix_spec = MatmulSpec.new(1, h, capacity).batched(BatchStrides(heads, capacity, capacity * h, h)) \
+            .causal_left(offset)
+
+        def three_calls():
+            gpu.matmul(score_spec, q, k, scores)
+            gpu.causal_softmax(scores, 1, 0.125, offset)
+            gpu.matmul(mix_spec, scores, v, o)
+
+        for name, body in (("fused_us", fused), ("three_calls_us", three_calls)):
+            graph = HipGraph(gpu.stream, lambda: [body() for _ in range(12)])
+            graph.launch()
+            ms = timed(events, gpu.stream, graph.launch, repeats) / 12
+            graph.close()
+            out.setdefault(f"cached={cached}", {})[name] = round(ms * 1e3, 2)
+    for t in (q, o, k, v, scores):
+        t.free()
+    return out
 
 
 DECODE_PMC_POOL_BYTES = 640 << 20

@@ -311,7 +311,12 @@ typedef struct sn_attention_shape {
  * keys >= 1 (SN_ERR_SHAPE); buffers too small for the shape
  * (SN_ERR_LENGTH_MISMATCH);
  * out or probabilities overlapping an input or each other (SN_ERR_ALIASING).
- * Within the fp32 tolerance of the three calls. */
+ * Within the fp32 tolerance of the three calls. With at most 4 queries per
+ * head and no probabilities (a decode step against the cache,
+ * attention.rs:274-320), the keys are split over workgroups whose partial
+ * results are merged in a fixed order through the context's workspace and
+ * arrival counters, so calls on one context must not overlap (as for
+ * sn_matmul's split products); deterministic. */
 int sn_causal_attention(sn_context *context, const sn_attention_shape *shape, const float *q, size_t q_len,
                         const float *k, size_t k_len, const float *v, size_t v_len, float *out, size_t out_len,
                         float *probabilities, size_t probabilities_len);

@@ -42,6 +42,7 @@
 #include <cstdint>
 #include <type_traits>
 
+#include "gemm_common.h"
 #include "gemm_internal.h"
 
 
@@ -714,12 +715,304 @@ void attention_score_grad_kernel(ScoreGradArgs args) {
     }
 }
 
+// Decode-shaped attention: a few queries per head (a decode step's one new
+// position, or a handful) against a long run of cached keys, without the
+// probabilities. The query-block kernel above would give each head one
+// workgroup, reading the whole cache alone, with 31 of every 32 MFMA columns
+// empty. Here the keys are split into 64-key chunks, one workgroup each:
+//  * 256 threads; a key row of h floats is read by h / 4 lanes (16 bytes
+//    each), so a pass covers 1024 / h rows and a chunk takes h / 16 passes,
+//    every K and V load issued before the first use;
+//  * a score is a lane's 4-term dot product summed over the row's lanes by
+//    an xor butterfly (every lane ends with the same value), scaled and
+//    masked as causal_softmax does; the chunk's maximum m_c, sum l_c of
+//    e^(x - m_c) and partial O_c = sum of e^(x - m_c) V follow by the same
+//    butterflies over the rows of a wave, then over the four waves through
+//    LDS, in a fixed order;
+//  * each chunk writes (O_c, m_c, l_c) per query to the workspace with
+//    device-coherent stores, waits for them, and bumps its head's arrival
+//    counter; the last chunk to arrive merges them, O = sum e^(m_c - m) O_c
+//    / sum e^(m_c - m) l_c with m the largest m_c (kept as a running
+//    maximum, the sums rescaled as it grows), all its threads folding chunks
+//    in a fixed order, and resets the counter. Deterministic: no atomics on
+//    data.
+constexpr int kDecodeKeys = 64;     // keys per workgroup
+constexpr int kDecodeQueries = 4;   // most queries per head
+constexpr int kDecodeThreads = 256;
+
+template <int H>
+struct DecodeGeometry {
+    static constexpr int LANES = H / 4;                       // lanes per key row
+    static constexpr int ROWS = kDecodeThreads / LANES;       // rows per pass
+    static constexpr int PASSES = kDecodeKeys / ROWS;         // passes per chunk
+    static constexpr int RECORD = H + 4;                      // floats per (chunk, query): O_c, m_c, l_c, pad
+    static_assert(PASSES * ROWS == kDecodeKeys && LANES <= 64, "whole passes");
+};
+
+struct DecodeArgs {
+    const float* q;
+    const float* k;
+    const float* v;
+    float* o;
+    float* ws;           // [heads][chunks][NQ][RECORD]
+    uint32_t* counters;  // [heads], zero between calls
+    int64_t queries, keys;
+    int64_t q_stride, kv_stride;
+    int64_t query_offset;
+    int32_t chunks;
+    float scale;
+};
+
+// NQ: queries per head the registers and records are laid out for (1, 2 or
+// 4; the launch picks the least that holds a.queries).
+template <int H, int NQ>
+__global__ __launch_bounds__(kDecodeThreads) void decode_attention_kernel(DecodeArgs a) {
+#pragma clang fp contract(off)
+    using D = DecodeGeometry<H>;
+    __shared__ float wave_values[4][NQ];
+    __shared__ f32x4 wave_out[4][NQ][H / 4];
+    __shared__ bool arrived_last;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int li = tid % D::LANES;    // 16-byte piece of the row
+    const int slot = tid / D::LANES;  // row within a pass
+    const int64_t head = blockIdx.y;
+    const int chunk = blockIdx.x;
+    const int64_t key0 = int64_t(chunk) * kDecodeKeys;
+    const int nq = int(a.queries);
+
+    const float* kh = a.k + head * a.kv_stride;
+    const float* vh = a.v + head * a.kv_stride;
+    const float* qh = a.q + head * a.q_stride;
+    f32x4 kr[D::PASSES], vr[D::PASSES], qr[NQ];
+#pragma unroll
+    for (int i = 0; i < D::PASSES; ++i) {
+        const int64_t key = key0 + i * D::ROWS + slot;
+        const bool ok = key < a.keys;
+        kr[i] = ok ? *reinterpret_cast<const f32x4*>(kh + key * H + 4 * li) : f32x4{0.f, 0.f, 0.f, 0.f};
+        vr[i] = ok ? *reinterpret_cast<const f32x4*>(vh + key * H + 4 * li) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int j = 0; j < NQ; ++j)
+        qr[j] = j < nq ? *reinterpret_cast<const f32x4*>(qh + j * H + 4 * li) : f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // Scaled, masked scores; the chunk's maximum per query.
+    float x[D::PASSES][NQ];
+    float m_c[NQ];
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) m_c[j] = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < D::PASSES; ++i) {
+        const int64_t key = key0 + i * D::ROWS + slot;
+#pragma unroll
+        for (int j = 0; j < NQ; ++j) {
+            float dot = kr[i][0] * qr[j][0];
+#pragma unroll
+            for (int e = 1; e < 4; ++e) dot = dot + kr[i][e] * qr[j][e];
+#pragma unroll
+            for (int o = 1; o < D::LANES; o <<= 1) dot = dot + __shfl_xor(dot, o);
+            const bool visible = j < nq && key < a.keys && key <= j + a.query_offset;
+            x[i][j] = visible ? dot * a.scale : -INFINITY;
+            m_c[j] = fmaxf(m_c[j], x[i][j]);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+#pragma unroll
+        for (int o = D::LANES; o < 64; o <<= 1) m_c[j] = fmaxf(m_c[j], __shfl_xor(m_c[j], o));
+        if (lane == 0) wave_values[wave][j] = m_c[j];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < NQ; ++j)
+        m_c[j] = fmaxf(fmaxf(wave_values[0][j], wave_values[1][j]), fmaxf(wave_values[2][j], wave_values[3][j]));
+    __syncthreads();
+
+    // e^(x - m_c), the chunk's sums and partial outputs (0 for a query that
+    // sees none of the chunk's keys).
+    float l_c[NQ];
+    f32x4 o_c[NQ];
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+        l_c[j] = 0.f;
+        o_c[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < D::PASSES; ++i) {
+            const float e = m_c[j] == -INFINITY ? 0.f : exp_of(x[i][j] - m_c[j]);
+            l_c[j] = l_c[j] + e;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) o_c[j][d] = o_c[j][d] + e * vr[i][d];
+        }
+#pragma unroll
+        for (int o = D::LANES; o < 64; o <<= 1) {
+            l_c[j] = l_c[j] + __shfl_xor(l_c[j], o);
+#pragma unroll
+            for (int d = 0; d < 4; ++d) o_c[j][d] = o_c[j][d] + __shfl_xor(o_c[j][d], o);
+        }
+        if (lane == 0) wave_values[wave][j] = l_c[j];
+        if (lane < D::LANES) wave_out[wave][j][li] = o_c[j];
+    }
+    __syncthreads();
+
+    // One chunk: it is the whole answer, O = O_c / l_c.
+    if (a.chunks == 1) {
+        if (tid < nq * (H / 4)) {
+            const int j = tid / (H / 4), piece = tid % (H / 4);
+            const f32x4 sum = ((wave_out[0][j][piece] + wave_out[1][j][piece]) + wave_out[2][j][piece]) +
+                              wave_out[3][j][piece];
+            const float l_sum = ((wave_values[0][j] + wave_values[1][j]) + wave_values[2][j]) + wave_values[3][j];
+            f32x4 out;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) out[d] = sum[d] / l_sum;
+            *reinterpret_cast<f32x4*>(a.o + (head * a.queries + j) * H + 4 * piece) = out;
+        }
+        return;
+    }
+
+    // This chunk's records, device-coherent: thread t writes query t / (h / 4),
+    // 16-byte piece t % (h / 4) of O_c; thread j < NQ also m_c, l_c.
+    const __amdgpu_buffer_rsrc_t mine = gemm::buffer_of(a.ws + (head * a.chunks + chunk) * NQ * D::RECORD);
+    if (tid < NQ * (H / 4)) {
+        const int j = tid / (H / 4), piece = tid % (H / 4);
+        const f32x4 sum = ((wave_out[0][j][piece] + wave_out[1][j][piece]) + wave_out[2][j][piece]) +
+                          wave_out[3][j][piece];
+        gemm::buffer_store4_coherent(mine, int32_t((j * D::RECORD + 4 * piece) * 4), sum);
+    }
+    if (tid < NQ) {
+        const float l_sum = ((wave_values[0][tid] + wave_values[1][tid]) + wave_values[2][tid]) + wave_values[3][tid];
+        gemm::buffer_store4_coherent(mine, int32_t((tid * D::RECORD + H) * 4), f32x4{m_c[tid], l_sum, 0.f, 0.f});
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's record stores are complete device-wide
+    __syncthreads();
+    uint32_t* counter = a.counters + head;
+    if (tid == 0)
+        arrived_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                       uint32_t(a.chunks - 1);
+    __syncthreads();
+    if (!arrived_last) return;
+
+    // Last to arrive: merge the chunks. Thread group g (h / 4 threads, one
+    // 16-byte piece of O each) folds chunks g, g + GROUPS, ... in order
+    // (device-coherent loads, 8 chunks' records in flight at a time),
+    // rescaling its running sums to each new maximum; group 0 then folds the
+    // groups' results in group order. Deterministic. Every query sees key 0,
+    // so group 0's maximum is finite from its first chunk on, and a group
+    // with no chunk (or only chunks a query does not reach) contributes 0.
+    constexpr int PIECES = H / 4;
+    constexpr int GROUPS = kDecodeThreads / PIECES;
+    constexpr int kBatch = 8;
+    __shared__ f32x4 group_out[GROUPS][PIECES];
+    __shared__ float group_m[GROUPS], group_l[GROUPS];
+    const int piece = tid % PIECES, g = tid / PIECES;
+    const __amdgpu_buffer_rsrc_t all = gemm::buffer_of(a.ws + head * a.chunks * NQ * D::RECORD);
+    auto fold = [](float& m, float& l, f32x4& acc, float m_c, float l_c, const f32x4& part)
+                    __attribute__((always_inline)) {
+        const float m_new = fmaxf(m, m_c);
+        if (m_new == -INFINITY) return;  // nothing seen yet on either side
+        const float kept = exp_of(m - m_new);
+        const float w = exp_of(m_c - m_new);
+        l = l * kept + w * l_c;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) acc[d] = acc[d] * kept + w * part[d];
+        m = m_new;
+    };
+    for (int j = 0; j < nq; ++j) {
+        float m = -INFINITY, l = 0.f;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        for (int c0 = g; c0 < a.chunks; c0 += kBatch * GROUPS) {
+            f32x4 ml[kBatch], part[kBatch];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                const int c = c0 + u * GROUPS;
+                const bool ok = c < a.chunks;
+                ml[u] = gemm::buffer_load4_coherent(all, ok ? int32_t(((c * NQ + j) * D::RECORD + H) * 4)
+                                                            : gemm::kOutOfRange);
+                part[u] = gemm::buffer_load4_coherent(all, ok ? int32_t(((c * NQ + j) * D::RECORD + 4 * piece) * 4)
+                                                              : gemm::kOutOfRange);
+            }
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u)
+                if (c0 + u * GROUPS < a.chunks) fold(m, l, acc, ml[u][0], ml[u][1], part[u]);
+        }
+        group_out[g][piece] = acc;
+        if (piece == 0) {
+            group_m[g] = m;
+            group_l[g] = l;
+        }
+        __syncthreads();
+        if (g == 0) {
+            float mm = -INFINITY, ll = 0.f;
+            f32x4 total = {0.f, 0.f, 0.f, 0.f};
+            for (int k = 0; k < GROUPS; ++k) fold(mm, ll, total, group_m[k], group_l[k], group_out[k][piece]);
+            f32x4 out;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) out[d] = total[d] / ll;
+            *reinterpret_cast<f32x4*>(a.o + (head * a.queries + j) * H + 4 * piece) = out;
+        }
+        __syncthreads();
+    }
+    if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+namespace {
+
+// Chunks of the decode form for `a`, or 0 when the query-block kernel runs:
+// probabilities requested, more than kDecodeQueries queries, or no room for
+// the records and counters.
+int64_t decode_chunks(const CausalAttentionArgs& a) {
+    if (a.p != nullptr || a.queries > kDecodeQueries || a.heads > 65535) return 0;
+    const int64_t visible = std::min(a.keys, a.queries + a.query_offset);  // keys the last query sees
+    const int64_t chunks = (visible + kDecodeKeys - 1) / kDecodeKeys;
+    const int64_t record_bytes = int64_t(kDecodeQueries) * (a.head_dim + 4) * 4;
+    if (chunks < 1 || chunks > 65535 || chunks * record_bytes >= gemm::kMaxBufferOffset) return 0;
+    if (size_t(a.heads) > a.counter_count || a.counters == nullptr || a.workspace == nullptr ||
+        size_t(a.heads * chunks * record_bytes) > a.workspace_bytes)
+        return 0;
+    return chunks;
+}
 
 }  // namespace
 
 hipError_t launch_causal_attention(const CausalAttentionArgs& a, hipStream_t stream) {
     if (a.heads == 0 || a.queries == 0) return hipSuccess;
+    if (const int64_t chunks = decode_chunks(a); chunks > 0) {
+        DecodeArgs args;
+        args.q = a.q;
+        args.k = a.k;
+        args.v = a.v;
+        args.o = a.o;
+        args.ws = a.workspace;
+        args.counters = a.counters;
+        args.queries = a.queries;
+        args.keys = a.keys;
+        args.q_stride = a.q_stride;
+        args.kv_stride = a.kv_stride;
+        args.query_offset = a.query_offset;
+        args.chunks = int32_t(chunks);
+        args.scale = a.scale;
+        const dim3 grid(unsigned(chunks), unsigned(a.heads));
+        auto launch = [&](auto h) {
+            constexpr int H = decltype(h)::value;
+            if (a.queries == 1)
+                hipLaunchKernelGGL((decode_attention_kernel<H, 1>), grid, dim3(kDecodeThreads), 0, stream, args);
+            else if (a.queries == 2)
+                hipLaunchKernelGGL((decode_attention_kernel<H, 2>), grid, dim3(kDecodeThreads), 0, stream, args);
+            else
+                hipLaunchKernelGGL((decode_attention_kernel<H, 4>), grid, dim3(kDecodeThreads), 0, stream, args);
+        };
+        switch (a.head_dim) {
+            case 32: launch(std::integral_constant<int, 32>{}); break;
+            case 64: launch(std::integral_constant<int, 64>{}); break;
+            case 128: launch(std::integral_constant<int, 128>{}); break;
+            default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
     AttentionArgs args;
     args.q = a.q;
     args.k = a.k;

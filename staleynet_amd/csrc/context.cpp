@@ -559,6 +559,10 @@ int sn_causal_attention(sn_context* ctx, const sn_attention_shape* shape, const 
     args.kv_stride = int64_t(a.heads > 1 ? a.kv_stride : kv_rows);
     args.query_offset = int64_t(a.query_offset);
     args.scale = a.scale;
+    args.workspace = ctx->env.workspace;
+    args.workspace_bytes = ctx->env.workspace_bytes;
+    args.counters = ctx->env.counters;
+    args.counter_count = ctx->env.counter_count;
     if (!sn::causal_attention_supported(args)) return SN_ERR_UNSUPPORTED;
     hipError_t err = hipSetDevice(ctx->device);
     if (err == hipSuccess) err = sn::launch_causal_attention(args, ctx->stream);

@@ -66,6 +66,12 @@ struct CausalAttentionArgs {
     int64_t q_stride = 0, kv_stride = 0;
     int64_t query_offset = 0;
     float scale = 1.f;
+    // The context's workspace and arrival counters: the decode form (at most
+    // 4 queries per head, no probabilities) keeps per-chunk records there.
+    float* workspace = nullptr;
+    size_t workspace_bytes = 0;
+    uint32_t* counters = nullptr;
+    size_t counter_count = 0;
 };
 hipError_t launch_causal_attention(const CausalAttentionArgs& args, hipStream_t stream);
 // Head dims 32, 64, 128; 16-byte aligned pointers and strides; per-head

@@ -95,6 +95,34 @@ def test_decode_query_against_a_partly_written_cache(gpu):
     assert oracle.relative_error(ep, gp) < TOLERANCE
 
 
+@pytest.mark.parametrize("heads,queries,keys,h,offset,kv_stride", [
+    (12, 1, 1408, 64, 700, None),    # a decode step: 701 of 1408 cached positions (11 key chunks)
+    (12, 1, 1408, 64, 1407, None),   # a full cache (22 chunks)
+    (12, 1, 1408, 64, 0, None),      # the first position: one key
+    (3, 4, 300, 32, 100, None),      # four new positions, head dim 32
+    (2, 3, 2000, 128, 1990, None),   # head dim 128, keys run out before the last query's horizon
+    (2, 2, 64, 64, 0, None),         # one chunk; the queries see 1 and 2 keys
+    (4, 1, 500, 64, 499, 0),         # K and V shared by every head
+])
+def test_decode_form_matches_the_three_calls(gpu, heads, queries, keys, h, offset, kv_stride):
+    # At most 4 queries per head and no probabilities: the keys are split into 64-key chunks
+    # whose partial softmax sums and outputs the last chunk of each head merges.
+    q_stride = queries * h
+    kv_stride = keys * h if kv_stride is None else kv_stride
+    eo, go, _, _ = run(gpu, heads, queries, keys, h, 0.125, offset, q_stride=q_stride, kv_stride=kv_stride,
+                       seed=heads + queries + keys, with_p=False)
+    assert np.all(np.isfinite(go))
+    assert oracle.relative_error(eo, go) < TOLERANCE
+
+
+def test_decode_form_is_deterministic_and_reusable(gpu):
+    # Repeated calls (the arrival counters are reset by each call's last chunk) give the same bits.
+    first = run(gpu, 12, 1, 1408, 64, 0.125, 1000, q_stride=64, kv_stride=1408 * 64, seed=21, with_p=False)[1]
+    for _ in range(3):
+        again = run(gpu, 12, 1, 1408, 64, 0.125, 1000, q_stride=64, kv_stride=1408 * 64, seed=21, with_p=False)[1]
+        assert np.array_equal(first, again)
+
+
 def test_keys_and_values_shared_by_every_head(gpu):
     eo, go, ep, gp = run(gpu, 3, 64, 64, 64, 0.125, 0, kv_stride=0, seed=4)
     assert oracle.relative_error(eo, go) < TOLERANCE
