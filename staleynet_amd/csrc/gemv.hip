@@ -321,13 +321,25 @@ __global__ __launch_bounds__(64 * waves_for<MT>()) void gemv_kernel(GemvArgs arg
     if (!arrived_last) return;
 
     // Last to arrive: every slice's partials are complete; add them in slice
-    // order (device-coherent loads) and apply the combine.
+    // order (device-coherent loads, up to 16 slices' in flight at once: the
+    // decode products split K into 3 to 16 slices, and each round trip is
+    // most of a microsecond) and apply the combine.
     if (out_ok) {
+        constexpr int kBatch = 16;
         const __amdgpu_buffer_rsrc_t all = gemm::buffer_of(args.ws + batch * args.splits * per_matrix + n0);
         f32x4 sum = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-        for (int s = 0; s < args.splits; ++s)
-            sum += gemm::buffer_load4_coherent(all, int32_t((s * per_matrix + om * args.n + 4 * oc) * 4));
+        for (int s0 = 0; s0 < args.splits; s0 += kBatch) {
+            f32x4 part[kBatch];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                const int s = s0 + u;
+                part[u] = gemm::buffer_load4_coherent(
+                    all, s < args.splits ? int32_t((s * per_matrix + om * args.n + 4 * oc) * 4) : gemm::kOutOfRange);
+            }
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u)
+                if (s0 + u < args.splits) sum += part[u];
+        }
         float* dst = args.y + batch * args.stride_y + om * args.n + out_col;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
