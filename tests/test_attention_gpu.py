@@ -96,16 +96,18 @@ def test_decode_query_against_a_partly_written_cache(gpu):
 
 
 @pytest.mark.parametrize("heads,queries,keys,h,offset,kv_stride", [
-    (12, 1, 1408, 64, 700, None),    # a decode step: 701 of 1408 cached positions (11 key chunks)
-    (12, 1, 1408, 64, 1407, None),   # a full cache (22 chunks)
+    (12, 1, 1408, 64, 700, None),    # a decode step: 701 of 1408 cached positions (6 key chunks)
+    (12, 1, 1408, 64, 1407, None),   # a full cache (11 chunks)
     (12, 1, 1408, 64, 0, None),      # the first position: one key
-    (3, 4, 300, 32, 100, None),      # four new positions, head dim 32
+    (3, 4, 300, 32, 100, None),      # four new positions, head dim 32 (one chunk)
+    (3, 4, 700, 32, 600, None),      # four new positions over 5 chunks
+    (2, 2, 900, 64, 800, None),      # two new positions over 7 chunks
     (2, 3, 2000, 128, 1990, None),   # head dim 128, keys run out before the last query's horizon
     (2, 2, 64, 64, 0, None),         # one chunk; the queries see 1 and 2 keys
     (4, 1, 500, 64, 499, 0),         # K and V shared by every head
 ])
 def test_decode_form_matches_the_three_calls(gpu, heads, queries, keys, h, offset, kv_stride):
-    # At most 4 queries per head and no probabilities: the keys are split into 64-key chunks
+    # At most 4 queries per head and no probabilities: the keys are split into 128-key chunks
     # whose partial softmax sums and outputs the last chunk of each head merges.
     q_stride = queries * h
     kv_stride = keys * h if kv_stride is None else kv_stride
