@@ -95,6 +95,9 @@ struct GemvArgs {
     float* ws;
     uint32_t* counters;
     int64_t m, n, k;
+    int64_t k_limit;       // keys actually multiplied: k, or the last row's horizon + 1 (causal left)
+    int64_t query_offset;  // causal left: x[m][k] counts only for k <= m + query_offset
+    int32_t causal_left;
     int64_t stride_x, stride_w, stride_y;
     int64_t k_per_split;
     int32_t column_blocks;
@@ -127,7 +130,7 @@ __global__ __launch_bounds__(64 * waves_for<MT>()) void gemv_kernel(GemvArgs arg
     const int64_t batch = blockIdx.z;
     const int64_t n0 = int64_t(blockIdx.x) * kColumns;
     const int64_t k_begin = int64_t(split) * args.k_per_split;
-    const int64_t k_end = min(args.k, k_begin + args.k_per_split);
+    const int64_t k_end = min(args.k_limit, k_begin + args.k_per_split);
     const int passes = int((k_end - k_begin + kPassRows - 1) / kPassRows);
 
     const float* x = args.x + batch * args.stride_x;
@@ -169,7 +172,9 @@ __global__ __launch_bounds__(64 * waves_for<MT>()) void gemv_kernel(GemvArgs arg
             const int e = tid + i * kThreads;
             const int r = e / MT;
             const int m = e % MT;
-            const bool ok = m < args.m && k0 + r < k_end;
+            // Causal left: the stored left matrix is 0 past row m's horizon
+            // (the tiled kernels zero it in LDS the same way).
+            const bool ok = m < args.m && k0 + r < k_end && (!args.causal_left || k0 + r <= m + args.query_offset);
             xs[i] = gemm::buffer_load1(x_rsrc, ok ? int32_t((m * args.k + k0 + r) * 4) : gemm::kOutOfRange);
         }
     };
@@ -363,24 +368,33 @@ int64_t pass_rows_for(int64_t m) {
                                                                                : pass_rows<16, LPR>();
 }
 
+// Keys a product multiplies: all K, or with a causal left mask up to the last
+// row's horizon (the left matrix is 0 past it, and the right operand's rows
+// there, such as an unwritten cache tail, are not read).
+int64_t keys_used(const Problem& p) {
+    if (p.mask != SN_MASK_CAUSAL_LEFT) return p.k;
+    return std::max<int64_t>(1, std::min(p.k, p.m - 1 + p.query_offset + 1));
+}
+
 GemvPlan gemv_plan(const Problem& p) {
+    const int64_t k = keys_used(p);
     GemvPlan plan;
     plan.lanes_per_row = 16;
     plan.pass_rows = pass_rows_for<16>(p.m);
     plan.column_blocks = int((p.n + 63) / 64);
     const int64_t slabs = int64_t(plan.column_blocks) * p.batch;
-    int64_t rows_per_split = std::max<int64_t>(p.k, 1);
+    int64_t rows_per_split = std::max<int64_t>(k, 1);
     if (slabs < kUnsplitSlabs) {
         // Enough slices for about `target` workgroups, each a whole
         // number of 16-row groups (4 waves x 4 rows; on the 8-wave path a
         // slice's last group may leave waves idle).
-        const int64_t groups = (std::max<int64_t>(p.k, 1) + 15) / 16;
+        const int64_t groups = (std::max<int64_t>(k, 1) + 15) / 16;
         const int64_t target = p.m <= 4 ? kSplitTargetFewRows : kSplitTargetManyRows;
         const int64_t want = std::min<int64_t>(groups, (target + slabs - 1) / slabs);
         rows_per_split = 16 * ((groups + want - 1) / want);
     }
     plan.k_per_split = rows_per_split;
-    plan.splits = int((std::max<int64_t>(p.k, 1) + rows_per_split - 1) / rows_per_split);
+    plan.splits = int((std::max<int64_t>(k, 1) + rows_per_split - 1) / rows_per_split);
     return plan;
 }
 
@@ -395,6 +409,9 @@ hipError_t launch_rows(const Problem& p, const Env& env, const GemvPlan& plan, h
     args.m = p.m;
     args.n = p.n;
     args.k = p.k;
+    args.k_limit = keys_used(p);
+    args.query_offset = p.query_offset;
+    args.causal_left = p.mask == SN_MASK_CAUSAL_LEFT ? 1 : 0;
     args.stride_x = p.stride_a;
     args.stride_w = p.stride_b;
     args.stride_y = p.stride_c;
@@ -422,9 +439,11 @@ hipError_t launch_width(const Problem& p, const Env& env, const GemvPlan& plan, 
 
 bool gemv_applies(const Problem& p, const Env& env) {
     // Row-major x (K-contiguous) and row-major W (N-contiguous), aligned for
-    // 16-byte loads; no mask; few rows; grid dimensions, counters and the
-    // split-K workspace large enough; a pass's offsets within 31 bits.
-    if (!(p.m >= 1 && p.m <= kMaxRows && p.k >= 1 && p.mask == SN_MASK_NONE && p.a_k_contiguous &&
+    // 16-byte loads; no mask or a causal left mask; few rows; grid
+    // dimensions, counters and the split-K workspace large enough; a pass's
+    // offsets within 31 bits.
+    if (!(p.m >= 1 && p.m <= kMaxRows && p.k >= 1 && (p.mask == SN_MASK_NONE || p.mask == SN_MASK_CAUSAL_LEFT) &&
+          p.a_k_contiguous &&
           !p.b_k_contiguous && p.lda == p.k && p.ldb == p.n && p.n % 4 == 0 && p.stride_b % 4 == 0 &&
           gemm::aligned16(p.b) && p.batch <= 65535 && p.n < (int64_t(1) << 30)))
         return false;

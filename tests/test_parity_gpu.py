@@ -276,6 +276,27 @@ def test_causal_left_mask(gpu, offset, transposed):
     check(expected, simple, 1e-6)
 
 
+@pytest.mark.parametrize("m,offset", [(1, 700), (4, 300), (16, 40)])
+def test_causal_left_few_rows_skip_the_masked_part_and_the_unwritten_tail(gpu, m, offset):
+    # The decode mix (attention.rs:314-316) on the few-row path: P [m, capacity] holds garbage past
+    # row r's horizon r + offset, and V's rows past the last row's horizon are an unwritten cache
+    # tail (NaN here): neither may reach the result.
+    capacity, h, count = 1408, 64, 3
+    p = oracle.random_values(count * m * capacity, 40).reshape(count, m, capacity)
+    visible = causal_visible(m, capacity, offset)
+    p_clean = np.where(visible, p, 0).astype(np.float32)
+    p_dirty = np.where(visible, p, 1e4).astype(np.float32)
+    v = oracle.random_values(count * capacity * h, 41).reshape(count, capacity, h)
+    v_dirty = v.copy()
+    v_dirty[:, m + offset:, :] = np.nan
+    spec = MatmulSpec.new(m, h, capacity).batched(BatchStrides(count, m * capacity, capacity * h, m * h))
+    initial = np.zeros(count * m * h, np.float32)
+    expected = expected_for(spec, p_clean.ravel(), v.ravel(), initial)
+    actual = run_gpu(gpu, spec.causal_left(offset), p_dirty.ravel(), v_dirty.ravel(), initial)
+    assert np.all(np.isfinite(actual))
+    check(expected, actual, 1e-5)
+
+
 # ---- bf16-input variant ---------------------------------------------------------
 
 @pytest.mark.parametrize("variant", ["NN", "TN", "NT", "TT"])
