@@ -349,6 +349,8 @@ int matmul_with_bias(sn_context* ctx, const sn_matmul_spec* spec, const float* l
         err = sn::launch_gemm_simple(p, ctx->stream);
     } else if (!bf16 && sn::gemv_applies(p, ctx->env)) {
         err = sn::launch_gemv(p, ctx->env, ctx->stream);
+    } else if (!bf16 && sn::gemv_nt_applies(p)) {
+        err = sn::launch_gemv_nt(p, ctx->stream);
     } else {
         if (sn::gemm_workspace_bytes(p, bf16, ctx->env) > ctx->env.workspace_bytes) return SN_ERR_WORKSPACE;
         err = bf16 ? sn::launch_gemm_bf16(p, ctx->env, ctx->stream) : sn::launch_gemm_f32(p, ctx->env, ctx->stream);

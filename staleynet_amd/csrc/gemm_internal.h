@@ -50,6 +50,10 @@ hipError_t launch_gemm_simple(const Problem& p, hipStream_t stream);
 // hipErrorNotSupported when the shape is not one it handles.
 hipError_t launch_gemv(const Problem& p, const Env& env, hipStream_t stream);
 bool gemv_applies(const Problem& p, const Env& env);
+// Products of at most 4 rows against a right operand stored [n][k] (the
+// decode step's scores against the cache); hipErrorNotSupported otherwise.
+hipError_t launch_gemv_nt(const Problem& p, hipStream_t stream);
+bool gemv_nt_applies(const Problem& p);
 
 // Fused causal attention forward (attention.hip): O = causal_softmax(scale *
 // Q K^T) V per head, and optionally the probabilities P. Q [heads][queries]

@@ -435,6 +435,91 @@ hipError_t launch_width(const Problem& p, const Env& env, const GemvPlan& plan, 
     return launch_rows<16, LPR>(p, env, plan, stream);
 }
 
+// Few-row products against a K-contiguous right operand (right_transposed):
+// the decode step's attention scores against the cache (attention.rs:307-310,
+// MatmulSpec::new(n, capacity, h).right_transposed()), where each output is
+// the dot product of one of x's rows with one of B's rows. The tiled kernels
+// would spend a 128x128 tile per 128 keys on a single row. Here 16 lanes read
+// a row of B 16 bytes at a time (a 256-thread workgroup covers 64 rows of B
+// in 4 passes), each lane keeps 4-term dot products per row of x, and an xor
+// butterfly over the 16 lanes sums them. Outputs past a causal mask's
+// horizon are written 0 (or left alone when accumulating); rows of B past
+// the last row's horizon are not read.
+constexpr int kNtRows = 64;      // rows of B per workgroup
+constexpr int kNtMaxRows = 4;    // rows of x
+
+struct GemvNtArgs {
+    const float* x;  // [m][k], rows k floats apart
+    const float* w;  // B stored [n][k], rows ldb floats apart
+    float* y;        // [m][n]
+    int64_t m, n, k, ldb;
+    int64_t n_limit;  // rows of B any output needs (n, or the last row's horizon + 1 under the mask)
+    int64_t stride_x, stride_w, stride_y;
+    int64_t query_offset;
+    int32_t causal;
+    int32_t accumulate;
+    float scale;
+};
+
+template <int MT>
+__global__ __launch_bounds__(256) void gemv_nt_kernel(GemvNtArgs a) {
+#pragma clang fp contract(off)
+    const int tid = threadIdx.x;
+    const int li = tid % 16;    // 16-byte piece of a row
+    const int slot = tid / 16;  // row of B within a pass
+    const int64_t batch = blockIdx.y;
+    const int64_t n_base = int64_t(blockIdx.x) * kNtRows;
+    const float* x = a.x + batch * a.stride_x;
+    const float* w = a.w + batch * a.stride_w;
+    float* y = a.y + batch * a.stride_y;
+    float acc[4][MT];
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+        for (int j = 0; j < MT; ++j) acc[p][j] = 0.f;
+    for (int64_t k0 = 4 * li; k0 < a.k; k0 += 64) {
+        f32x4 xv[MT];
+#pragma unroll
+        for (int j = 0; j < MT; ++j)
+            xv[j] = j < a.m ? *reinterpret_cast<const f32x4*>(x + j * a.k + k0) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int64_t row = n_base + 16 * p + slot;
+            if (row < a.n_limit) {
+                const f32x4 bv = *reinterpret_cast<const f32x4*>(w + row * a.ldb + k0);
+#pragma unroll
+                for (int j = 0; j < MT; ++j) {
+                    float d = bv[0] * xv[j][0];
+#pragma unroll
+                    for (int e = 1; e < 4; ++e) d = d + bv[e] * xv[j][e];
+                    acc[p][j] = acc[p][j] + d;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+        for (int j = 0; j < MT; ++j)
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) acc[p][j] = acc[p][j] + __shfl_xor(acc[p][j], o);
+    // Lane j of each row's 16 writes x row j's output for that row of B.
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const int64_t row = n_base + 16 * p + slot;
+#pragma unroll
+        for (int j = 0; j < MT; ++j) {
+            if (li != j || j >= a.m || row >= a.n) continue;
+            float* dst = y + j * a.n + row;
+            if (a.causal && row > j + a.query_offset) {
+                if (!a.accumulate) *dst = 0.f;
+            } else {
+                gemm::write_output(dst, acc[p][j], a.scale, a.accumulate != 0);
+            }
+        }
+    }
+}
+
 }  // namespace
 
 bool gemv_applies(const Problem& p, const Env& env) {
@@ -456,6 +541,45 @@ bool gemv_applies(const Problem& p, const Env& env) {
     const size_t partials = size_t(plan.splits) * size_t(p.batch) * size_t(p.m) * size_t(p.n) * sizeof(float);
     return plan.splits <= 65535 && partials <= env.workspace_bytes &&
            size_t(p.batch) * size_t(plan.column_blocks) <= env.counter_count;
+}
+
+bool gemv_nt_applies(const Problem& p) {
+    // Row-major x, B stored [n][k] (right transposed), both 16-byte aligned
+    // with k and the strides multiples of 4; at most kNtMaxRows rows; no mask
+    // or a causal output mask; no fused bias; the grid within limits.
+    return p.m >= 1 && p.m <= kNtMaxRows && p.k >= 1 && p.k % 4 == 0 &&
+           (p.mask == SN_MASK_NONE || p.mask == SN_MASK_CAUSAL_OUTPUT) && p.bias == nullptr && p.a_k_contiguous &&
+           p.b_k_contiguous && p.lda == p.k && p.ldb % 4 == 0 && p.stride_a % 4 == 0 && p.stride_b % 4 == 0 &&
+           gemm::aligned16(p.a) && gemm::aligned16(p.b) && p.batch <= 65535 &&
+           (p.n + kNtRows - 1) / kNtRows <= 0x7FFFFFFF;
+}
+
+hipError_t launch_gemv_nt(const Problem& p, hipStream_t stream) {
+    if (!gemv_nt_applies(p)) return hipErrorNotSupported;
+    GemvNtArgs a;
+    a.x = p.a;
+    a.w = p.b;
+    a.y = p.c;
+    a.m = p.m;
+    a.n = p.n;
+    a.k = p.k;
+    a.ldb = p.ldb;
+    a.n_limit = p.mask == SN_MASK_CAUSAL_OUTPUT ? std::min(p.n, p.m - 1 + p.query_offset + 1) : p.n;
+    a.stride_x = p.stride_a;
+    a.stride_w = p.stride_b;
+    a.stride_y = p.stride_c;
+    a.query_offset = p.query_offset;
+    a.causal = p.mask == SN_MASK_CAUSAL_OUTPUT ? 1 : 0;
+    a.accumulate = p.accumulate ? 1 : 0;
+    a.scale = p.scale;
+    const dim3 grid(unsigned((p.n + kNtRows - 1) / kNtRows), unsigned(p.batch));
+    if (p.m == 1)
+        hipLaunchKernelGGL(gemv_nt_kernel<1>, grid, dim3(256), 0, stream, a);
+    else if (p.m == 2)
+        hipLaunchKernelGGL(gemv_nt_kernel<2>, grid, dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL(gemv_nt_kernel<4>, grid, dim3(256), 0, stream, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_gemv(const Problem& p, const Env& env, hipStream_t stream) {

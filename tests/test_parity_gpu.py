@@ -297,6 +297,38 @@ def test_causal_left_few_rows_skip_the_masked_part_and_the_unwritten_tail(gpu, m
     check(expected, actual, 1e-5)
 
 
+@pytest.mark.parametrize("m,k,offset,accumulate", [(1, 64, 700, False), (3, 200, 90, True), (4, 128, 0, False),
+                                                    (2, 64, None, True), (3, 130, 50, False)])
+def test_few_rows_against_a_transposed_right_operand(gpu, m, k, offset, accumulate):
+    # The decode scores S = q K^T against the cache (attention.rs:307-310): at most 4 rows of x
+    # against B stored [n][k]. K a multiple of 4 takes the few-row kernel (several 64-float chunks at
+    # k = 128, 200); k = 130 takes the tiled kernels. With the causal output mask, rows of B past the
+    # last row's horizon are an unwritten cache tail (NaN here) and are not read; masked outputs are
+    # 0 (overwrite) or left as they were (accumulate).
+    n, count = 1408, 3
+    x = oracle.random_values(count * m * k, 50)
+    b = oracle.random_values(count * n * k, 51).reshape(count, n, k)
+    spec = MatmulSpec.new(m, n, k).right_transposed().batched(BatchStrides(count, m * k, n * k, m * n)).scaled(0.125)
+    if accumulate:
+        spec = spec.accumulate()
+    initial = oracle.random_values(count * m * n, 52)
+    expected = expected_for(spec, x, b.ravel(), initial).reshape(count, m, n)
+    if offset is None:
+        actual = run_gpu(gpu, spec, x, b.ravel(), initial).reshape(count, m, n)
+        check(expected.ravel(), actual.ravel(), 1e-5)
+        return
+    b_dirty = b.copy()
+    b_dirty[:, m + offset:, :] = np.nan
+    actual = run_gpu(gpu, spec.causal_output(offset), x, b_dirty.ravel(), initial).reshape(count, m, n)
+    visible = np.broadcast_to(causal_visible(m, n, offset), actual.shape)
+    check(expected[visible], actual[visible], 1e-5)
+    masked = actual[~visible]
+    if accumulate:
+        assert np.array_equal(masked, initial.reshape(count, m, n)[~visible])
+    else:
+        assert np.all(masked == 0.0)
+
+
 # ---- bf16-input variant ---------------------------------------------------------
 
 @pytest.mark.parametrize("variant", ["NN", "TN", "NT", "TT"])
