@@ -1,8 +1,9 @@
 """Captured sequences replay to the same results as eager calls.
 
-The decode bench replays a captured HIP graph of sn_matmul calls. This
-checks the library state a replay relies on: the split-K workspace and the
-arrival counters a few-row product resets itself. The graph is replayed
+The decode bench replays a captured HIP graph of sn_matmul calls (and of
+decode-step attention). This checks the library state a replay relies on: the
+split-K workspace and the arrival counters a few-row product or a decode-form
+attention resets itself. The graph is replayed
 three times with eager work and synchronizations between the replays; each
 replay must equal the eager result bit for bit (every kernel sums in a fixed
 order)."""
@@ -57,6 +58,54 @@ def test_graph_replays_match_eager_results(gpu):
             gpu.matmul(MatmulSpec.new(64, 64, 64), ones, ones, other)
             gpu.matmul(MatmulSpec.new(2, 3072, 768), tensors[0][1], tensors[0][2], gpu.zeros(Shape(2, 3072)))
             reset()
+            gpu.synchronize()
+    finally:
+        graph.close()
+
+
+def test_graph_replays_of_a_decode_attention_step(gpu):
+    # One decode step's attention for two layers, as the reference calls it (masked scores against the
+    # cache, causal_softmax, masked mix: the few-row kernels) and through the fused decode form (key
+    # chunks merged through the workspace and arrival counters), captured once and replayed three
+    # times with eager work between the replays; each replay must equal the eager result bit for bit.
+    from staleynet_amd.gemm import BatchStrides
+
+    heads, capacity, h, cached = 12, 1408, 64, 900
+    offset = cached - 1
+    q = gpu.upload(Shape(heads, h), oracle.random_values(heads * h, 60))
+    k = gpu.upload(Shape(heads * capacity, h), oracle.random_values(heads * capacity * h, 61))
+    v = gpu.upload(Shape(heads * capacity, h), oracle.random_values(heads * capacity * h, 62))
+    scores = gpu.zeros(Shape(heads, capacity))
+    mixed, fused = gpu.zeros(Shape(heads, h)), gpu.zeros(Shape(heads, h))
+    score_spec = MatmulSpec.new(1, capacity, h).right_transposed().batched(
+        BatchStrides(heads, h, capacity * h, capacity)).causal_output(offset)
+    mix_spec = MatmulSpec.new(1, h, capacity).batched(BatchStrides(heads, capacity, capacity * h, h)).causal_left(offset)
+
+    def step():
+        for _ in range(2):
+            gpu.matmul(score_spec, q, k, scores)
+            gpu.causal_softmax(scores, 1, 0.125, offset)
+            gpu.matmul(mix_spec, scores, v, mixed)
+            gpu.causal_attention(q, k, v, fused, heads, 1, capacity, h, 0.125, query_offset=offset, q_stride=h,
+                                 kv_stride=capacity * h)
+
+    step()
+    eager = (gpu.download(mixed), gpu.download(fused))
+    assert oracle.relative_error(eager[0], eager[1]) < 1e-5
+    graph = HipGraph(gpu.stream, step)
+    try:
+        for replay in range(3):
+            for t in (scores, mixed, fused):
+                gpu.fill_zero(t)
+            graph.launch()
+            gpu.synchronize()
+            assert np.array_equal(gpu.download(mixed), eager[0]), f"replay {replay}: three calls"
+            assert np.array_equal(gpu.download(fused), eager[1]), f"replay {replay}: fused"
+            # Eager work between replays on the same workspace and counters.
+            gpu.causal_attention(q, k, v, gpu.zeros(Shape(heads, h)), heads, 1, capacity, h, 0.125, query_offset=100,
+                                 q_stride=h, kv_stride=capacity * h)
+            gpu.matmul(MatmulSpec.new(2, 3072, 768), gpu.zeros(Shape(2, 768)), gpu.zeros(Shape(768, 3072)),
+                       gpu.zeros(Shape(2, 3072)))
             gpu.synchronize()
     finally:
         graph.close()
