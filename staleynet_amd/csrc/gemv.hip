@@ -68,6 +68,8 @@ constexpr int kUnsplitSlabs = 256;
 // and read back, so fewer than one per CU: measured on the c4 layer weights,
 // 128 (M <= 4) and 192 (M = 16) beat both 48 and 512.
 constexpr int kSplitTargetFewRows = 128;
+constexpr int kSplitTargetFewRowsNarrow = 96;
+constexpr int kNarrowSlabs = 16;
 constexpr int kSplitTargetManyRows = 192;
 
 // Rows of x from which the products go to the matrix cores: 16 output rows
@@ -389,7 +391,10 @@ GemvPlan gemv_plan(const Problem& p) {
         // number of 16-row groups (4 waves x 4 rows; on the 8-wave path a
         // slice's last group may leave waves idle).
         const int64_t groups = (std::max<int64_t>(k, 1) + 15) / 16;
-        const int64_t target = p.m <= 4 ? kSplitTargetFewRows : kSplitTargetManyRows;
+        // Narrow weights (16 column blocks or fewer: the 768-wide out and down
+        // products) do better with fewer, longer slices when there are few rows.
+        const int64_t target = p.m > 4 ? kSplitTargetManyRows
+                               : slabs <= kNarrowSlabs ? kSplitTargetFewRowsNarrow : kSplitTargetFewRows;
         const int64_t want = std::min<int64_t>(groups, (target + slabs - 1) / slabs);
         rows_per_split = 16 * ((groups + want - 1) / want);
     }
