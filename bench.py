@@ -51,12 +51,44 @@ SEED = 1234
 METRIC = "GEMM TFLOP/s and % fp32 MFMA peak (111.5M train set); decode GEMV GB/s, 1 GPU"
 
 
+_HIP = None
+
+
+def hip_runtime() -> ctypes.CDLL:
+    """libamdhip64 with the signature of every entry point this file calls declared, so
+    handles and sizes cross the ctypes boundary at their C widths (hipError_t results are
+    C ints)."""
+    global _HIP
+    if _HIP is None:
+        hip = ctypes.CDLL("libamdhip64.so")
+        handle, handle_p = ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)
+        signatures = {
+            "hipEventCreate": [handle_p],
+            "hipEventRecord": [handle, handle],
+            "hipEventSynchronize": [handle],
+            "hipEventElapsedTime": [ctypes.POINTER(ctypes.c_float), handle, handle],
+            "hipEventDestroy": [handle],
+            "hipDeviceSynchronize": [],
+            "hipStreamBeginCapture": [handle, ctypes.c_int],
+            "hipStreamEndCapture": [handle, handle_p],
+            "hipGraphInstantiate": [handle_p, handle, handle_p, ctypes.c_char_p, ctypes.c_size_t],
+            "hipGraphLaunch": [handle, handle],
+            "hipGraphExecDestroy": [handle],
+            "hipGraphDestroy": [handle],
+        }
+        for name, argtypes in signatures.items():
+            function = getattr(hip, name)
+            function.argtypes = argtypes
+            function.restype = ctypes.c_int
+        _HIP = hip
+    return _HIP
+
+
 class HipEvents:
     """hipEvent timing on an explicit stream (the library's own)."""
 
     def __init__(self):
-        self.hip = ctypes.CDLL("libamdhip64.so")
-        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.hip = hip_runtime()
 
     def create(self) -> ctypes.c_void_p:
         event = ctypes.c_void_p()
@@ -88,7 +120,7 @@ class HipGraph:
     CAPTURE_RELAXED = 2
 
     def __init__(self, stream: int, record):
-        hip = ctypes.CDLL("libamdhip64.so")
+        hip = hip_runtime()
         self.hip, self.stream = hip, ctypes.c_void_p(stream)
         graph = ctypes.c_void_p()
         assert hip.hipStreamBeginCapture(self.stream, self.CAPTURE_RELAXED) == 0
@@ -98,7 +130,7 @@ class HipGraph:
             assert hip.hipStreamEndCapture(self.stream, ctypes.byref(graph)) == 0
         self.graph = graph
         self.exec = ctypes.c_void_p()
-        assert hip.hipGraphInstantiate(ctypes.byref(self.exec), graph, None, None, 0) == 0
+        assert hip.hipGraphInstantiate(ctypes.byref(self.exec), graph, None, None, ctypes.c_size_t(0)) == 0
 
     def launch(self) -> None:
         assert self.hip.hipGraphLaunch(self.exec, self.stream) == 0

@@ -377,6 +377,62 @@ int sn_upload_tokens(sn_context *context, const uint32_t *host, size_t count, ui
 int sn_download_tokens(sn_context *context, const uint32_t *device, size_t count, uint32_t *host);
 int sn_free_tokens(sn_context *context, uint32_t *buffer);
 
+/* ---- launch geometry (host only) ------------------------------------------ */
+/* The kernel family a product runs on, as sn_plan_matmul reports it. */
+#define SN_PATH_NONE 0u            /* rows or cols of 0: nothing is launched */
+#define SN_PATH_REFERENCE_ORDER 1u /* SN_KERNEL_SIMPLE: one thread per output */
+#define SN_PATH_FEW_ROWS 2u        /* decode GEMV: at most 16 rows, right operand row-major */
+#define SN_PATH_FEW_ROWS_NT 3u     /* at most 4 rows against a right operand stored [cols][inner] */
+#define SN_PATH_F32_DIRECT 4u      /* fp32 tiles, operands loaded straight into LDS */
+#define SN_PATH_F32_REGISTER 5u    /* fp32 tiles, operands staged through registers (unaligned) */
+#define SN_PATH_BF16_STAGED 6u     /* bf16: both operands first rounded into the workspace */
+#define SN_PATH_BF16_DIRECT 7u     /* bf16: fp32 LDS stages rounded per fragment */
+#define SN_PATH_BF16_REGISTER 8u   /* bf16: register-staged (unaligned) operands */
+
+/* How one product is launched: the role of the reference's launch geometry
+ * (`launch::matmul_tiles` / `matmul_blocks`, crates/staleynet-cuda/src/
+ * launch.rs:28-48), for this library's kernels. A launch holds
+ * `batches_per_launch` matrices of the batch; each matrix is split into
+ * `splits` slices of `k_per_split` inner elements and tiles_m x tiles_n
+ * output tiles of tile_rows x tile_cols (for the few-row paths: tiles_n
+ * column blocks, or blocks of rows of the right operand, and tiles_m = 1).
+ * A tiled launch's workgroup w covers the (matrix, slice, tile) that
+ * sn_tile_map gives for it. */
+typedef struct sn_launch_plan {
+    uint32_t path;                /* SN_PATH_* */
+    uint32_t threads;             /* threads per workgroup */
+    uint32_t tile_rows, tile_cols;
+    uint32_t tiles_m, tiles_n;
+    uint32_t splits;
+    uint32_t reserved;            /* 0 */
+    uint64_t k_per_split;
+    uint64_t batches_per_launch;
+    uint64_t workgroups;          /* of one launch holding batches_per_launch matrices */
+    uint64_t launches;            /* kernel launches of the product (split-K reduce not counted) */
+    uint64_t workspace_bytes;     /* split-K partial sums and staged operands */
+} sn_launch_plan;
+
+/* The plan sn_matmul would follow for `spec` with context kernel `kernel`
+ * (SN_KERNEL_*) on a device of `cu_count` compute units whose context has a
+ * workspace of `workspace_bytes`: pure host code, no device needed. The
+ * operand addresses are only inspected for alignment (a path may need
+ * 16-byte aligned operands); they are never dereferenced. Returns the
+ * status sn_matmul_validate would, with every operand length taken as
+ * sufficient; SN_ERR_WORKSPACE when the product would not fit. */
+int sn_plan_matmul(const sn_matmul_spec *spec, uint32_t kernel, const float *left, const float *right,
+                   const float *output, uint32_t cu_count, size_t workspace_bytes, sn_launch_plan *plan);
+
+/* The tiled kernels' map from workgroup id to (matrix of the launch, K
+ * slice, tile row, tile column), for workgroups 0 .. workgroups - 1 of a
+ * launch of `workgroups` over tiles_m x tiles_n tiles and `splits` slices
+ * per matrix: the same function the kernels evaluate on the device. Ids are
+ * regrouped so that each of the 8 XCDs (which receive workgroups
+ * round-robin) holds a contiguous range. Each output array holds
+ * `workgroups` entries. SN_ERR_NULL_ARGUMENT or SN_ERR_OVERFLOW (more than
+ * 2^31 workgroups, or a zero count). */
+int sn_tile_map(uint32_t workgroups, uint32_t tiles_m, uint32_t tiles_n, uint32_t splits, uint32_t *matrix,
+                uint32_t *slice, uint32_t *tile_row, uint32_t *tile_col);
+
 /* A short English description of a status code (never null). */
 const char *sn_status_string(int status);
 

@@ -785,11 +785,14 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attention_kernel(Decode
     const float* kh = a.k + head * a.kv_stride;
     const float* vh = a.v + head * a.kv_stride;
     const float* qh = a.q + head * a.q_stride;
+    // Keys the last query sees: rows of the cache past them (an unwritten
+    // tail, possibly NaN or Inf) are never read, since 0 * NaN would leak.
+    const int64_t visible = min(a.keys, a.queries + a.query_offset);
     f32x4 kr[D::PASSES], vr[D::PASSES], qr[NQ];
 #pragma unroll
     for (int i = 0; i < D::PASSES; ++i) {
         const int64_t key = key0 + i * D::ROWS + slot;
-        const bool ok = key < a.keys;
+        const bool ok = key < visible;
         kr[i] = ok ? *reinterpret_cast<const f32x4*>(kh + key * H + 4 * li) : f32x4{0.f, 0.f, 0.f, 0.f};
         vr[i] = ok ? *reinterpret_cast<const f32x4*>(vh + key * H + 4 * li) : f32x4{0.f, 0.f, 0.f, 0.f};
     }

@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <cstddef>
 #include <cstdint>
 #include <cstring>
 #include <new>
@@ -19,6 +20,23 @@ struct sn_context {
     uint32_t kernel = SN_KERNEL_MFMA_F32;
     sn::Env env;
 };
+
+// The C structs' layouts are part of the ABI a Rust #[repr(C)] binding
+// mirrors (x86-64 / aarch64 LP64): sizes and field offsets pinned here.
+static_assert(sizeof(sn_matmul_spec) == 88 && offsetof(sn_matmul_spec, left_storage) == 24 &&
+                  offsetof(sn_matmul_spec, batch_count) == 32 && offsetof(sn_matmul_spec, scale) == 64 &&
+                  offsetof(sn_matmul_spec, write) == 68 && offsetof(sn_matmul_spec, mask) == 72 &&
+                  offsetof(sn_matmul_spec, precision) == 76 && offsetof(sn_matmul_spec, query_offset) == 80,
+              "sn_matmul_spec layout");
+static_assert(sizeof(sn_attention_shape) == 64 && offsetof(sn_attention_shape, query_offset) == 48 &&
+                  offsetof(sn_attention_shape, scale) == 56,
+              "sn_attention_shape layout");
+static_assert(sizeof(sn_head_layout) == 64 && offsetof(sn_head_layout, time_offset) == 56, "sn_head_layout layout");
+static_assert(sizeof(sn_cross_entropy_head) == 40 && offsetof(sn_cross_entropy_head, grad_scale) == 32,
+              "sn_cross_entropy_head layout");
+static_assert(sizeof(sn_launch_plan) == 72 && offsetof(sn_launch_plan, k_per_split) == 32 &&
+                  offsetof(sn_launch_plan, workspace_bytes) == 64,
+              "sn_launch_plan layout");
 
 namespace {
 
@@ -291,6 +309,48 @@ int sn_matmul_validate(const sn_matmul_spec* spec, size_t left_len, size_t right
 
 namespace {
 
+// The kernels' description of a validated spec (ops/matmul.rs:24-32 for
+// the storage conventions), with `bias` (null: none) fused into the
+// epilogue unless the product is masked.
+sn::Problem problem_of(const sn_matmul_spec* spec, const float* left, const float* right, float* output,
+                       const float* bias) {
+    sn::Problem p;
+    p.a = left;
+    p.b = right;
+    p.c = output;
+    p.m = int64_t(spec->rows);
+    p.n = int64_t(spec->cols);
+    p.k = int64_t(spec->inner);
+    // Left [rows, inner]: row-major is K-contiguous (ld = inner); transposed
+    // storage keeps it as [inner, rows] (ld = rows). Right [inner, cols]:
+    // row-major is N-contiguous (ld = cols); transposed is [cols, inner],
+    // K-contiguous (ld = inner).
+    p.a_k_contiguous = spec->left_storage == SN_ROW_MAJOR;
+    p.lda = p.a_k_contiguous ? p.k : p.m;
+    p.b_k_contiguous = spec->right_storage == SN_TRANSPOSED;
+    p.ldb = p.b_k_contiguous ? p.k : p.n;
+    p.batch = int64_t(spec->batch_count);
+    p.stride_a = int64_t(spec->batch_left);
+    p.stride_b = int64_t(spec->batch_right);
+    p.stride_c = int64_t(spec->batch_output);
+    p.scale = spec->scale;
+    p.accumulate = spec->write == SN_ACCUMULATE;
+    p.mask = spec->mask;
+    p.query_offset = int64_t(spec->query_offset);
+    // A masked product takes its bias afterwards (the kernels fuse it only
+    // into unmasked epilogues).
+    p.bias = p.mask != SN_MASK_NONE ? nullptr : bias;
+    return p;
+}
+
+// The kernel a call runs: the context's choice, overridden by the spec's
+// precision.
+uint32_t kernel_for(uint32_t context_kernel, uint32_t precision) {
+    if (precision == SN_PRECISION_F32 && context_kernel == SN_KERNEL_MFMA_BF16) return SN_KERNEL_MFMA_F32;
+    if (precision == SN_PRECISION_BF16) return SN_KERNEL_MFMA_BF16;
+    return context_kernel;
+}
+
 // sn_matmul and sn_matmul_bias: validation, then the product with `bias`
 // (null: none) added in its epilogue, or, for a masked spec, after it by the
 // bias kernel.
@@ -310,51 +370,12 @@ int matmul_with_bias(sn_context* ctx, const sn_matmul_spec* spec, const float* l
     if (bias != nullptr && overlaps(output, need.output, bias, bias_len)) return SN_ERR_ALIASING;
     if (spec->rows == 0 || spec->cols == 0) return SN_OK;
 
-    sn::Problem p;
-    p.a = left;
-    p.b = right;
-    p.c = output;
-    p.m = int64_t(spec->rows);
-    p.n = int64_t(spec->cols);
-    p.k = int64_t(spec->inner);
-    // Left [rows, inner]: row-major is K-contiguous (ld = inner); transposed
-    // storage keeps it as [inner, rows] (ld = rows). Right [inner, cols]:
-    // row-major is N-contiguous (ld = cols); transposed is [cols, inner],
-    // K-contiguous (ld = inner). See ops/matmul.rs:24-32.
-    p.a_k_contiguous = spec->left_storage == SN_ROW_MAJOR;
-    p.lda = p.a_k_contiguous ? p.k : p.m;
-    p.b_k_contiguous = spec->right_storage == SN_TRANSPOSED;
-    p.ldb = p.b_k_contiguous ? p.k : p.n;
-    p.batch = int64_t(spec->batch_count);
-    p.stride_a = int64_t(spec->batch_left);
-    p.stride_b = int64_t(spec->batch_right);
-    p.stride_c = int64_t(spec->batch_output);
-    p.scale = spec->scale;
-    p.accumulate = spec->write == SN_ACCUMULATE;
-    p.mask = spec->mask;
-    p.query_offset = int64_t(spec->query_offset);
-    // A masked product takes its bias afterwards (the kernels fuse it only
-    // into unmasked epilogues).
-    const bool bias_after = bias != nullptr && p.mask != SN_MASK_NONE;
-    p.bias = bias_after ? nullptr : bias;
-
-    uint32_t kernel = ctx->kernel;
-    if (spec->precision == SN_PRECISION_F32 && kernel == SN_KERNEL_MFMA_BF16) kernel = SN_KERNEL_MFMA_F32;
-    if (spec->precision == SN_PRECISION_BF16) kernel = SN_KERNEL_MFMA_BF16;
-
+    const sn::Problem p = problem_of(spec, left, right, output, bias);
+    const bool bias_after = bias != nullptr && p.bias == nullptr;
+    const uint32_t kernel = kernel_for(ctx->kernel, spec->precision);
+    if (sn::describe_matmul(p, kernel, ctx->env).workspace_bytes > ctx->env.workspace_bytes) return SN_ERR_WORKSPACE;
     hipError_t err = hipSetDevice(ctx->device);
-    if (err != hipSuccess) return status(err);
-    const bool bf16 = kernel == SN_KERNEL_MFMA_BF16;
-    if (kernel == SN_KERNEL_SIMPLE) {
-        err = sn::launch_gemm_simple(p, ctx->stream);
-    } else if (!bf16 && sn::gemv_applies(p, ctx->env)) {
-        err = sn::launch_gemv(p, ctx->env, ctx->stream);
-    } else if (!bf16 && sn::gemv_nt_applies(p)) {
-        err = sn::launch_gemv_nt(p, ctx->stream);
-    } else {
-        if (sn::gemm_workspace_bytes(p, bf16, ctx->env) > ctx->env.workspace_bytes) return SN_ERR_WORKSPACE;
-        err = bf16 ? sn::launch_gemm_bf16(p, ctx->env, ctx->stream) : sn::launch_gemm_f32(p, ctx->env, ctx->stream);
-    }
+    if (err == hipSuccess) err = sn::launch_matmul(p, kernel, ctx->env, ctx->stream);
     if (err == hipSuccess && bias_after)
         err = sn::launch_add_row_bias(output, p.m, p.n, p.batch, p.stride_c, bias, ctx->stream);
     return status(err);
@@ -380,6 +401,40 @@ int sn_matmul_bias(sn_context* ctx, const sn_matmul_spec* spec, const float* lef
     if (spec->batch_count > 1 && spec->batch_output < spec->rows * spec->cols) return SN_ERR_UNSUPPORTED;
     if (ctx == nullptr || (bias == nullptr && bias_len > 0)) return SN_ERR_NULL_ARGUMENT;
     return matmul_with_bias(ctx, spec, left, left_len, right, right_len, bias, bias_len, output, output_len);
+}
+
+int sn_plan_matmul(const sn_matmul_spec* spec, uint32_t kernel, const float* left, const float* right,
+                   const float* output, uint32_t cu_count, size_t workspace_bytes, sn_launch_plan* plan) {
+    if (plan == nullptr) return SN_ERR_NULL_ARGUMENT;
+    std::memset(plan, 0, sizeof(*plan));
+    Lengths need;
+    const int rc = check_spec(spec, &need);
+    if (rc != SN_OK) return rc;
+    if (kernel > SN_KERNEL_SIMPLE) return SN_ERR_UNSUPPORTED;
+    const sn::Problem p = problem_of(spec, left, right, const_cast<float*>(output), nullptr);
+    // A context's environment as sn_context_create would set it up; the
+    // workspace and counters are never touched, only their sizes and the
+    // workspace's alignment matter (a device allocation is 2 MiB aligned).
+    sn::Env env;
+    env.cu_count = cu_count > 0 ? int(cu_count) : 256;
+    env.workspace_bytes = workspace_bytes;
+    env.workspace = workspace_bytes > 0 ? reinterpret_cast<float*>(uintptr_t(1) << 44) : nullptr;
+    env.counters = reinterpret_cast<uint32_t*>(uintptr_t(1) << 45);
+    env.counter_count = kCounterCount;
+    const sn::LaunchShape s = sn::describe_matmul(p, kernel_for(kernel, spec->precision), env);
+    plan->path = s.path;
+    plan->threads = s.threads;
+    plan->tile_rows = uint32_t(s.tile_m);
+    plan->tile_cols = uint32_t(s.tile_n);
+    plan->tiles_m = uint32_t(s.tiles_m);
+    plan->tiles_n = uint32_t(s.tiles_n);
+    plan->splits = uint32_t(s.splits);
+    plan->k_per_split = uint64_t(s.k_per_split);
+    plan->batches_per_launch = uint64_t(s.batches_per_launch);
+    plan->workgroups = uint64_t(s.workgroups);
+    plan->launches = uint64_t(s.launches);
+    plan->workspace_bytes = uint64_t(s.workspace_bytes);
+    return s.workspace_bytes > workspace_bytes ? SN_ERR_WORKSPACE : SN_OK;
 }
 
 int sn_add_row_bias(sn_context* ctx, float* output, size_t rows, size_t cols, const float* bias, size_t bias_len) {

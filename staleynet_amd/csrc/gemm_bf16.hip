@@ -136,10 +136,11 @@ __global__ __launch_bounds__(T::THREADS) void gemm_bf16_kernel(Args args) {
 
 template <class T, bool A_K, bool B_K, bool BUF>
 hipError_t launch_tiles_bf16(const Problem& p, const Env& env, const Plan& plan, hipStream_t stream) {
+    const LaunchShape shape = tiled_shape<T>(p, plan, SN_PATH_NONE);
+    if (shape.batches_per_launch < 1) return hipErrorInvalidConfiguration;
     Args args = make_args<T>(p, env, plan);
     const int64_t per_batch = int64_t(plan.tiles_m) * plan.tiles_n * plan.splits;
-    const int64_t chunk = batches_per_launch(per_batch, T::THREADS, p.batch);
-    if (chunk < 1) return hipErrorInvalidConfiguration;
+    const int64_t chunk = shape.batches_per_launch;
     for (int64_t first = 0; first < p.batch; first += chunk) {
         const int64_t count = std::min<int64_t>(chunk, p.batch - first);
         args.batch_base = first;
@@ -172,14 +173,15 @@ using TileNarrow = Tile<256, 64, 32, 4, 1>;
 
 }  // namespace
 
-size_t bf16_workspace_bytes(const Problem& p, const Env& env) {
-    if (bf16_staged_applies(p, env)) return bf16_staged_workspace_bytes(p, env);
-    if (bf16_dma_applies(p)) return bf16_dma_workspace_bytes(p, env);
-    const Plan plan = p.n <= 64 ? plan_for<TileNarrow>(p, env) : plan_for<TileSquare>(p, env);
-    return plan.splits > 1 ? size_t(plan.splits) * size_t(p.m) * size_t(p.n) * sizeof(float) : 0;
-}
-
 }  // namespace gemm
+
+LaunchShape describe_gemm_bf16(const Problem& p, const Env& env) {
+    if (gemm::bf16_staged_applies(p, env)) return gemm::describe_bf16_staged(p, env);
+    if (gemm::bf16_dma_applies(p)) return gemm::describe_bf16_dma(p, env);
+    if (p.n <= 64)
+        return gemm::tiled_shape<gemm::TileNarrow>(p, gemm::plan_for<gemm::TileNarrow>(p, env), SN_PATH_BF16_REGISTER);
+    return gemm::tiled_shape<gemm::TileSquare>(p, gemm::plan_for<gemm::TileSquare>(p, env), SN_PATH_BF16_REGISTER);
+}
 
 hipError_t launch_gemm_bf16(const Problem& p, const Env& env, hipStream_t stream) {
     if (gemm::bf16_staged_applies(p, env)) return gemm::launch_gemm_bf16_staged(p, env, stream);

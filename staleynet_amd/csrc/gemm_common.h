@@ -386,7 +386,8 @@ using LoaderFor = typename std::conditional<
 // tiles of a split share its slices of A and B). Within a split the tiles
 // are walked as a raster grouped kGroupM tile rows high, keeping the A rows
 // and B columns an XCD reuses in its own L2.
-__device__ __forceinline__ void tile_coordinates(int bid, int blocks, int tiles_m, int tiles_n, int splits, int& batch,
+// Host-callable too: the host planner (sn_tile_map) evaluates the same map.
+__host__ __device__ inline void tile_coordinates(int bid, int blocks, int tiles_m, int tiles_n, int splits, int& batch,
                                                  int& split, int& tm, int& tn) {
     const int xcd = bid % kXcds;
     const int local = bid / kXcds;
@@ -401,7 +402,7 @@ __device__ __forceinline__ void tile_coordinates(int bid, int blocks, int tiles_
     const int per_group = kGroupM * tiles_n;
     const int group = id / per_group;
     const int first_m = group * kGroupM;
-    const int group_rows = min(tiles_m - first_m, kGroupM);
+    const int group_rows = tiles_m - first_m < kGroupM ? tiles_m - first_m : kGroupM;
     const int within = id % per_group;
     tm = first_m + within % group_rows;
     tn = within / group_rows;
@@ -413,6 +414,28 @@ __device__ __forceinline__ void tile_coordinates(int bid, int blocks, int tiles_
 inline int64_t batches_per_launch(int64_t per_batch, int threads, int64_t batch) {
     const int64_t fit = ((int64_t(1) << 32) - 1) / threads / per_batch;
     return fit < batch ? fit : batch;
+}
+
+// The launch of a tiled product under `plan`: matrices per launch (0 when
+// one matrix alone is too large), the grid and the split-K partials. The
+// tiled launchers take their grid from here.
+template <class T>
+LaunchShape tiled_shape(const Problem& p, int tiles_m, int tiles_n, int splits, int64_t k_per_split, uint32_t path) {
+    LaunchShape s;
+    s.path = path;
+    s.threads = T::THREADS;
+    s.tile_m = T::BM;
+    s.tile_n = T::BN;
+    s.tiles_m = tiles_m;
+    s.tiles_n = tiles_n;
+    s.splits = splits;
+    s.k_per_split = k_per_split;
+    const int64_t per_batch = int64_t(tiles_m) * tiles_n * splits;
+    s.batches_per_launch = batches_per_launch(per_batch, T::THREADS, p.batch);
+    s.workgroups = s.batches_per_launch * per_batch;
+    s.launches = s.batches_per_launch > 0 ? (p.batch + s.batches_per_launch - 1) / s.batches_per_launch : 0;
+    s.workspace_bytes = splits > 1 ? size_t(splits) * size_t(p.m) * size_t(p.n) * sizeof(float) : 0;
+    return s;
 }
 
 // The reference's combine (kernels/matmul.rs:166-168), the product and the
@@ -651,6 +674,11 @@ Plan plan_for(const Problem& p, const Env& env, const SplitCost& cost = SplitCos
 }
 
 template <class T>
+LaunchShape tiled_shape(const Problem& p, const Plan& plan, uint32_t path) {
+    return tiled_shape<T>(p, plan.tiles_m, plan.tiles_n, plan.splits, plan.k_per_split, path);
+}
+
+template <class T>
 Args make_args(const Problem& p, const Env& env, const Plan& plan) {
     Args args;
     args.a = p.a;
@@ -679,29 +707,25 @@ Args make_args(const Problem& p, const Env& env, const Plan& plan) {
 }
 
 // The direct-to-LDS fp32 kernel (gemm_dma.hip): whether it serves `p`
-// (aligned operands) and its launcher.
+// (aligned operands), its launch shape and its launcher.
 bool dma_applies(const Problem& p);
+LaunchShape describe_f32_dma(const Problem& p, const Env& env);
 hipError_t launch_gemm_f32_dma(const Problem& p, const Env& env, hipStream_t stream);
-size_t f32_dma_workspace_bytes(const Problem& p, const Env& env);
 // The bf16 variant of the direct-to-LDS kernel: whether it serves `p`, its
-// launcher and the split-K workspace it uses.
+// launch shape (with the split-K workspace it uses) and its launcher.
 bool bf16_dma_applies(const Problem& p);
+LaunchShape describe_bf16_dma(const Problem& p, const Env& env);
 hipError_t launch_gemm_bf16_dma(const Problem& p, const Env& env, hipStream_t stream);
-size_t bf16_dma_workspace_bytes(const Problem& p, const Env& env);
 // bf16 with both operands first staged as bf16 in the workspace (gemm_dma.hip):
 // whether it serves `p` (unmasked, aligned, staged operands fit), its
-// launcher and the workspace it uses (staged operands and partial sums).
+// launch shape (workspace: staged operands and partial sums) and launcher.
 bool bf16_staged_applies(const Problem& p, const Env& env);
+LaunchShape describe_bf16_staged(const Problem& p, const Env& env);
 hipError_t launch_gemm_bf16_staged(const Problem& p, const Env& env, hipStream_t stream);
-size_t bf16_staged_workspace_bytes(const Problem& p, const Env& env);
 
 // Adds the split-K partial sums in split order and applies the combine
 // (defined in gemm_mfma.hip).
 hipError_t launch_splitk_reduce(const Problem& p, const Env& env, int splits, hipStream_t stream);
-
-// Split-K workspace each kernel family would use for `p` (0 = no split).
-size_t f32_workspace_bytes(const Problem& p, const Env& env);
-size_t bf16_workspace_bytes(const Problem& p, const Env& env);
 
 }  // namespace gemm
 }  // namespace sn

@@ -562,14 +562,20 @@ SplitCost split_cost() {
     return cost;
 }
 
+template <class C, int FEED>
+Plan dma_plan(const Problem& p, const Env& env) {
+    return plan_for<typename C::T>(p, env, split_cost<C, FEED>());
+}
+
 template <class C, bool A_K, bool B_K, int FEED>
 hipError_t launch_dma_tiles(const Problem& p, const Env& env, hipStream_t stream) {
     using T = typename C::T;
-    const Plan plan = plan_for<T>(p, env, split_cost<C, FEED>());
+    const Plan plan = dma_plan<C, FEED>(p, env);
+    const LaunchShape shape = tiled_shape<T>(p, plan, SN_PATH_NONE);
+    if (shape.batches_per_launch < 1) return hipErrorInvalidConfiguration;
     Args args = make_args<T>(p, env, plan);
     const int64_t per_batch = int64_t(plan.tiles_m) * plan.tiles_n * plan.splits;
-    const int64_t chunk = batches_per_launch(per_batch, T::THREADS, p.batch);
-    if (chunk < 1) return hipErrorInvalidConfiguration;
+    const int64_t chunk = shape.batches_per_launch;
     for (int64_t first = 0; first < p.batch; first += chunk) {
         const int64_t count = std::min<int64_t>(chunk, p.batch - first);
         args.batch_base = first;
@@ -617,30 +623,54 @@ bool config_applies(const Problem& p) {
     return buffers_ok<typename C::T>(p);
 }
 
+// The tile configuration each direct-to-LDS family takes for `p`, handed
+// to `f` (the launchers, applicability checks and launch shapes all choose
+// through these).
+template <class F>
+auto with_f32_dma_config(const Problem& p, F&& f) {
+    return p.n <= 64 ? f(DmaNarrow{}) : f(DmaSquare{});
+}
+
+template <class F>
+auto with_bf16_dma_config(const Problem& p, F&& f) {
+    if (p.n <= 64) return f(Bf16Narrow{});
+    if (p.n >= kBf16WideColumns) return f(Bf16Wide{});
+    return f(Bf16Square{});
+}
+
 }  // namespace
 
 // Operands 16-byte aligned with 16-byte-multiple leading dimensions and
 // batch strides, and every per-lane offset of one K-step within the buffer
 // offset range (the same conditions as the buffer-load path of gemm_mfma.hip).
 bool dma_applies(const Problem& p) {
-    return p.n <= 64 ? config_applies<DmaNarrow>(p) : config_applies<DmaSquare>(p);
+    return with_f32_dma_config(p, [&](auto c) { return config_applies<decltype(c)>(p); });
 }
 
 bool bf16_dma_applies(const Problem& p) {
-    if (p.n <= 64) return config_applies<Bf16Narrow>(p);
-    if (p.n >= kBf16WideColumns) return config_applies<Bf16Wide>(p);
-    return config_applies<Bf16Square>(p);
+    return with_bf16_dma_config(p, [&](auto c) { return config_applies<decltype(c)>(p); });
+}
+
+LaunchShape describe_f32_dma(const Problem& p, const Env& env) {
+    return with_f32_dma_config(p, [&](auto c) {
+        using C = decltype(c);
+        return tiled_shape<typename C::T>(p, dma_plan<C, kFeedF32>(p, env), SN_PATH_F32_DIRECT);
+    });
+}
+
+LaunchShape describe_bf16_dma(const Problem& p, const Env& env) {
+    return with_bf16_dma_config(p, [&](auto c) {
+        using C = decltype(c);
+        return tiled_shape<typename C::T>(p, dma_plan<C, kFeedRound>(p, env), SN_PATH_BF16_DIRECT);
+    });
 }
 
 hipError_t launch_gemm_f32_dma(const Problem& p, const Env& env, hipStream_t stream) {
-    if (p.n <= 64) return launch_dma_layout<DmaNarrow, kFeedF32>(p, env, stream);
-    return launch_dma_layout<DmaSquare, kFeedF32>(p, env, stream);
+    return with_f32_dma_config(p, [&](auto c) { return launch_dma_layout<decltype(c), kFeedF32>(p, env, stream); });
 }
 
 hipError_t launch_gemm_bf16_dma(const Problem& p, const Env& env, hipStream_t stream) {
-    if (p.n <= 64) return launch_dma_layout<Bf16Narrow, kFeedRound>(p, env, stream);
-    if (p.n >= kBf16WideColumns) return launch_dma_layout<Bf16Wide, kFeedRound>(p, env, stream);
-    return launch_dma_layout<Bf16Square, kFeedRound>(p, env, stream);
+    return with_bf16_dma_config(p, [&](auto c) { return launch_dma_layout<decltype(c), kFeedRound>(p, env, stream); });
 }
 
 // ---- bf16 operands staged in the workspace -------------------------------
@@ -698,7 +728,7 @@ using Bf16StagedSquare = DmaConfig<Tile<128, 128, 32, 2, 2>, 2>;
 using Bf16StagedWide = DmaConfig<Tile<128, 256, 32, 2, 4>, 3>;
 
 template <class F>
-hipError_t with_staged_config(const Problem& q, F&& f) {
+auto with_staged_config(const Problem& q, F&& f) {
     if (q.n >= kBf16WideColumns) return f(Bf16StagedWide{});
     return f(Bf16StagedSquare{});
 }
@@ -733,28 +763,19 @@ hipError_t launch_gemm_bf16_staged(const Problem& p, const Env& env, hipStream_t
     return with_staged_config(q, [&](auto c) { return launch_dma_tiles<decltype(c), true, true, kFeedBf16>(q, rest, stream); });
 }
 
-size_t bf16_staged_workspace_bytes(const Problem& p, const Env& env) {
+LaunchShape describe_bf16_staged(const Problem& p, const Env& env) {
     const Staging st = staging_for(p);
     const Problem q = staged_problem(p, st, env);
     const Env rest = staged_env(env, st);
-    const Plan plan = q.n >= kBf16WideColumns
-                          ? plan_for<Bf16StagedWide::T>(q, rest, split_cost<Bf16StagedWide, kFeedBf16>())
-                          : plan_for<Bf16StagedSquare::T>(q, rest, split_cost<Bf16StagedSquare, kFeedBf16>());
-    const size_t partials = plan.splits > 1 ? size_t(plan.splits) * size_t(p.m) * size_t(p.n) * sizeof(float) : 0;
-    return st.a_bytes + st.b_bytes + partials;
-}
-
-size_t f32_dma_workspace_bytes(const Problem& p, const Env& env) {
-    const Plan plan = p.n <= 64 ? plan_for<DmaNarrow::T>(p, env, split_cost<DmaNarrow, kFeedF32>())
-                                : plan_for<DmaSquare::T>(p, env, split_cost<DmaSquare, kFeedF32>());
-    return plan.splits > 1 ? size_t(plan.splits) * size_t(p.m) * size_t(p.n) * sizeof(float) : 0;
-}
-
-size_t bf16_dma_workspace_bytes(const Problem& p, const Env& env) {
-    const Plan plan = p.n <= 64 ? plan_for<Bf16Narrow::T>(p, env, split_cost<Bf16Narrow, kFeedRound>())
-                      : p.n >= kBf16WideColumns ? plan_for<Bf16Wide::T>(p, env, split_cost<Bf16Wide, kFeedRound>())
-                                                : plan_for<Bf16Square::T>(p, env, split_cost<Bf16Square, kFeedRound>());
-    return plan.splits > 1 ? size_t(plan.splits) * size_t(p.m) * size_t(p.n) * sizeof(float) : 0;
+    LaunchShape shape = with_staged_config(q, [&](auto c) {
+        using C = decltype(c);
+        return tiled_shape<typename C::T>(q, dma_plan<C, kFeedBf16>(q, rest), SN_PATH_BF16_STAGED);
+    });
+    // The staged product counts k in pairs of bf16; its partial sums follow
+    // the staged operands in the workspace.
+    shape.k_per_split *= 2;
+    shape.workspace_bytes += st.a_bytes + st.b_bytes;
+    return shape;
 }
 
 }  // namespace gemm

@@ -42,6 +42,31 @@ struct Env {
     int cu_count = 256;
 };
 
+// How a product is launched (sn_launch_plan's fields): the kernel family,
+// its tiles, K slices and grid. Each launcher below computes its grid with
+// the describe_* function of its family, so the two cannot disagree.
+struct LaunchShape {
+    uint32_t path = 0;  // SN_PATH_*
+    uint32_t threads = 0;
+    int32_t tile_m = 0, tile_n = 0;
+    int32_t tiles_m = 0, tiles_n = 0, splits = 1;
+    int64_t k_per_split = 0;
+    int64_t batches_per_launch = 0;
+    int64_t workgroups = 0;
+    int64_t launches = 0;
+    size_t workspace_bytes = 0;
+};
+LaunchShape describe_gemm_f32(const Problem& p, const Env& env);
+LaunchShape describe_gemm_bf16(const Problem& p, const Env& env);
+LaunchShape describe_gemm_simple(const Problem& p);
+LaunchShape describe_gemv(const Problem& p);
+LaunchShape describe_gemv_nt(const Problem& p);
+
+// The routing of sn_matmul: which family serves `p` under context kernel
+// `kernel` (SN_KERNEL_*), and that family's launch.
+LaunchShape describe_matmul(const Problem& p, uint32_t kernel, const Env& env);
+hipError_t launch_matmul(const Problem& p, uint32_t kernel, const Env& env, hipStream_t stream);
+
 // Launchers; each returns hipSuccess or the launch error.
 hipError_t launch_gemm_f32(const Problem& p, const Env& env, hipStream_t stream);
 hipError_t launch_gemm_bf16(const Problem& p, const Env& env, hipStream_t stream);

@@ -218,10 +218,11 @@ __global__ __launch_bounds__(256) void splitk_reduce4_kernel(const f32x4* __rest
 
 template <class T, bool A_K, bool B_K, bool BUF>
 hipError_t launch_tiles(const Problem& p, const Env& env, const Plan& plan, hipStream_t stream) {
+    const LaunchShape shape = tiled_shape<T>(p, plan, SN_PATH_NONE);
+    if (shape.batches_per_launch < 1) return hipErrorInvalidConfiguration;
     Args args = make_args<T>(p, env, plan);
     const int64_t per_batch = int64_t(plan.tiles_m) * plan.tiles_n * plan.splits;
-    const int64_t chunk = batches_per_launch(per_batch, T::THREADS, p.batch);
-    if (chunk < 1) return hipErrorInvalidConfiguration;
+    const int64_t chunk = shape.batches_per_launch;
     for (int64_t first = 0; first < p.batch; first += chunk) {
         const int64_t count = std::min<int64_t>(chunk, p.batch - first);
         args.batch_base = first;
@@ -271,13 +272,14 @@ hipError_t launch_splitk_reduce(const Problem& p, const Env& env, int splits, hi
     return hipGetLastError();
 }
 
-size_t f32_workspace_bytes(const Problem& p, const Env& env) {
-    if (dma_applies(p)) return f32_dma_workspace_bytes(p, env);
-    const Plan plan = use_narrow(p) ? plan_for<TileNarrow>(p, env) : plan_for<TileSquare>(p, env);
-    return plan.splits > 1 ? size_t(plan.splits) * size_t(p.m) * size_t(p.n) * sizeof(float) : 0;
-}
-
 }  // namespace gemm
+
+LaunchShape describe_gemm_f32(const Problem& p, const Env& env) {
+    if (gemm::dma_applies(p)) return gemm::describe_f32_dma(p, env);
+    if (gemm::use_narrow(p))
+        return gemm::tiled_shape<gemm::TileNarrow>(p, gemm::plan_for<gemm::TileNarrow>(p, env), SN_PATH_F32_REGISTER);
+    return gemm::tiled_shape<gemm::TileSquare>(p, gemm::plan_for<gemm::TileSquare>(p, env), SN_PATH_F32_REGISTER);
+}
 
 hipError_t launch_gemm_f32(const Problem& p, const Env& env, hipStream_t stream) {
     if (gemm::dma_applies(p)) return gemm::launch_gemm_f32_dma(p, env, stream);
@@ -286,7 +288,7 @@ hipError_t launch_gemm_f32(const Problem& p, const Env& env, hipStream_t stream)
 }
 
 size_t gemm_workspace_bytes(const Problem& p, bool bf16, const Env& env) {
-    return bf16 ? gemm::bf16_workspace_bytes(p, env) : gemm::f32_workspace_bytes(p, env);
+    return bf16 ? describe_gemm_bf16(p, env).workspace_bytes : describe_gemm_f32(p, env).workspace_bytes;
 }
 
 }  // namespace sn

@@ -55,6 +55,22 @@ __global__ __launch_bounds__(256) void gemm_simple_kernel(SimpleArgs p) {
 
 }  // namespace
 
+LaunchShape describe_gemm_simple(const Problem& p) {
+    LaunchShape s;
+    s.path = SN_PATH_REFERENCE_ORDER;
+    s.threads = 256;
+    s.tile_m = 16;
+    s.tile_n = 16;
+    s.tiles_m = int32_t((p.m + 15) / 16);
+    s.tiles_n = int32_t((p.n + 15) / 16);
+    s.splits = 1;
+    s.k_per_split = p.k;
+    s.batches_per_launch = std::min<int64_t>(65535, p.batch);
+    s.workgroups = int64_t(s.tiles_m) * s.tiles_n * s.batches_per_launch;
+    s.launches = (p.batch + 65534) / 65535;
+    return s;
+}
+
 hipError_t launch_gemm_simple(const Problem& p, hipStream_t stream) {
     SimpleArgs args{p.a, p.b, p.c, p.m, p.n, p.k, p.lda, p.ldb, p.stride_a, p.stride_b, p.stride_c, 0,
                     p.query_offset, p.a_k_contiguous, p.b_k_contiguous, p.accumulate, int32_t(p.mask), p.scale,

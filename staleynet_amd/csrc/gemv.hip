@@ -587,6 +587,40 @@ hipError_t launch_gemv_nt(const Problem& p, hipStream_t stream) {
     return hipGetLastError();
 }
 
+LaunchShape describe_gemv(const Problem& p) {
+    const GemvPlan plan = gemv_plan(p);
+    LaunchShape s;
+    s.path = SN_PATH_FEW_ROWS;
+    s.threads = p.m <= 4 ? 64 * waves_for<4>() : 64 * waves_for<16>();
+    s.tile_m = int32_t(p.m);
+    s.tile_n = 4 * plan.lanes_per_row;
+    s.tiles_m = 1;
+    s.tiles_n = plan.column_blocks;
+    s.splits = plan.splits;
+    s.k_per_split = plan.k_per_split;
+    s.batches_per_launch = p.batch;
+    s.workgroups = int64_t(plan.column_blocks) * plan.splits * p.batch;
+    s.launches = 1;
+    s.workspace_bytes = plan.splits > 1 ? size_t(plan.splits) * size_t(p.batch) * size_t(p.m) * size_t(p.n) * 4 : 0;
+    return s;
+}
+
+LaunchShape describe_gemv_nt(const Problem& p) {
+    LaunchShape s;
+    s.path = SN_PATH_FEW_ROWS_NT;
+    s.threads = 256;
+    s.tile_m = int32_t(p.m);
+    s.tile_n = kNtRows;
+    s.tiles_m = 1;
+    s.tiles_n = int32_t((p.n + kNtRows - 1) / kNtRows);
+    s.splits = 1;
+    s.k_per_split = p.k;
+    s.batches_per_launch = p.batch;
+    s.workgroups = int64_t(s.tiles_n) * p.batch;
+    s.launches = 1;
+    return s;
+}
+
 hipError_t launch_gemv(const Problem& p, const Env& env, hipStream_t stream) {
     if (!gemv_applies(p, env)) return hipErrorNotSupported;
     const GemvPlan plan = gemv_plan(p);

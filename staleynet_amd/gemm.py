@@ -205,6 +205,21 @@ class CCrossEntropyHead(ctypes.Structure):
                 ("grad_scale", ctypes.c_float)]
 
 
+class CLaunchPlan(ctypes.Structure):
+    """``sn_launch_plan``: how one product is launched (the role of launch.rs:28-48)."""
+    _fields_ = [("path", ctypes.c_uint32), ("threads", ctypes.c_uint32), ("tile_rows", ctypes.c_uint32),
+                ("tile_cols", ctypes.c_uint32), ("tiles_m", ctypes.c_uint32), ("tiles_n", ctypes.c_uint32),
+                ("splits", ctypes.c_uint32), ("reserved", ctypes.c_uint32), ("k_per_split", ctypes.c_uint64),
+                ("batches_per_launch", ctypes.c_uint64), ("workgroups", ctypes.c_uint64),
+                ("launches", ctypes.c_uint64), ("workspace_bytes", ctypes.c_uint64)]
+
+
+# sn_launch_plan.path values (include/staleynet_gemm.h).
+PATH_NONE, PATH_REFERENCE_ORDER, PATH_FEW_ROWS, PATH_FEW_ROWS_NT = 0, 1, 2, 3
+PATH_F32_DIRECT, PATH_F32_REGISTER, PATH_BF16_STAGED, PATH_BF16_DIRECT, PATH_BF16_REGISTER = 4, 5, 6, 7, 8
+TILED_PATHS = (PATH_F32_DIRECT, PATH_F32_REGISTER, PATH_BF16_STAGED, PATH_BF16_DIRECT, PATH_BF16_REGISTER)
+
+
 class CAttentionShape(ctypes.Structure):
     _fields_ = [("heads", ctypes.c_size_t), ("queries", ctypes.c_size_t), ("keys", ctypes.c_size_t),
                 ("head_dim", ctypes.c_size_t), ("q_stride", ctypes.c_size_t), ("kv_stride", ctypes.c_size_t),
@@ -345,13 +360,19 @@ def _library() -> ctypes.CDLL:
         lib.sn_merge_heads.argtypes = [ctx, ctypes.c_void_p, size, ctypes.c_void_p, size,
                                        ctypes.POINTER(CHeadLayout)]
         lib.sn_softmax_backward.argtypes = [ctx, ctypes.c_void_p, size, size, ctypes.c_void_p, size, size]
+        lib.sn_plan_matmul.argtypes = [ctypes.POINTER(CMatmulSpec), ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p,
+                                       ctypes.c_void_p, ctypes.c_uint32, size, ctypes.POINTER(CLaunchPlan)]
+        u32p = ctypes.POINTER(ctypes.c_uint32)
+        lib.sn_tile_map.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, u32p, u32p,
+                                    u32p, u32p]
         for name in ("sn_context_create", "sn_context_create_with_workspace", "sn_context_destroy",
                      "sn_context_bind", "sn_context_set_kernel", "sn_context_get_kernel", "sn_synchronize",
                      "sn_alloc_zeroed", "sn_free", "sn_upload", "sn_download", "sn_copy_from_host", "sn_fill_zero",
                      "sn_matmul_validate", "sn_matmul", "sn_fill_normal", "sn_copy_device", "sn_read_sum",
                      "sn_add_row_bias", "sn_accumulate_column_sums", "sn_matmul_bias", "sn_causal_softmax",
                      "sn_softmax_backward", "sn_cross_entropy", "sn_upload_tokens", "sn_download_tokens",
-                     "sn_free_tokens", "sn_split_heads", "sn_merge_heads"):
+                     "sn_free_tokens", "sn_split_heads", "sn_merge_heads", "sn_causal_attention",
+                     "sn_causal_attention_score_grad", "sn_plan_matmul", "sn_tile_map"):
             getattr(lib, name).restype = ctypes.c_int
         _lib = lib
     return _lib
@@ -370,6 +391,34 @@ def validate(spec: MatmulSpec, left_len: int, right_len: int, output_len: int) -
     """``sn_matmul_validate``: the host checks of ``Gpu::matmul`` as a pure function."""
     c = spec.to_c()
     return int(_library().sn_matmul_validate(ctypes.byref(c), left_len, right_len, output_len))
+
+
+# A device allocation's alignment (2 MiB): operands at such addresses take the aligned paths.
+ALIGNED_ADDRESS = 1 << 40
+
+
+def plan(spec: MatmulSpec, kernel: int = 0, cu_count: int = 256, workspace_bytes: int = 1536 << 20,
+         left: int = ALIGNED_ADDRESS, right: int = 2 * ALIGNED_ADDRESS, output: int = 3 * ALIGNED_ADDRESS) -> CLaunchPlan:
+    """``sn_plan_matmul``: the launch ``Gpu::matmul`` would make for ``spec`` (host only; the operand
+    addresses are only inspected for alignment). Raises GpuError on a rejected spec."""
+    c = spec.to_c()
+    out = CLaunchPlan()
+    rc = _library().sn_plan_matmul(ctypes.byref(c), kernel, left, right, output, cu_count, workspace_bytes,
+                                   ctypes.byref(out))
+    if rc != SN_OK:
+        raise GpuError(rc, "plan_matmul")
+    return out
+
+
+def tile_map(workgroups: int, tiles_m: int, tiles_n: int, splits: int):
+    """``sn_tile_map``: (matrix, slice, tile row, tile column) of each workgroup of a tiled launch,
+    as four uint32 arrays."""
+    arrays = [np.zeros(workgroups, np.uint32) for _ in range(4)]
+    pointers = [a.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)) for a in arrays]
+    rc = _library().sn_tile_map(workgroups, tiles_m, tiles_n, splits, *pointers)
+    if rc != SN_OK:
+        raise GpuError(rc, "tile_map")
+    return tuple(arrays)
 
 
 @dataclass(frozen=True)

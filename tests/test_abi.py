@@ -189,3 +189,20 @@ def test_context_creation_without_a_gpu_fails_cleanly():
     handle = ctypes.c_void_p()
     assert lib.sn_context_create(0, ctypes.byref(handle)) == gemm.SN_ERR_NO_DEVICE
     assert not handle.value
+
+
+def test_struct_layouts_match_the_header():
+    # The layouts a Rust #[repr(C)] binding mirrors (LP64): sizes and the offsets after each
+    # 4-byte field, where padding would show up. context.cpp pins the same with static_assert.
+    spec = gemm.CMatmulSpec
+    assert ctypes.sizeof(spec) == 88
+    assert [spec.left_storage.offset, spec.batch_count.offset, spec.scale.offset, spec.write.offset,
+            spec.mask.offset, spec.precision.offset, spec.query_offset.offset] == [24, 32, 64, 68, 72, 76, 80]
+    shape = gemm.CAttentionShape
+    assert ctypes.sizeof(shape) == 64 and shape.query_offset.offset == 48 and shape.scale.offset == 56
+    layout = gemm.CHeadLayout
+    assert ctypes.sizeof(layout) == 64 and layout.time_offset.offset == 56
+    head = gemm.CCrossEntropyHead
+    assert ctypes.sizeof(head) == 40 and head.grad_scale.offset == 32
+    plan = gemm.CLaunchPlan
+    assert ctypes.sizeof(plan) == 72 and plan.k_per_split.offset == 32 and plan.workspace_bytes.offset == 64

@@ -117,6 +117,34 @@ def test_decode_form_matches_the_three_calls(gpu, heads, queries, keys, h, offse
     assert oracle.relative_error(eo, go) < TOLERANCE
 
 
+@pytest.mark.parametrize("heads,queries,keys,h,offset", [
+    (12, 1, 1408, 64, 700),     # 6 chunks, the last one partly past the horizon
+    (3, 4, 700, 32, 300),       # four queries: the tail starts at 304
+    (2, 2, 900, 128, 129),      # the tail starts inside the second chunk
+])
+def test_decode_form_never_reads_the_unwritten_cache_tail(gpu, heads, queries, keys, h, offset):
+    # A decode step's cache holds queries + offset written positions; the rest (the tail) is never
+    # written. The reference's cache is zero-initialised, so its three calls see zeros there; here
+    # the tail holds NaN, which must not reach the result (0 * NaN would).
+    rng = np.random.default_rng(heads * 7 + offset)
+    q = rng.normal(0, 1, heads * queries * h).astype(np.float32)
+    k = rng.normal(0, 1, heads * keys * h).astype(np.float32).reshape(heads, keys, h)
+    v = rng.normal(0, 1, heads * keys * h).astype(np.float32).reshape(heads, keys, h)
+    written = queries + offset
+    k[:, written:, :] = 0.0
+    v[:, written:, :] = 0.0
+    expected, _ = reference(q, k.ravel(), v.ravel(), heads, queries, keys, h, 0.125, offset, queries * h, keys * h)
+    k_dirty, v_dirty = k.copy(), v.copy()
+    k_dirty[:, written:, :] = np.nan
+    v_dirty[:, written:, :] = np.nan
+    Q, K, V = (gpu.upload(Shape.vector(x.size), x.ravel()) for x in (q, k_dirty, v_dirty))
+    out = gpu.zeros(Shape.vector(heads * queries * h))
+    gpu.causal_attention(Q, K, V, out, heads, queries, keys, h, 0.125, offset)
+    got = gpu.download(out)
+    assert np.all(np.isfinite(got))
+    assert oracle.relative_error(expected, got) < TOLERANCE
+
+
 def test_decode_form_is_deterministic_and_reusable(gpu):
     # Repeated calls (the arrival counters are reset by each call's last chunk) give the same bits.
     first = run(gpu, 12, 1, 1408, 64, 0.125, 1000, q_stride=64, kv_stride=1408 * 64, seed=21, with_p=False)[1]

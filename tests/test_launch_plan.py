@@ -1,0 +1,181 @@
+"""CPU tests of the launch geometry, the counterpart of the reference's launch.rs unit tests
+(crates/staleynet-cuda/src/launch.rs:59-113): the grid ``sn_plan_matmul`` reports for a product
+(the same describe functions the launchers take their grids from) and the workgroup -> (matrix,
+K slice, tile) map the tiled kernels evaluate on the device (``sn_tile_map``, the same function).
+For every product of configs 0-4 and the attention batches: each (matrix, slice, tile) is covered by
+exactly one workgroup, the slices cover K, and the batch regrouping gives each XCD whole matrices.
+No GPU is used."""
+import numpy as np
+import pytest
+
+from staleynet_amd import gemm
+from staleynet_amd.gemm import BatchStrides, MatmulKernel, MatmulSpec, Precision
+
+XCDS = 8
+MODELS = {  # (tokens, width, ffn) of configs 0, 1, 2
+    "c0": (4 * 512, 256, 1024),
+    "c1": (8 * 1024, 512, 2048),
+    "c2": (16 * 2048, 768, 3072),
+}
+
+
+def linear_products(tokens, d, f):
+    """Every product of one training step's Linears (linear.rs:43-63) and the 16-codebook head."""
+    for i, o in ((d, 3 * d), (d, d), (d, f), (f, d), (d, 16 * 1024)):
+        yield f"NN {tokens}x{o}x{i}", MatmulSpec.new(tokens, o, i)
+        yield f"TN {i}x{o}x{tokens}", MatmulSpec.new(i, o, tokens).left_transposed().accumulate()
+        yield f"NT {tokens}x{i}x{o}", MatmulSpec.new(tokens, i, o).right_transposed()
+
+
+def attention_products(bh=192, t=2048, h=64):
+    """Config 3's six products (attention.rs:206-260), dense and causal."""
+    per = BatchStrides(bh, t * h, t * h, t * t)
+    scores = MatmulSpec.new(t, t, h).right_transposed().batched(per)
+    mix = MatmulSpec.new(t, h, t).batched(BatchStrides(bh, t * t, t * h, t * h))
+    dv = MatmulSpec.new(t, h, t).left_transposed().batched(BatchStrides(bh, t * t, t * h, t * h))
+    yield "S", scores
+    yield "S causal", scores.causal_output()
+    yield "O", mix
+    yield "O causal", mix.causal_left()
+    yield "dV causal", dv.causal_left()
+    yield "dQ causal", mix.scaled(0.125).causal_left()
+
+
+def decode_products():
+    """Config 4: M in {1, 4, 16} against the 111.5M weights and the head (decode.rs:123-161)."""
+    for m in (1, 4, 16):
+        for k, n in ((768, 2304), (768, 768), (768, 3072), (3072, 768), (768, 16384)):
+            yield f"decode M={m} {k}x{n}", MatmulSpec.new(m, n, k)
+    # The decode scores and mix against a 1408-position cache, 12 heads.
+    yield "decode scores", MatmulSpec.new(1, 1408, 64).right_transposed().batched(
+        BatchStrides(12, 64, 1408 * 64, 1408)).causal_output(700)
+    yield "decode mix", MatmulSpec.new(1, 64, 1408).batched(BatchStrides(12, 1408, 1408 * 64, 64)).causal_left(700)
+
+
+def all_products():
+    for name, (tokens, d, f) in MODELS.items():
+        for label, spec in linear_products(tokens, d, f):
+            yield f"{name} {label}", spec, MatmulKernel.MfmaF32
+    for label, spec in linear_products(*MODELS["c2"]):
+        yield f"c2 bf16 {label}", spec.with_precision(Precision.Bf16), MatmulKernel.MfmaF32
+    for label, spec in attention_products():
+        yield f"c3 {label}", spec, MatmulKernel.MfmaF32
+    for label, spec in attention_products(bh=12 * 16, t=2048, h=64):
+        if "causal" in label:
+            yield f"c3 bf16 {label}", spec.with_precision(Precision.Bf16), MatmulKernel.MfmaF32
+    for label, spec in decode_products():
+        yield f"c4 {label}", spec, MatmulKernel.MfmaF32
+
+
+CASES = list(all_products())
+
+
+def check_tiled_cover(plan):
+    """Every (matrix, slice, tile row, tile column) of one launch is produced exactly once."""
+    matrix, split, tm, tn = gemm.tile_map(plan.workgroups, plan.tiles_m, plan.tiles_n, plan.splits)
+    assert matrix.max() < plan.batches_per_launch and split.max() < plan.splits
+    assert tm.max() < plan.tiles_m and tn.max() < plan.tiles_n
+    key = ((matrix.astype(np.int64) * plan.splits + split) * plan.tiles_m + tm) * plan.tiles_n + tn
+    assert len(np.unique(key)) == plan.workgroups == plan.batches_per_launch * plan.splits * plan.tiles_m * plan.tiles_n
+    return matrix, split
+
+
+@pytest.mark.parametrize("label,spec,kernel", CASES, ids=[c[0] for c in CASES])
+def test_every_tile_and_slice_is_launched_once(label, spec, kernel):
+    plan = gemm.plan(spec, int(kernel))
+    k = spec.inner
+    if spec.mask == gemm.Mask.CausalLeft and plan.path == gemm.PATH_FEW_ROWS:
+        # The decode mix multiplies keys up to the last row's horizon only; the cache tail is not read.
+        k = min(k, spec.rows + spec.query_offset)
+    assert plan.splits >= 1 and plan.k_per_split >= 1
+    # The slices cover K: the last one starts inside it.
+    assert (plan.splits - 1) * plan.k_per_split < max(k, 1) <= plan.splits * plan.k_per_split
+    if plan.path in gemm.TILED_PATHS:
+        assert plan.tiles_m == -(-spec.rows // plan.tile_rows) and plan.tiles_n == -(-spec.cols // plan.tile_cols)
+        assert plan.launches * plan.batches_per_launch >= spec.batch.count
+        assert (plan.launches - 1) * plan.batches_per_launch < spec.batch.count
+        if plan.splits > 1:  # slices are whole K-steps
+            step = 64 if plan.path == gemm.PATH_BF16_STAGED else 32
+            assert plan.k_per_split % step == 0
+        check_tiled_cover(plan)
+    elif plan.path == gemm.PATH_FEW_ROWS:
+        assert spec.rows <= 16 and plan.tiles_n == -(-spec.cols // 64) and plan.k_per_split % 16 == 0
+        assert plan.workgroups == plan.tiles_n * plan.splits * spec.batch.count
+    else:
+        assert plan.path == gemm.PATH_FEW_ROWS_NT and spec.rows <= 4 and plan.splits == 1
+
+
+def test_configs_take_the_expected_kernel_families():
+    assert gemm.plan(MatmulSpec.new(32768, 2304, 768)).path == gemm.PATH_F32_DIRECT
+    assert gemm.plan(MatmulSpec.new(32768, 2304, 768).with_precision(Precision.Bf16)).path == gemm.PATH_BF16_STAGED
+    assert gemm.plan(MatmulSpec.new(1, 2304, 768)).path == gemm.PATH_FEW_ROWS
+    assert gemm.plan(MatmulSpec.new(1, 1408, 64).right_transposed()).path == gemm.PATH_FEW_ROWS_NT
+    # Masked bf16 products keep their fp32 stages (rounded per fragment).
+    assert gemm.plan(MatmulSpec.new(2048, 64, 2048).causal_left().with_precision(Precision.Bf16)).path == \
+        gemm.PATH_BF16_DIRECT
+    # Unaligned operands go through registers.
+    assert gemm.plan(MatmulSpec.new(130, 197, 100)).path == gemm.PATH_F32_REGISTER
+    assert gemm.plan(MatmulSpec.new(256, 256, 256), left=gemm.ALIGNED_ADDRESS + 4).path == gemm.PATH_F32_REGISTER
+    assert gemm.plan(MatmulSpec.new(2, 3, 4), int(MatmulKernel.Simple)).path == gemm.PATH_REFERENCE_ORDER
+    assert gemm.plan(MatmulSpec.new(0, 3, 4)).path == gemm.PATH_NONE
+
+
+def test_tiles_round_up_and_keep_the_batch_axis():
+    # launch.rs:88-99: a ragged edge adds a tile; the batch stays on the grid.
+    spec = MatmulSpec.new(129, 257, 64).batched(BatchStrides(3, 129 * 64, 64 * 257, 129 * 257))
+    plan = gemm.plan(spec)
+    assert (plan.tile_rows, plan.tile_cols) == (128, 128)
+    assert (plan.tiles_m, plan.tiles_n, plan.splits) == (2, 3, 1)
+    assert plan.batches_per_launch == 3 and plan.launches == 1 and plan.workgroups == 18 and plan.threads == 256
+    # An output 64 columns wide takes the narrow tile (three workgroups per CU).
+    narrow = gemm.plan(MatmulSpec.new(2048, 64, 2048))
+    assert (narrow.tile_rows, narrow.tile_cols) == (128, 64)
+    # The reference-order kernel: 16x16 threads per 16x16 outputs (launch.rs:77-86's shape).
+    simple = gemm.plan(spec, int(MatmulKernel.Simple))
+    assert (simple.tile_rows, simple.tile_cols, simple.threads) == (16, 16, 256)
+    assert (simple.tiles_m, simple.tiles_n, simple.batches_per_launch) == (9, 17, 3)
+
+
+def test_split_k_only_for_few_tiles_and_within_the_workspace():
+    # c2's weight gradients (K = 32768, 36-768 tiles) split K; the forward products do not.
+    assert gemm.plan(MatmulSpec.new(32768, 2304, 768)).splits == 1
+    dw = MatmulSpec.new(768, 768, 32768).left_transposed().accumulate()
+    full = gemm.plan(dw)
+    assert full.splits > 1 and full.workspace_bytes == full.splits * 768 * 768 * 4
+    # A smaller workspace caps the slices; none leaves a single pass.
+    capped = gemm.plan(dw, workspace_bytes=4 * 768 * 768 * 4)
+    assert 1 < capped.splits <= 4
+    assert gemm.plan(dw, workspace_bytes=0).splits == 1
+    # Masked and batched products never split.
+    assert all(p.splits == 1 for p in (gemm.plan(s) for _, s in attention_products()))
+
+
+def test_batched_launches_give_each_xcd_whole_matrices():
+    # 192 attention matrices of 256 tiles: every XCD receives 24 whole heads, so the causal mix of
+    # full and skipped tiles is the same on every XCD.
+    plan = gemm.plan(MatmulSpec.new(2048, 2048, 64).right_transposed().batched(
+        BatchStrides(192, 2048 * 64, 2048 * 64, 2048 * 2048)).causal_output())
+    matrix, _ = check_tiled_cover(plan)
+    xcd = np.arange(plan.workgroups) % XCDS
+    for x in range(XCDS):
+        heads, counts = np.unique(matrix[xcd == x], return_counts=True)
+        assert len(heads) == 192 // XCDS and np.all(counts == plan.tiles_m * plan.tiles_n)
+        assert heads.max() - heads.min() == len(heads) - 1  # a contiguous run
+
+
+def test_split_products_give_each_xcd_whole_slices():
+    plan = gemm.plan(MatmulSpec.new(768, 768, 32768).left_transposed().accumulate())
+    _, split = check_tiled_cover(plan)
+    xcd = np.arange(plan.workgroups) % XCDS
+    tiles = plan.tiles_m * plan.tiles_n
+    for x in range(XCDS):
+        slices, counts = np.unique(split[xcd == x], return_counts=True)
+        # Whole slices, except where a slice straddles two XCDs' ranges.
+        assert np.sum(counts == tiles) >= len(slices) - 2
+
+
+def test_tile_map_rejects_bad_arguments():
+    with pytest.raises(gemm.GpuError):
+        gemm.tile_map(0, 1, 1, 1)
+    with pytest.raises(gemm.GpuError):
+        gemm.plan(MatmulSpec.new(2, 3, 4).batched(BatchStrides(0, 0, 0, 0)))
