@@ -307,14 +307,14 @@ int sn_matmul_validate(const sn_matmul_spec* spec, size_t left_len, size_t right
 
 }  // extern "C"
 
-namespace {
+namespace sn {
 
 // The kernels' description of a validated spec (ops/matmul.rs:24-32 for
 // the storage conventions), with `bias` (null: none) fused into the
 // epilogue unless the product is masked.
-sn::Problem problem_of(const sn_matmul_spec* spec, const float* left, const float* right, float* output,
+Problem problem_of(const sn_matmul_spec* spec, const float* left, const float* right, float* output,
                        const float* bias) {
-    sn::Problem p;
+    Problem p;
     p.a = left;
     p.b = right;
     p.c = output;
@@ -351,13 +351,8 @@ uint32_t kernel_for(uint32_t context_kernel, uint32_t precision) {
     return context_kernel;
 }
 
-// sn_matmul and sn_matmul_bias: validation, then the product with `bias`
-// (null: none) added in its epilogue, or, for a masked spec, after it by the
-// bias kernel.
-int matmul_with_bias(sn_context* ctx, const sn_matmul_spec* spec, const float* left, size_t left_len,
-                     const float* right, size_t right_len, const float* bias, size_t bias_len, float* output,
-                     size_t output_len) {
-    if (ctx == nullptr) return SN_ERR_NULL_ARGUMENT;
+int check_matmul_call(const sn_matmul_spec* spec, const float* left, size_t left_len, const float* right,
+                      size_t right_len, const float* bias, size_t bias_len, const float* output, size_t output_len) {
     int rc = sn_matmul_validate(spec, left_len, right_len, output_len);
     if (rc != SN_OK) return rc;
     Lengths need;
@@ -368,11 +363,27 @@ int matmul_with_bias(sn_context* ctx, const sn_matmul_spec* spec, const float* l
     if (overlaps(output, need.output, left, need.left) || overlaps(output, need.output, right, need.right))
         return SN_ERR_ALIASING;
     if (bias != nullptr && overlaps(output, need.output, bias, bias_len)) return SN_ERR_ALIASING;
+    return SN_OK;
+}
+
+}  // namespace sn
+
+namespace {
+
+// sn_matmul and sn_matmul_bias: validation, then the product with `bias`
+// (null: none) added in its epilogue, or, for a masked spec, after it by the
+// bias kernel.
+int matmul_with_bias(sn_context* ctx, const sn_matmul_spec* spec, const float* left, size_t left_len,
+                     const float* right, size_t right_len, const float* bias, size_t bias_len, float* output,
+                     size_t output_len) {
+    if (ctx == nullptr) return SN_ERR_NULL_ARGUMENT;
+    const int rc = sn::check_matmul_call(spec, left, left_len, right, right_len, bias, bias_len, output, output_len);
+    if (rc != SN_OK) return rc;
     if (spec->rows == 0 || spec->cols == 0) return SN_OK;
 
-    const sn::Problem p = problem_of(spec, left, right, output, bias);
+    const sn::Problem p = sn::problem_of(spec, left, right, output, bias);
     const bool bias_after = bias != nullptr && p.bias == nullptr;
-    const uint32_t kernel = kernel_for(ctx->kernel, spec->precision);
+    const uint32_t kernel = sn::kernel_for(ctx->kernel, spec->precision);
     if (sn::describe_matmul(p, kernel, ctx->env).workspace_bytes > ctx->env.workspace_bytes) return SN_ERR_WORKSPACE;
     hipError_t err = hipSetDevice(ctx->device);
     if (err == hipSuccess) err = sn::launch_matmul(p, kernel, ctx->env, ctx->stream);
@@ -411,7 +422,7 @@ int sn_plan_matmul(const sn_matmul_spec* spec, uint32_t kernel, const float* lef
     const int rc = check_spec(spec, &need);
     if (rc != SN_OK) return rc;
     if (kernel > SN_KERNEL_SIMPLE) return SN_ERR_UNSUPPORTED;
-    const sn::Problem p = problem_of(spec, left, right, const_cast<float*>(output), nullptr);
+    const sn::Problem p = sn::problem_of(spec, left, right, const_cast<float*>(output), nullptr);
     // A context's environment as sn_context_create would set it up; the
     // workspace and counters are never touched, only their sizes and the
     // workspace's alignment matter (a device allocation is 2 MiB aligned).
@@ -421,7 +432,7 @@ int sn_plan_matmul(const sn_matmul_spec* spec, uint32_t kernel, const float* lef
     env.workspace = workspace_bytes > 0 ? reinterpret_cast<float*>(uintptr_t(1) << 44) : nullptr;
     env.counters = reinterpret_cast<uint32_t*>(uintptr_t(1) << 45);
     env.counter_count = kCounterCount;
-    const sn::LaunchShape s = sn::describe_matmul(p, kernel_for(kernel, spec->precision), env);
+    const sn::LaunchShape s = sn::describe_matmul(p, sn::kernel_for(kernel, spec->precision), env);
     plan->path = s.path;
     plan->threads = s.threads;
     plan->tile_rows = uint32_t(s.tile_m);

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <cstdint>
 
+#include "staleynet_gemm.h"
+
 namespace sn {
 
 // One (batched) product in the kernels' terms. "K-contiguous" means element
@@ -61,6 +63,17 @@ LaunchShape describe_gemm_bf16(const Problem& p, const Env& env);
 LaunchShape describe_gemm_simple(const Problem& p);
 LaunchShape describe_gemv(const Problem& p);
 LaunchShape describe_gemv_nt(const Problem& p);
+
+// sn_matmul's host side (context.cpp): the checks of a call (the reference's
+// asserts, null operands, an output overlapping an input), the kernels'
+// description of a checked spec with `bias` (null: none) fused unless the
+// product is masked, and the kernel a call runs (the context's choice,
+// overridden by the spec's precision).
+int check_matmul_call(const sn_matmul_spec* spec, const float* left, size_t left_len, const float* right,
+                      size_t right_len, const float* bias, size_t bias_len, const float* output, size_t output_len);
+Problem problem_of(const sn_matmul_spec* spec, const float* left, const float* right, float* output,
+                   const float* bias);
+uint32_t kernel_for(uint32_t context_kernel, uint32_t precision);
 
 // The routing of sn_matmul: which family serves `p` under context kernel
 // `kernel` (SN_KERNEL_*), and that family's launch.

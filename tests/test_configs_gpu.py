@@ -177,6 +177,145 @@ def test_attention_products_match_the_oracle(gpu, attention, index, masked):
     assert error < TOLERANCE, f"{name} masked={masked}: relative error {error}"
 
 
+# ---- config 3 at its full batch: 192 heads, sampled -------------------------------------------
+# The launches bench.py times: 16 x 12 = 192 heads of T = 2048, h = 64, whose batch the tiled
+# kernels deal over the XCDs in whole heads. Each product is checked on 65536 sampled outputs,
+# each computed by the oracle in the reference's order; the fused kernels on 1024 sampled
+# (head, query) rows, each the oracle's three calls (or the backward's calls) on that row alone,
+# which is the same arithmetic as the full calls give that row.
+
+BH3, ROWS3 = 192, 1024
+
+
+@pytest.fixture(scope="module")
+def attention_full(gpu):
+    """Q, K, V, dO ~ N(0, 1) in device memory; P and dS from the fused kernels (causal matrices with
+    zeros past the diagonal, inputs of the products here), and the host copies."""
+    q, k, v, do = (normal(gpu, Shape(BH3 * T, H), 500 + i) for i in range(4))
+    o = gpu.zeros(Shape(BH3 * T, H))
+    p = gpu.zeros(Shape(BH3 * T, T))
+    gpu.causal_attention(q, k, v, o, BH3, T, T, H, 0.125, probabilities=p)
+    ds = gpu.zeros(Shape(BH3 * T, T))
+    dq = gpu.zeros(Shape(BH3 * T, H))
+    gpu.causal_attention_score_grad(do, v, o, p, ds, BH3, T, T, H, k=k, q_grad=dq, scale=0.125)
+    dev = {"q": q, "k": k, "v": v, "do": do, "o": o, "p": p, "ds": ds, "dq": dq}
+    host = {name: gpu.download(t) for name, t in dev.items()}
+    yield host, dev
+    for t in dev.values():
+        t.free()
+
+
+def full_batch_specs():
+    head, score = T * H, T * T
+    per_head = lambda left, right, out: BatchStrides(BH3, left, right, out)  # noqa: E731
+    return [
+        ("scores", MatmulSpec.new(T, T, H).right_transposed().batched(per_head(head, head, score)), "q", "k", "out"),
+        ("mix", MatmulSpec.new(T, H, T).batched(per_head(score, head, head)), "p", "v", "left"),
+        ("prob_grad", MatmulSpec.new(T, T, H).right_transposed().batched(per_head(head, head, score)), "do", "v",
+         "out"),
+        ("value_grad", MatmulSpec.new(T, H, T).left_transposed().batched(per_head(score, head, head)), "p", "do",
+         "left"),
+        ("query_grad", MatmulSpec.new(T, H, T).scaled(0.125).batched(per_head(score, head, head)), "ds", "k",
+         "left"),
+        ("key_grad", MatmulSpec.new(T, H, T).left_transposed().scaled(0.125).batched(per_head(score, head, head)),
+         "ds", "q", "left"),
+    ]
+
+
+@pytest.mark.parametrize("masked", [False, True], ids=["dense", "causal"])
+@pytest.mark.parametrize("index", range(6), ids=[a[0] for a in full_batch_specs()])
+def test_attention_products_over_all_192_heads(gpu, attention_full, index, masked):
+    host, dev = attention_full
+    name, spec, left, right, kind = full_batch_specs()[index]
+    print(f"c3 192 heads: {name} masked={masked}", flush=True)
+    if masked:
+        spec = spec.causal_output() if kind == "out" else spec.causal_left()
+    out = gpu.zeros(Shape(BH3 * spec.rows, spec.cols))
+    gpu.matmul(spec, dev[left], dev[right], out)
+    actual = gpu.download(out)
+    out.free()
+    rng = np.random.default_rng(index + 10 * masked)
+    picks = rng.choice(actual.size, size=SAMPLES, replace=False)
+    b, rest = np.divmod(picks, spec.rows * spec.cols)
+    r, c = np.divmod(rest, spec.cols)
+    got = actual[picks]
+    assert np.all(np.isfinite(got))
+    expected = oracle.matmul_elements_parallel(product_of(spec), host[left], host[right], b, r, c)
+    if masked and kind == "out":
+        visible = c <= r
+        assert np.all(got[~visible] == 0.0)
+        error = oracle.relative_error(expected[visible], got[visible])
+    else:
+        error = oracle.relative_error(expected, got)
+    assert error < TOLERANCE, f"{name} masked={masked}: relative error {error}"
+    # Every head is represented in the sample.
+    assert len(np.unique(b)) == BH3
+
+
+def sampled_rows(seed):
+    rng = np.random.default_rng(seed)
+    picks = rng.choice(BH3 * T, size=ROWS3, replace=False)
+    return np.divmod(picks, T)
+
+
+def one_row(rows, cols, inner, right_transposed=False, scale=1.0):
+    return oracle.Product(rows, cols, inner, False, right_transposed, 1, 0, 0, 0, scale, False)
+
+
+def test_fused_forward_over_all_192_heads(gpu, attention_full):
+    # sn_causal_attention at config 3's full batch against the three calls of attention.rs:206-213.
+    host, _ = attention_full
+    heads, queries = sampled_rows(1)
+    o_err, p_err = [], []
+    expected_o, got_o, expected_p, got_p = [], [], [], []
+    for b, r in zip(heads, queries):
+        row = b * T + r
+        k_head, v_head = host["k"][b * T * H:(b + 1) * T * H], host["v"][b * T * H:(b + 1) * T * H]
+        s = np.zeros(T, np.float32)
+        oracle.matmul(one_row(1, T, H, right_transposed=True), host["q"][row * H:(row + 1) * H], k_head, s)
+        oracle.causal_softmax(s, 1, T, 0.125, int(r))  # query r of its head sees keys 0 ..= r
+        o = np.zeros(H, np.float32)
+        oracle.matmul(one_row(1, H, T), s, v_head, o)
+        expected_o.append(o)
+        got_o.append(host["o"][row * H:(row + 1) * H])
+        expected_p.append(s)
+        got_p.append(host["p"][row * T:(row + 1) * T])
+    assert len(np.unique(heads)) > 150
+    for name, e, g in (("O", expected_o, got_o), ("P", expected_p, got_p)):
+        e, g = np.concatenate(e), np.concatenate(g)
+        assert np.all(np.isfinite(g))
+        error = oracle.relative_error(e, g)
+        print(f"fused forward {name}: {error:.2e}")
+        assert error < TOLERANCE
+
+
+def test_fused_score_and_query_gradients_over_all_192_heads(gpu, attention_full):
+    # sn_causal_attention_score_grad (with dQ) at config 3's full batch against the backward's dP
+    # product, softmax_backward and dQ product (attention.rs:238-253), given the same P.
+    host, _ = attention_full
+    heads, queries = sampled_rows(2)
+    expected_ds, got_ds, expected_dq, got_dq = [], [], [], []
+    for b, r in zip(heads, queries):
+        row = b * T + r
+        k_head, v_head = host["k"][b * T * H:(b + 1) * T * H], host["v"][b * T * H:(b + 1) * T * H]
+        dp = np.zeros(T, np.float32)
+        oracle.matmul(one_row(1, T, H, right_transposed=True), host["do"][row * H:(row + 1) * H], v_head, dp)
+        p = host["p"][row * T:(row + 1) * T].copy()
+        oracle.softmax_backward(p, dp, T)
+        dq = np.zeros(H, np.float32)
+        oracle.matmul(one_row(1, H, T, scale=0.125), dp, k_head, dq)
+        expected_ds.append(dp)
+        got_ds.append(host["ds"][row * T:(row + 1) * T])
+        expected_dq.append(dq)
+        got_dq.append(host["dq"][row * H:(row + 1) * H])
+    for name, e, g in (("dS", expected_ds, got_ds), ("dQ", expected_dq, got_dq)):
+        e, g = np.concatenate(e), np.concatenate(g)
+        assert np.all(np.isfinite(g))
+        error = oracle.relative_error(e, g)
+        print(f"fused score gradient {name}: {error:.2e}")
+        assert error < TOLERANCE
+
+
 # ---- config 4: decode shapes ----------------------------------------------------------------
 
 @pytest.mark.parametrize("rows", [1, 4, 16])
@@ -222,7 +361,7 @@ def test_cached_decode_attention_matches_the_oracle(gpu, cached):
 
 # ---- bf16-input variant at config 2 ----------------------------------------------------------
 
-@pytest.mark.parametrize("layer", ["qkv", "down", "head"])
+@pytest.mark.parametrize("layer", ["qkv", "out", "up", "down", "head"])
 def test_bf16_products_within_the_stated_tolerance(gpu, layer):
     """bf16 inputs with fp32 accumulation against the fp32 oracle: max relative
     error below 2e-2 (the variant's stated tolerance)."""

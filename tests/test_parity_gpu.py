@@ -19,7 +19,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle
-from staleynet_amd.gemm import (BatchStrides, MatmulKernel, MatmulPanic, MatmulSpec, Shape, SN_ERR_ALIASING,
+from staleynet_amd.gemm import (BatchStrides, MatmulKernel, MatmulPanic, MatmulSpec, Precision, Shape, SN_ERR_ALIASING,
                                 SN_ERR_EMPTY_BATCH, SN_ERR_LEFT_TOO_SMALL, SN_ERR_OUTPUT_TOO_SMALL)
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -434,6 +434,85 @@ def test_bf16_without_room_to_stage_takes_the_fp32_staged_kernel():
         assert np.array_equal(expected_for(spec, left, right, initial), actual)
     finally:
         small.close()
+
+
+# bf16 under the causal masks (the attention products at bf16 precision: fp32 LDS stages rounded per
+# fragment, with the masks applied in the stages). Integers of magnitude <= 8 are exact in bf16 and
+# every partial sum stays far below 2^24, so the result is exact whatever the order: a masked value
+# that leaks, a tile skipped wrongly or a wrong offset cannot hide.
+
+@pytest.mark.parametrize("offset", [0, 45])
+@pytest.mark.parametrize("accumulate", [False, True])
+def test_bf16_causal_output_mask_is_exact_on_integers(gpu, offset, accumulate):
+    # S = Q K^T per head (attention.rs:206-209) with masked tiles skipped.
+    t, h, count = 300, 64, 2
+    rng = np.random.default_rng(offset + 3 * accumulate)
+    q = rng.integers(-8, 9, size=count * t * h).astype(np.float32)
+    k = rng.integers(-8, 9, size=count * t * h).astype(np.float32)
+    initial = rng.integers(-8, 9, size=count * t * t).astype(np.float32)
+    spec = MatmulSpec.new(t, t, h).right_transposed().batched(BatchStrides(count, t * h, t * h, t * t)).scaled(0.5)
+    if accumulate:
+        spec = spec.accumulate()
+    dense = expected_for(spec, q, k, initial).reshape(count, t, t)
+    actual = run_gpu(gpu, spec.causal_output(offset).with_precision(Precision.Bf16), q, k,
+                     initial).reshape(count, t, t)
+    visible = np.broadcast_to(causal_visible(t, t, offset), dense.shape)
+    assert np.array_equal(dense[visible], actual[visible])
+    masked = actual[~visible]
+    if accumulate:
+        assert np.array_equal(masked, initial.reshape(count, t, t)[~visible])
+    else:
+        assert np.all(masked == 0.0)
+
+
+@pytest.mark.parametrize("offset", [0, 45])
+@pytest.mark.parametrize("transposed", [False, True])
+@pytest.mark.parametrize("accumulate", [False, True])
+def test_bf16_causal_left_mask_is_exact_on_integers(gpu, offset, transposed, accumulate):
+    # O = P V (NN) and dV = P^T dO, dK = s dS^T Q (TN) with P causal (attention.rs:212-213,
+    # 244-260); the masked part of P holds large garbage that must not reach the result.
+    t, h, count = 280, 64, 2
+    rng = np.random.default_rng(10 + offset + 2 * transposed + accumulate)
+    p = rng.integers(-8, 9, size=(count, t, t)).astype(np.float32)
+    visible = causal_visible(t, t, offset)
+    p_clean = np.where(visible, p, 0).astype(np.float32)
+    p_dirty = np.where(visible, p, 1e4).astype(np.float32)
+    v = rng.integers(-8, 9, size=count * t * h).astype(np.float32)
+    spec = MatmulSpec.new(t, h, t).batched(BatchStrides(count, t * t, t * h, t * h)).scaled(0.125)
+    if transposed:
+        spec = spec.left_transposed()
+    initial = np.zeros(count * t * h, np.float32)
+    if accumulate:
+        spec = spec.accumulate()
+        initial = rng.integers(-8, 9, size=count * t * h).astype(np.float32)
+    expected = expected_for(spec, p_clean.ravel(), v, initial)
+    actual = run_gpu(gpu, spec.causal_left(offset).with_precision(Precision.Bf16), p_dirty.ravel(), v, initial)
+    assert np.array_equal(expected, actual)
+
+
+@pytest.mark.parametrize("mask", ["output", "left"])
+def test_bf16_causal_masks_within_the_stated_tolerance(gpu, mask):
+    # N(0, 1)-like inputs at config 3's head shape (T = 2048, h = 64, two heads), against the fp32
+    # oracle at the variant's 2e-2.
+    t, h, count = 2048, 64, 2
+    if mask == "output":
+        spec = MatmulSpec.new(t, t, h).right_transposed().batched(BatchStrides(count, t * h, t * h, t * t))
+        left = oracle.random_values(count * t * h, 61)
+        right = oracle.random_values(count * t * h, 62)
+        expected = expected_for(spec, left, right, np.zeros(count * t * t, np.float32)).reshape(count, t, t)
+        actual = run_gpu(gpu, spec.causal_output().with_precision(Precision.Bf16), left, right,
+                         np.zeros(count * t * t, np.float32)).reshape(count, t, t)
+        visible = np.broadcast_to(causal_visible(t, t, 0), expected.shape)
+        check(expected[visible], actual[visible], 2e-2)
+        assert np.all(actual[~visible] == 0.0)
+    else:
+        p = np.where(causal_visible(t, t, 0), oracle.random_values(count * t * t, 63).reshape(count, t, t),
+                     0).astype(np.float32).ravel()
+        right = oracle.random_values(count * t * h, 64)
+        spec = MatmulSpec.new(t, h, t).left_transposed().batched(BatchStrides(count, t * t, t * h, t * h))
+        initial = np.zeros(count * t * h, np.float32)
+        check(expected_for(spec, p, right, initial),
+              run_gpu(gpu, spec.causal_left().with_precision(Precision.Bf16), p, right, initial), 2e-2)
 
 
 # ---- decode-shaped products (few rows, row-major weight) ------------------------------
