@@ -377,6 +377,30 @@ int sn_upload_tokens(sn_context *context, const uint32_t *host, size_t count, ui
 int sn_download_tokens(sn_context *context, const uint32_t *device, size_t count, uint32_t *host);
 int sn_free_tokens(sn_context *context, uint32_t *buffer);
 
+/* ---- the allocation-free variant ------------------------------------------ */
+/* The most scratch sn_matmul_noalloc's kernels use for split-K partial sums
+ * (and bf16 staged operands); 64 KiB of arrival counters come on top. */
+#define SN_NOALLOC_WORKSPACE_BYTES ((size_t)64 << 20)
+
+/* sn_matmul without a context and without allocating anything. It has no
+ * counterpart in the reference (whose Gpu::matmul, ops/matmul.rs:146-171,
+ * needs no scratch); it is for callers that cannot allocate device memory:
+ * code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc. The product runs on the calling thread's current device, on
+ * `stream` (a hipStream_t; null is the default stream), with the kernel the
+ * spec's precision names (default and F32: fp32 matrix cores; BF16: bf16
+ * inputs). Its scratch is a device array of the library's, one per device,
+ * held from the library's load until the process ends: 64 KiB of arrival
+ * counters (cleared on the first call on each device) and
+ * SN_NOALLOC_WORKSPACE_BYTES for partial sums. A product that would need
+ * more partial sums than that splits K into fewer slices (within the fp32
+ * tolerance of sn_matmul's result; bit-identical when both plans agree);
+ * one that cannot fit returns SN_ERR_WORKSPACE. The same checks and codes as
+ * sn_matmul. Calls that overlap on one device (other streams or threads)
+ * share the array and race. */
+int sn_matmul_noalloc(const sn_matmul_spec *spec, const float *left, size_t left_len, const float *right,
+                      size_t right_len, float *output, size_t output_len, void *stream);
+
 /* ---- launch geometry (host only) ------------------------------------------ */
 /* The kernel family a product runs on, as sn_plan_matmul reports it. */
 #define SN_PATH_NONE 0u            /* rows or cols of 0: nothing is launched */

@@ -362,6 +362,8 @@ def _library() -> ctypes.CDLL:
         lib.sn_softmax_backward.argtypes = [ctx, ctypes.c_void_p, size, size, ctypes.c_void_p, size, size]
         lib.sn_plan_matmul.argtypes = [ctypes.POINTER(CMatmulSpec), ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p,
                                        ctypes.c_void_p, ctypes.c_uint32, size, ctypes.POINTER(CLaunchPlan)]
+        lib.sn_matmul_noalloc.argtypes = [ctypes.POINTER(CMatmulSpec), ctypes.c_void_p, size, ctypes.c_void_p, size,
+                                          ctypes.c_void_p, size, ctypes.c_void_p]
         u32p = ctypes.POINTER(ctypes.c_uint32)
         lib.sn_tile_map.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, u32p, u32p,
                                     u32p, u32p]
@@ -372,7 +374,7 @@ def _library() -> ctypes.CDLL:
                      "sn_add_row_bias", "sn_accumulate_column_sums", "sn_matmul_bias", "sn_causal_softmax",
                      "sn_softmax_backward", "sn_cross_entropy", "sn_upload_tokens", "sn_download_tokens",
                      "sn_free_tokens", "sn_split_heads", "sn_merge_heads", "sn_causal_attention",
-                     "sn_causal_attention_score_grad", "sn_plan_matmul", "sn_tile_map"):
+                     "sn_causal_attention_score_grad", "sn_plan_matmul", "sn_tile_map", "sn_matmul_noalloc"):
             getattr(lib, name).restype = ctypes.c_int
         _lib = lib
     return _lib
