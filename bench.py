@@ -25,7 +25,10 @@ The printed JSON line is the driver's contract plus:
   decode token's 49 products in sequence;
 - ``linear_bias``: config 2's Linear forward as the reference calls it (matmul, then
   add_row_bias) against the fused sn_matmul_bias, and the bias-gradient column sums;
-- ``head_cross_entropy``: the head's 16 per-codebook cross-entropy calls at config 2.
+- ``head_cross_entropy``: the head's 16 per-codebook cross-entropy calls at config 2;
+- ``published``: the reference's own published products (the only GEMM numbers it publishes, on
+  Jetsons) with its timing method, fp32 and bf16; configs 0 and 1 as whole training sets; config 2's
+  two weakest products.
 """
 from __future__ import annotations
 
@@ -138,6 +141,23 @@ class HipGraph:
     def close(self) -> None:
         self.hip.hipGraphExecDestroy(self.exec)
         self.hip.hipGraphDestroy(self.graph)
+
+
+class PlainReplay:
+    """HipGraph's interface without a graph: `launch` issues the recorded calls directly. Used by
+    --plain-launches, so that a profiled run captures no HIP graph."""
+
+    def __init__(self, stream: int, record):
+        self.record = record
+
+    def launch(self) -> None:
+        self.record()
+
+    def close(self) -> None:
+        pass
+
+
+REPLAY = HipGraph
 
 
 def timed(events: HipEvents, stream: int, body, repeats: int) -> float:
@@ -426,7 +446,7 @@ def measure_decode(gpu: Gpu, events: HipEvents, pool_bytes: int = 640 << 20, rep
     best = 0.0
     for blocks in (1024, 2048, 4096):
         part = gpu.zeros(Shape(blocks, 1))
-        graph = HipGraph(gpu.stream, lambda: [gpu.read_sum(w, part) for w in pool])
+        graph = REPLAY(gpu.stream, lambda: [gpu.read_sum(w, part) for w in pool])
         graph.launch()
         ms = timed(events, gpu.stream, graph.launch, repeats) / copies
         graph.close()
@@ -445,7 +465,7 @@ def measure_decode(gpu: Gpu, events: HipEvents, pool_bytes: int = 640 << 20, rep
             x, y = gpu.zeros(Shape(m, k)), gpu.zeros(Shape(m, n))
             gpu.fill_normal(x, SEED, 999)
             spec = MatmulSpec.new(m, n, k)
-            graph = HipGraph(gpu.stream, lambda: [gpu.matmul(spec, x, w, y) for w in pool])
+            graph = REPLAY(gpu.stream, lambda: [gpu.matmul(spec, x, w, y) for w in pool])
             graph.launch()
             ms = timed(events, gpu.stream, graph.launch, repeats) / copies
             graph.close()
@@ -460,10 +480,33 @@ def measure_decode(gpu: Gpu, events: HipEvents, pool_bytes: int = 640 << 20, rep
         gpu.fill_normal(w, SEED, 2000 + i, 0.0, 0.02)
         weights.append((w, gpu.zeros(Shape(1, k)), gpu.zeros(Shape(1, n)), MatmulSpec.new(1, n, k)))
     token_bytes = sum(decode_bytes(1, k, n) for k, n in layers)
-    graph = HipGraph(gpu.stream, lambda: [gpu.matmul(spec, x, w, y) for w, x, y, spec in weights])
+    graph = REPLAY(gpu.stream, lambda: [gpu.matmul(spec, x, w, y) for w, x, y, spec in weights])
     graph.launch()
     ms = timed(events, gpu.stream, graph.launch, 5)
     graph.close()
+    # What bounds the layer products: the per-launch floor (the smallest product, replayed 96 times)
+    # and the same products with their weight resident in the Infinity Cache (96 launches over two
+    # weights) against the HBM-resident rates above.
+    x, w, y = gpu.zeros(Shape(1, 4)), gpu.zeros(Shape(4, 64)), gpu.zeros(Shape(1, 64))
+    tiny = MatmulSpec.new(1, 64, 4)
+    graph = REPLAY(gpu.stream, lambda: [gpu.matmul(tiny, x, w, y) for _ in range(96)])
+    graph.launch()
+    result["launch_floor_us"] = round(timed(events, gpu.stream, graph.launch, repeats) / 96 * 1e3, 2)
+    graph.close()
+    for t in (x, w, y):
+        t.free()
+    result["cache_resident_us"] = {}
+    for name, k, n in DECODE_SHAPES:
+        pair = [gpu.zeros(Shape(k, n)) for _ in range(2)]
+        x, y = gpu.zeros(Shape(1, k)), gpu.zeros(Shape(1, n))
+        spec = MatmulSpec.new(1, n, k)
+        graph = REPLAY(gpu.stream, lambda: [gpu.matmul(spec, x, pair[i % 2], y) for i in range(96)])
+        graph.launch()
+        result["cache_resident_us"][f"M=1 {name} {k}x{n}"] = round(timed(events, gpu.stream, graph.launch, repeats)
+                                                                   / 96 * 1e3, 2)
+        graph.close()
+        for t in pair + [x, y]:
+            t.free()
     result["attention"] = measure_decode_attention(gpu, events, repeats)
     head = result["per_shape_gbs"][f"M=1 head {DECODE_SHAPES[4][1]}x{DECODE_SHAPES[4][2]}"]
     result["head_m1_frac_hbm_peak"] = round(head / PEAK_HBM_GBS, 4)
@@ -503,7 +546,7 @@ def measure_decode_attention(gpu: Gpu, events: HipEvents, repeats: int = 3):
             gpu.matmul(mix_spec, scores, v, o)
 
         for name, body in (("fused_us", fused), ("three_calls_us", three_calls)):
-            graph = HipGraph(gpu.stream, lambda: [body() for _ in range(12)])
+            graph = REPLAY(gpu.stream, lambda: [body() for _ in range(12)])
             graph.launch()
             ms = timed(events, gpu.stream, graph.launch, repeats) / 12
             graph.close()
@@ -554,6 +597,146 @@ def run_decode_pmc_workload(gpu: Gpu) -> int:
     for t in pool + [x, y]:
         t.free()
     return len(launches)
+
+
+DECODE_ATTENTION = dict(heads=12, capacity=1408, head_dim=64, cached=701)
+
+
+def decode_attention_bytes(kind: str, heads: int, capacity: int, h: int, visible: int) -> int:
+    """Algorithmic bytes of one decode-attention launch (one query per head, `visible` cached keys):
+    the fused form reads q and the visible K and V rows and writes o; the reference's three calls
+    are the scores product (q, visible K rows in; the whole [heads, capacity] score row out),
+    causal_softmax (visible scores in, the whole row out) and the mix (visible P and V rows in, o out)."""
+    return 4 * {"fused": 2 * heads * visible * h + 2 * heads * h,
+                "scores": heads * visible * h + heads * h + heads * capacity,
+                "softmax": heads * visible + heads * capacity,
+                "mix": heads * visible + heads * visible * h + heads * h}[kind]
+
+
+def run_decode_attention_pmc_workload(gpu: Gpu, pool_bytes: int = DECODE_PMC_POOL_BYTES) -> int:
+    """One decode step's attention (12 heads, one query against a 1408-position cache holding 701)
+    over a pool of distinct caches larger than the 256 MB Infinity Cache, one plain launch per call:
+    the fused decode form over the whole pool, then the reference's three calls over it."""
+    a = DECODE_ATTENTION
+    heads, capacity, h, offset = a["heads"], a["capacity"], a["head_dim"], a["cached"] - 1
+    copies = max(2, -(-pool_bytes // (8 * heads * capacity * h)))
+    caches = []
+    for i in range(copies):
+        k, v = gpu.zeros(Shape(heads * capacity, h)), gpu.zeros(Shape(heads * capacity, h))
+        gpu.fill_normal(k, SEED, 6000 + 2 * i)
+        gpu.fill_normal(v, SEED, 6001 + 2 * i)
+        caches.append((k, v))
+    q, o = gpu.zeros(Shape(heads, h)), gpu.zeros(Shape(heads, h))
+    scores = gpu.zeros(Shape(heads, capacity))
+    gpu.fill_normal(q, SEED, 5999)
+    score_spec = MatmulSpec.new(1, capacity, h).right_transposed().batched(
+        BatchStrides(heads, h, capacity * h, capacity)).causal_output(offset)
+    mix_spec = MatmulSpec.new(1, h, capacity).batched(BatchStrides(heads, capacity, capacity * h, h)).causal_left(offset)
+    for k, v in caches:
+        gpu.causal_attention(q, k, v, o, heads, 1, capacity, h, 0.125, query_offset=offset, q_stride=h,
+                             kv_stride=capacity * h)
+    for k, v in caches:
+        gpu.matmul(score_spec, q, k, scores)
+        gpu.causal_softmax(scores, 1, 0.125, offset)
+        gpu.matmul(mix_spec, scores, v, o)
+    gpu.synchronize()
+    for t in [q, o, scores] + [t for pair in caches for t in pair]:
+        t.free()
+    return 4 * copies
+
+
+def summarize_kernel_pmc(fetch_csv: str, write_csv: str, trace_csv: str, copy_mib: int, algorithmic: dict) -> str:
+    """Per kernel (name holding a key of `algorithmic`, bytes per launch): mean HBM read and write
+    bytes per dispatch (FETCH_SIZE, WRITE_SIZE, copy-calibrated as in summarize_pmc) and mean
+    duration from a kernel-trace run of the same workload."""
+    fetch, write = _per_dispatch(fetch_csv, "FETCH_SIZE"), _per_dispatch(write_csv, "WRITE_SIZE")
+    copy_bytes = copy_mib << 20
+    pick = lambda table, key: next(v for k, v in table.items() if key in k)  # noqa: E731
+    f_factor = pick(fetch, COPY_KERNEL_KEY)[-1] * 1024 / copy_bytes
+    w_factor = pick(write, COPY_KERNEL_KEY)[-1] * 1024 / copy_bytes
+    lines = [f"copy kernel ({copy_mib} MiB read + {copy_mib} MiB written): factors {f_factor:.4f} (fetch), "
+             f"{w_factor:.4f} (write)", "",
+             f"{'kernel':>28} {'launches':>8} {'alg KB':>8} {'HBM rd KB':>10} {'HBM wr KB':>10} "
+             f"{'traffic/alg':>11} {'kernel us':>10} {'alg GB/s':>9} {'HBM GB/s':>9}"]
+    for key, alg in algorithmic.items():
+        f = [v for name, values in fetch.items() if key in name for v in values]
+        w = [v for name, values in write.items() if key in name for v in values]
+        ns = _trace_durations(trace_csv, key)
+        if not f or not w or not ns:
+            continue
+        rd = sum(f) / len(f) * 1024 / f_factor
+        wr = sum(w) / len(w) * 1024 / w_factor
+        t = sum(ns) / len(ns)
+        lines.append(f"{key:>28} {len(ns):>8} {alg / 1e3:>8.1f} {rd / 1e3:>10.1f} {wr / 1e3:>10.1f} "
+                     f"{(rd + wr) / alg:>11.3f} {t / 1e3:>10.2f} {alg / t:>9.0f} {(rd + wr) / t:>9.0f}")
+    return "\n".join(lines)
+
+
+def decode_attention_algorithmic() -> dict:
+    a = DECODE_ATTENTION
+    args = (a["heads"], a["capacity"], a["head_dim"], a["cached"])
+    return {"decode_attention_kernel": decode_attention_bytes("fused", *args),
+            "gemv_nt_kernel": decode_attention_bytes("scores", *args),
+            "causal_softmax": decode_attention_bytes("softmax", *args),
+            "gemv_kernel": decode_attention_bytes("mix", *args)}
+
+
+# ---- the reference's published shapes, configs 0 and 1, the weakest config-2 products ------
+
+# The only GEMM numbers the reference publishes (book/src/experiments.md:50-52, paper/appendix.tex:49-51,
+# paper/body.tex:1261-1263): row-major NN forward products timed by `staleynet bench`
+# (crates/staleynet-cli/src/commands/bench.rs:131-140), on NVIDIA Jetsons. (label, M, N, K,
+# Orin NX register-blocked GFLOP/s, AGX Thor TF32 tensor-core GFLOP/s.)
+PUBLISHED = [
+    ("QKV projection", 2048, 768, 256, 579.0, 929.0),
+    ("FFN expand", 2048, 1024, 256, 450.6, 730.0),
+    ("output heads (4 codebooks)", 2048, 4096, 256, 458.5, 970.0),
+]
+MODEL_7M = dict(name="7.1M", blocks=6, width=256, ffn=1024, heads_width=16 * 1024, tokens=4 * 512)
+MODEL_43M = dict(name="42.9M", blocks=8, width=512, ffn=2048, heads_width=16 * 1024, tokens=8 * 1024)
+
+
+def reference_method_ms(events: HipEvents, stream: int, body) -> float:
+    """The reference's bench timing (bench.rs:117-128; experiments.md:42-47): the mean of 5 runs
+    after 1 warm-up, and the median of 3 such measurements."""
+    return sorted(timed(events, stream, body, 5) for _ in range(3))[1]
+
+
+def measure_published(gpu: Gpu, events: HipEvents, set_per_shape: dict):
+    """The reference's published products on one MI355X, fp32 and bf16, beside the Jetson figures
+    (context only: other hardware, and the reference benches zero-filled operands where these are
+    seeded); configs 0 and 1 as whole training sets; config 2's two weakest products."""
+    result = {"method": "mean of 5 launches after 1 warm-up, median of 3 (bench.rs:117-128); GFLOP/s = 2MNK/t",
+              "products": {}}
+    for label, m, n, k, orin, thor in PUBLISHED:
+        x, w, y = gpu.zeros(Shape(m, k)), gpu.zeros(Shape(k, n)), gpu.zeros(Shape(m, n))
+        gpu.fill_normal(x, SEED, 5000)
+        gpu.fill_normal(w, SEED, 5001, 0.0, 0.02)
+        spec = MatmulSpec.new(m, n, k)
+        entry = {}
+        for name, s in (("fp32", spec), ("bf16", spec.with_precision(Precision.Bf16))):
+            ms = reference_method_ms(events, gpu.stream, lambda: gpu.matmul(s, x, w, y))
+            entry[f"gflops_{name}"] = round(s.flops() / (ms * 1e-3) / 1e9, 1)
+            entry[f"us_{name}"] = round(ms * 1e3, 2)
+        entry["reference_orin_nx_blocked_gflops"] = orin
+        entry["reference_agx_thor_tf32_gflops"] = thor
+        result["products"][f"{label} {m}x{n}x{k} NN"] = entry
+        for t in (x, w, y):
+            t.free()
+    for model, key in ((MODEL_7M, "config0_7.1M_set"), (MODEL_43M, "config1_42.9M_set")):
+        calls, buffers = build_set(gpu, model)
+        flops = sum(spec.flops() for _, _, spec, _ in calls)
+        ms, per_call = measure_set(gpu, events, calls, 3, 1)
+        _, per_layout, _ = summarize_set(calls, per_call, PEAK_FP32_TFLOPS)
+        result[key] = {"tflops": round(flops / (ms * 1e-3) / 1e12, 2), "ms_per_step": round(ms, 3),
+                       "frac_fp32_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 4),
+                       "gemms": len(calls), "tflop": round(flops / 1e12, 4), "per_layout": per_layout}
+        for buf in buffers:
+            for t in (buf.x, buf.w, buf.dy, buf.y, buf.dx, buf.dw):
+                t.free()
+    result["config2_weakest"] = {k: {"tflops": v, "frac_fp32_peak": round(v / PEAK_FP32_TFLOPS, 4)}
+                                 for k, v in sorted(set_per_shape.items(), key=lambda kv: kv[1])[:2]}
+    return result
 
 
 # ---- Linear's bias kernels (SURVEY next row: the steps either side of NN and TN) ---------
@@ -902,9 +1085,19 @@ def main() -> int:
     parser.add_argument("--summarize-decode-pmc", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "KERNEL_TRACE_CSV"),
                         help="print the decode GEMV's HBM bytes and GB/s per product from two --pmc runs and a "
                              "kernel-trace run of --decode-pmc, and exit (no GPU)")
+    parser.add_argument("--decode-attention-pmc", action="store_true",
+                        help="run only the decode-attention counter workload (the fused decode form, then the "
+                             "reference's three calls, over a pool of caches; with --copy-calibration-mib, the "
+                             "calibration copy first) and exit")
+    parser.add_argument("--summarize-kernel-pmc", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "KERNEL_TRACE_CSV"),
+                        help="print HBM bytes and durations per decode-attention kernel from two --pmc runs and a "
+                             "kernel-trace run of --decode-attention-pmc, and exit (no GPU)")
     parser.add_argument("--one-attention", choices=["forward", "forward_p", "score_grad", "score_grad_dq"],
                         help="run only config 3's fused attention kernel 1 + 5 times and exit: the workload of the "
                              "attention counter profiles")
+    parser.add_argument("--plain-launches", action="store_true",
+                        help="replay the decode measurements' launches directly instead of from HIP graphs (for "
+                             "profiled runs: the timings then include host launch costs)")
     parser.add_argument("--one-product", nargs=2, metavar=("LAYOUT", "PRECISION"),
                         help="run only config 2's qkv product (NN, TN or NT; f32 or bf16) 1 + 5 times and exit: "
                              "the workload of the per-kernel counter profiles")
@@ -919,10 +1112,17 @@ def main() -> int:
     if args.summarize_counters:
         print(summarize_counters(args.summarize_counters))
         return 0
+    if args.summarize_kernel_pmc:
+        print(summarize_kernel_pmc(*args.summarize_kernel_pmc, args.copy_calibration_mib or 1024,
+                                   decode_attention_algorithmic()))
+        return 0
     if args.summarize_decode_pmc:
         print(summarize_decode_pmc(*args.summarize_decode_pmc, args.copy_calibration_mib or 1024))
         return 0
 
+    if args.plain_launches:
+        global REPLAY
+        REPLAY = PlainReplay
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: the GEMM path runs on one device and its sharding is a design "
               f"note, not a measured path; got --gpus {args.gpus}", file=sys.stderr)
@@ -958,6 +1158,10 @@ def main() -> int:
         dst.free()
     if args.decode_pmc:
         print(json.dumps({"decode_pmc_launches": run_decode_pmc_workload(gpu)}))
+        gpu.close()
+        return 0
+    if args.decode_attention_pmc:
+        print(json.dumps({"decode_attention_pmc_launches": run_decode_attention_pmc_workload(gpu)}))
         gpu.close()
         return 0
     calls, _buffers = build_set(gpu)
@@ -1020,6 +1224,7 @@ def main() -> int:
         result["head_cross_entropy"] = measure_loss(gpu, events, _buffers)
         result["attention"] = measure_attention(gpu, events)
         result["decode"] = measure_decode(gpu, events)
+        result["published"] = measure_published(gpu, events, per_shape)
 
     if not args.no_cpu:
         projected_s, sampled_flops, sampled_s, samples = cpu_baseline(gpu, calls, args.cpu_budget)

@@ -118,3 +118,38 @@ def test_trace_summary_lists_kernels_and_compares_the_roofline_kernel(tmp_path):
     text = bench.summarize_trace(str(stats), str(line))
     assert "fill_normal_kernel" in text
     assert "rocprof average 1.0000 ms over 49 launches; bench.py HIP-event mean 1.0100 ms (ratio 1.010)" in text
+
+
+def test_kernel_counter_summary_recovers_known_bytes_and_rates(tmp_path):
+    # Three decode-attention kernels, each reading 1.5x and writing 0.5x its algorithmic bytes in a
+    # duration that gives 2 TB/s on the algorithmic bytes; FETCH_SIZE reports half of the bytes read.
+    algorithmic = bench.decode_attention_algorithmic()
+    names = {"decode_attention_kernel": "void sn::(anonymous namespace)::decode_attention_kernel<64, 1>(Args)",
+             "gemv_nt_kernel": "void sn::(anonymous namespace)::gemv_nt_kernel<1>(Args)",
+             "gemv_kernel": "void sn::(anonymous namespace)::gemv_kernel<1, 16>(Args)"}
+    fetch, write = [(1, COPY, "FETCH_SIZE", 1024 * 1024 // 2)], [(1, COPY, "WRITE_SIZE", 1024 * 1024)]
+    trace = []
+    dispatch = 10
+    for key, name in names.items():
+        alg = algorithmic[key]
+        for _ in range(4):
+            fetch.append((dispatch, name, "FETCH_SIZE", 1.5 * alg / 2 / 1024))
+            write.append((dispatch, name, "WRITE_SIZE", 0.5 * alg / 1024))
+            trace.append((dispatch, name, 1000, 1000 + int(round(alg / 2000.0))))
+            dispatch += 1
+    write_counters(tmp_path / "f.csv", fetch)
+    write_counters(tmp_path / "w.csv", write)
+    with open(tmp_path / "t.csv", "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(["Dispatch_Id", "Kernel_Name", "Start_Timestamp", "End_Timestamp"])
+        for row in trace:
+            w.writerow([row[0], row[1], row[2], row[3]])
+    text = bench.summarize_kernel_pmc(str(tmp_path / "f.csv"), str(tmp_path / "w.csv"), str(tmp_path / "t.csv"),
+                                      1024, algorithmic)
+    rows = {line.split()[0]: line.split() for line in text.splitlines()[3:] if line.strip()}
+    assert set(rows) == set(names)
+    for key, r in rows.items():
+        assert int(r[1]) == 4
+        assert float(r[5]) == pytest.approx(2.0, abs=2e-3)          # traffic / algorithmic
+        assert float(r[7]) == pytest.approx(2000, rel=2e-3)         # algorithmic GB/s
+        assert float(r[8]) == pytest.approx(4000, rel=2e-3)         # HBM GB/s
