@@ -386,30 +386,60 @@ def measure_attention(gpu: Gpu, events: HipEvents, repeats: int = 3):
         "three_calls_ms": round(unfused_ms, 3), "fused_ms": round(fused_ms, 3),
         "fused_with_probabilities_ms": round(fused_p_ms, 3),
         "fused_tflops_on_visible_work": round(2 * causal_flops / (fused_ms * 1e-3) / 1e12, 1)}
+    # One layer's attention training kernels, two ways. Keeping P: the fused forward with the
+    # probabilities, the fused score gradient with dQ, and the causal dV and dK products. Without
+    # P (sn_causal_attention_with_stats + sn_causal_attention_backward): the forward keeps 16
+    # bytes per query, the backward recomputes S and dP (7 products' MFMAs over the visible
+    # pairs against the reference's 4).
+    keeping_p_ms = (fused_p_ms + fused_grad_q_ms + result["products"]["dV = P^T.dO"]["causal_ms"]
+                    + result["products"]["dK = s.dS^T.Q"]["causal_ms"])
+    stats = gpu.zeros(Shape.vector(2 * heads * t))
+    stats_ms = timed(events, gpu.stream, lambda: gpu.causal_attention_with_stats(q, k, v, o, stats, heads, t, t, h,
+                                                                                 0.125), repeats)
+    backward_p_free_ms = timed(events, gpu.stream, lambda: gpu.causal_attention_backward(
+        q, k, v, o, do, stats, dq, dk, dv, heads, t, t, h, 0.125), repeats)
+    stats.free()
+    result["training_kernels"] = {
+        "keeping_probabilities_ms": round(keeping_p_ms, 3),
+        "probability_free_ms": round(stats_ms + backward_p_free_ms, 3),
+        "forward_with_stats_ms": round(stats_ms, 3), "backward_ms": round(backward_p_free_ms, 3),
+        "backward_tflops_on_reference_work": round(4 * causal_flops / (backward_p_free_ms * 1e-3) / 1e12, 1),
+        "backward_tflops_executed": round(7 * causal_flops / (backward_p_free_ms * 1e-3) / 1e12, 1),
+        "probability_bytes_not_kept": 4 * heads * t * t}
     return result
 
 
 def run_one_attention(gpu: Gpu, events: HipEvents, kind: str) -> dict:
     """Config 3's fused attention kernel alone (192 heads, T = 2048, h = 64), one warm-up and five
     timed calls: `forward` (O only), `forward_p` (O and the probabilities), `score_grad` (dS from
-    dO, V, O, P) or `score_grad_dq` (with dQ): the workload of the attention counter profiles."""
+    dO, V, O, P), `score_grad_dq` (with dQ), `forward_stats` (O and the row statistics) or
+    `backward` (dQ, dK, dV from the statistics, no P): the workload of the attention counter
+    profiles."""
     heads, t, h = 16 * 12, 2048, 64
     q, k, v, o, do, dq = (gpu.zeros(Shape(heads * t, h)) for _ in range(6))
     p, ds = gpu.zeros(Shape(heads * t, t)), gpu.zeros(Shape(heads * t, t))
     for i, tensor in enumerate((q, k, v, do)):
         gpu.fill_normal(tensor, SEED, 900 + i)
+    dk, dv = gpu.zeros(Shape(heads * t, h)), gpu.zeros(Shape(heads * t, h))
+    stats = gpu.zeros(Shape.vector(2 * heads * t))
     if kind.startswith("score_grad"):  # the gradient reads the forward's O and P
         gpu.causal_attention(q, k, v, o, heads, t, t, h, 0.125, probabilities=p)
+    if kind == "backward":  # ... this one O and the statistics
+        gpu.causal_attention_with_stats(q, k, v, o, stats, heads, t, t, h, 0.125)
     calls = {
         "forward": lambda: gpu.causal_attention(q, k, v, o, heads, t, t, h, 0.125),
         "forward_p": lambda: gpu.causal_attention(q, k, v, o, heads, t, t, h, 0.125, probabilities=p),
         "score_grad": lambda: gpu.causal_attention_score_grad(do, v, o, p, ds, heads, t, t, h),
         "score_grad_dq": lambda: gpu.causal_attention_score_grad(do, v, o, p, ds, heads, t, t, h, k=k, q_grad=dq,
                                                                  scale=0.125),
+        "forward_stats": lambda: gpu.causal_attention_with_stats(q, k, v, o, stats, heads, t, t, h, 0.125),
+        "backward": lambda: gpu.causal_attention_backward(q, k, v, o, do, stats, dq, dk, dv, heads, t, t, h, 0.125),
     }
     ms = timed(events, gpu.stream, calls[kind], 5)
     visible = heads * t * (t + 1) // 2
-    products = {"forward": 2, "forward_p": 2, "score_grad": 1, "score_grad_dq": 2}[kind]
+    # The reference's products the call stands for (the backward executes 7 products' MFMAs for its 4).
+    products = {"forward": 2, "forward_p": 2, "score_grad": 1, "score_grad_dq": 2, "forward_stats": 2,
+                "backward": 4}[kind]
     return {"attention": kind, "ms": round(ms, 4),
             "tflops_on_visible_work": round(products * 2 * h * visible / (ms * 1e-3) / 1e12, 1)}
 
@@ -1092,7 +1122,8 @@ def main() -> int:
     parser.add_argument("--summarize-kernel-pmc", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "KERNEL_TRACE_CSV"),
                         help="print HBM bytes and durations per decode-attention kernel from two --pmc runs and a "
                              "kernel-trace run of --decode-attention-pmc, and exit (no GPU)")
-    parser.add_argument("--one-attention", choices=["forward", "forward_p", "score_grad", "score_grad_dq"],
+    parser.add_argument("--one-attention", choices=["forward", "forward_p", "score_grad", "score_grad_dq",
+                                                    "forward_stats", "backward"],
                         help="run only config 3's fused attention kernel 1 + 5 times and exit: the workload of the "
                              "attention counter profiles")
     parser.add_argument("--plain-launches", action="store_true",

@@ -343,6 +343,39 @@ int sn_causal_attention_score_grad(sn_context *context, const sn_attention_shape
                                    const float *probabilities, size_t probabilities_len, float *grad,
                                    size_t grad_len, const float *k, size_t k_len, float *q_grad, size_t q_grad_len);
 
+/* ---- training attention without the probabilities in memory -------------- */
+/* sn_causal_attention's forward for training without P: O, and per query
+ * the softmax statistics the backward below rebuilds P from: stats[head]
+ * [query] = {m, l}, m the largest of the query's scaled visible scores and l
+ * the sum of e^(x - m) over them (2 floats per query, 8-byte aligned). No
+ * counterpart in the reference, whose forward keeps P (attention.rs:
+ * 206-213). The same checks and codes as sn_causal_attention; stats must not
+ * overlap another buffer. */
+int sn_causal_attention_with_stats(sn_context *context, const sn_attention_shape *shape, const float *q,
+                                   size_t q_len, const float *k, size_t k_len, const float *v, size_t v_len,
+                                   float *out, size_t out_len, float *stats, size_t stats_len);
+
+/* The attention backward from the forward's output and statistics instead
+ * of its probabilities: what CausalSelfAttention::backward (crates/
+ * staleynet-model/src/layers/attention.rs:238-260) computes with the dP and
+ * dV products, softmax_backward and the dQ and dK products, without any
+ * [queries, keys] matrix in memory. q, k, v as for sn_causal_attention;
+ * out: the forward's O [heads][queries][head_dim], dense; d_out: dO, laid
+ * out as q (q_stride apart per head); stats: the forward's
+ * sn_causal_attention_with_stats statistics. Writes q_grad = scale * dS K
+ * [heads][queries][head_dim], k_grad = scale * dS^T Q and v_grad = P^T dO
+ * [heads][keys][head_dim], all dense, with dS = P * (dO V^T - D) and D per
+ * query = sum over h of dO * O (softmax_backward's projection, since O =
+ * P V). Within the fp32 tolerance of the reference's calls; deterministic
+ * (no atomics). Uses 12 bytes of the context's workspace per query
+ * (SN_ERR_WORKSPACE); the same shape codes as sn_causal_attention; an
+ * output overlapping an input or another output is SN_ERR_ALIASING. */
+int sn_causal_attention_backward(sn_context *context, const sn_attention_shape *shape, const float *q, size_t q_len,
+                                 const float *k, size_t k_len, const float *v, size_t v_len, const float *out,
+                                 size_t out_len, const float *d_out, size_t d_out_len, const float *stats,
+                                 size_t stats_len, float *q_grad, size_t q_grad_len, float *k_grad,
+                                 size_t k_grad_len, float *v_grad, size_t v_grad_len);
+
 /* ---- the head's consumer: per-codebook softmax cross-entropy ------------- */
 /* An empty target slot (crates/staleynet-cuda/src/kernels/mod.rs:46). */
 #define SN_EMPTY_TOKEN 0xFFFFFFFFu

@@ -42,6 +42,7 @@
 #include <cstdint>
 #include <type_traits>
 
+#include "attention_common.h"
 #include "gemm_common.h"
 #include "gemm_internal.h"
 
@@ -49,68 +50,15 @@
 namespace sn {
 namespace {
 
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef __attribute__((address_space(3))) void* lds_void;
-
-constexpr int kWaves = 4;
-constexpr int kQueries = 32 * kWaves;  // per workgroup
-constexpr int kKeys = 64;              // per LDS stage
-constexpr int32_t kRecords = 0x7FFFFFFF;
-constexpr int32_t kOutOfRange = int32_t(0x80000000u);
-constexpr int32_t kRawBufferFormat = 0x00020000;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const float* base) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, kRecords, kRawBufferFormat);
-}
-
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, const void* lds, int32_t offset) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void)lds, 16, offset, 0, 0, 0);
-}
-
-// Waits until at most PENDING of this wave's vector-memory loads are in
-// flight (vmcnt; the other counters left at their maxima).
-template <int PENDING>
-__device__ __forceinline__ void wait_loads() {
-    static_assert(PENDING >= 0 && PENDING < 64, "vmcnt is 6 bits");
-    __builtin_amdgcn_s_waitcnt(0x0F70 | (PENDING & 15) | ((PENDING >> 4) << 14));
-}
-
-// e^d as 2^(d log2 e) on the transcendental unit (v_exp_f32, about 1 ulp).
-// d is a difference x - m already rounded as causal_softmax rounds it, so
-// rounding d log2 e adds at most |d| 2^-24 to the exponent: a relative error
-// under 2e-6 for every probability above e^-20, whatever the logits' size.
-// d = -inf gives 0.
-constexpr float kLog2e = 1.44269504088896340736f;
-__device__ __forceinline__ float exp_of(float d) { return __builtin_amdgcn_exp2f(d * kLog2e); }
-
-// Workgroup barrier that does not wait for loads still in flight (the
-// direct-to-LDS loads of the next stage); LDS reads are completed first.
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
-
-template <int H, int KEYS = kKeys>
-struct Geometry {
-    static constexpr int SLOTS = H / 4;                        // 16-byte chunks per row
-    static constexpr int SWIZZLE = SLOTS < 16 ? SLOTS - 1 : 15;  // row bits XORed into the chunk index
-    static constexpr int CHUNKS = H / 16;                      // 16-deep MFMA chunks over h
-    static constexpr int OBLOCKS = H / 32;                     // 32-row accumulator blocks of O^T
-    static constexpr int STAGE_SLOTS = KEYS * SLOTS;           // f32x4 per operand per stage
-    static constexpr int LOADS = STAGE_SLOTS / (64 * kWaves);  // load instructions per wave per operand
-    static_assert(H == 32 || H == 64 || H == 128, "head dims 32, 64, 128");
-    static_assert(STAGE_SLOTS % (64 * kWaves) == 0, "whole load instructions per wave");
-};
+using namespace attn;
 
 struct AttentionArgs {
     const float* q;
     const float* k;
     const float* v;
     float* o;
-    float* p;  // null: no probabilities
+    float* p;      // null: no probabilities
+    float* stats;  // null, or per query {m, l}: the maximum of its scaled visible scores and the sum of e^(x - m)
     int64_t queries, keys;
     int64_t q_stride, kv_stride;  // floats between heads
     int64_t query_offset;
@@ -332,6 +280,9 @@ void causal_attention_kernel(AttentionArgs args) {
     }
     wait_loads<0>();  // the loads past the end land before the stages are reused
 
+    // The row statistics the recomputing backward needs (both lanes of a query hold the same m, l).
+    if (args.stats != nullptr && q < args.queries && half == 0)
+        *reinterpret_cast<float2*>(args.stats + 2 * (head * args.queries + q)) = make_float2(m, l);
     // O = O^T / l: lane l holds h rows 32 b + 4 half + 8 (r / 4) + (r % 4) of its query.
     if (q < args.queries) {
         float* orow = args.o + (head * args.queries + q) * H;
@@ -968,7 +919,7 @@ namespace {
 // probabilities requested, more than kDecodeQueries queries, or no room for
 // the records and counters.
 int64_t decode_chunks(const CausalAttentionArgs& a) {
-    if (a.p != nullptr || a.queries > kDecodeQueries || a.heads > 65535) return 0;
+    if (a.p != nullptr || a.stats != nullptr || a.queries > kDecodeQueries || a.heads > 65535) return 0;
     const int64_t visible = std::min(a.keys, a.queries + a.query_offset);  // keys the last query sees
     const int64_t chunks = (visible + kDecodeKeys - 1) / kDecodeKeys;
     const int64_t record_bytes = int64_t(kDecodeQueries) * (a.head_dim + 4) * 4;
@@ -1022,6 +973,7 @@ hipError_t launch_causal_attention(const CausalAttentionArgs& a, hipStream_t str
     args.v = a.v;
     args.o = a.o;
     args.p = a.p;
+    args.stats = a.stats;
     args.queries = a.queries;
     args.keys = a.keys;
     args.q_stride = a.q_stride;
@@ -1043,7 +995,9 @@ hipError_t launch_causal_attention(const CausalAttentionArgs& a, hipStream_t str
 bool causal_attention_supported(const CausalAttentionArgs& a) {
     const bool dims = a.head_dim == 32 || a.head_dim == 64 || a.head_dim == 128;
     const bool aligned = aligned16(a.q) && aligned16(a.k) && aligned16(a.v) && aligned16(a.o) &&
-                         (a.p == nullptr || aligned16(a.p)) && a.q_stride % 4 == 0 && a.kv_stride % 4 == 0;
+                         (a.p == nullptr || aligned16(a.p)) &&
+                         (a.stats == nullptr || (reinterpret_cast<uintptr_t>(a.stats) & 7) == 0) &&
+                         a.q_stride % 4 == 0 && a.kv_stride % 4 == 0;
     // Per-head buffer offsets (keys x h floats) within 31 bits; the grid within 32 bits.
     const bool offsets = a.keys * a.head_dim * 4 < (int64_t(1) << 31) - 4096;
     const int64_t query_blocks = (a.queries + kQueries - 1) / kQueries;

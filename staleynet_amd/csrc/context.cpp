@@ -583,42 +583,71 @@ int sn_causal_softmax(sn_context* ctx, float* scores, size_t rows, size_t keys, 
     return status(err);
 }
 
-int sn_causal_attention(sn_context* ctx, const sn_attention_shape* shape, const float* q, size_t q_len,
-                        const float* k, size_t k_len, const float* v, size_t v_len, float* out, size_t out_len,
-                        float* probabilities, size_t probabilities_len) {
-    if (ctx == nullptr || shape == nullptr) return SN_ERR_NULL_ARGUMENT;
-    const sn_attention_shape& a = *shape;
-    if (a.heads == 0 || a.queries == 0) return SN_OK;
+}  // extern "C"
+
+namespace {
+
+// Element counts an attention call's buffers must hold (SN_OK or the code).
+struct AttentionNeed {
+    size_t q = 0, kv = 0, o = 0, p = 0, kv_dense = 0;
+};
+
+int attention_need(const sn_attention_shape& a, AttentionNeed* need) {
     if (a.keys == 0) return SN_ERR_SHAPE;
     if (a.head_dim != 32 && a.head_dim != 64 && a.head_dim != 128) return SN_ERR_UNSUPPORTED;
     const size_t limit = size_t(1) << 60;
-    size_t q_rows, kv_rows, q_last, kv_last, q_need, kv_need, o_need, head_rows, p_rows, p_need = 0;
+    size_t q_rows, kv_rows, q_last, kv_last, o_need, head_rows, p_rows, kv_dense;
     if (mul_overflows(a.queries, a.head_dim, &q_rows) || mul_overflows(a.keys, a.head_dim, &kv_rows) ||
         mul_overflows(a.heads - 1, a.q_stride, &q_last) || mul_overflows(a.heads - 1, a.kv_stride, &kv_last) ||
         mul_overflows(a.heads, q_rows, &o_need) || mul_overflows(a.heads, a.queries, &head_rows) ||
-        mul_overflows(head_rows, a.keys, &p_rows) || a.heads >= limit || a.queries >= limit || q_rows >= limit ||
-        kv_rows >= limit || q_last >= limit || kv_last >= limit || o_need >= limit || p_rows >= limit ||
+        mul_overflows(head_rows, a.keys, &p_rows) || mul_overflows(a.heads, kv_rows, &kv_dense) ||
+        a.heads >= limit || a.queries >= limit || q_rows >= limit || kv_rows >= limit || q_last >= limit ||
+        kv_last >= limit || o_need >= limit || p_rows >= limit || kv_dense >= limit ||
         a.query_offset >= (size_t(1) << 62))
         return SN_ERR_OVERFLOW;
-    q_need = q_last + q_rows;
-    kv_need = kv_last + kv_rows;
-    if (probabilities != nullptr) p_need = p_rows;
-    if (q_len < q_need || k_len < kv_need || v_len < kv_need || out_len < o_need ||
-        (probabilities != nullptr && probabilities_len < p_need))
+    need->q = q_last + q_rows;
+    need->kv = kv_last + kv_rows;
+    need->o = o_need;
+    need->p = p_rows;
+    need->kv_dense = kv_dense;
+    return SN_OK;
+}
+
+// sn_causal_attention and its variant with the row statistics.
+int causal_attention_call(sn_context* ctx, const sn_attention_shape* shape, const float* q, size_t q_len,
+                          const float* k, size_t k_len, const float* v, size_t v_len, float* out, size_t out_len,
+                          float* probabilities, size_t probabilities_len, float* stats, size_t stats_len) {
+    if (ctx == nullptr || shape == nullptr) return SN_ERR_NULL_ARGUMENT;
+    const sn_attention_shape& a = *shape;
+    if (a.heads == 0 || a.queries == 0) return SN_OK;
+    AttentionNeed need;
+    const int rc = attention_need(a, &need);
+    if (rc != SN_OK) return rc;
+    const size_t p_need = probabilities != nullptr ? need.p : 0;
+    const size_t s_need = stats != nullptr ? 2 * need.o / a.head_dim : 0;
+    if (q_len < need.q || k_len < need.kv || v_len < need.kv || out_len < need.o ||
+        (probabilities != nullptr && probabilities_len < p_need) || (stats != nullptr && stats_len < s_need))
         return SN_ERR_LENGTH_MISMATCH;
     if (q == nullptr || k == nullptr || v == nullptr || out == nullptr) return SN_ERR_NULL_ARGUMENT;
-    if (overlaps(out, o_need, q, q_need) || overlaps(out, o_need, k, kv_need) || overlaps(out, o_need, v, kv_need))
+    if (overlaps(out, need.o, q, need.q) || overlaps(out, need.o, k, need.kv) || overlaps(out, need.o, v, need.kv))
         return SN_ERR_ALIASING;
     if (probabilities != nullptr &&
-        (overlaps(probabilities, p_need, q, q_need) || overlaps(probabilities, p_need, k, kv_need) ||
-         overlaps(probabilities, p_need, v, kv_need) || overlaps(probabilities, p_need, out, o_need)))
+        (overlaps(probabilities, p_need, q, need.q) || overlaps(probabilities, p_need, k, need.kv) ||
+         overlaps(probabilities, p_need, v, need.kv) || overlaps(probabilities, p_need, out, need.o)))
         return SN_ERR_ALIASING;
+    if (stats != nullptr &&
+        (overlaps(stats, s_need, q, need.q) || overlaps(stats, s_need, k, need.kv) ||
+         overlaps(stats, s_need, v, need.kv) || overlaps(stats, s_need, out, need.o) ||
+         overlaps(stats, s_need, probabilities, p_need)))
+        return SN_ERR_ALIASING;
+    const size_t q_rows = a.queries * a.head_dim, kv_rows = a.keys * a.head_dim;
     sn::CausalAttentionArgs args;
     args.q = q;
     args.k = k;
     args.v = v;
     args.o = out;
     args.p = probabilities;
+    args.stats = stats;
     args.heads = int64_t(a.heads);
     args.queries = int64_t(a.queries);
     args.keys = int64_t(a.keys);
@@ -634,6 +663,81 @@ int sn_causal_attention(sn_context* ctx, const sn_attention_shape* shape, const 
     if (!sn::causal_attention_supported(args)) return SN_ERR_UNSUPPORTED;
     hipError_t err = hipSetDevice(ctx->device);
     if (err == hipSuccess) err = sn::launch_causal_attention(args, ctx->stream);
+    return status(err);
+}
+
+}  // namespace
+
+extern "C" {
+
+int sn_causal_attention(sn_context* ctx, const sn_attention_shape* shape, const float* q, size_t q_len,
+                        const float* k, size_t k_len, const float* v, size_t v_len, float* out, size_t out_len,
+                        float* probabilities, size_t probabilities_len) {
+    return causal_attention_call(ctx, shape, q, q_len, k, k_len, v, v_len, out, out_len, probabilities,
+                                 probabilities_len, nullptr, 0);
+}
+
+int sn_causal_attention_with_stats(sn_context* ctx, const sn_attention_shape* shape, const float* q, size_t q_len,
+                                   const float* k, size_t k_len, const float* v, size_t v_len, float* out,
+                                   size_t out_len, float* stats, size_t stats_len) {
+    if (stats == nullptr) return SN_ERR_NULL_ARGUMENT;
+    return causal_attention_call(ctx, shape, q, q_len, k, k_len, v, v_len, out, out_len, nullptr, 0, stats,
+                                 stats_len);
+}
+
+int sn_causal_attention_backward(sn_context* ctx, const sn_attention_shape* shape, const float* q, size_t q_len,
+                                 const float* k, size_t k_len, const float* v, size_t v_len, const float* out,
+                                 size_t out_len, const float* d_out, size_t d_out_len, const float* stats,
+                                 size_t stats_len, float* q_grad, size_t q_grad_len, float* k_grad,
+                                 size_t k_grad_len, float* v_grad, size_t v_grad_len) {
+    if (ctx == nullptr || shape == nullptr) return SN_ERR_NULL_ARGUMENT;
+    const sn_attention_shape& a = *shape;
+    if (a.heads == 0 || a.queries == 0) return SN_OK;
+    AttentionNeed need;
+    const int rc = attention_need(a, &need);
+    if (rc != SN_OK) return rc;
+    const size_t s_need = 2 * need.o / a.head_dim;
+    if (q_len < need.q || k_len < need.kv || v_len < need.kv || out_len < need.o || d_out_len < need.q ||
+        stats_len < s_need || q_grad_len < need.o || k_grad_len < need.kv_dense || v_grad_len < need.kv_dense)
+        return SN_ERR_LENGTH_MISMATCH;
+    if (q == nullptr || k == nullptr || v == nullptr || out == nullptr || d_out == nullptr || stats == nullptr ||
+        q_grad == nullptr || k_grad == nullptr || v_grad == nullptr)
+        return SN_ERR_NULL_ARGUMENT;
+    const float* inputs[6] = {q, k, v, out, d_out, stats};
+    const size_t input_lens[6] = {need.q, need.kv, need.kv, need.o, need.q, s_need};
+    float* outputs[3] = {q_grad, k_grad, v_grad};
+    const size_t output_lens[3] = {need.o, need.kv_dense, need.kv_dense};
+    for (int o = 0; o < 3; ++o) {
+        for (int i = 0; i < 6; ++i)
+            if (overlaps(outputs[o], output_lens[o], inputs[i], input_lens[i])) return SN_ERR_ALIASING;
+        for (int p = o + 1; p < 3; ++p)
+            if (overlaps(outputs[o], output_lens[o], outputs[p], output_lens[p])) return SN_ERR_ALIASING;
+    }
+    sn::AttentionBackwardArgs args;
+    args.q = q;
+    args.k = k;
+    args.v = v;
+    args.out = out;
+    args.d_out = d_out;
+    args.stats = stats;
+    args.q_grad = q_grad;
+    args.k_grad = k_grad;
+    args.v_grad = v_grad;
+    args.workspace = ctx->env.workspace;
+    args.workspace_bytes = ctx->env.workspace_bytes;
+    args.heads = int64_t(a.heads);
+    args.queries = int64_t(a.queries);
+    args.keys = int64_t(a.keys);
+    args.head_dim = int64_t(a.head_dim);
+    args.q_stride = int64_t(a.heads > 1 ? a.q_stride : a.queries * a.head_dim);
+    args.kv_stride = int64_t(a.heads > 1 ? a.kv_stride : a.keys * a.head_dim);
+    args.query_offset = int64_t(a.query_offset);
+    args.scale = a.scale;
+    if (size_t(a.heads) * 3 * ((a.queries + 3) / 4 * 4) * sizeof(float) > ctx->env.workspace_bytes)
+        return SN_ERR_WORKSPACE;
+    if (!sn::attention_backward_supported(args)) return SN_ERR_UNSUPPORTED;
+    hipError_t err = hipSetDevice(ctx->device);
+    if (err == hipSuccess) err = sn::launch_attention_backward(args, ctx->stream);
     return status(err);
 }
 

@@ -104,6 +104,9 @@ struct CausalAttentionArgs {
     const float* v = nullptr;
     float* o = nullptr;
     float* p = nullptr;
+    // Null, or per query {m, l} [heads][queries][2]: the maximum of its scaled
+    // visible scores and the sum of e^(x - m) (for the recomputing backward).
+    float* stats = nullptr;
     int64_t heads = 0, queries = 0, keys = 0, head_dim = 0;
     int64_t q_stride = 0, kv_stride = 0;
     int64_t query_offset = 0;
@@ -140,6 +143,35 @@ struct AttentionScoreGradArgs {
 };
 hipError_t launch_attention_score_grad(const AttentionScoreGradArgs& args, hipStream_t stream);
 bool attention_score_grad_supported(const AttentionScoreGradArgs& args);
+
+// The attention backward that recomputes the probabilities instead of
+// reading them (attention_backward.hip): from Q, K, V, the forward's O and
+// row statistics, and dO, the three gradients CausalSelfAttention::backward
+// leaves (layers/attention.rs:238-260): dV = P^T dO, dQ = scale dS K,
+// dK = scale dS^T Q with dS = P * (dO V^T - D), D = sum over h of dO * O.
+// Q and dO [heads][queries][h] (q_stride apart per head), K and V
+// [heads][keys][h] (kv_stride apart), O and dQ [heads][queries][h] dense,
+// dK and dV [heads][keys][h] dense, stats [heads][queries][2]. The workspace
+// holds 12 bytes per query (m, 1/l, D; queries rounded up to 4).
+struct AttentionBackwardArgs {
+    const float* q = nullptr;
+    const float* k = nullptr;
+    const float* v = nullptr;
+    const float* out = nullptr;
+    const float* d_out = nullptr;
+    const float* stats = nullptr;
+    float* q_grad = nullptr;
+    float* k_grad = nullptr;
+    float* v_grad = nullptr;
+    float* workspace = nullptr;
+    size_t workspace_bytes = 0;
+    int64_t heads = 0, queries = 0, keys = 0, head_dim = 0;
+    int64_t q_stride = 0, kv_stride = 0;
+    int64_t query_offset = 0;
+    float scale = 1.f;
+};
+hipError_t launch_attention_backward(const AttentionBackwardArgs& args, hipStream_t stream);
+bool attention_backward_supported(const AttentionBackwardArgs& args);
 
 // Rounds an fp32 operand to bf16 (nearest-even) into dst[batch][rows][kp],
 // K-contiguous, zeros for k in [k, kp) (bf16_stage.hip). Element (r, k) of

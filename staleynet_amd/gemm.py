@@ -360,6 +360,9 @@ def _library() -> ctypes.CDLL:
         lib.sn_merge_heads.argtypes = [ctx, ctypes.c_void_p, size, ctypes.c_void_p, size,
                                        ctypes.POINTER(CHeadLayout)]
         lib.sn_softmax_backward.argtypes = [ctx, ctypes.c_void_p, size, size, ctypes.c_void_p, size, size]
+        lib.sn_causal_attention_with_stats.argtypes = [ctx, ctypes.POINTER(CAttentionShape)] + \
+            [ctypes.c_void_p, size] * 5
+        lib.sn_causal_attention_backward.argtypes = [ctx, ctypes.POINTER(CAttentionShape)] + [ctypes.c_void_p, size] * 9
         lib.sn_plan_matmul.argtypes = [ctypes.POINTER(CMatmulSpec), ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p,
                                        ctypes.c_void_p, ctypes.c_uint32, size, ctypes.POINTER(CLaunchPlan)]
         lib.sn_matmul_noalloc.argtypes = [ctypes.POINTER(CMatmulSpec), ctypes.c_void_p, size, ctypes.c_void_p, size,
@@ -374,7 +377,8 @@ def _library() -> ctypes.CDLL:
                      "sn_add_row_bias", "sn_accumulate_column_sums", "sn_matmul_bias", "sn_causal_softmax",
                      "sn_softmax_backward", "sn_cross_entropy", "sn_upload_tokens", "sn_download_tokens",
                      "sn_free_tokens", "sn_split_heads", "sn_merge_heads", "sn_causal_attention",
-                     "sn_causal_attention_score_grad", "sn_plan_matmul", "sn_tile_map", "sn_matmul_noalloc"):
+                     "sn_causal_attention_score_grad", "sn_plan_matmul", "sn_tile_map", "sn_matmul_noalloc", "sn_causal_attention_with_stats",
+                     "sn_causal_attention_backward"):
             getattr(lib, name).restype = ctypes.c_int
         _lib = lib
     return _lib
@@ -661,6 +665,44 @@ class Gpu:
         if rc == SN_ERR_LENGTH_MISMATCH:
             raise AssertionError("causal_attention_score_grad: a buffer is too small for the shape")
         self._check(rc, "causal_attention_score_grad")
+
+    def causal_attention_with_stats(self, q: Tensor, k: Tensor, v: Tensor, out: Tensor, stats: Tensor, heads: int,
+                                    queries: int, keys: int, head_dim: int, scale: float, query_offset: int = 0,
+                                    q_stride: int | None = None, kv_stride: int | None = None) -> None:
+        """Training forward without the probabilities (``sn_causal_attention_with_stats``): ``out`` = O as
+        ``causal_attention`` gives it, ``stats`` = per query {m, l}, from which the backward rebuilds P."""
+        shape = CAttentionShape(heads, queries, keys, head_dim,
+                                queries * head_dim if q_stride is None else q_stride,
+                                keys * head_dim if kv_stride is None else kv_stride, query_offset, scale)
+        rc = _library().sn_causal_attention_with_stats(
+            self._ctx, ctypes.byref(shape), ctypes.c_void_p(q.pointer), len(q), ctypes.c_void_p(k.pointer), len(k),
+            ctypes.c_void_p(v.pointer), len(v), ctypes.c_void_p(out.pointer), len(out),
+            ctypes.c_void_p(stats.pointer), len(stats))
+        if rc == SN_ERR_SHAPE:
+            raise AssertionError("causal_attention_with_stats: no keys")
+        if rc == SN_ERR_LENGTH_MISMATCH:
+            raise AssertionError("causal_attention_with_stats: a buffer is too small for the shape")
+        self._check(rc, "causal_attention_with_stats")
+
+    def causal_attention_backward(self, q: Tensor, k: Tensor, v: Tensor, out: Tensor, d_out: Tensor, stats: Tensor,
+                                  q_grad: Tensor, k_grad: Tensor, v_grad: Tensor, heads: int, queries: int, keys: int,
+                                  head_dim: int, scale: float, query_offset: int = 0, q_stride: int | None = None,
+                                  kv_stride: int | None = None) -> None:
+        """The attention backward from O and the statistics (``sn_causal_attention_backward``):
+        ``q_grad``, ``k_grad``, ``v_grad`` = the grads.queries, grads.keys and grads.values that
+        CausalSelfAttention::backward (layers/attention.rs:238-260) leaves, with no P or dS in memory."""
+        shape = CAttentionShape(heads, queries, keys, head_dim,
+                                queries * head_dim if q_stride is None else q_stride,
+                                keys * head_dim if kv_stride is None else kv_stride, query_offset, scale)
+        args = [self._ctx, ctypes.byref(shape)]
+        for t in (q, k, v, out, d_out, stats, q_grad, k_grad, v_grad):
+            args += [ctypes.c_void_p(t.pointer), len(t)]
+        rc = _library().sn_causal_attention_backward(*args)
+        if rc == SN_ERR_SHAPE:
+            raise AssertionError("causal_attention_backward: no keys")
+        if rc == SN_ERR_LENGTH_MISMATCH:
+            raise AssertionError("causal_attention_backward: a buffer is too small for the shape")
+        self._check(rc, "causal_attention_backward")
 
     def softmax_backward(self, probabilities: Tensor, grad: Tensor) -> None:
         """``Gpu::softmax_backward`` (ops/attention.rs:76-92), in place on ``grad``."""

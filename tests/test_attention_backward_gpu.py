@@ -1,0 +1,145 @@
+"""GPU parity of the training attention that keeps no probabilities in memory: the forward with row
+statistics (``sn_causal_attention_with_stats``) and the backward that rebuilds P from them
+(``sn_causal_attention_backward``), against the oracle's restatement of the reference's calls in
+CausalSelfAttention::forward and ::backward (crates/staleynet-model/src/layers/attention.rs:206-260):
+the scores product, causal_softmax (reference.rs:100-119), the dP and dV products, softmax_backward
+(reference.rs:121-137) and the dQ and dK products (reference.rs:19-38), at the reference's fp32
+tolerance. Cases: ragged blocks, query offsets, more or fewer keys than queries, head dims 32 / 64 /
+128, config 3's size, reruns bit-identical, and the entry point's checks."""
+import numpy as np
+import pytest
+
+from oracle import oracle
+from staleynet_amd.gemm import GpuError, Shape
+
+pytestmark = pytest.mark.gpu
+
+TOLERANCE = 1e-5  # kernels_match_reference.rs:12
+
+
+def product(rows, cols, inner, lt=False, rt=False, batch=(1, 0, 0, 0), scale=1.0):
+    return oracle.Product(rows, cols, inner, lt, rt, batch[0], batch[1], batch[2], batch[3], scale, False)
+
+
+def reference(q, k, v, d_out, heads, queries, keys, h, scale, offset):
+    """The reference's forward and backward calls on the oracle: O, P's row maximum and sum, dQ, dK, dV."""
+    qb, kb, sb = queries * h, keys * h, queries * keys
+    scores = np.zeros(heads * sb, np.float32)
+    oracle.matmul_parallel(product(queries, keys, h, rt=True, batch=(heads, qb, kb, sb)), q, k, scores)
+    visible = np.minimum(np.arange(queries) + offset + 1, keys)
+    scaled = scores.reshape(heads, queries, keys) * np.float32(scale)
+    mask = np.arange(keys)[None, :] < visible[:, None]
+    row_max = np.where(mask[None], scaled, -np.inf).max(axis=2)
+    p = scores.copy()
+    oracle.causal_softmax(p, queries, keys, scale, offset)
+    out = np.zeros(heads * qb, np.float32)
+    oracle.matmul_parallel(product(queries, h, keys, batch=(heads, sb, kb, qb)), p, v, out)
+    dp = np.zeros(heads * sb, np.float32)
+    oracle.matmul_parallel(product(queries, keys, h, rt=True, batch=(heads, qb, kb, sb)), d_out, v, dp)
+    dv = np.zeros(heads * kb, np.float32)
+    oracle.matmul_parallel(product(keys, h, queries, lt=True, batch=(heads, sb, qb, kb)), p, d_out, dv)
+    oracle.softmax_backward(p, dp, keys)
+    dq = np.zeros(heads * qb, np.float32)
+    oracle.matmul_parallel(product(queries, h, keys, batch=(heads, sb, kb, qb), scale=scale), dp, k, dq)
+    dk = np.zeros(heads * kb, np.float32)
+    oracle.matmul_parallel(product(keys, h, queries, lt=True, batch=(heads, sb, qb, kb), scale=scale), dp, q, dk)
+    return out, row_max, dq, dk, dv
+
+
+def run(gpu, heads, queries, keys, h, scale, offset, seed):
+    rng = np.random.default_rng(seed)
+    q = rng.normal(0, 1, heads * queries * h).astype(np.float32)
+    k = rng.normal(0, 1, heads * keys * h).astype(np.float32)
+    v = rng.normal(0, 1, heads * keys * h).astype(np.float32)
+    d_out = rng.normal(0, 1, heads * queries * h).astype(np.float32)
+    Q, K, V, dO = (gpu.upload(Shape.vector(x.size), x) for x in (q, k, v, d_out))
+    O = gpu.upload(Shape.vector(heads * queries * h), np.full(heads * queries * h, np.nan, np.float32))
+    stats = gpu.zeros(Shape.vector(2 * heads * queries))
+    gpu.causal_attention_with_stats(Q, K, V, O, stats, heads, queries, keys, h, scale, offset)
+    dQ = gpu.upload(Shape.vector(heads * queries * h), np.full(heads * queries * h, np.nan, np.float32))
+    dK, dV = (gpu.upload(Shape.vector(heads * keys * h), np.full(heads * keys * h, np.nan, np.float32))
+              for _ in range(2))
+    gpu.causal_attention_backward(Q, K, V, O, dO, stats, dQ, dK, dV, heads, queries, keys, h, scale, offset)
+    got = {name: gpu.download(t) for name, t in (("out", O), ("stats", stats), ("dq", dQ), ("dk", dK), ("dv", dV))}
+    for t in (Q, K, V, dO, O, stats, dQ, dK, dV):
+        t.free()
+    return (q, k, v, d_out), got
+
+
+CASES = [
+    (2, 128, 128, 64, 0, 0.125),     # one query block and one key block, square causal
+    (3, 200, 200, 64, 0, 0.125),     # ragged second blocks
+    (2, 100, 300, 64, 200, 0.125),   # a cached prefix: more keys than queries
+    (2, 96, 96, 32, 0, 0.17),        # head dim 32 (config 0)
+    (1, 64, 130, 128, 66, 0.09),     # head dim 128
+    (2, 37, 37, 64, 0, 1.0),         # fewer queries than a wave's block
+    (1, 300, 260, 64, 0, 0.125),     # keys run out before the diagonal
+    (2, 512, 512, 32, 0, 0.17),      # head dim 32 over several blocks
+    (2, 384, 448, 128, 64, 0.09),    # head dim 128 over several blocks, with an offset
+    (2, 260, 700, 64, 300, 0.125),   # keys 560.. are seen by no query: their gradients are 0
+]
+
+
+@pytest.mark.parametrize("heads,queries,keys,h,offset,scale", CASES)
+def test_backward_without_probabilities_matches_the_reference_calls(gpu, heads, queries, keys, h, offset, scale):
+    print(f"backward heads={heads} queries={queries} keys={keys} h={h} offset={offset}", flush=True)
+    inputs, got = run(gpu, heads, queries, keys, h, scale, offset, seed=queries + keys + h)
+    out, row_max, dq, dk, dv = reference(*inputs, heads, queries, keys, h, scale, offset)
+    for name, expected in (("out", out), ("dq", dq), ("dk", dk), ("dv", dv)):
+        assert np.all(np.isfinite(got[name])), name
+        error = oracle.relative_error(expected, got[name])
+        assert error < TOLERANCE, f"{name}: relative error {error}"
+    # The statistics: m is exactly the largest scaled visible score (a maximum, order-free, of the
+    # same products up to their rounding); l >= 1 (the maximum's own term).
+    stats = got["stats"].reshape(heads, queries, 2)
+    assert oracle.relative_error(row_max.ravel(), stats[..., 0].ravel()) < TOLERANCE
+    assert np.all(stats[..., 1] >= 1.0)
+    # Keys that no query sees get zero gradients.
+    seen = min(keys, queries + offset)
+    assert not np.any(got["dk"].reshape(heads, keys, h)[:, seen:])
+    assert not np.any(got["dv"].reshape(heads, keys, h)[:, seen:])
+
+
+def test_forward_with_stats_gives_the_same_output(gpu):
+    # The statistics are an extra output of the same kernel: O is bit for bit sn_causal_attention's.
+    heads, t, h = 2, 300, 64
+    rng = np.random.default_rng(9)
+    q, k, v = (rng.normal(0, 1, heads * t * h).astype(np.float32) for _ in range(3))
+    Q, K, V = (gpu.upload(Shape.vector(x.size), x) for x in (q, k, v))
+    plain, with_stats = gpu.zeros(Shape.vector(heads * t * h)), gpu.zeros(Shape.vector(heads * t * h))
+    stats = gpu.zeros(Shape.vector(2 * heads * t))
+    gpu.causal_attention(Q, K, V, plain, heads, t, t, h, 0.125)
+    gpu.causal_attention_with_stats(Q, K, V, with_stats, stats, heads, t, t, h, 0.125)
+    assert np.array_equal(gpu.download(plain), gpu.download(with_stats))
+
+
+def test_config_3_heads_at_full_size_and_determinism(gpu):
+    # Two of config 3's 192 heads: T = 2048, h = 64, scale 1/8; reruns give the same bits.
+    heads, t, h = 2, 2048, 64
+    inputs, got = run(gpu, heads, t, t, h, 0.125, 0, seed=31)
+    out, _, dq, dk, dv = reference(*inputs, heads, t, t, h, 0.125, 0)
+    errors = {name: oracle.relative_error(e, got[name]) for name, e in (("dq", dq), ("dk", dk), ("dv", dv))}
+    print(" ".join(f"{k} {e:.2e}" for k, e in errors.items()))
+    assert all(e < TOLERANCE for e in errors.values()), errors
+    _, again = run(gpu, heads, t, t, h, 0.125, 0, seed=31)
+    for name in ("dq", "dk", "dv"):
+        assert np.array_equal(got[name], again[name]), name
+
+
+def test_entry_point_checks(gpu):
+    heads, t, h = 2, 64, 64
+    bufs = [gpu.zeros(Shape.vector(heads * t * h)) for _ in range(8)]
+    q, k, v, o, do, dq, dk, dv = bufs
+    stats = gpu.zeros(Shape.vector(2 * heads * t))
+    with pytest.raises(AssertionError, match="too small"):
+        gpu.causal_attention_backward(q, k, v, o, do, gpu.zeros(Shape.vector(10)), dq, dk, dv, heads, t, t, h, 1.0)
+    with pytest.raises(AssertionError, match="no keys"):
+        gpu.causal_attention_backward(q, k, v, o, do, stats, dq, dk, dv, heads, t, 0, h, 1.0)
+    with pytest.raises(GpuError):  # a gradient overlapping an input
+        gpu.causal_attention_backward(q, k, v, o, do, stats, q, dk, dv, heads, t, t, h, 1.0)
+    with pytest.raises(GpuError):  # two gradients in one buffer
+        gpu.causal_attention_backward(q, k, v, o, do, stats, dq, dq, dv, heads, t, t, h, 1.0)
+    with pytest.raises(GpuError):  # head dim 48
+        gpu.causal_attention_backward(q, k, v, o, do, stats, dq, dk, dv, heads, t, t, 48, 1.0)
+    for b in bufs + [stats]:
+        b.free()
