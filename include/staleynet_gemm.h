@@ -445,6 +445,7 @@ int sn_matmul_noalloc(const sn_matmul_spec *spec, const float *left, size_t left
 #define SN_PATH_BF16_STAGED 6u     /* bf16: both operands first rounded into the workspace */
 #define SN_PATH_BF16_DIRECT 7u     /* bf16: fp32 LDS stages rounded per fragment */
 #define SN_PATH_BF16_REGISTER 8u   /* bf16: register-staged (unaligned) operands */
+#define SN_PATH_BF16_WIDE 9u       /* bf16: 256x256 tiles rounding fp32 operands as they load */
 
 /* How one product is launched: the role of the reference's launch geometry
  * (`launch::matmul_tiles` / `matmul_blocks`, crates/staleynet-cuda/src/

@@ -20,7 +20,8 @@ INCLUDE = os.path.join(REPO_ROOT, "include")
 
 SOURCES = ["context.cpp", "gemm_mfma.hip", "gemm_dma.hip", "gemm_bf16.hip", "gemm_simple.hip", "gemv.hip", "bias.hip",
            "softmax.hip", "loss.hip", "heads.hip", "attention.hip", "bf16_stage.hip",
-           "synth.hip", "route.hip", "noalloc.hip", "attention_backward.hip"]
+           "synth.hip", "route.hip", "noalloc.hip", "attention_backward.hip",
+           "gemm_bf16_wide.hip"]
 
 # Packed-fp32 instructions are switched off: some of their forms have given
 # wrong results on these machines, and the kernels here never need them.

@@ -716,6 +716,12 @@ hipError_t launch_gemm_f32_dma(const Problem& p, const Env& env, hipStream_t str
 bool bf16_dma_applies(const Problem& p);
 LaunchShape describe_bf16_dma(const Problem& p, const Env& env);
 hipError_t launch_gemm_bf16_dma(const Problem& p, const Env& env, hipStream_t stream);
+// The 256 x 256 bf16 kernel that rounds fp32 operands as it loads them
+// (gemm_bf16_wide.hip): whether it serves `p` (unmasked, aligned, large
+// enough; partial sums fit), its launch shape and launcher.
+bool bf16_wide_applies(const Problem& p, const Env& env);
+LaunchShape describe_bf16_wide(const Problem& p, const Env& env);
+hipError_t launch_gemm_bf16_wide(const Problem& p, const Env& env, hipStream_t stream);
 // bf16 with both operands first staged as bf16 in the workspace (gemm_dma.hip):
 // whether it serves `p` (unmasked, aligned, staged operands fit), its
 // launch shape (workspace: staged operands and partial sums) and launcher.

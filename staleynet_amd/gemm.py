@@ -217,7 +217,9 @@ class CLaunchPlan(ctypes.Structure):
 # sn_launch_plan.path values (include/staleynet_gemm.h).
 PATH_NONE, PATH_REFERENCE_ORDER, PATH_FEW_ROWS, PATH_FEW_ROWS_NT = 0, 1, 2, 3
 PATH_F32_DIRECT, PATH_F32_REGISTER, PATH_BF16_STAGED, PATH_BF16_DIRECT, PATH_BF16_REGISTER = 4, 5, 6, 7, 8
-TILED_PATHS = (PATH_F32_DIRECT, PATH_F32_REGISTER, PATH_BF16_STAGED, PATH_BF16_DIRECT, PATH_BF16_REGISTER)
+PATH_BF16_WIDE = 9
+TILED_PATHS = (PATH_F32_DIRECT, PATH_F32_REGISTER, PATH_BF16_STAGED, PATH_BF16_DIRECT, PATH_BF16_REGISTER,
+               PATH_BF16_WIDE)
 
 
 class CAttentionShape(ctypes.Structure):

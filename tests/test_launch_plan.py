@@ -108,6 +108,15 @@ def test_every_tile_and_slice_is_launched_once(label, spec, kernel):
 def test_configs_take_the_expected_kernel_families():
     assert gemm.plan(MatmulSpec.new(32768, 2304, 768)).path == gemm.PATH_F32_DIRECT
     assert gemm.plan(MatmulSpec.new(32768, 2304, 768).with_precision(Precision.Bf16)).path == gemm.PATH_BF16_STAGED
+    # bf16 weight and input gradients round their fp32 operands as they load them, 256 x 256 tiles.
+    wgrad = gemm.plan(MatmulSpec.new(768, 2304, 32768).left_transposed().with_precision(Precision.Bf16))
+    assert wgrad.path == gemm.PATH_BF16_WIDE and (wgrad.tile_rows, wgrad.tile_cols) == (256, 256)
+    assert wgrad.splits > 1
+    dgrad = gemm.plan(MatmulSpec.new(32768, 768, 2304).right_transposed().with_precision(Precision.Bf16))
+    assert dgrad.path == gemm.PATH_BF16_WIDE
+    # Too narrow for a quarter tile: the staged kernels keep it.
+    assert gemm.plan(MatmulSpec.new(32768, 64, 768).right_transposed().with_precision(Precision.Bf16)).path != \
+        gemm.PATH_BF16_WIDE
     assert gemm.plan(MatmulSpec.new(1, 2304, 768)).path == gemm.PATH_FEW_ROWS
     assert gemm.plan(MatmulSpec.new(1, 1408, 64).right_transposed()).path == gemm.PATH_FEW_ROWS_NT
     # Masked bf16 products keep their fp32 stages (rounded per fragment).
