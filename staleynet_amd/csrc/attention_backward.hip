@@ -148,6 +148,28 @@ struct ChunkReads {
         for (int i = 0; i < 2 * G::CHUNKS; ++i) launder(off[i]);
     }
     // 32 rows (32 sub .. of the stage) against the 32 columns held in `reg`.
+    // The same, with the 32 columns' values read from LDS rows laid out as a
+    // stage (`rows`: the first of the 32; row r's swizzle is r & SWIZZLE,
+    // which is col & SWIZZLE for row 32 i + col, so the offsets are shared).
+    __device__ __forceinline__ f32x16 product_lds(const f32x4* stage, int sub, const f32x4* rows) const {
+        const char* base = reinterpret_cast<const char*>(stage) + 32 * sub * G::SLOTS * 16;
+        const char* other = reinterpret_cast<const char*>(rows);
+        f32x16 acc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+#pragma unroll
+        for (int c = 0; c < G::CHUNKS; ++c) {
+            const f32x4 lo = *reinterpret_cast<const f32x4*>(base + off[2 * c]);
+            const f32x4 hi = *reinterpret_cast<const f32x4*>(base + off[2 * c + 1]);
+            const f32x4 ylo = *reinterpret_cast<const f32x4*>(other + off[2 * c]);
+            const f32x4 yhi = *reinterpret_cast<const f32x4*>(other + off[2 * c + 1]);
+            const float x[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            const float y[8] = {ylo[0], ylo[1], ylo[2], ylo[3], yhi[0], yhi[1], yhi[2], yhi[3]};
+#pragma unroll
+            for (int s = 0; s < 8; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x[s], y[s], acc, 0, 0, 0);
+        }
+        return acc;
+    }
     __device__ __forceinline__ f32x16 product(const f32x4* stage, int sub, const float (&reg)[G::CHUNKS][8]) const {
         const char* base = reinterpret_cast<const char*>(stage) + 32 * sub * G::SLOTS * 16;
         f32x16 acc;
@@ -406,6 +428,229 @@ void attention_key_grad_kernel(KeyGradArgs a) {
     }
 }
 
+// Key blocks with K and V in LDS, for head dims 32 and 64: eight waves, wave
+// w taking key group w % 4 (32 keys) against query half w / 4 of every stage
+// (stage rows 32 (w / 4) .. + 31). No wave holds K or V in registers, so
+// two share each SIMD; the K and V rows are read from LDS by the same
+// swizzled chunk reads as the stage rows. At the end the two halves' partial
+// dV^T and dK^T meet in LDS and are added in a fixed order (half 0, then
+// half 1): deterministic. (K, V and the stages of h = 128 exceed the LDS, so
+// that head dim keeps the register kernel above.)
+constexpr int kLdsKeyWaves = 8;
+
+template <int H>
+__global__ __launch_bounds__(64 * kLdsKeyWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attention_key_grad_lds_kernel(KeyGradArgs a) {
+#pragma clang fp contract(off)
+    using G = Geometry<H>;  // 64 queries per stage
+    constexpr int W = kLdsKeyWaves;
+    constexpr int LOADS = G::STAGE_SLOTS / (64 * W);  // stage loads per wave and operand
+    constexpr int KV_SLOTS = kKeyBlock * G::SLOTS;
+    constexpr int KV_LOADS = KV_SLOTS / (64 * W);
+    static_assert(H <= 64 && G::STAGE_SLOTS % (64 * W) == 0 && KV_SLOTS % (64 * W) == 0, "whole loads per wave");
+    // Partial sums handed over at the end: 2 x OBLOCKS accumulators per lane
+    // of the four half-1 waves, in the stages' space.
+    constexpr int HANDOFF_FLOATS = 4 * 2 * G::OBLOCKS * 16 * 64;
+    static_assert(HANDOFF_FLOATS <= 4 * G::STAGE_SLOTS * 4, "the hand-off fits in the stages");
+    __shared__ f32x4 kv_lds[2][KV_SLOTS];
+    __shared__ f32x4 stages[4][G::STAGE_SLOTS];  // Q stage 0, Q stage 1, dO stage 0, dO stage 1
+    __shared__ f32x4 r_stage0[W][64], r_stage1[W][64];
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    auto q_of = [&](auto stage) __attribute__((always_inline)) -> f32x4* { return stages[decltype(stage)::value]; };
+    auto d_of = [&](auto stage) __attribute__((always_inline)) -> f32x4* {
+        return stages[2 + decltype(stage)::value];
+    };
+    auto r_of = [&](auto stage) __attribute__((always_inline)) -> f32x4* {
+        if constexpr (decltype(stage)::value == 0) return r_stage0[0];
+        else return r_stage1[0];
+    };
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int group = wave % 4;  // key group
+    const int qh = wave / 4;     // query half of each stage
+    const int col = lane & 31;
+    const int half = lane >> 5;
+
+    const int64_t block = blockIdx.x;
+    const int64_t head = block % a.heads;
+    const int64_t k_first = (block / a.heads) * kKeyBlock;
+    const int64_t k_wave = k_first + 32 * group;
+    const int64_t key = k_wave + col;
+    const bool key_ok = key < a.keys;
+    const int64_t q_seen = max(int64_t(0), k_first - a.query_offset);
+    const int64_t q_begin = q_seen / kKeys * kKeys;
+    const int stages_total = q_begin < a.queries ? int((a.queries - q_begin + kKeys - 1) / kKeys) : 0;
+
+    const float* q_head = a.q + head * a.q_stride;
+    const float* d_head = a.d_out + head * a.q_stride;
+    const int64_t plane = plane_of(a.queries);
+    const float* r_head = a.rows + head * 3 * plane;
+
+    // K and V of the block's 128 keys into LDS, swizzled as the stages (rows
+    // past the last key read zeros).
+    {
+        const __amdgpu_buffer_rsrc_t k_rsrc = buffer_of(a.k + head * a.kv_stride + k_first * H);
+        const __amdgpu_buffer_rsrc_t v_rsrc = buffer_of(a.v + head * a.kv_stride + k_first * H);
+        const int32_t rows_left = int32_t(min(a.keys - k_first, int64_t(kKeyBlock)));
+#pragma unroll
+        for (int u = 0; u < KV_LOADS; ++u) {
+            const int e = 64 * (wave * KV_LOADS + u) + lane;
+            const int row = e / G::SLOTS;
+            const int32_t off = row < rows_left ? (row * H + 4 * ((e % G::SLOTS) ^ (row & G::SWIZZLE))) * 4 : kOutOfRange;
+            dma16(k_rsrc, kv_lds[0] + 64 * (wave * KV_LOADS + u), off);
+            dma16(v_rsrc, kv_lds[1] + 64 * (wave * KV_LOADS + u), off);
+        }
+    }
+    int32_t stage_row[LOADS], stage_off[LOADS];
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+        const int e = 64 * (wave * LOADS + u) + lane;
+        const int row = e / G::SLOTS;
+        stage_row[u] = row;
+        stage_off[u] = (row * H + 4 * ((e % G::SLOTS) ^ (row & G::SWIZZLE))) * 4;
+    }
+    const int32_t record_off = int32_t(((lane / 16) * plane + 4 * (lane % 16)) * 4);
+
+    auto issue = [&](auto stage, int64_t q0) __attribute__((always_inline)) {
+        f32x4* qs = q_of(stage);
+        f32x4* ds = d_of(stage);
+        const __amdgpu_buffer_rsrc_t q_rsrc = buffer_of(q_head + q0 * H);
+        const __amdgpu_buffer_rsrc_t d_rsrc = buffer_of(d_head + q0 * H);
+        const int32_t rows_left = int32_t(min(a.queries - q0, int64_t(kKeys)));  // wave-uniform
+#pragma unroll
+        for (int u = 0; u < LOADS; ++u) {
+            const int32_t off = stage_row[u] < rows_left ? stage_off[u] : kOutOfRange;
+            dma16(q_rsrc, qs + 64 * (wave * LOADS + u), off);
+            dma16(d_rsrc, ds + 64 * (wave * LOADS + u), off);
+        }
+        const __amdgpu_buffer_rsrc_t r_rsrc = buffer_of(r_head + q0);
+        dma16(r_rsrc, r_of(stage) + 64 * wave, lane < 48 && 4 * (lane % 16) < rows_left ? record_off : kOutOfRange);
+    };
+    ColumnReads<H> columns(col, half);
+    ChunkReads<H> chunks(col, half);
+    f32x16 dv[G::OBLOCKS], dk[G::OBLOCKS];
+#pragma unroll
+    for (int b = 0; b < G::OBLOCKS; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            dv[b][r] = 0.f;
+            dk[b][r] = 0.f;
+        }
+
+    // This wave's block of a stage: queries sub0 .. + 31 (rows 32 qh ..)
+    // against its 32 keys, as the register kernel's block_grad.
+    auto block_grad = [&](auto stage, auto masked, int64_t sub0) __attribute__((always_inline)) {
+        constexpr bool MASKED = decltype(masked)::value;
+        const f32x4* qs = q_of(stage);
+        const f32x4* ds = d_of(stage);
+        int record = 64 * wave + half;
+        launder(record);
+        const f32x4* rs = r_of(stage) + record;
+        int kv_row = 32 * group * G::SLOTS;
+        launder(kv_row);
+        chunks.launder_all();
+        columns.launder_all();
+        const f32x16 s = chunks.product_lds(qs, qh, kv_lds[0] + kv_row);
+        __builtin_amdgcn_sched_barrier(0);
+        const f32x16 dp = chunks.product_lds(ds, qh, kv_lds[1] + kv_row);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            __builtin_amdgcn_sched_barrier(0);
+            const int slot = 8 * qh + 2 * g;
+            const f32x4 m4 = rs[slot], il4 = rs[16 + slot], d4 = rs[32 + slot];
+            float p[4], gr[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float shifted = s[4 * g + j] * a.scale - m4[j];
+                float pr = exp_of(shifted) * il4[j];
+                if (MASKED) {
+                    const int64_t query = sub0 + 8 * g + 4 * half + j;
+                    pr = key_ok && query < a.queries && key <= query + a.query_offset ? pr : 0.f;
+                }
+                p[j] = pr;
+                const float difference = dp[4 * g + j] - d4[j];
+                gr[j] = pr * difference;
+            }
+#pragma unroll
+            for (int b = 0; b < G::OBLOCKS; ++b)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    dv[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(columns.read(ds, qh, g, j, b), p[j], dv[b], 0, 0, 0);
+                    dk[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(columns.read(qs, qh, g, j, b), gr[j], dk[b], 0, 0, 0);
+                }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    using Masked = std::true_type;
+    using Whole = std::false_type;
+    auto compute = [&](auto stage, int64_t q0) __attribute__((always_inline)) {
+        const int64_t sub0 = q0 + 32 * qh;
+        // Wave-uniform: skipped when none of the block's queries sees the wave's first key.
+        if (sub0 < a.queries && sub0 + 31 + a.query_offset >= k_wave && k_wave < a.keys) {
+            if (sub0 + a.query_offset >= k_wave + 31 && sub0 + 32 <= a.queries && k_wave + 32 <= a.keys)
+                block_grad(stage, Whole{}, sub0);
+            else
+                block_grad(stage, Masked{}, sub0);
+        }
+    };
+    // K and V go first, so the first wait (all but one stage's loads)
+    // covers them too.
+    constexpr int kStageLoads = 2 * LOADS + 1;
+    issue(I0{}, q_begin);
+    issue(I1{}, q_begin + kKeys);
+    for (int st = 0; st < stages_total; st += 2) {
+        const int64_t q0 = q_begin + int64_t(st) * kKeys;
+        wait_loads<kStageLoads>();
+        lds_barrier();
+        compute(I0{}, q0);
+        lds_barrier();
+        issue(I0{}, q0 + 2 * kKeys);
+        wait_loads<kStageLoads>();
+        lds_barrier();
+        if (st + 1 < stages_total) compute(I1{}, q0 + kKeys);
+        lds_barrier();
+        issue(I1{}, q0 + 3 * kKeys);
+    }
+    wait_loads<0>();
+    lds_barrier();  // every wave is done with the stages (and K, V)
+
+    // Half 1 hands its partial sums to half 0 through the stages' space
+    // (lane-consecutive, conflict-free); half 0 adds them and writes.
+    float* handoff = reinterpret_cast<float*>(stages[0]) + group * (2 * G::OBLOCKS * 16 * 64) + lane;
+    if (qh == 1) {
+#pragma unroll
+        for (int b = 0; b < G::OBLOCKS; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                handoff[((2 * b) * 16 + r) * 64] = dv[b][r];
+                handoff[((2 * b + 1) * 16 + r) * 64] = dk[b][r];
+            }
+    }
+    lds_barrier();
+    if (qh == 0 && key_ok) {
+        float* vrow = a.v_grad + (head * a.keys + key) * H;
+        float* krow = a.k_grad + (head * a.keys + key) * H;
+#pragma unroll
+        for (int b = 0; b < G::OBLOCKS; ++b)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                f32x4 vo, ko;
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const int r = 4 * g + s;
+                    vo[s] = dv[b][r] + handoff[((2 * b) * 16 + r) * 64];
+                    const float sum = dk[b][r] + handoff[((2 * b + 1) * 16 + r) * 64];
+                    ko[s] = a.scale * sum;
+                }
+                *reinterpret_cast<f32x4*>(vrow + 32 * b + 4 * half + 8 * g) = vo;
+                *reinterpret_cast<f32x4*>(krow + 32 * b + 4 * half + 8 * g) = ko;
+            }
+    }
+}
+
 struct QueryGradArgs {
     const float* q;
     const float* k;
@@ -617,8 +862,12 @@ hipError_t launch_backward(const AttentionBackwardArgs& a, hipStream_t stream) {
     KeyGradArgs ka{a.q, a.k, a.v, a.d_out, rows, a.k_grad, a.v_grad, a.queries, a.keys, a.q_stride,
                    a.kv_stride, a.query_offset, a.heads, a.scale};
     const int64_t key_blocks = (a.keys + kKeyBlock - 1) / kKeyBlock;
-    hipLaunchKernelGGL(attention_key_grad_kernel<H>, dim3(unsigned(a.heads * key_blocks)), dim3(64 * kWaves), 0,
-                       stream, ka);
+    if constexpr (H <= 64)
+        hipLaunchKernelGGL(attention_key_grad_lds_kernel<H>, dim3(unsigned(a.heads * key_blocks)),
+                           dim3(64 * kLdsKeyWaves), 0, stream, ka);
+    else
+        hipLaunchKernelGGL(attention_key_grad_kernel<H>, dim3(unsigned(a.heads * key_blocks)), dim3(64 * kWaves), 0,
+                           stream, ka);
     err = hipGetLastError();
     if (err != hipSuccess) return err;
 
