@@ -1,24 +1,29 @@
-// bf16-input GEMM that rounds the fp32 operands as it loads them: the role of
-// the reference's TF32 tensor-core kernel (crates/staleynet-cuda/src/kernels/
-// matmul.rs:357-448) for large aligned products, with no staging pass.
+// bf16-input GEMM that rounds fp32 operands as it loads them: the role of the
+// reference's TF32 tensor-core kernel (crates/staleynet-cuda/src/kernels/
+// matmul.rs:357-448) for large aligned products.
 //
 // The operands stay fp32 in HBM, so per FLOP this kernel reads twice the bytes
 // a kernel on bf16 copies would; it makes up for it with the largest tile the
 // registers allow and a deep prefetch, instead of paying a separate pass that
-// reads every operand, writes a bf16 copy and reads that copy back.
+// reads every operand, writes a bf16 copy and reads that copy back. When one
+// operand is much smaller than the other (the weight, in the Linear forward
+// and input-gradient products), that one alone is rounded into the workspace
+// first (launch_stage_bf16: cheap, and then read at 2 bytes an element by
+// every tile row), and only the other is rounded as it loads.
 //  * 256 x 256 output tile, eight waves (two per SIMD) of 64 x 128;
 //  * 32 k per step (the fp32 loaders' geometry, gemm_common.h), two steps of
-//    global loads in flight in two register sets (128 KB per CU), so the
-//    loads of a step have two steps' MFMAs to arrive;
+//    global loads in flight in two register sets (128 KB per CU with both
+//    operands fp32, 96 KB with one staged), so the loads of a step have two
+//    steps' MFMAs to arrive;
 //  * each step rounds the next step's registers to bf16 (nearest-even,
 //    v_cvt_pk_bf16_f32) into the other of two bf16 LDS stages, between its
 //    two 16-deep MFMA chunks, and issues the loads of the step after next;
 //  * one barrier per step, waiting on LDS only (the loads in flight are
 //    waited for by count, never drained).
-// The LDS stage layout, loaders and epilogue are those of the register-staged
-// bf16 kernel (gemm_bf16.hip), with the LDS writes addressed from one base per
-// lane; v_mfma_f32_32x32x16_bf16 takes eight consecutive k per lane, one
-// ds_read_b128 per 32-row fragment.
+// The LDS stage layout, fp32 loaders and epilogue are those of the
+// register-staged bf16 kernel (gemm_bf16.hip), with the LDS writes addressed
+// from one base per lane; v_mfma_f32_32x32x16_bf16 takes eight consecutive k
+// per lane, one ds_read_b128 per 32-row fragment.
 #include "gemm_common.h"
 
 namespace sn {
@@ -28,6 +33,7 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 using WideTile = Tile<256, 256, 32, 4, 2>;
+
 
 template <int PENDING>
 __device__ __forceinline__ void wait_vector_loads() {
@@ -95,17 +101,71 @@ template <bool K_CONTIGUOUS, int ROWS, int BK, int THREADS>
 using WideLoaderFor = typename std::conditional<K_CONTIGUOUS, WideKLoader<ROWS, BK, THREADS>,
                                                 WideRowLoader<ROWS, BK, THREADS>>::type;
 
+// An operand already rounded to bf16 and laid out K-contiguous in the
+// workspace (launch_stage_bf16: [rows][kp], kp = K rounded up to 8, zeros
+// past K): vector v of a thread is one 16-byte octet (8 consecutive k) of
+// row tid / 4 + v x THREADS / 4, so four lanes read a row's 32 k (64
+// contiguous bytes) and each writes its octet's LDS slot as it came. `ld` is
+// kp, in bf16 elements; `base` points at the operand (batch offsets in
+// floats, kp being even).
+template <int ROWS, int BK, int THREADS>
+struct StagedLoader {
+    static constexpr int OCTETS = BK / 8;
+    static constexpr int PER_THREAD = ROWS * OCTETS / THREADS;
+    // A b128 write phase is 8 lanes (128 bytes over 32 banks): two rows x
+    // four octets. A plane of 258 slots puts the octets 8 banks apart and the
+    // rows 4: conflict-free. (Planes 4 slots longer put octets 0 and 2 on the
+    // same banks; the counters showed it.)
+    static constexpr int BF16_PAD = 2;
+    static_assert(ROWS * OCTETS % THREADS == 0 && THREADS % OCTETS == 0, "whole slots per thread");
+    f32x4 reg[PER_THREAD];  // 8 bf16 each, as loaded
+    int32_t offset[PER_THREAD];
+
+    __device__ __forceinline__ void init(int64_t ld, int64_t row0, int64_t rows, int tid) {
+#pragma unroll
+        for (int v = 0; v < PER_THREAD; ++v) {
+            const int r = tid / OCTETS + v * (THREADS / OCTETS);
+            offset[v] = row0 + r < rows ? int32_t((r * ld + 8 * (tid % OCTETS)) * 2) : kOutOfRange;
+        }
+    }
+
+    __device__ __forceinline__ void load(const float* __restrict__ base, int64_t ld, int64_t row0, int64_t,
+                                         int64_t k0, int64_t k_end, int tid) {
+        const uint16_t* tile = reinterpret_cast<const uint16_t*>(base) + row0 * ld + k0;
+        const __amdgpu_buffer_rsrc_t rsrc = buffer_of(reinterpret_cast<const float*>(tile));
+        const bool k_valid = k0 + 8 * (tid % OCTETS) < k_end;
+#pragma unroll
+        for (int v = 0; v < PER_THREAD; ++v) reg[v] = buffer_load4(rsrc, k_valid ? offset[v] : kOutOfRange);
+    }
+
+    __device__ __forceinline__ void store_bf16(uint16_t* lds, int tid) const {
+        using O = OctetPlanes<ROWS, BK, BF16_PAD>;
+        int base = ((tid % OCTETS) * O::PLANE + tid / OCTETS) * 16;
+        launder(base);
+        char* p = reinterpret_cast<char*>(lds) + base;
+#pragma unroll
+        for (int v = 0; v < PER_THREAD; ++v) *reinterpret_cast<f32x4*>(p + v * (THREADS / OCTETS) * 16) = reg[v];
+    }
+};
+
+// Which operand the workspace holds as bf16: none, the left or the right.
+enum StagedSide { kStageNone = 0, kStageLeft = 1, kStageRight = 2 };
+
+template <bool K_CONTIGUOUS, bool STAGED, int ROWS, int BK, int THREADS>
+using OperandLoader = typename std::conditional<STAGED, StagedLoader<ROWS, BK, THREADS>,
+                                                WideLoaderFor<K_CONTIGUOUS, ROWS, BK, THREADS>>::type;
+
 // Vector-memory instructions one loader issues per step.
 template <class L>
 constexpr int loads_per_step() {
     return sizeof(L::reg) / sizeof(f32x4);
 }
 
-template <bool A_K, bool B_K>
+template <bool A_K, bool B_K, int SIDE>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_bf16_wide_kernel(Args args) {
     using T = WideTile;
-    using LA = WideLoaderFor<A_K, T::BM, T::BK, T::THREADS>;
-    using LB = WideLoaderFor<B_K, T::BN, T::BK, T::THREADS>;
+    using LA = OperandLoader<A_K, SIDE == kStageLeft, T::BM, T::BK, T::THREADS>;
+    using LB = OperandLoader<B_K, SIDE == kStageRight, T::BN, T::BK, T::THREADS>;
     using OA = OctetPlanes<T::BM, T::BK, LA::BF16_PAD>;
     using OB = OctetPlanes<T::BN, T::BK, LB::BF16_PAD>;
     constexpr int kSetLoads = loads_per_step<LA>() + loads_per_step<LB>();
@@ -130,13 +190,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const float* a = args.a + batch * args.stride_a;
     const float* b = args.b + batch * args.stride_b;
 
-    // Two register sets per operand: set s holds the steps of parity s.
-    LA la[2];
-    LB lb[2];
+    // NSETS register sets per operand: set j holds the steps s with s % NSETS
+    // == j, loaded NSETS - 1 steps ahead of their hand-off to LDS. (A third
+    // set, which fits when one operand is staged, measured no faster.)
+    constexpr int NSETS = 2;
+    LA la[NSETS];
+    LB lb[NSETS];
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-        la[s].init(args.lda, m0, args.m, tid);
-        lb[s].init(args.ldb, n0, args.n, tid);
+    for (int j = 0; j < NSETS; ++j) {
+        la[j].init(args.lda, m0, args.m, tid);
+        lb[j].init(args.ldb, n0, args.n, tid);
     }
 
     f32x16 acc[T::FM][T::FN];
@@ -156,11 +219,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         la[S].load(a, args.lda, m0, args.m, k0, k_end, tid);
         lb[S].load(b, args.ldb, n0, args.n, k0, k_end, tid);
     };
-    // Rounds register set S into LDS stage S.
-    auto stage = [&](auto set) __attribute__((always_inline)) {
+    // Rounds register set S into LDS stage L.
+    auto stage = [&](auto set, auto lds) __attribute__((always_inline)) {
         constexpr int S = decltype(set)::value;
-        la[S].store_bf16(lds_a[S], tid);
-        lb[S].store_bf16(lds_b[S], tid);
+        constexpr int L = decltype(lds)::value;
+        la[S].store_bf16(lds_a[L], tid);
+        lb[S].store_bf16(lds_b[L], tid);
     };
     // Fragments of one 16-deep chunk of LDS stage S, and its MFMAs.
     auto read_chunk = [&](auto set, int c, bf16x8 (&fa)[T::FM], bf16x8 (&fb)[T::FN]) __attribute__((always_inline)) {
@@ -181,44 +245,46 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
     };
     // One step from LDS stage S: the first chunk's fragments and MFMAs, the
-    // next stage's hand-off (`between`: the other register set's loads
-    // waited for by count, rounded into the other stage, then reloaded),
-    // and the second chunk.
+    // next stage's hand-off (`between`: the next step's register set waited
+    // for by count, rounded into the other stage, then reloaded), and the
+    // second chunk.
     auto step_from = [&](auto set, auto between) __attribute__((always_inline)) {
         bf16x8 fa0[T::FM], fb0[T::FN], fa1[T::FM], fb1[T::FN];
         read_chunk(set, 0, fa0, fb0);
         multiply_chunk(fa0, fb0);
-        wait_vector_loads<kSetLoads>();
         between();
         read_chunk(set, 1, fa1, fb1);
         multiply_chunk(fa1, fb1);
     };
 
     using I0 = std::integral_constant<int, 0>;
-    using I1 = std::integral_constant<int, 1>;
     const int steps = k_end > k_begin ? int((k_end - k_begin + T::BK - 1) / T::BK) : 0;
+    // Step s (s % 2 == J) computes from LDS stage J while the set holding
+    // step s + 1 is waited for (the later set stays in flight), rounded into
+    // the other stage and reloaded with step s + 1 + NSETS.
+    auto do_step = [&](auto j, int s) __attribute__((always_inline)) {
+        constexpr int J = decltype(j)::value;
+        using Stage = std::integral_constant<int, J % 2>;
+        using NextSet = std::integral_constant<int, (J + 1) % NSETS>;
+        using NextStage = std::integral_constant<int, (J + 1) % 2>;
+        step_from(Stage{}, [&]() __attribute__((always_inline)) {
+            wait_vector_loads<(NSETS - 1) * kSetLoads>();
+            stage(NextSet{}, NextStage{});
+            issue(NextSet{}, s + 1 + NSETS);
+        });
+        stage_barrier();
+    };
     if (steps > 0) {
         issue(I0{}, 0);
-        issue(I1{}, 1);
-        wait_vector_loads<kSetLoads>();  // set 0 (step 0) is in
-        stage(I0{});
-        issue(I0{}, 2);
+        issue(std::integral_constant<int, 1>{}, 1);
+        wait_vector_loads<(NSETS - 1) * kSetLoads>();  // set 0 (step 0) is in
+        stage(I0{}, I0{});
+        issue(I0{}, NSETS);
         stage_barrier();
-        // Step s computes from stage s % 2 while set (s + 1) % 2, holding
-        // step s + 1, is rounded into the other stage and reloaded with step
-        // s + 3; set s % 2 (step s + 2) stays in flight.
         for (int s = 0; s < steps; s += 2) {
-            step_from(I0{}, [&]() __attribute__((always_inline)) {
-                stage(I1{});
-                issue(I1{}, s + 3);
-            });
-            stage_barrier();
+            do_step(std::integral_constant<int, 0>{}, s);
             if (s + 1 >= steps) break;
-            step_from(I1{}, [&]() __attribute__((always_inline)) {
-                stage(I0{});
-                issue(I0{}, s + 4);
-            });
-            stage_barrier();
+            do_step(std::integral_constant<int, 1>{}, s + 1);
         }
         wait_vector_loads<0>();
     }
@@ -238,7 +304,75 @@ Plan wide_plan(const Problem& p, const Env& env) {
     return plan_for<WideTile>(p, env, cost);
 }
 
-template <bool A_K, bool B_K>
+// The operand the workspace holds as bf16, and the product as the kernel
+// sees it (that operand K-contiguous bf16 in the workspace, ld = kp; the
+// partial sums after it).
+struct WideStaging {
+    int side = kStageNone;
+    int64_t kp = 0;
+    int64_t copies = 0;  // 1 when the operand is shared by the whole batch
+    size_t bytes = 0;
+    Problem q;
+    Env rest;
+};
+
+size_t round256(size_t bytes) { return (bytes + 255) / 256 * 256; }
+
+
+
+// Stages the operand with fewer elements (the weight, for the Linear
+// products) when it has at most half the other's elements and fits beside
+// the partial sums: rounding it once costs 6 bytes an element, while every
+// tile row (or column) that reads it then fetches 2 bytes an element
+// instead of 4. Measured on c2's set (596 TFLOP/s against 558 with nothing
+// staged): a quarter as the bound 595, any smaller operand 592 (the square
+// weight gradients then pay the staging for no gain).
+constexpr int kStageRatio = 2;
+WideStaging wide_staging(const Problem& p, const Env& env) {
+    WideStaging st;
+    st.q = p;
+    st.rest = env;
+    const int64_t a_copies = p.stride_a == 0 ? 1 : p.batch;
+    const int64_t b_copies = p.stride_b == 0 ? 1 : p.batch;
+    const double a_elems = double(p.m) * double(a_copies), b_elems = double(p.n) * double(b_copies);
+    int side = kStageNone;
+    if (b_elems * kStageRatio <= a_elems) side = kStageRight;
+    else if (a_elems * kStageRatio <= b_elems) side = kStageLeft;
+    if (side == kStageNone || env.workspace == nullptr || p.batch > 65535) return st;
+    const int64_t rows = side == kStageLeft ? p.m : p.n;
+    const int64_t copies = side == kStageLeft ? a_copies : b_copies;
+    const int64_t kp = (p.k + 7) / 8 * 8;
+    const size_t bytes = round256(size_t(copies) * size_t(rows) * size_t(kp) * 2);
+    if (bytes >= env.workspace_bytes) return st;
+    Problem q = p;
+    const float* staged = env.workspace;
+    if (side == kStageLeft) {
+        q.a = staged;
+        q.lda = kp;
+        q.stride_a = copies > 1 ? rows * kp / 2 : 0;
+        q.a_k_contiguous = true;
+    } else {
+        q.b = staged;
+        q.ldb = kp;
+        q.stride_b = copies > 1 ? rows * kp / 2 : 0;
+        q.b_k_contiguous = true;
+    }
+    Env rest = env;
+    rest.workspace = reinterpret_cast<float*>(reinterpret_cast<char*>(env.workspace) + bytes);
+    rest.workspace_bytes = env.workspace_bytes - bytes;
+    const Plan plan = wide_plan(q, rest);
+    if (plan.splits > 1 && size_t(plan.splits) * size_t(p.m) * size_t(p.n) * sizeof(float) > rest.workspace_bytes)
+        return st;
+    st.side = side;
+    st.kp = kp;
+    st.copies = copies;
+    st.bytes = bytes;
+    st.q = q;
+    st.rest = rest;
+    return st;
+}
+
+template <bool A_K, bool B_K, int SIDE>
 hipError_t launch_wide(const Problem& p, const Env& env, const Plan& plan, hipStream_t stream) {
     const LaunchShape shape = tiled_shape<WideTile>(p, plan, SN_PATH_BF16_WIDE);
     if (shape.batches_per_launch < 1) return hipErrorInvalidConfiguration;
@@ -248,7 +382,7 @@ hipError_t launch_wide(const Problem& p, const Env& env, const Plan& plan, hipSt
     for (int64_t first = 0; first < p.batch; first += chunk) {
         const int64_t count = std::min<int64_t>(chunk, p.batch - first);
         args.batch_base = first;
-        hipLaunchKernelGGL((gemm_bf16_wide_kernel<A_K, B_K>), dim3(unsigned(count * per_batch)),
+        hipLaunchKernelGGL((gemm_bf16_wide_kernel<A_K, B_K, SIDE>), dim3(unsigned(count * per_batch)),
                            dim3(WideTile::THREADS), 0, stream, args);
         hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
@@ -260,31 +394,48 @@ hipError_t launch_wide(const Problem& p, const Env& env, const Plan& plan, hipSt
 }  // namespace
 
 // Unmasked products with 128-bit-loadable operands (buffers_ok) whose output
-// fills at least a quarter of a 256 x 256 tile each way, in every layout but
-// NN (a K-contiguous left operand times a row-contiguous right one: the
-// forward Linear). Measured on c2's products, this kernel takes the weight
-// gradients (TN) from 310-549 to 397-574 TFLOP/s and the input gradients
-// (NT) from 464-616 to 512-775 against staging both operands as bf16
-// (gemm_dma.hip), while the staged path stays 1-5 % ahead on NN, whose
-// right operand (the weight) is small to stage and whose row-contiguous
-// loads cost this kernel more LDS writes per step.
+// fills at least a quarter of a 256 x 256 tile each way, and room for the
+// partial sums. Measured on c2's products against staging both operands as
+// bf16 for the 128 x 256 kernel (gemm_dma.hip): weight gradients (TN)
+// 310-549 -> 394-755 TFLOP/s, input gradients (NT) 464-616 -> 517-826,
+// forward (NN) 430-601 -> 496-693.
 bool bf16_wide_applies(const Problem& p, const Env& env) {
-    if (p.a_k_contiguous && !p.b_k_contiguous) return false;
     if (p.mask != SN_MASK_NONE || p.m < 128 || p.n < 128 || !buffers_ok<WideTile>(p)) return false;
+    const WideStaging st = wide_staging(p, env);
+    if (st.side != kStageNone) return true;
     const Plan plan = wide_plan(p, env);
     return plan.splits <= 1 || size_t(plan.splits) * size_t(p.m) * size_t(p.n) * sizeof(float) <= env.workspace_bytes;
 }
 
 LaunchShape describe_bf16_wide(const Problem& p, const Env& env) {
-    return tiled_shape<WideTile>(p, wide_plan(p, env), SN_PATH_BF16_WIDE);
+    const WideStaging st = wide_staging(p, env);
+    LaunchShape shape = tiled_shape<WideTile>(st.q, wide_plan(st.q, st.rest), SN_PATH_BF16_WIDE);
+    shape.workspace_bytes += st.bytes;
+    return shape;
 }
 
 hipError_t launch_gemm_bf16_wide(const Problem& p, const Env& env, hipStream_t stream) {
-    const Plan plan = wide_plan(p, env);
-    if (p.a_k_contiguous && p.b_k_contiguous) return launch_wide<true, true>(p, env, plan, stream);
-    if (p.a_k_contiguous) return launch_wide<true, false>(p, env, plan, stream);
-    if (p.b_k_contiguous) return launch_wide<false, true>(p, env, plan, stream);
-    return launch_wide<false, false>(p, env, plan, stream);
+    const WideStaging st = wide_staging(p, env);
+    const Problem& q = st.q;
+    const Plan plan = wide_plan(q, st.rest);
+    if (st.side == kStageLeft) {
+        hipError_t err = launch_stage_bf16(p.a, p.a_k_contiguous, p.lda, p.m, p.k, st.kp, st.copies, p.stride_a,
+                                           reinterpret_cast<uint16_t*>(env.workspace), stream);
+        if (err != hipSuccess) return err;
+        if (q.b_k_contiguous) return launch_wide<true, true, kStageLeft>(q, st.rest, plan, stream);
+        return launch_wide<true, false, kStageLeft>(q, st.rest, plan, stream);
+    }
+    if (st.side == kStageRight) {
+        hipError_t err = launch_stage_bf16(p.b, p.b_k_contiguous, p.ldb, p.n, p.k, st.kp, st.copies, p.stride_b,
+                                           reinterpret_cast<uint16_t*>(env.workspace), stream);
+        if (err != hipSuccess) return err;
+        if (q.a_k_contiguous) return launch_wide<true, true, kStageRight>(q, st.rest, plan, stream);
+        return launch_wide<false, true, kStageRight>(q, st.rest, plan, stream);
+    }
+    if (p.a_k_contiguous && p.b_k_contiguous) return launch_wide<true, true, kStageNone>(p, env, plan, stream);
+    if (p.a_k_contiguous) return launch_wide<true, false, kStageNone>(p, env, plan, stream);
+    if (p.b_k_contiguous) return launch_wide<false, true, kStageNone>(p, env, plan, stream);
+    return launch_wide<false, false, kStageNone>(p, env, plan, stream);
 }
 
 }  // namespace gemm

@@ -6,9 +6,11 @@ against the oracle's restatement of reference::matmul (reference.rs:10-38).
 Integers of magnitude <= 16 are exact in bf16, their products are exact and every partial sum here
 stays below 2^24, so those cases must match bit for bit in any summation order: ragged tiles on both
 output axes, a K tail that is not a whole 32-deep step, split K, batches with a shared operand,
-accumulate with a scale. Rounding to nearest even is pinned by hand-derived cases, and random inputs
-are held to the bf16 tolerance (2e-2, device.rs:51-66). Each case first checks that the launch plan
-really takes this kernel."""
+accumulate with a scale; and the products where the smaller operand is first rounded into the
+workspace (K-contiguous bf16, from either stored layout) while the other is rounded as it loads.
+Rounding to nearest even is pinned by hand-derived cases, and random inputs are held to the bf16
+tolerance (2e-2, device.rs:51-66). Each case first checks that the launch plan really takes this
+kernel."""
 import numpy as np
 import pytest
 
@@ -79,6 +81,26 @@ def test_wide_is_exact_on_integers(gpu, variant, rows, cols, inner):
     assert np.array_equal(expected(spec, left, right, initial), run_bf16(gpu, spec, left, right, initial))
 
 
+@pytest.mark.parametrize("variant,rows,cols,inner", [
+    ("NN", 1024, 256, 100),   # right operand (row-contiguous) staged through the transposing kernel
+    ("NT", 600, 260, 96),     # right operand (K-contiguous) staged row by row
+    ("TN", 256, 640, 300),    # left operand (row-contiguous) staged, right rounded as loaded
+    ("TT", 260, 600, 64),     # left staged, right K-contiguous
+    ("NN", 2100, 300, 1000),  # ragged edges, K = 31 steps + 8, split K
+])
+def test_wide_with_one_operand_staged_is_exact_on_integers(gpu, variant, rows, cols, inner):
+    print(f"wide staged {variant} {rows}x{cols}x{inner}", flush=True)
+    rng = np.random.default_rng(rows + 5 * cols + inner)
+    left = rng.integers(-16, 17, size=rows * inner).astype(np.float32)
+    right = rng.integers(-16, 17, size=inner * cols).astype(np.float32)
+    initial = rng.integers(-8, 9, size=rows * cols).astype(np.float32)
+    spec = layout(MatmulSpec.new(rows, cols, inner), variant).scaled(0.5).accumulate()
+    plan = wide_plan(spec)
+    partials = plan.splits * rows * cols * 4 if plan.splits > 1 else 0
+    assert plan.workspace_bytes > partials  # the staged operand sits in the workspace
+    assert np.array_equal(expected(spec, left, right, initial), run_bf16(gpu, spec, left, right, initial))
+
+
 def test_wide_split_k_is_exact_on_integers(gpu):
     # A weight-gradient shape whose 9 output tiles take K in slices, reduced in slice order.
     rows, cols, inner = 768, 640, 4096
@@ -92,6 +114,7 @@ def test_wide_split_k_is_exact_on_integers(gpu):
     assert np.array_equal(expected(spec, left, right, initial), run_bf16(gpu, spec, left, right, initial))
 
 
+# "left" and "right": the shared operand is the smaller one and is staged once for the batch.
 @pytest.mark.parametrize("shared", ["none", "left", "right"])
 def test_wide_batches_and_shared_operands(gpu, shared):
     batches, rows, cols, inner = 3, 256, 300, 64

@@ -107,13 +107,17 @@ def test_every_tile_and_slice_is_launched_once(label, spec, kernel):
 
 def test_configs_take_the_expected_kernel_families():
     assert gemm.plan(MatmulSpec.new(32768, 2304, 768)).path == gemm.PATH_F32_DIRECT
-    assert gemm.plan(MatmulSpec.new(32768, 2304, 768).with_precision(Precision.Bf16)).path == gemm.PATH_BF16_STAGED
-    # bf16 weight and input gradients round their fp32 operands as they load them, 256 x 256 tiles.
+    # Large bf16 products round their fp32 operands as they load them, 256 x 256 tiles; the forward
+    # and input-gradient products first round the (smaller) weight into the workspace.
+    forward = gemm.plan(MatmulSpec.new(32768, 2304, 768).with_precision(Precision.Bf16))
+    assert forward.path == gemm.PATH_BF16_WIDE and (forward.tile_rows, forward.tile_cols) == (256, 256)
+    assert forward.splits == 1 and forward.workspace_bytes == 2304 * 768 * 2  # the staged weight
     wgrad = gemm.plan(MatmulSpec.new(768, 2304, 32768).left_transposed().with_precision(Precision.Bf16))
-    assert wgrad.path == gemm.PATH_BF16_WIDE and (wgrad.tile_rows, wgrad.tile_cols) == (256, 256)
-    assert wgrad.splits > 1
+    assert wgrad.path == gemm.PATH_BF16_WIDE and wgrad.splits > 1
     dgrad = gemm.plan(MatmulSpec.new(32768, 768, 2304).right_transposed().with_precision(Precision.Bf16))
-    assert dgrad.path == gemm.PATH_BF16_WIDE
+    assert dgrad.path == gemm.PATH_BF16_WIDE and dgrad.workspace_bytes == 768 * 2304 * 2
+    # Too small for the wide tiles: operands staged as bf16 for the 128-wide kernels.
+    assert gemm.plan(MatmulSpec.new(96, 2304, 768).with_precision(Precision.Bf16)).path == gemm.PATH_BF16_STAGED
     # Too narrow for a quarter tile: the staged kernels keep it.
     assert gemm.plan(MatmulSpec.new(32768, 64, 768).right_transposed().with_precision(Precision.Bf16)).path != \
         gemm.PATH_BF16_WIDE
