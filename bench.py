@@ -1,6 +1,6 @@
 """Benchmark of the GEMM hot path on one MI355X.
 
-Headline workload (BASELINE.json metric, config 2): the 111.5M model's
+Headline workload (the driver's metric, config 2): the 111.5M model's
 training GEMM set, exactly as the reference's model issues it through
 ``Gpu::matmul``:
 - 12 blocks x {QKV 768->2304, out-proj 768->768, FFN up 768->3072, FFN down 3072->768};
@@ -769,7 +769,7 @@ def measure_published(gpu: Gpu, events: HipEvents, set_per_shape: dict):
     return result
 
 
-# ---- Linear's bias kernels (SURVEY next row: the steps either side of NN and TN) ---------
+# ---- Linear's bias kernels (the steps either side of the NN and TN products) -----------
 
 def measure_linear(gpu: Gpu, events: HipEvents, buffers, repeats: int = 5):
     """Config 2's Linear layers (block 0's four and the head): the forward as the reference

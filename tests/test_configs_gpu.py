@@ -1,4 +1,4 @@
-"""GPU parity at the BASELINE configurations' shapes, through the C ABI.
+"""GPU parity at the benchmark configurations' shapes (configs 0-4), through the C ABI.
 
 Inputs are seeded synthetic data generated in device memory (the same bytes
 are downloaded for the oracle): activations and gradients ~N(0,1), weights
