@@ -342,6 +342,9 @@ WideStaging wide_staging(const Problem& p, const Env& env) {
     const int64_t rows = side == kStageLeft ? p.m : p.n;
     const int64_t copies = side == kStageLeft ? a_copies : b_copies;
     const int64_t kp = (p.k + 7) / 8 * 8;
+    // The staged loader's per-lane byte offsets span a tile's rows (32-bit).
+    if ((int64_t(WideTile::BM > WideTile::BN ? WideTile::BM : WideTile::BN) * kp + 64) * 2 >= kMaxBufferOffset)
+        return st;
     const size_t bytes = round256(size_t(copies) * size_t(rows) * size_t(kp) * 2);
     if (bytes >= env.workspace_bytes) return st;
     Problem q = p;

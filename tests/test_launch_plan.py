@@ -116,6 +116,14 @@ def test_configs_take_the_expected_kernel_families():
     assert wgrad.path == gemm.PATH_BF16_WIDE and wgrad.splits > 1
     dgrad = gemm.plan(MatmulSpec.new(32768, 768, 2304).right_transposed().with_precision(Precision.Bf16))
     assert dgrad.path == gemm.PATH_BF16_WIDE and dgrad.workspace_bytes == 768 * 2304 * 2
+    # A staged operand keeps 32-bit offsets across a tile's rows: with K in the millions the weight
+    # gradient rounds both operands as they load instead (its workspace holds only partial sums).
+    huge = gemm.plan(MatmulSpec.new(256, 640, 5_000_000).left_transposed().with_precision(Precision.Bf16),
+                     workspace_bytes=1 << 40)
+    assert huge.path == gemm.PATH_BF16_WIDE and huge.workspace_bytes == huge.splits * 256 * 640 * 4
+    long_k = gemm.plan(MatmulSpec.new(256, 640, 500_000).left_transposed().with_precision(Precision.Bf16),
+                       workspace_bytes=1 << 40)
+    assert long_k.workspace_bytes == long_k.splits * 256 * 640 * 4 + 256 * 500_000 * 2  # x^T staged
     # Too small for the wide tiles: operands staged as bf16 for the 128-wide kernels.
     assert gemm.plan(MatmulSpec.new(96, 2304, 768).with_precision(Precision.Bf16)).path == gemm.PATH_BF16_STAGED
     # Too narrow for a quarter tile: the staged kernels keep it.
