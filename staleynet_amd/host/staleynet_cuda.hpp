@@ -21,6 +21,9 @@
 //                     the three calls of crates/staleynet-model/src/layers/attention.rs:206-213)
 //   Gpu::causal_attention_score_grad (the dP product and softmax_backward in one launch; no
 //                     reference counterpart: crates/staleynet-model/src/layers/attention.rs:238-248)
+//   Gpu::causal_attention_with_stats, Gpu::causal_attention_backward (the forward keeping per-query
+//                     statistics instead of the probabilities, and the backward that recomputes
+//                     them; no reference counterpart: layers/attention.rs:206-213 and :238-260)
 // The reference panics on undersized operands; here that is a thrown
 // staleynet_cuda::Panic carrying the same message. Driver errors (the
 // reference's Err(DriverError)) are thrown as staleynet_cuda::GpuError.
@@ -423,6 +426,26 @@ class Gpu {
                                              out.data(), out.len(), probabilities.data(), probabilities.len(),
                                              grad.data(), grad.len(), k ? k->data() : nullptr, k ? k->len() : 0,
                                              q_grad ? q_grad->data() : nullptr, q_grad ? q_grad->len() : 0));
+    }
+
+    // The fused forward keeping, per query, the maximum m of its scaled visible scores and the sum
+    // l of e^(x - m) (2 floats, in `stats`) instead of the probabilities
+    // (sn_causal_attention_with_stats); `out` is causal_attention's O.
+    void causal_attention_with_stats(const Tensor& q, const Tensor& k, const Tensor& v, Tensor& out, Tensor& stats,
+                                     const sn_attention_shape& shape) const {
+        check(sn_causal_attention_with_stats(context_, &shape, q.data(), q.len(), k.data(), k.len(), v.data(), v.len(),
+                                             out.data(), out.len(), stats.data(), stats.len()));
+    }
+
+    // The attention backward from O, dO and those statistics (sn_causal_attention_backward): the
+    // query, key and value gradients CausalSelfAttention::backward leaves, with no P or dS in memory.
+    void causal_attention_backward(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& out,
+                                   const Tensor& d_out, const Tensor& stats, Tensor& q_grad, Tensor& k_grad,
+                                   Tensor& v_grad, const sn_attention_shape& shape) const {
+        check(sn_causal_attention_backward(context_, &shape, q.data(), q.len(), k.data(), k.len(), v.data(), v.len(),
+                                           out.data(), out.len(), d_out.data(), d_out.len(), stats.data(), stats.len(),
+                                           q_grad.data(), q_grad.len(), k_grad.data(), k_grad.len(), v_grad.data(),
+                                           v_grad.len()));
     }
 
     sn_context* raw() const { return context_; }

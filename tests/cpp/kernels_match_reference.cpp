@@ -284,6 +284,27 @@ int main() {
         Tensor ds = gpu.zeros(Shape::new_(heads * t, t));
         gpu.causal_attention_score_grad(dot, vt, oref, pref, ds, shape);
         expect(relative_error(dp, gpu.download(ds)) < tolerance(MatmulKernel::Blocked), "causal_attention_score_grad");
+
+        // Training without the probabilities: the forward with statistics gives causal_attention's O
+        // bit for bit, and the backward from it gives the dQ, dK and dV products of attention.rs:250-260
+        // (dp now holds dS) and :244-247 on the oracle's calls.
+        std::vector<float> dq(heads * t * h, 0.f), dk(heads * t * h, 0.f), dv(heads * t * h, 0.f);
+        reference_matmul(MatmulSpec::new_(t, h, t).scaled(0.125f).batched(BatchStrides{heads, t * t, t * h, t * h}),
+                         dp, k, dq);
+        reference_matmul(
+            MatmulSpec::new_(t, h, t).left_transposed().scaled(0.125f).batched(BatchStrides{heads, t * t, t * h, t * h}),
+            dp, q, dk);
+        reference_matmul(MatmulSpec::new_(t, h, t).left_transposed().batched(BatchStrides{heads, t * t, t * h, t * h}),
+                         scores, d_out, dv);
+        Tensor o_stats = gpu.zeros(Shape::new_(heads * t, h)), stats = gpu.zeros(Shape::vector(2 * heads * t));
+        gpu.causal_attention_with_stats(qt, kt, vt, o_stats, stats, shape);
+        expect(gpu.download(o_stats) == gpu.download(ot), "causal_attention_with_stats output");
+        Tensor dqt = gpu.zeros(Shape::new_(heads * t, h)), dkt = gpu.zeros(Shape::new_(heads * t, h)),
+               dvt = gpu.zeros(Shape::new_(heads * t, h));
+        gpu.causal_attention_backward(qt, kt, vt, o_stats, dot, stats, dqt, dkt, dvt, shape);
+        expect(relative_error(dq, gpu.download(dqt)) < tolerance(MatmulKernel::Blocked), "causal_attention_backward dQ");
+        expect(relative_error(dk, gpu.download(dkt)) < tolerance(MatmulKernel::Blocked), "causal_attention_backward dK");
+        expect(relative_error(dv, gpu.download(dvt)) < tolerance(MatmulKernel::Blocked), "causal_attention_backward dV");
     }
 
     std::printf("%d of %d cases passed\n", cases - failures + (panicked ? 1 : 0), cases + 1);
