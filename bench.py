@@ -24,7 +24,9 @@ The printed JSON line is the driver's contract plus:
   from a HIP graph over a weight pool larger than the 256 MB Infinity Cache, and one
   decode token's 49 products in sequence;
 - ``linear_bias``: config 2's Linear forward as the reference calls it (matmul, then
-  add_row_bias) against the fused sn_matmul_bias, and the bias-gradient column sums;
+  add_row_bias) against the fused sn_matmul_bias, the bias-gradient column sums, and the weight
+  and bias gradients as two calls (matmul, then accumulate_column_sums) against the one
+  sn_matmul_column_sums call;
 - ``head_cross_entropy``: the head's 16 per-codebook cross-entropy calls at config 2;
 - ``published``: the reference's own published products (the only GEMM numbers it publishes, on
   Jetsons) with its timing method, fp32 and bf16; configs 0 and 1 as whole training sets; config 2's
@@ -775,7 +777,9 @@ def measure_linear(gpu: Gpu, events: HipEvents, buffers, repeats: int = 5):
     """Config 2's Linear layers (block 0's four and the head): the forward as the reference
     calls it (matmul, then add_row_bias; linear.rs:46-47) against the fused sn_matmul_bias, and
     the bias gradient (accumulate_column_sums, linear.rs:59), with the bias kernels' HBM rates
-    (add_row_bias: 8 bytes per output element; column sums: 4 bytes per input element)."""
+    (add_row_bias: 8 bytes per output element; column sums: 4 bytes per input element); and the
+    weight and bias gradients as the reference calls them (matmul, then accumulate_column_sums;
+    linear.rs:54-59) against sn_matmul_column_sums, the sums taken inside the product."""
     layers = [b for b, (label, _, _) in zip(buffers, training_set()) if label.startswith("b0.") or label == "head"]
     names = ["qkv", "out", "up", "down", "head"]
     result = {}
@@ -795,12 +799,21 @@ def measure_linear(gpu: Gpu, events: HipEvents, buffers, repeats: int = 5):
         fused = timed(events, gpu.stream, lambda: gpu.matmul_bias(spec, buf.x, buf.w, bias, buf.y), repeats)
         bias_ms = timed(events, gpu.stream, lambda: gpu.add_row_bias(buf.y, bias), repeats)
         sums_ms = timed(events, gpu.stream, lambda: gpu.accumulate_column_sums(buf.dy, sums), repeats)
+        grad = MatmulSpec.new(k, n, m).left_transposed().accumulate()
+        gpu.matmul_column_sums(grad, buf.x, buf.dy, buf.dw, sums)
+        grads_separate = timed(events, gpu.stream, lambda: (gpu.matmul(grad, buf.x, buf.dy, buf.dw),
+                                                             gpu.accumulate_column_sums(buf.dy, sums)), repeats)
+        grads_fused = timed(events, gpu.stream, lambda: gpu.matmul_column_sums(grad, buf.x, buf.dy, buf.dw, sums),
+                            repeats)
         result[f"{name} {m}x{n}x{k}"] = {
             "forward_separate_ms": round(separate, 4), "forward_fused_ms": round(fused, 4),
             "fused_saving_pct": round(100 * (1 - fused / separate), 1),
             "add_row_bias_gbs": round(8 * m * n / (bias_ms * 1e-3) / 1e9, 1),
             "column_sums_ms": round(sums_ms, 4),
-            "column_sums_gbs": round(4 * m * n / (sums_ms * 1e-3) / 1e9, 1)}
+            "column_sums_gbs": round(4 * m * n / (sums_ms * 1e-3) / 1e9, 1),
+            "weight_bias_grads_separate_ms": round(grads_separate, 4),
+            "weight_bias_grads_fused_ms": round(grads_fused, 4),
+            "grads_fused_saving_pct": round(100 * (1 - grads_fused / grads_separate), 1)}
         bias.free()
         sums.free()
     return result

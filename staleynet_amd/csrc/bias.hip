@@ -203,8 +203,13 @@ hipError_t launch_column_sums(const float* in, int64_t rows, int64_t cols, float
                            rows_per_slice, env.workspace);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
+    return launch_column_sums_finish(env.workspace, slices, cols, sums, stream);
+}
+
+hipError_t launch_column_sums_finish(const float* partial, int64_t slices, int64_t cols, float* sums,
+                                     hipStream_t stream) {
     hipLaunchKernelGGL(column_sums_finish_kernel, dim3(unsigned((cols + kThreads - 1) / kThreads)), dim3(kThreads), 0,
-                       stream, env.workspace, slices, cols, sums);
+                       stream, partial, slices, cols, sums);
     return hipGetLastError();
 }
 

@@ -370,6 +370,53 @@ int check_matmul_call(const sn_matmul_spec* spec, const float* left, size_t left
 
 namespace {
 
+// sn_plan_matmul and sn_plan_matmul_column_sums: the launch the call would
+// make, from host code only.
+int plan_of(const sn_matmul_spec* spec, uint32_t kernel, const float* left, const float* right, const float* output,
+            uint32_t cu_count, size_t workspace_bytes, bool column_sums, sn_launch_plan* plan) {
+    if (plan == nullptr) return SN_ERR_NULL_ARGUMENT;
+    std::memset(plan, 0, sizeof(*plan));
+    Lengths need;
+    const int rc = check_spec(spec, &need);
+    if (rc != SN_OK) return rc;
+    if (kernel > SN_KERNEL_SIMPLE) return SN_ERR_UNSUPPORTED;
+    if (column_sums && (spec->right_storage != SN_ROW_MAJOR || spec->batch_count != 1)) return SN_ERR_UNSUPPORTED;
+    sn::Problem p = sn::problem_of(spec, left, right, const_cast<float*>(output), nullptr);
+    // A context's environment as sn_context_create would set it up; the
+    // workspace and counters are never touched, only their sizes and the
+    // workspace's alignment matter (a device allocation is 2 MiB aligned).
+    sn::Env env;
+    env.cu_count = cu_count > 0 ? int(cu_count) : 256;
+    env.workspace_bytes = workspace_bytes;
+    env.workspace = workspace_bytes > 0 ? reinterpret_cast<float*>(uintptr_t(1) << 44) : nullptr;
+    env.counters = reinterpret_cast<uint32_t*>(uintptr_t(1) << 45);
+    env.counter_count = kCounterCount;
+    const uint32_t k = sn::kernel_for(kernel, spec->precision);
+    sn::LaunchShape s;
+    if (column_sums) {
+        // Only the sums' address matters to the plan, and only its being
+        // non-null: any aligned stand-in will do.
+        p.column_sums = reinterpret_cast<float*>(uintptr_t(1) << 46);
+        s = sn::describe_matmul_column_sums(p, k, env);
+        if (sn::f32_column_sums_fused(p, k, env)) s.path = SN_PATH_F32_DIRECT_SUMS;
+    } else {
+        s = sn::describe_matmul(p, k, env);
+    }
+    plan->path = s.path;
+    plan->threads = s.threads;
+    plan->tile_rows = uint32_t(s.tile_m);
+    plan->tile_cols = uint32_t(s.tile_n);
+    plan->tiles_m = uint32_t(s.tiles_m);
+    plan->tiles_n = uint32_t(s.tiles_n);
+    plan->splits = uint32_t(s.splits);
+    plan->k_per_split = uint64_t(s.k_per_split);
+    plan->batches_per_launch = uint64_t(s.batches_per_launch);
+    plan->workgroups = uint64_t(s.workgroups);
+    plan->launches = uint64_t(s.launches);
+    plan->workspace_bytes = uint64_t(s.workspace_bytes);
+    return s.workspace_bytes > workspace_bytes ? SN_ERR_WORKSPACE : SN_OK;
+}
+
 // sn_matmul and sn_matmul_bias: validation, then the product with `bias`
 // (null: none) added in its epilogue, or, for a masked spec, after it by the
 // bias kernel.
@@ -416,36 +463,12 @@ int sn_matmul_bias(sn_context* ctx, const sn_matmul_spec* spec, const float* lef
 
 int sn_plan_matmul(const sn_matmul_spec* spec, uint32_t kernel, const float* left, const float* right,
                    const float* output, uint32_t cu_count, size_t workspace_bytes, sn_launch_plan* plan) {
-    if (plan == nullptr) return SN_ERR_NULL_ARGUMENT;
-    std::memset(plan, 0, sizeof(*plan));
-    Lengths need;
-    const int rc = check_spec(spec, &need);
-    if (rc != SN_OK) return rc;
-    if (kernel > SN_KERNEL_SIMPLE) return SN_ERR_UNSUPPORTED;
-    const sn::Problem p = sn::problem_of(spec, left, right, const_cast<float*>(output), nullptr);
-    // A context's environment as sn_context_create would set it up; the
-    // workspace and counters are never touched, only their sizes and the
-    // workspace's alignment matter (a device allocation is 2 MiB aligned).
-    sn::Env env;
-    env.cu_count = cu_count > 0 ? int(cu_count) : 256;
-    env.workspace_bytes = workspace_bytes;
-    env.workspace = workspace_bytes > 0 ? reinterpret_cast<float*>(uintptr_t(1) << 44) : nullptr;
-    env.counters = reinterpret_cast<uint32_t*>(uintptr_t(1) << 45);
-    env.counter_count = kCounterCount;
-    const sn::LaunchShape s = sn::describe_matmul(p, sn::kernel_for(kernel, spec->precision), env);
-    plan->path = s.path;
-    plan->threads = s.threads;
-    plan->tile_rows = uint32_t(s.tile_m);
-    plan->tile_cols = uint32_t(s.tile_n);
-    plan->tiles_m = uint32_t(s.tiles_m);
-    plan->tiles_n = uint32_t(s.tiles_n);
-    plan->splits = uint32_t(s.splits);
-    plan->k_per_split = uint64_t(s.k_per_split);
-    plan->batches_per_launch = uint64_t(s.batches_per_launch);
-    plan->workgroups = uint64_t(s.workgroups);
-    plan->launches = uint64_t(s.launches);
-    plan->workspace_bytes = uint64_t(s.workspace_bytes);
-    return s.workspace_bytes > workspace_bytes ? SN_ERR_WORKSPACE : SN_OK;
+    return plan_of(spec, kernel, left, right, output, cu_count, workspace_bytes, false, plan);
+}
+
+int sn_plan_matmul_column_sums(const sn_matmul_spec* spec, uint32_t kernel, const float* left, const float* right,
+                               const float* output, uint32_t cu_count, size_t workspace_bytes, sn_launch_plan* plan) {
+    return plan_of(spec, kernel, left, right, output, cu_count, workspace_bytes, true, plan);
 }
 
 int sn_add_row_bias(sn_context* ctx, float* output, size_t rows, size_t cols, const float* bias, size_t bias_len) {
@@ -794,6 +817,32 @@ int sn_causal_attention_score_grad(sn_context* ctx, const sn_attention_shape* sh
     if (!sn::attention_score_grad_supported(args)) return SN_ERR_UNSUPPORTED;
     hipError_t err = hipSetDevice(ctx->device);
     if (err == hipSuccess) err = sn::launch_attention_score_grad(args, ctx->stream);
+    return status(err);
+}
+
+int sn_matmul_column_sums(sn_context* ctx, const sn_matmul_spec* spec, const float* left, size_t left_len,
+                          const float* right, size_t right_len, float* output, size_t output_len, float* sums,
+                          size_t sums_len) {
+    int rc = sn_matmul_validate(spec, left_len, right_len, output_len);
+    if (rc != SN_OK) return rc;
+    if (spec->right_storage != SN_ROW_MAJOR || spec->batch_count != 1) return SN_ERR_UNSUPPORTED;
+    if (sums_len != spec->cols) return SN_ERR_LENGTH_MISMATCH;
+    if (ctx == nullptr || (sums == nullptr && sums_len > 0)) return SN_ERR_NULL_ARGUMENT;
+    rc = sn::check_matmul_call(spec, left, left_len, right, right_len, nullptr, 0, output, output_len);
+    if (rc != SN_OK) return rc;
+    if (spec->cols == 0) return SN_OK;
+    const size_t right_used = spec->inner * spec->cols;
+    if (overlaps(sums, sums_len, output, spec->rows * spec->cols) || overlaps(sums, sums_len, right, right_used) ||
+        overlaps(sums, sums_len, left, spec->rows * spec->inner))
+        return SN_ERR_ALIASING;
+
+    sn::Problem p = sn::problem_of(spec, left, right, output, nullptr);
+    p.column_sums = sums;
+    const uint32_t kernel = sn::kernel_for(ctx->kernel, spec->precision);
+    if (sn::describe_matmul_column_sums(p, kernel, ctx->env).workspace_bytes > ctx->env.workspace_bytes)
+        return SN_ERR_WORKSPACE;
+    hipError_t err = hipSetDevice(ctx->device);
+    if (err == hipSuccess) err = sn::launch_matmul_column_sums(p, kernel, ctx->env, ctx->stream);
     return status(err);
 }
 

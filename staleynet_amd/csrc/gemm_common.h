@@ -102,6 +102,7 @@ struct Args {
     int32_t mask;
     float scale;
     const float* bias;  // null, or one value per column added after the combine
+    float* column_sums; // null, or the right operand's column sums over K, accumulated (see Problem)
 };
 
 template <int BM_, int BN_, int BK_, int WAVES_M_, int WAVES_N_>
@@ -703,6 +704,7 @@ Args make_args(const Problem& p, const Env& env, const Plan& plan) {
     args.mask = int(p.mask);
     args.scale = p.scale;
     args.bias = p.bias;
+    args.column_sums = p.column_sums;
     return args;
 }
 
@@ -722,6 +724,13 @@ hipError_t launch_gemm_bf16_dma(const Problem& p, const Env& env, hipStream_t st
 bool bf16_wide_applies(const Problem& p, const Env& env);
 LaunchShape describe_bf16_wide(const Problem& p, const Env& env);
 hipError_t launch_gemm_bf16_wide(const Problem& p, const Env& env, hipStream_t stream);
+// The fp32 direct-to-LDS product that also adds the right operand's column
+// sums into p.column_sums (gemm_dma.hip): whether it serves `p` (batch 1,
+// unmasked, no bias, right operand row-contiguous, aligned), its launch shape
+// (workspace: the product's partial sums and N per K slice) and launcher.
+bool f32_column_sums_applies(const Problem& p);
+LaunchShape describe_f32_column_sums(const Problem& p, const Env& env);
+hipError_t launch_gemm_f32_column_sums(const Problem& p, const Env& env, hipStream_t stream);
 // bf16 with both operands first staged as bf16 in the workspace (gemm_dma.hip):
 // whether it serves `p` (unmasked, aligned, staged operands fit), its
 // launch shape (workspace: staged operands and partial sums) and launcher.

@@ -305,9 +305,10 @@ __device__ __forceinline__ void lds_barrier() {
 // wait count, fixed. The loop is unrolled by STAGES so that every LDS
 // access names a statically known stage array; the compiler then never
 // waits on loads into the other stages before its LDS reads.
-template <class T, int STAGES, bool A_K, bool B_K, int FEED>
+template <class T, int STAGES, bool A_K, bool B_K, int FEED, bool COLSUM = false>
 __device__ __forceinline__ void dma_tile(const Args& args) {
     static_assert(STAGES >= 2 && STAGES <= 4, "two to four LDS stages");
+    static_assert(!COLSUM || (!B_K && FEED == kFeedF32), "column sums of a row-contiguous fp32 right operand");
     constexpr int WAVES = T::THREADS / 64;
     constexpr int A_SLOTS = T::BM * T::BK / 4;
     constexpr int B_SLOTS = T::BN * T::BK / 4;
@@ -395,6 +396,15 @@ __device__ __forceinline__ void dma_tile(const Args& args) {
     // The second half starts the loads STAGES steps ahead into stage S and
     // reads the next stage's chunk 0 into f0 while chunk 1 is multiplied.
     // No LDS read is waited for with the matrix cores idle.
+    // Column sums of the right operand (COLSUM; the workgroups of the first
+    // tile row only): a stage holds B as [k][column], BN columns a k row;
+    // thread t sums column t % BN over k rows (t / BN) x KPART .. + KPART - 1
+    // of every stage, in k order, while the stage's MFMAs run.
+    constexpr int PARTS = T::THREADS / T::BN;
+    constexpr int KPART = T::BK / PARTS;
+    static_assert(!COLSUM || (T::THREADS % T::BN == 0 && T::BK % PARTS == 0), "whole column parts");
+    const bool colsum_tile = COLSUM && tm == 0;  // uniform over the workgroup
+    float colsum = 0.f;
     auto first_half = [&](auto stage) {
         constexpr int S = decltype(stage)::value;
         __builtin_amdgcn_sched_barrier(0);
@@ -402,6 +412,14 @@ __device__ __forceinline__ void dma_tile(const Args& args) {
         multiply_chunk<T, FEED>(f0, acc);
         interleave<T, FEED, 0, DS>();
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (COLSUM) {
+            if (colsum_tile) {
+                const float* column = reinterpret_cast<const float*>(stage_b[S]) + (tid / T::BN) * KPART * T::BN +
+                                      tid % T::BN;
+#pragma unroll
+                for (int kk = 0; kk < KPART; ++kk) colsum = colsum + column[kk * T::BN];
+            }
+        }
     };
     auto sync = [&] {
         wait_loads<LOADS_PER_STEP * (STAGES - 2)>();
@@ -504,6 +522,29 @@ __device__ __forceinline__ void dma_tile(const Args& args) {
     }
 
     const bool partial = args.splits > 1;
+    if constexpr (COLSUM) {
+        if (colsum_tile) {
+            // The column parts meet in LDS and are added in part order; the
+            // sum over this slice of K is added to the sums (one slice) or
+            // left for the reduce after the product's partial sums (several).
+            lds_barrier();  // every wave is done with the stages
+            float* parts = reinterpret_cast<float*>(stage_a[0]);
+            parts[tid] = colsum;  // part tid / BN, column tid % BN
+            lds_barrier();
+            if (tid < T::BN) {
+                float total = parts[tid];
+#pragma unroll
+                for (int q = 1; q < PARTS; ++q) total = total + parts[q * T::BN + tid];
+                const int64_t c = n0 + tid;
+                if (c < args.n) {
+                    if (partial)
+                        args.ws[int64_t(args.splits) * args.m * args.n + int64_t(split) * args.n + c] = total;
+                    else
+                        args.column_sums[c] = args.column_sums[c] + total;
+                }
+            }
+        }
+    }
     float* out = partial ? args.ws + ((batch_local * int64_t(args.splits) + split) * args.m) * args.n : c_batch;
     write_tile<T, true>(args, acc, out, m0, n0, wave_m, wave_n, lane, partial);
 }
@@ -524,6 +565,16 @@ __attribute__((amdgpu_waves_per_eu(dma_waves_per_eu<typename C::T, C::STAGES>(),
                                    dma_waves_per_eu<typename C::T, C::STAGES>())))
 void gemm_f32_dma_kernel(Args args) {
     dma_tile<typename C::T, C::STAGES, A_K, B_K, kFeedF32>(args);
+}
+
+// The fp32 product with the right operand's column sums over K (Linear's
+// weight and bias gradients in one pass).
+template <class C, bool A_K>
+__global__ __launch_bounds__(C::T::THREADS)
+__attribute__((amdgpu_waves_per_eu(dma_waves_per_eu<typename C::T, C::STAGES>(),
+                                   dma_waves_per_eu<typename C::T, C::STAGES>())))
+void gemm_f32_dma_colsum_kernel(Args args) {
+    dma_tile<typename C::T, C::STAGES, A_K, false, kFeedF32, true>(args);
 }
 
 // bf16-input / fp32-accumulate variant (SN_PRECISION_BF16): the same loads,
@@ -671,6 +722,61 @@ hipError_t launch_gemm_f32_dma(const Problem& p, const Env& env, hipStream_t str
 
 hipError_t launch_gemm_bf16_dma(const Problem& p, const Env& env, hipStream_t stream) {
     return with_bf16_dma_config(p, [&](auto c) { return launch_dma_layout<decltype(c), kFeedRound>(p, env, stream); });
+}
+
+// ---- The weight-gradient product with Linear's bias gradient -------------
+
+namespace {
+
+// Each K slice also leaves N partial column sums after the product's M x N
+// partials: the split count is chosen as if the workspace were M / (M + 1)
+// of its size, so that both fit.
+template <class C>
+Plan column_sums_plan(const Problem& p, const Env& env) {
+    Env e = env;
+    e.workspace_bytes = env.workspace_bytes / size_t(p.m + 1) * size_t(p.m);
+    return dma_plan<C, kFeedF32>(p, e);
+}
+
+template <class C, bool A_K>
+hipError_t launch_column_sums_tiles(const Problem& p, const Env& env, hipStream_t stream) {
+    using T = typename C::T;
+    const Plan plan = column_sums_plan<C>(p, env);
+    const Args args = make_args<T>(p, env, plan);
+    const int64_t workgroups = int64_t(plan.tiles_m) * plan.tiles_n * plan.splits;
+    hipLaunchKernelGGL((gemm_f32_dma_colsum_kernel<C, A_K>), dim3(unsigned(workgroups)), dim3(T::THREADS), 0, stream,
+                       args);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess || plan.splits == 1) return err;
+    err = launch_splitk_reduce(p, env, plan.splits, stream);
+    if (err != hipSuccess) return err;
+    return launch_column_sums_finish(env.workspace + int64_t(plan.splits) * p.m * p.n, plan.splits, p.n,
+                                     p.column_sums, stream);
+}
+
+}  // namespace
+
+bool f32_column_sums_applies(const Problem& p) {
+    return p.batch == 1 && p.m > 0 && p.k > 0 && p.mask == SN_MASK_NONE && !p.b_k_contiguous && p.bias == nullptr &&
+           dma_applies(p);
+}
+
+LaunchShape describe_f32_column_sums(const Problem& p, const Env& env) {
+    return with_f32_dma_config(p, [&](auto c) {
+        using C = decltype(c);
+        const Plan plan = column_sums_plan<C>(p, env);
+        LaunchShape s = tiled_shape<typename C::T>(p, plan, SN_PATH_F32_DIRECT);
+        if (plan.splits > 1) s.workspace_bytes += size_t(plan.splits) * size_t(p.n) * sizeof(float);
+        return s;
+    });
+}
+
+hipError_t launch_gemm_f32_column_sums(const Problem& p, const Env& env, hipStream_t stream) {
+    return with_f32_dma_config(p, [&](auto c) {
+        using C = decltype(c);
+        return p.a_k_contiguous ? launch_column_sums_tiles<C, true>(p, env, stream)
+                                : launch_column_sums_tiles<C, false>(p, env, stream);
+    });
 }
 
 // ---- bf16 operands staged in the workspace -------------------------------

@@ -31,6 +31,10 @@ struct Problem {
     // rounded separately. Only for unmasked products (the C entry point runs
     // a masked one as the product and then the bias kernel).
     const float* bias = nullptr;
+    // Linear's bias gradient, fused into the weight-gradient product: sums
+    // [c] += the sum over K of the right operand's column c (stored row-major
+    // [K][N]). Only for the fp32 direct-to-LDS kernel, batch 1, unmasked.
+    float* column_sums = nullptr;
 };
 
 // What a launch may use beyond its operands: the context's split-K scratch,
@@ -193,6 +197,19 @@ hipError_t launch_add_row_bias(float* out, int64_t rows, int64_t cols, int64_t b
 hipError_t launch_column_sums(const float* in, int64_t rows, int64_t cols, float* sums, const Env& env,
                               hipStream_t stream);
 size_t column_sums_workspace_bytes(int64_t rows, int64_t cols, const Env& env);
+// sums[c] += the sum of partial[s * cols + c] over s = 0 .. slices - 1,
+// eight accumulators taken in slice order, then added together in order.
+hipError_t launch_column_sums_finish(const float* partial, int64_t slices, int64_t cols, float* sums,
+                                     hipStream_t stream);
+
+// The weight-gradient product with the bias gradient (sn_matmul_column_sums):
+// p.column_sums[c] += the sum over K of the right operand's column c, beside
+// the product. Fused into the fp32 direct-to-LDS kernel where that serves `p`
+// (see f32_column_sums_fused), else the product and then launch_column_sums.
+// The workspace bytes are the larger of the two steps'.
+bool f32_column_sums_fused(const Problem& p, uint32_t kernel, const Env& env);
+LaunchShape describe_matmul_column_sums(const Problem& p, uint32_t kernel, const Env& env);
+hipError_t launch_matmul_column_sums(const Problem& p, uint32_t kernel, const Env& env, hipStream_t stream);
 
 // The row-wise kernels between the attention products (softmax.hip).
 hipError_t launch_causal_softmax(float* scores, int64_t rows, int64_t queries, int64_t keys, float scale,

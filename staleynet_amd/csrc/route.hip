@@ -48,6 +48,31 @@ hipError_t launch_matmul(const Problem& p, uint32_t kernel, const Env& env, hipS
     return kernel == SN_KERNEL_MFMA_BF16 ? launch_gemm_bf16(p, env, stream) : launch_gemm_f32(p, env, stream);
 }
 
+bool f32_column_sums_fused(const Problem& p, uint32_t kernel, const Env& env) {
+    return kernel == SN_KERNEL_MFMA_F32 && family_of(p, kernel, env) == Family::Tiled && gemm::f32_column_sums_applies(p);
+}
+
+LaunchShape describe_matmul_column_sums(const Problem& p, uint32_t kernel, const Env& env) {
+    if (p.n == 0) return LaunchShape{};
+    if (f32_column_sums_fused(p, kernel, env)) return gemm::describe_f32_column_sums(p, env);
+    Problem product = p;
+    product.column_sums = nullptr;
+    LaunchShape s = describe_matmul(product, kernel, env);
+    s.workspace_bytes = std::max(s.workspace_bytes, column_sums_workspace_bytes(p.k, p.n, env));
+    return s;
+}
+
+hipError_t launch_matmul_column_sums(const Problem& p, uint32_t kernel, const Env& env, hipStream_t stream) {
+    if (p.n == 0) return hipSuccess;
+    if (f32_column_sums_fused(p, kernel, env)) return gemm::launch_gemm_f32_column_sums(p, env, stream);
+    Problem product = p;
+    product.column_sums = nullptr;
+    hipError_t err = launch_matmul(product, kernel, env, stream);
+    if (err != hipSuccess) return err;
+    // The stored right operand is [K][N] (row-contiguous, one matrix).
+    return launch_column_sums(p.b, p.k, p.n, p.column_sums, env, stream);
+}
+
 }  // namespace sn
 
 extern "C" int sn_tile_map(uint32_t workgroups, uint32_t tiles_m, uint32_t tiles_n, uint32_t splits,

@@ -217,9 +217,9 @@ class CLaunchPlan(ctypes.Structure):
 # sn_launch_plan.path values (include/staleynet_gemm.h).
 PATH_NONE, PATH_REFERENCE_ORDER, PATH_FEW_ROWS, PATH_FEW_ROWS_NT = 0, 1, 2, 3
 PATH_F32_DIRECT, PATH_F32_REGISTER, PATH_BF16_STAGED, PATH_BF16_DIRECT, PATH_BF16_REGISTER = 4, 5, 6, 7, 8
-PATH_BF16_WIDE = 9
+PATH_BF16_WIDE, PATH_F32_DIRECT_SUMS = 9, 10
 TILED_PATHS = (PATH_F32_DIRECT, PATH_F32_REGISTER, PATH_BF16_STAGED, PATH_BF16_DIRECT, PATH_BF16_REGISTER,
-               PATH_BF16_WIDE)
+               PATH_BF16_WIDE, PATH_F32_DIRECT_SUMS)
 
 
 class CAttentionShape(ctypes.Structure):
@@ -342,6 +342,8 @@ def _library() -> ctypes.CDLL:
         lib.sn_accumulate_column_sums.argtypes = [ctx, ctypes.c_void_p, size, size, ctypes.c_void_p, size]
         lib.sn_matmul_bias.argtypes = [ctx, ctypes.POINTER(CMatmulSpec), ctypes.c_void_p, size, ctypes.c_void_p,
                                        size, ctypes.c_void_p, size, ctypes.c_void_p, size]
+        lib.sn_matmul_column_sums.argtypes = [ctx, ctypes.POINTER(CMatmulSpec), ctypes.c_void_p, size,
+                                              ctypes.c_void_p, size, ctypes.c_void_p, size, ctypes.c_void_p, size]
         lib.sn_causal_softmax.argtypes = [ctx, ctypes.c_void_p, size, size, size, ctypes.c_float, size]
         lib.sn_causal_attention.argtypes = [ctx, ctypes.POINTER(CAttentionShape), ctypes.c_void_p, size,
                                             ctypes.c_void_p, size, ctypes.c_void_p, size, ctypes.c_void_p, size,
@@ -379,7 +381,7 @@ def _library() -> ctypes.CDLL:
                      "sn_add_row_bias", "sn_accumulate_column_sums", "sn_matmul_bias", "sn_causal_softmax",
                      "sn_softmax_backward", "sn_cross_entropy", "sn_upload_tokens", "sn_download_tokens",
                      "sn_free_tokens", "sn_split_heads", "sn_merge_heads", "sn_causal_attention",
-                     "sn_causal_attention_score_grad", "sn_plan_matmul", "sn_tile_map", "sn_matmul_noalloc", "sn_causal_attention_with_stats",
+                     "sn_causal_attention_score_grad", "sn_plan_matmul", "sn_plan_matmul_column_sums", "sn_matmul_column_sums", "sn_tile_map", "sn_matmul_noalloc", "sn_causal_attention_with_stats",
                      "sn_causal_attention_backward"):
             getattr(lib, name).restype = ctypes.c_int
         _lib = lib
@@ -415,6 +417,20 @@ def plan(spec: MatmulSpec, kernel: int = 0, cu_count: int = 256, workspace_bytes
                                    ctypes.byref(out))
     if rc != SN_OK:
         raise GpuError(rc, "plan_matmul")
+    return out
+
+
+def plan_column_sums(spec: MatmulSpec, kernel: int = 0, cu_count: int = 256, workspace_bytes: int = 1536 << 20,
+                     left: int = ALIGNED_ADDRESS, right: int = 2 * ALIGNED_ADDRESS,
+                     output: int = 3 * ALIGNED_ADDRESS) -> CLaunchPlan:
+    """``sn_plan_matmul_column_sums``: the launch ``Gpu.matmul_column_sums`` would make (host only);
+    path ``PATH_F32_DIRECT_SUMS`` when the column sums ride in the product's kernel."""
+    c = spec.to_c()
+    out = CLaunchPlan()
+    rc = _library().sn_plan_matmul_column_sums(ctypes.byref(c), kernel, left, right, output, cu_count,
+                                               workspace_bytes, ctypes.byref(out))
+    if rc != SN_OK:
+        raise GpuError(rc, "plan_matmul_column_sums")
     return out
 
 
@@ -598,6 +614,20 @@ class Gpu:
         if rc in _VALIDATION_CODES:
             raise MatmulPanic(rc)
         self._check(rc, "matmul_bias")
+
+    def matmul_column_sums(self, spec: MatmulSpec, left: Tensor, right: Tensor, output: Tensor, sums: Tensor) -> None:
+        """``Linear::backward``'s weight-gradient ``matmul`` then ``accumulate_column_sums`` of the same
+        output gradient (linear.rs:54-59) in one call (``sn_matmul_column_sums``): the product as ``matmul``
+        computes it and ``sums[c] += Σ_k right[k, c]``, the sums taken while the right operand's tiles pass
+        through LDS where the fp32 direct-to-LDS kernel serves the product."""
+        c = spec.to_c()
+        rc = _library().sn_matmul_column_sums(self._ctx, ctypes.byref(c), ctypes.c_void_p(left.pointer), len(left),
+                                              ctypes.c_void_p(right.pointer), len(right),
+                                              ctypes.c_void_p(output.pointer), len(output),
+                                              ctypes.c_void_p(sums.pointer), len(sums))
+        if rc in _VALIDATION_CODES:
+            raise MatmulPanic(rc)
+        self._check(rc, "matmul_column_sums")
 
     def add_row_bias(self, output: Tensor, bias: Tensor) -> None:
         """``Gpu::add_row_bias`` (ops/elementwise.rs:30-41): ``output[r, c] += bias[c]``."""

@@ -11,6 +11,9 @@
 //   Gpu::add_row_bias, Gpu::accumulate_column_sums crates/staleynet-cuda/src/ops/elementwise.rs:30-58
 //   Gpu::matmul_bias (matmul + add_row_bias fused; no reference counterpart: the two calls of
 //                     Linear::forward, crates/staleynet-model/src/layers/linear.rs:46-47)
+//   Gpu::matmul_column_sums (matmul + accumulate_column_sums of the right operand fused; no
+//                     reference counterpart: the two calls of Linear::backward,
+//                     crates/staleynet-model/src/layers/linear.rs:54-59)
 //   Shape, Tensor                                  crates/staleynet-cuda/src/device.rs:210-275
 //   TokenBuffer, Gpu::upload_tokens                crates/staleynet-cuda/src/device.rs:35-36, :194-197
 //   Gpu::causal_softmax, Gpu::softmax_backward     crates/staleynet-cuda/src/ops/attention.rs:54-92
@@ -345,6 +348,16 @@ class Gpu {
         const sn_matmul_spec c = spec.to_ffi();
         check(sn_matmul_bias(context_, &c, left.data(), left.len(), right.data(), right.len(), bias.data(),
                              bias.len(), output.data(), output.len()));
+    }
+
+    // `matmul` then `accumulate_column_sums(right, sums)`, in one call (sn_matmul_column_sums; the
+    // right operand row-major, the spec unbatched).
+    void matmul_column_sums(const MatmulSpec& spec, const Tensor& left, const Tensor& right, Tensor& output,
+                            Tensor& sums) const {
+        check(sn_context_set_kernel(context_, abi_kernel(matmul_kernel)));
+        const sn_matmul_spec c = spec.to_ffi();
+        check(sn_matmul_column_sums(context_, &c, left.data(), left.len(), right.data(), right.len(), output.data(),
+                                    output.len(), sums.data(), sums.len()));
     }
 
     TokenBuffer upload_tokens(const std::vector<uint32_t>& tokens) const {

@@ -154,6 +154,32 @@ int main() {
             ++failures;
             std::printf("FAIL matmul_bias differs from matmul + add_row_bias\n");
         }
+        // Linear::backward's weight and bias gradients in one call: the product's bits are matmul's,
+        // and on integer inputs the column sums are exact in any order.
+        {
+            const size_t n = 260, k = 100, m = 132;
+            std::vector<float> xi(k * m), dyi(k * n);
+            for (size_t i = 0; i < xi.size(); ++i) xi[i] = float(int((i * 7919) % 33) - 16);
+            for (size_t i = 0; i < dyi.size(); ++i) dyi[i] = float(int((i * 104729) % 33) - 16);
+            const Tensor xg = gpu.upload(Shape::new_(k, m), xi), dyg = gpu.upload(Shape::new_(k, n), dyi);
+            const MatmulSpec grad = MatmulSpec::new_(m, n, k).left_transposed().accumulate();
+            Tensor dw_fused = gpu.zeros(Shape::new_(m, n)), dw_separate = gpu.zeros(Shape::new_(m, n));
+            Tensor db = gpu.upload(Shape::vector(n), std::vector<float>(n, 1.f));
+            gpu.matmul_column_sums(grad, xg, dyg, dw_fused, db);
+            gpu.matmul(grad, xg, dyg, dw_separate);
+            std::vector<float> db_expected(n, 1.f), db_scratch(n);
+            oracle_accumulate_column_sums(dyi.data(), k, n, db_expected.data(), db_scratch.data());
+            ++cases;
+            if (gpu.download(dw_fused) != gpu.download(dw_separate)) {
+                ++failures;
+                std::printf("FAIL matmul_column_sums product differs from matmul\n");
+            }
+            ++cases;
+            if (gpu.download(db) != db_expected) {
+                ++failures;
+                std::printf("FAIL matmul_column_sums sums differ from the row-order sums\n");
+            }
+        }
         bool length_panic = false;
         try {
             Tensor out = gpu.zeros(Shape::new_(rows, cols));

@@ -124,6 +124,24 @@ def test_bias_entry_points_check_lengths_before_touching_the_device():
     assert gemm.status_string(gemm.SN_ERR_LENGTH_MISMATCH) == "bias or sums length must equal the matrix's columns"
 
 
+def test_matmul_column_sums_checks_before_touching_the_device():
+    # The weight-gradient spec of linear.rs:54-56 with the bias gradient's length check of
+    # ops/elementwise.rs:46; only an unbatched product with a row-major right operand is served.
+    lib = gemm.library()
+    spec = MatmulSpec.new(4, 5, 3).left_transposed().accumulate()
+    c = spec.to_c()
+    assert lib.sn_matmul_column_sums(None, ctypes.byref(c), None, 11, None, 15, None, 20, None, 5) == \
+        gemm.SN_ERR_LEFT_TOO_SMALL
+    assert lib.sn_matmul_column_sums(None, ctypes.byref(c), None, 12, None, 15, None, 20, None, 4) == \
+        gemm.SN_ERR_LENGTH_MISMATCH
+    assert lib.sn_matmul_column_sums(None, ctypes.byref(c), None, 12, None, 15, None, 20, None, 5) == \
+        gemm.SN_ERR_NULL_ARGUMENT
+    for bad in (spec.right_transposed(), spec.batched(gemm.BatchStrides(2, 12, 15, 20))):
+        b = bad.to_c()
+        assert lib.sn_matmul_column_sums(None, ctypes.byref(b), None, 24, None, 30, None, 40, None, 5) == \
+            gemm.SN_ERR_UNSUPPORTED
+
+
 def test_row_wise_kernels_check_shapes_before_touching_the_device():
     # ops/attention.rs:59 (rows % queries) and :79 (equal shapes) are asserts in the reference.
     lib = gemm.library()

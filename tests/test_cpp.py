@@ -23,4 +23,4 @@ def test_reference_sweep_through_the_cpp_mirror():
     proc = subprocess.run([BINARY], capture_output=True, text=True, timeout=300)
     print(proc.stdout)
     assert proc.returncode == 0, proc.stdout + proc.stderr
-    assert "181 of 181 cases passed" in proc.stdout
+    assert "183 of 183 cases passed" in proc.stdout

@@ -105,6 +105,38 @@ def test_every_tile_and_slice_is_launched_once(label, spec, kernel):
         assert plan.path == gemm.PATH_FEW_ROWS_NT and spec.rows <= 4 and plan.splits == 1
 
 
+def test_weight_gradients_take_the_column_sums_into_the_product():
+    # Linear::backward's dW += x^T dY with db += column sums of dY (linear.rs:54-59), at the
+    # configurations' shapes: the fp32 product keeps its plan, and each K slice adds N floats of sums.
+    for inputs, outputs in ((768, 2304), (768, 768), (768, 3072), (3072, 768), (256, 768), (96, 48)):
+        spec = MatmulSpec.new(inputs, outputs, 32768).left_transposed().accumulate()
+        product = gemm.plan(spec)
+        fused = gemm.plan_column_sums(spec)
+        assert product.path == gemm.PATH_F32_DIRECT and fused.path == gemm.PATH_F32_DIRECT_SUMS
+        assert (fused.splits, fused.k_per_split, fused.tiles_m, fused.tiles_n) == \
+            (product.splits, product.k_per_split, product.tiles_m, product.tiles_n)
+        extra = fused.splits * outputs * 4 if fused.splits > 1 else 0
+        assert fused.workspace_bytes == product.workspace_bytes + extra
+        check_tiled_cover(fused)
+    # A workspace that holds the product's partial sums but not the sums beside them: fewer slices.
+    spec = MatmulSpec.new(768, 2304, 32768).left_transposed().accumulate()
+    product = gemm.plan(spec)
+    tight = gemm.plan_column_sums(spec, workspace_bytes=product.workspace_bytes)
+    assert tight.path == gemm.PATH_F32_DIRECT_SUMS and tight.splits < product.splits
+    assert tight.workspace_bytes <= product.workspace_bytes
+    # bf16, a right operand whose rows are not 16-byte multiples: the product, then the column sums,
+    # with the larger of the two workspaces.
+    bf16 = spec.with_precision(Precision.Bf16)
+    assert gemm.plan_column_sums(bf16).path == gemm.PATH_BF16_WIDE
+    assert gemm.plan_column_sums(bf16).workspace_bytes == gemm.plan(bf16).workspace_bytes
+    odd = MatmulSpec.new(96, 50, 300).left_transposed()
+    assert gemm.plan_column_sums(odd).path == gemm.PATH_F32_REGISTER
+    # The unsupported forms are rejected by the planner as by the call.
+    for bad in (spec.right_transposed(), spec.batched(gemm.BatchStrides(2, 0, 0, 768 * 2304))):
+        with pytest.raises(gemm.GpuError):
+            gemm.plan_column_sums(bad)
+
+
 def test_configs_take_the_expected_kernel_families():
     assert gemm.plan(MatmulSpec.new(32768, 2304, 768)).path == gemm.PATH_F32_DIRECT
     # Large bf16 products round their fp32 operands as they load them, 256 x 256 tiles; the forward
