@@ -38,6 +38,7 @@ import argparse
 import ctypes
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -898,6 +899,47 @@ def cpu_baseline(gpu: Gpu, calls, budget_s: float, workers: int = 1):
     return projected_s, sampled_flops, sampled_s, samples
 
 
+def parse_rocminfo_gpu(text: str):
+    """(compute units, max engine clock in MHz) of the first gfx9 GPU agent in `rocminfo` output,
+    or None when no such agent is listed."""
+    agent = None
+    for line in text.splitlines():
+        key, _, value = line.strip().partition(":")
+        key, value = key.strip(), value.strip()
+        if key == "Name":
+            if agent and agent.get("gpu") and "cus" in agent and "mhz" in agent:
+                break
+            agent = {"gpu": value.startswith("gfx9")}
+        elif agent is not None and agent["gpu"]:
+            if key == "Compute Unit" and value.isdigit():
+                agent["cus"] = int(value)
+            elif key == "Max Clock Freq. (MHz)" and value.isdigit():
+                agent["mhz"] = int(value)
+    if agent and agent.get("gpu") and "cus" in agent and "mhz" in agent:
+        return agent["cus"], agent["mhz"]
+    return None
+
+
+def device_peaks() -> dict:
+    """The peaks recomputed from the device's own compute-unit count and maximum engine clock
+    (rocminfo), beside the published figures the fractions use: fp32 matrix 256 FLOP per clock
+    per CU, bf16 dense 4096."""
+    try:
+        text = subprocess.run([os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "bin", "rocminfo")],
+                              stdout=subprocess.PIPE, stderr=subprocess.DEVNULL, text=True, timeout=60).stdout
+    except (OSError, subprocess.SubprocessError):
+        return {"source": "rocminfo unavailable"}
+    found = parse_rocminfo_gpu(text)
+    if found is None:
+        return {"source": "rocminfo lists no gfx9 GPU agent"}
+    cus, mhz = found
+    return {"source": "rocminfo", "compute_units": cus, "max_engine_clock_mhz": mhz,
+            "fp32_matrix_tflops_from_clock": round(cus * 256 * mhz * 1e6 / 1e12, 1),
+            "bf16_dense_tflops_from_clock": round(cus * 4096 * mhz * 1e6 / 1e12, 1),
+            "published_fp32_tflops": PEAK_FP32_TFLOPS, "published_bf16_tflops": PEAK_BF16_TFLOPS,
+            "published_hbm_gbs": PEAK_HBM_GBS}
+
+
 def _cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -1246,6 +1288,7 @@ def main() -> int:
                                " + 16x1024 codebook head x {NN, NT, TN}, M=32768",
                    "gemms_per_step": len(calls), "tflop_per_step": round(set_flops / 1e12, 4)},
         "frac_fp32_peak": round(value / PEAK_FP32_TFLOPS, 4),
+        "device_peaks": device_peaks(),
         "roofline": roofline,
         "per_layout": per_layout,
         "per_shape_tflops": per_shape,

@@ -153,3 +153,33 @@ def test_kernel_counter_summary_recovers_known_bytes_and_rates(tmp_path):
         assert float(r[5]) == pytest.approx(2.0, abs=2e-3)          # traffic / algorithmic
         assert float(r[7]) == pytest.approx(2000, rel=2e-3)         # algorithmic GB/s
         assert float(r[8]) == pytest.approx(4000, rel=2e-3)         # HBM GB/s
+
+
+ROCMINFO = """*******
+Agent 1
+*******
+  Name:                    AMD EPYC 9575F 64-Core Processor
+  Marketing Name:          AMD EPYC 9575F 64-Core Processor
+  Compute Unit:            128
+  Max Clock Freq. (MHz):   3300
+*******
+Agent 2
+*******
+  Name:                    gfx950
+  Marketing Name:          AMD Instinct MI355X
+  Max Clock Freq. (MHz):   2400
+  Compute Unit:            256
+*******
+Agent 3
+*******
+  Name:                    gfx950
+  Compute Unit:            256
+  Max Clock Freq. (MHz):   2100
+"""
+
+
+def test_device_peaks_come_from_the_first_gpu_agent():
+    # The CPU agent is skipped; the first gfx9 agent's CU count and clock give the peaks.
+    assert bench.parse_rocminfo_gpu(ROCMINFO) == (256, 2400)
+    assert bench.parse_rocminfo_gpu(ROCMINFO.split("Agent 2")[0]) is None
+    assert round(256 * 256 * 2400e6 / 1e12, 1) == bench.PEAK_FP32_TFLOPS
