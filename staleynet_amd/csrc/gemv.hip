@@ -119,7 +119,11 @@ __global__ __launch_bounds__(64 * waves_for<MT>()) void gemv_kernel(GemvArgs arg
     constexpr int kRowsPerLoad = 64 / LPR;
     constexpr int kColumns = 4 * LPR;
     constexpr int kPassRows = pass_rows<MT, LPR>();
-    __shared__ __attribute__((aligned(16))) float x_pass[2][kPassRows][MT];  // [row][m]
+    // x of a pass as [row][m], rows kXStride floats apart: an odd stride (for
+    // two or more rows of x) puts the consecutive rows that a wave's lanes
+    // write on distinct banks.
+    constexpr int kXStride = MT == 1 ? 1 : MT + 1;
+    __shared__ __attribute__((aligned(16))) float x_pass[2][kPassRows][kXStride];
     __shared__ f32x4 partial[kWaves][MT][LPR];
     __shared__ int arrived_last;
 
@@ -165,15 +169,19 @@ __global__ __launch_bounds__(64 * waves_for<MT>()) void gemv_kernel(GemvArgs arg
     // registers (issued before that pass's W loads, so that waiting for them
     // never waits for W) and later writes them to the pass's LDS buffer.
     // Branch-free buffer loads: values past the slice or past M read 0.
+    // Element e of the pass is row e % kPassRows of x's row e / kPassRows, so
+    // a wave's lanes read 64 consecutive k of one row of x (256 contiguous
+    // bytes; with the row index fastest a wave load touched up to 64 lines).
     constexpr int kXPerThread = kPassRows * MT / kThreads;
     static_assert(kPassRows * MT % kThreads == 0, "x of a pass is whole rounds of the workgroup");
+    static_assert(kPassRows % 64 == 0, "a wave's x lanes stay within one row of x");
     const __amdgpu_buffer_rsrc_t x_rsrc = gemm::buffer_of(x);
     auto load_x = [&](int64_t k0, float (&xs)[kXPerThread]) {
 #pragma unroll
         for (int i = 0; i < kXPerThread; ++i) {
             const int e = tid + i * kThreads;
-            const int r = e / MT;
-            const int m = e % MT;
+            const int r = e % kPassRows;
+            const int m = e / kPassRows;
             // Causal left: the stored left matrix is 0 past row m's horizon
             // (the tiled kernels zero it in LDS the same way).
             const bool ok = m < args.m && k0 + r < k_end && (!args.causal_left || k0 + r <= m + args.query_offset);
@@ -184,7 +192,7 @@ __global__ __launch_bounds__(64 * waves_for<MT>()) void gemv_kernel(GemvArgs arg
 #pragma unroll
         for (int i = 0; i < kXPerThread; ++i) {
             const int e = tid + i * kThreads;
-            x_pass[buf][e / MT][e % MT] = xs[i];
+            x_pass[buf][e % kPassRows][e / kPassRows] = xs[i];
         }
     };
 
@@ -221,7 +229,7 @@ __global__ __launch_bounds__(64 * waves_for<MT>()) void gemv_kernel(GemvArgs arg
             float xa[kLoads];
 #pragma unroll
             for (int u = 0; u < kLoads; ++u)
-                xa[u] = (lane & 15) < MT ? xr[u * kWaves * kRowsPerLoad * MT + (lane & 15)] : 0.f;
+                xa[u] = (lane & 15) < MT ? xr[u * kWaves * kRowsPerLoad * kXStride + (lane & 15)] : 0.f;
 #pragma unroll
             for (int u = 0; u < kLoads; ++u)
 #pragma unroll
@@ -235,7 +243,7 @@ __global__ __launch_bounds__(64 * waves_for<MT>()) void gemv_kernel(GemvArgs arg
             for (int u = 0; u < kLoads; ++u) {
                 if (u + 1 < kLoads) {
 #pragma unroll
-                    for (int m = 0; m < MT; ++m) xn[m] = xr[(u + 1) * kWaves * kRowsPerLoad * MT + m];
+                    for (int m = 0; m < MT; ++m) xn[m] = xr[(u + 1) * kWaves * kRowsPerLoad * kXStride + m];
                 }
 #pragma unroll
                 for (int m = 0; m < MT; ++m) acc[m] += xv[m] * cur[u];
