@@ -78,17 +78,19 @@ constexpr int kSplitTargetManyRows = 192;
 template <int MT>
 constexpr bool uses_mfma() { return MT >= 8; }
 
-// Loads in flight per lane: 16 for one or two rows of x and on the matrix
-// cores (whose accumulators are 16 registers per lane for any MT), 8 for
-// four rows, whose x values and accumulators need the registers (two waves
-// per SIMD throughout).
+// Loads in flight per lane: 16 for one or two rows of x, 8 for four rows,
+// whose x values and accumulators need the registers (two waves per SIMD
+// throughout). On the matrix cores (8 waves) shorter passes did better: 4
+// loads when a slab streams the whole of K (the head: 4.1 TB/s against 3.7
+// with 8), 2 when K is split into slices of a few hundred rows (the layer
+// weights, 3-7 % over 4; the head lost 12 % with 2).
 template <int MT>
-constexpr int loads_for() { return MT <= 2 ? 16 : 8; }
+constexpr int loads_for(bool split) { return MT <= 2 ? 16 : !uses_mfma<MT>() ? 8 : split ? 2 : 4; }
 template <int MT>
 constexpr int waves_for() { return uses_mfma<MT>() ? 8 : 4; }
 // Rows of W one pass covers: waves x loads x rows per wave load.
-template <int MT, int LPR>
-constexpr int pass_rows() { return waves_for<MT>() * loads_for<MT>() * (64 / LPR); }
+template <int MT, int LPR, int LOADS>
+constexpr int pass_rows() { return waves_for<MT>() * LOADS * (64 / LPR); }
 
 struct GemvArgs {
     const float* x;
@@ -110,15 +112,15 @@ struct GemvArgs {
 };
 
 // MT: rows of x the instantiation holds; LPR: lanes per row piece (the slab
-// is 4 * LPR columns wide).
-template <int MT, int LPR>
+// is 4 * LPR columns wide); LOADS: loads in flight per lane (loads_for).
+template <int MT, int LPR, int LOADS>
 __global__ __launch_bounds__(64 * waves_for<MT>()) void gemv_kernel(GemvArgs args) {
     constexpr int kWaves = waves_for<MT>();
     constexpr int kThreads = 64 * kWaves;
-    constexpr int kLoads = loads_for<MT>();
+    constexpr int kLoads = LOADS;
     constexpr int kRowsPerLoad = 64 / LPR;
     constexpr int kColumns = 4 * LPR;
-    constexpr int kPassRows = pass_rows<MT, LPR>();
+    constexpr int kPassRows = pass_rows<MT, LPR, LOADS>();
     // x of a pass as [row][m], rows kXStride floats apart: an odd stride (for
     // two or more rows of x) puts the consecutive rows that a wave's lanes
     // write on distinct banks.
@@ -373,9 +375,12 @@ struct GemvPlan {
 
 // Rows of a pass for the instantiation launch_width picks for m rows.
 template <int LPR>
-int64_t pass_rows_for(int64_t m) {
-    return m <= 2 ? pass_rows<2, LPR>() : m <= 4 ? pass_rows<4, LPR>() : m <= 8 ? pass_rows<8, LPR>()
-                                                                               : pass_rows<16, LPR>();
+int64_t pass_rows_for(int64_t m, bool split) {
+    if (m <= 2) return pass_rows<2, LPR, loads_for<2>(false)>();
+    if (m <= 4) return pass_rows<4, LPR, loads_for<4>(false)>();
+    if (m <= 8)
+        return split ? pass_rows<8, LPR, loads_for<8>(true)>() : pass_rows<8, LPR, loads_for<8>(false)>();
+    return split ? pass_rows<16, LPR, loads_for<16>(true)>() : pass_rows<16, LPR, loads_for<16>(false)>();
 }
 
 // Keys a product multiplies: all K, or with a causal left mask up to the last
@@ -390,7 +395,6 @@ GemvPlan gemv_plan(const Problem& p) {
     const int64_t k = keys_used(p);
     GemvPlan plan;
     plan.lanes_per_row = 16;
-    plan.pass_rows = pass_rows_for<16>(p.m);
     plan.column_blocks = int((p.n + 63) / 64);
     const int64_t slabs = int64_t(plan.column_blocks) * p.batch;
     int64_t rows_per_split = std::max<int64_t>(k, 1);
@@ -408,10 +412,11 @@ GemvPlan gemv_plan(const Problem& p) {
     }
     plan.k_per_split = rows_per_split;
     plan.splits = int((std::max<int64_t>(k, 1) + rows_per_split - 1) / rows_per_split);
+    plan.pass_rows = pass_rows_for<16>(p.m, plan.splits > 1);
     return plan;
 }
 
-template <int MT, int LPR>
+template <int MT, int LPR, int LOADS>
 hipError_t launch_rows(const Problem& p, const Env& env, const GemvPlan& plan, hipStream_t stream) {
     GemvArgs args;
     args.x = p.a;
@@ -434,18 +439,22 @@ hipError_t launch_rows(const Problem& p, const Env& env, const GemvPlan& plan, h
     args.accumulate = p.accumulate ? 1 : 0;
     args.scale = p.scale;
     args.bias = p.bias;
-    hipLaunchKernelGGL((gemv_kernel<MT, LPR>), dim3(plan.column_blocks, plan.splits, unsigned(p.batch)),
+    hipLaunchKernelGGL((gemv_kernel<MT, LPR, LOADS>), dim3(plan.column_blocks, plan.splits, unsigned(p.batch)),
                        dim3(64 * waves_for<MT>()), 0, stream, args);
     return hipGetLastError();
 }
 
 template <int LPR>
 hipError_t launch_width(const Problem& p, const Env& env, const GemvPlan& plan, hipStream_t stream) {
-    if (p.m == 1) return launch_rows<1, LPR>(p, env, plan, stream);
-    if (p.m <= 2) return launch_rows<2, LPR>(p, env, plan, stream);
-    if (p.m <= 4) return launch_rows<4, LPR>(p, env, plan, stream);
-    if (p.m <= 8) return launch_rows<8, LPR>(p, env, plan, stream);
-    return launch_rows<16, LPR>(p, env, plan, stream);
+    const bool split = plan.splits > 1;
+    if (p.m == 1) return launch_rows<1, LPR, loads_for<1>(false)>(p, env, plan, stream);
+    if (p.m <= 2) return launch_rows<2, LPR, loads_for<2>(false)>(p, env, plan, stream);
+    if (p.m <= 4) return launch_rows<4, LPR, loads_for<4>(false)>(p, env, plan, stream);
+    if (p.m <= 8)
+        return split ? launch_rows<8, LPR, loads_for<8>(true)>(p, env, plan, stream)
+                     : launch_rows<8, LPR, loads_for<8>(false)>(p, env, plan, stream);
+    return split ? launch_rows<16, LPR, loads_for<16>(true)>(p, env, plan, stream)
+                 : launch_rows<16, LPR, loads_for<16>(false)>(p, env, plan, stream);
 }
 
 // Few-row products against a K-contiguous right operand (right_transposed):
