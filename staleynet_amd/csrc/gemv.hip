@@ -78,14 +78,17 @@ constexpr int kSplitTargetManyRows = 192;
 template <int MT>
 constexpr bool uses_mfma() { return MT >= 8; }
 
-// Loads in flight per lane: 16 for one or two rows of x, 8 for four rows,
-// whose x values and accumulators need the registers (two waves per SIMD
-// throughout). On the matrix cores (8 waves) shorter passes did better: 4
-// loads when a slab streams the whole of K (the head: 4.1 TB/s against 3.7
-// with 8), 2 when K is split into slices of a few hundred rows (the layer
-// weights, 3-7 % over 4; the head lost 12 % with 2).
+// Loads in flight per lane (measured on the c4 weights): for one or two rows
+// of x, 16 when a slab streams the whole of K (the head) and 8 when K is split
+// into slices of a few hundred rows (the layer weights, 2-9 % over 16); 8 for
+// four rows, whose x values and accumulators need the registers (two waves
+// per SIMD throughout; 4 lost up to 8 %). On the matrix cores (8 waves)
+// shorter passes did better still: 4 loads for a whole K (the head: 4.1 TB/s
+// against 3.7 with 8), 2 for slices (3-7 % over 4; the head lost 12 % with 2).
 template <int MT>
-constexpr int loads_for(bool split) { return MT <= 2 ? 16 : !uses_mfma<MT>() ? 8 : split ? 2 : 4; }
+constexpr int loads_for(bool split) {
+    return MT <= 2 ? (split ? 8 : 16) : !uses_mfma<MT>() ? 8 : split ? 2 : 4;
+}
 template <int MT>
 constexpr int waves_for() { return uses_mfma<MT>() ? 8 : 4; }
 // Rows of W one pass covers: waves x loads x rows per wave load.
@@ -174,9 +177,11 @@ __global__ __launch_bounds__(64 * waves_for<MT>()) void gemv_kernel(GemvArgs arg
     // Element e of the pass is row e % kPassRows of x's row e / kPassRows, so
     // a wave's lanes read 64 consecutive k of one row of x (256 contiguous
     // bytes; with the row index fastest a wave load touched up to 64 lines).
-    constexpr int kXPerThread = kPassRows * MT / kThreads;
-    static_assert(kPassRows * MT % kThreads == 0, "x of a pass is whole rounds of the workgroup");
+    // A pass of fewer x values than threads leaves the last threads idle.
+    constexpr int kXElems = kPassRows * MT;
+    constexpr int kXPerThread = (kXElems + kThreads - 1) / kThreads;
     static_assert(kPassRows % 64 == 0, "a wave's x lanes stay within one row of x");
+    auto x_in_pass = [&](int e) { return kXElems % kThreads == 0 || e < kXElems; };
     const __amdgpu_buffer_rsrc_t x_rsrc = gemm::buffer_of(x);
     auto load_x = [&](int64_t k0, float (&xs)[kXPerThread]) {
 #pragma unroll
@@ -186,7 +191,8 @@ __global__ __launch_bounds__(64 * waves_for<MT>()) void gemv_kernel(GemvArgs arg
             const int m = e / kPassRows;
             // Causal left: the stored left matrix is 0 past row m's horizon
             // (the tiled kernels zero it in LDS the same way).
-            const bool ok = m < args.m && k0 + r < k_end && (!args.causal_left || k0 + r <= m + args.query_offset);
+            const bool ok = x_in_pass(e) && m < args.m && k0 + r < k_end &&
+                            (!args.causal_left || k0 + r <= m + args.query_offset);
             xs[i] = gemm::buffer_load1(x_rsrc, ok ? int32_t((m * args.k + k0 + r) * 4) : gemm::kOutOfRange);
         }
     };
@@ -194,7 +200,7 @@ __global__ __launch_bounds__(64 * waves_for<MT>()) void gemv_kernel(GemvArgs arg
 #pragma unroll
         for (int i = 0; i < kXPerThread; ++i) {
             const int e = tid + i * kThreads;
-            x_pass[buf][e % kPassRows][e / kPassRows] = xs[i];
+            if (x_in_pass(e)) x_pass[buf][e % kPassRows][e / kPassRows] = xs[i];
         }
     };
 
@@ -376,7 +382,7 @@ struct GemvPlan {
 // Rows of a pass for the instantiation launch_width picks for m rows.
 template <int LPR>
 int64_t pass_rows_for(int64_t m, bool split) {
-    if (m <= 2) return pass_rows<2, LPR, loads_for<2>(false)>();
+    if (m <= 2) return split ? pass_rows<2, LPR, loads_for<2>(true)>() : pass_rows<2, LPR, loads_for<2>(false)>();
     if (m <= 4) return pass_rows<4, LPR, loads_for<4>(false)>();
     if (m <= 8)
         return split ? pass_rows<8, LPR, loads_for<8>(true)>() : pass_rows<8, LPR, loads_for<8>(false)>();
@@ -447,8 +453,12 @@ hipError_t launch_rows(const Problem& p, const Env& env, const GemvPlan& plan, h
 template <int LPR>
 hipError_t launch_width(const Problem& p, const Env& env, const GemvPlan& plan, hipStream_t stream) {
     const bool split = plan.splits > 1;
-    if (p.m == 1) return launch_rows<1, LPR, loads_for<1>(false)>(p, env, plan, stream);
-    if (p.m <= 2) return launch_rows<2, LPR, loads_for<2>(false)>(p, env, plan, stream);
+    if (p.m == 1)
+        return split ? launch_rows<1, LPR, loads_for<1>(true)>(p, env, plan, stream)
+                     : launch_rows<1, LPR, loads_for<1>(false)>(p, env, plan, stream);
+    if (p.m <= 2)
+        return split ? launch_rows<2, LPR, loads_for<2>(true)>(p, env, plan, stream)
+                     : launch_rows<2, LPR, loads_for<2>(false)>(p, env, plan, stream);
     if (p.m <= 4) return launch_rows<4, LPR, loads_for<4>(false)>(p, env, plan, stream);
     if (p.m <= 8)
         return split ? launch_rows<8, LPR, loads_for<8>(true)>(p, env, plan, stream)
