@@ -71,6 +71,7 @@ constexpr int kSplitTargetFewRows = 128;
 constexpr int kSplitTargetFewRowsNarrow = 96;
 constexpr int kNarrowSlabs = 16;
 constexpr int kSplitTargetManyRows = 192;
+constexpr int kMinSliceGroups = 8;
 
 // Rows of x from which the products go to the matrix cores: 16 output rows
 // cost one v_mfma_f32_16x16x4f32 per 4 rows x 16 columns of W, where the
@@ -413,7 +414,10 @@ GemvPlan gemv_plan(const Problem& p) {
         // products) do better with fewer, longer slices when there are few rows.
         const int64_t target = p.m > 4 ? kSplitTargetManyRows
                                : slabs <= kNarrowSlabs ? kSplitTargetFewRowsNarrow : kSplitTargetFewRows;
-        const int64_t want = std::min<int64_t>(groups, (target + slabs - 1) / slabs);
+        // Slices of at least 8 groups (128 rows): the 768-deep out product
+        // took 5-11 % less time in 6 slices than in 8 (M = 1) or 16 (M = 16).
+        const int64_t want =
+            std::max<int64_t>(1, std::min<int64_t>(groups / kMinSliceGroups, (target + slabs - 1) / slabs));
         rows_per_split = 16 * ((groups + want - 1) / want);
     }
     plan.k_per_split = rows_per_split;

@@ -518,7 +518,8 @@ def test_bf16_causal_masks_within_the_stated_tolerance(gpu, mask):
 # ---- decode-shaped products (few rows, row-major weight) ------------------------------
 
 @pytest.mark.parametrize("rows,cols,inner", [(1, 8, 1), (3, 100, 37), (5, 772, 1000), (16, 260, 4100),
-                                             (7, 2304, 768), (2, 12, 20000)])
+                                             (7, 2304, 768), (2, 12, 20000), (1, 516, 1000), (2, 300, 777),
+                                             (16, 768, 784)])
 @pytest.mark.parametrize("accumulate", [False, True])
 def test_few_row_products_match_the_oracle(gpu, rows, cols, inner, accumulate):
     spec = MatmulSpec.new(rows, cols, inner).scaled(0.7)
