@@ -710,7 +710,7 @@ Args make_args(const Problem& p, const Env& env, const Plan& plan) {
 
 // The direct-to-LDS fp32 kernel (gemm_dma.hip): whether it serves `p`
 // (aligned operands), its launch shape and its launcher.
-bool dma_applies(const Problem& p);
+bool dma_applies(const Problem& p, const Env& env);
 LaunchShape describe_f32_dma(const Problem& p, const Env& env);
 hipError_t launch_gemm_f32_dma(const Problem& p, const Env& env, hipStream_t stream);
 // The bf16 variant of the direct-to-LDS kernel: whether it serves `p`, its
@@ -728,7 +728,7 @@ hipError_t launch_gemm_bf16_wide(const Problem& p, const Env& env, hipStream_t s
 // sums into p.column_sums (gemm_dma.hip): whether it serves `p` (batch 1,
 // unmasked, no bias, right operand row-contiguous, aligned), its launch shape
 // (workspace: the product's partial sums and N per K slice) and launcher.
-bool f32_column_sums_applies(const Problem& p);
+bool f32_column_sums_applies(const Problem& p, const Env& env);
 LaunchShape describe_f32_column_sums(const Problem& p, const Env& env);
 hipError_t launch_gemm_f32_column_sums(const Problem& p, const Env& env, hipStream_t stream);
 // bf16 with both operands first staged as bf16 in the workspace (gemm_dma.hip):

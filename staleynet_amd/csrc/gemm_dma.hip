@@ -262,10 +262,13 @@ __device__ __forceinline__ void mask_stage(f32x4* sa, int64_t m0, int64_t k0, in
     }
 }
 
-// Waves per SIMD that STAGES LDS stages allow (160 KB of LDS per CU).
+// Waves per SIMD that STAGES LDS stages allow (160 KB of LDS per CU), at
+// most 4: 128 registers a lane (the 64 x 64 tile's LDS would allow 5, whose
+// 96 registers spilled).
 template <class T, int STAGES>
 constexpr int dma_waves_per_eu() {
-    return (160 * 1024 / ((T::BM + T::BN) * T::BK * 4 * STAGES)) * (T::THREADS / 64) / 4;
+    const int by_lds = (160 * 1024 / ((T::BM + T::BN) * T::BK * 4 * STAGES)) * (T::THREADS / 64) / 4;
+    return by_lds < 4 ? by_lds : 4;
 }
 
 // Waits until at most PENDING of this wave's vector-memory instructions are
@@ -607,7 +610,7 @@ template <class C, int FEED>
 SplitCost split_cost() {
     using T = typename C::T;
     SplitCost cost;
-    cost.workgroups_per_cu = std::max(1, 160 * 1024 / ((T::BM + T::BN) * T::BK * 4 * C::STAGES));
+    cost.workgroups_per_cu = std::max(1, dma_waves_per_eu<T, C::STAGES>() * 4 / (T::THREADS / 64));
     cost.flops_per_cu = FEED == kFeedF32 ? 522e9 : FEED == kFeedRound ? 1.95e12 : 2.9e12;
     cost.k_per_index = FEED == kFeedBf16 ? 2 : 1;
     return cost;
@@ -677,9 +680,22 @@ bool config_applies(const Problem& p) {
 // The tile configuration each direct-to-LDS family takes for `p`, handed
 // to `f` (the launchers, applicability checks and launch shapes all choose
 // through these).
+// Products whose 128x128 plan (split K included) has fewer workgroups than
+// the device has CUs take 64x64 tiles (four waves of 32x32, five workgroups
+// per CU by LDS): config 0's products and the reference's published shapes
+// (2048 x 768 x 256: 96 tiles of 128 x 128 on 256 CUs). Measured: config 0's
+// set 43.6 -> 56.1 TFLOP/s, 2048 x 768 x 256 34 -> 54, 2048 x 1024 x 256
+// 45 -> 68; configs 1 and 2, whose plans fill the CUs, keep 128 x 128 (a
+// 128 x 64 tile below 256 tiles lost 6 % on config 2's 768 x 768 weight
+// gradient).
+using DmaSmall = DmaConfig<Tile<64, 64, 32, 2, 2>, 2>;
+
 template <class F>
-auto with_f32_dma_config(const Problem& p, F&& f) {
-    return p.n <= 64 ? f(DmaNarrow{}) : f(DmaSquare{});
+auto with_f32_dma_config(const Problem& p, const Env& env, F&& f) {
+    if (p.n <= 64) return f(DmaNarrow{});
+    const Plan square = dma_plan<DmaSquare, kFeedF32>(p, env);
+    const int64_t workgroups = int64_t(square.tiles_m) * square.tiles_n * square.splits * p.batch;
+    return workgroups < std::max(env.cu_count, 1) ? f(DmaSmall{}) : f(DmaSquare{});
 }
 
 template <class F>
@@ -694,8 +710,8 @@ auto with_bf16_dma_config(const Problem& p, F&& f) {
 // Operands 16-byte aligned with 16-byte-multiple leading dimensions and
 // batch strides, and every per-lane offset of one K-step within the buffer
 // offset range (the same conditions as the buffer-load path of gemm_mfma.hip).
-bool dma_applies(const Problem& p) {
-    return with_f32_dma_config(p, [&](auto c) { return config_applies<decltype(c)>(p); });
+bool dma_applies(const Problem& p, const Env& env) {
+    return with_f32_dma_config(p, env, [&](auto c) { return config_applies<decltype(c)>(p); });
 }
 
 bool bf16_dma_applies(const Problem& p) {
@@ -703,7 +719,7 @@ bool bf16_dma_applies(const Problem& p) {
 }
 
 LaunchShape describe_f32_dma(const Problem& p, const Env& env) {
-    return with_f32_dma_config(p, [&](auto c) {
+    return with_f32_dma_config(p, env, [&](auto c) {
         using C = decltype(c);
         return tiled_shape<typename C::T>(p, dma_plan<C, kFeedF32>(p, env), SN_PATH_F32_DIRECT);
     });
@@ -717,7 +733,7 @@ LaunchShape describe_bf16_dma(const Problem& p, const Env& env) {
 }
 
 hipError_t launch_gemm_f32_dma(const Problem& p, const Env& env, hipStream_t stream) {
-    return with_f32_dma_config(p, [&](auto c) { return launch_dma_layout<decltype(c), kFeedF32>(p, env, stream); });
+    return with_f32_dma_config(p, env, [&](auto c) { return launch_dma_layout<decltype(c), kFeedF32>(p, env, stream); });
 }
 
 hipError_t launch_gemm_bf16_dma(const Problem& p, const Env& env, hipStream_t stream) {
@@ -756,13 +772,13 @@ hipError_t launch_column_sums_tiles(const Problem& p, const Env& env, hipStream_
 
 }  // namespace
 
-bool f32_column_sums_applies(const Problem& p) {
+bool f32_column_sums_applies(const Problem& p, const Env& env) {
     return p.batch == 1 && p.m > 0 && p.k > 0 && p.mask == SN_MASK_NONE && !p.b_k_contiguous && p.bias == nullptr &&
-           dma_applies(p);
+           dma_applies(p, env);
 }
 
 LaunchShape describe_f32_column_sums(const Problem& p, const Env& env) {
-    return with_f32_dma_config(p, [&](auto c) {
+    return with_f32_dma_config(p, env, [&](auto c) {
         using C = decltype(c);
         const Plan plan = column_sums_plan<C>(p, env);
         LaunchShape s = tiled_shape<typename C::T>(p, plan, SN_PATH_F32_DIRECT);
@@ -772,7 +788,7 @@ LaunchShape describe_f32_column_sums(const Problem& p, const Env& env) {
 }
 
 hipError_t launch_gemm_f32_column_sums(const Problem& p, const Env& env, hipStream_t stream) {
-    return with_f32_dma_config(p, [&](auto c) {
+    return with_f32_dma_config(p, env, [&](auto c) {
         using C = decltype(c);
         return p.a_k_contiguous ? launch_column_sums_tiles<C, true>(p, env, stream)
                                 : launch_column_sums_tiles<C, false>(p, env, stream);

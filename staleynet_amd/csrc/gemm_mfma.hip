@@ -275,14 +275,14 @@ hipError_t launch_splitk_reduce(const Problem& p, const Env& env, int splits, hi
 }  // namespace gemm
 
 LaunchShape describe_gemm_f32(const Problem& p, const Env& env) {
-    if (gemm::dma_applies(p)) return gemm::describe_f32_dma(p, env);
+    if (gemm::dma_applies(p, env)) return gemm::describe_f32_dma(p, env);
     if (gemm::use_narrow(p))
         return gemm::tiled_shape<gemm::TileNarrow>(p, gemm::plan_for<gemm::TileNarrow>(p, env), SN_PATH_F32_REGISTER);
     return gemm::tiled_shape<gemm::TileSquare>(p, gemm::plan_for<gemm::TileSquare>(p, env), SN_PATH_F32_REGISTER);
 }
 
 hipError_t launch_gemm_f32(const Problem& p, const Env& env, hipStream_t stream) {
-    if (gemm::dma_applies(p)) return gemm::launch_gemm_f32_dma(p, env, stream);
+    if (gemm::dma_applies(p, env)) return gemm::launch_gemm_f32_dma(p, env, stream);
     if (gemm::use_narrow(p)) return gemm::dispatch_layout<gemm::TileNarrow>(p, env, stream);
     return gemm::dispatch_layout<gemm::TileSquare>(p, env, stream);
 }

@@ -49,7 +49,8 @@ hipError_t launch_matmul(const Problem& p, uint32_t kernel, const Env& env, hipS
 }
 
 bool f32_column_sums_fused(const Problem& p, uint32_t kernel, const Env& env) {
-    return kernel == SN_KERNEL_MFMA_F32 && family_of(p, kernel, env) == Family::Tiled && gemm::f32_column_sums_applies(p);
+    return kernel == SN_KERNEL_MFMA_F32 && family_of(p, kernel, env) == Family::Tiled &&
+           gemm::f32_column_sums_applies(p, env);
 }
 
 LaunchShape describe_matmul_column_sums(const Problem& p, uint32_t kernel, const Env& env) {
