@@ -402,9 +402,16 @@ hipError_t launch_wide(const Problem& p, const Env& env, const Plan& plan, hipSt
 // bf16 for the 128 x 256 kernel (gemm_dma.hip): weight gradients (TN)
 // 310-549 -> 394-755 TFLOP/s, input gradients (NT) 464-616 -> 517-826,
 // forward (NN) 430-601 -> 496-693.
+//
+// Products whose 256 x 256 plan leaves more than half the CUs idle (config 0's
+// products: 2048 x 768 x 256 is 24 tiles) take the 128-wide kernels instead:
+// config 0's bf16 set 52.0 -> 59.4 TFLOP/s, 2048 x 768 x 256 47 -> 55
+// (a whole-device threshold cost config 2's set 7 %).
 bool bf16_wide_applies(const Problem& p, const Env& env) {
     if (p.mask != SN_MASK_NONE || p.m < 128 || p.n < 128 || !buffers_ok<WideTile>(p)) return false;
     const WideStaging st = wide_staging(p, env);
+    const Plan fill = wide_plan(st.q, st.rest);
+    if (2 * int64_t(fill.tiles_m) * fill.tiles_n * fill.splits * p.batch < std::max(env.cu_count, 1)) return false;
     if (st.side != kStageNone) return true;
     const Plan plan = wide_plan(p, env);
     return plan.splits <= 1 || size_t(plan.splits) * size_t(p.m) * size_t(p.n) * sizeof(float) <= env.workspace_bytes;

@@ -158,6 +158,18 @@ def test_configs_take_the_expected_kernel_families():
     assert long_k.workspace_bytes == long_k.splits * 256 * 640 * 4 + 256 * 500_000 * 2  # x^T staged
     # Too small for the wide tiles: operands staged as bf16 for the 128-wide kernels.
     assert gemm.plan(MatmulSpec.new(96, 2304, 768).with_precision(Precision.Bf16)).path == gemm.PATH_BF16_STAGED
+    # 256 x 256 tiles that would leave more than half the CUs idle (config 0's 2048 x 768 x 256: 24 of
+    # them) also go to the 128-wide kernels; 128 tiles are enough.
+    small = gemm.plan(MatmulSpec.new(2048, 768, 256).with_precision(Precision.Bf16))
+    assert small.path == gemm.PATH_BF16_STAGED and (small.tile_rows, small.tile_cols) == (128, 128)
+    assert gemm.plan(MatmulSpec.new(2048, 4096, 256).with_precision(Precision.Bf16)).path == gemm.PATH_BF16_WIDE
+    assert gemm.plan(MatmulSpec.new(2048, 768, 256).with_precision(Precision.Bf16), cu_count=32).path == \
+        gemm.PATH_BF16_WIDE
+    # fp32: 64 x 64 tiles when the 128 x 128 plan has fewer workgroups than CUs.
+    f32_small = gemm.plan(MatmulSpec.new(2048, 768, 256))
+    assert f32_small.path == gemm.PATH_F32_DIRECT and (f32_small.tile_rows, f32_small.tile_cols) == (64, 64)
+    assert (gemm.plan(MatmulSpec.new(2048, 768, 256), cu_count=64).tile_rows,
+            gemm.plan(MatmulSpec.new(2048, 4096, 256)).tile_rows) == (128, 128)
     # Too narrow for a quarter tile: the staged kernels keep it.
     assert gemm.plan(MatmulSpec.new(32768, 64, 768).right_transposed().with_precision(Precision.Bf16)).path != \
         gemm.PATH_BF16_WIDE
