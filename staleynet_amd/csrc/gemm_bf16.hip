@@ -178,7 +178,7 @@ using TileNarrow = Tile<256, 64, 32, 4, 1>;
 LaunchShape describe_gemm_bf16(const Problem& p, const Env& env) {
     if (gemm::bf16_wide_applies(p, env)) return gemm::describe_bf16_wide(p, env);
     if (gemm::bf16_staged_applies(p, env)) return gemm::describe_bf16_staged(p, env);
-    if (gemm::bf16_dma_applies(p)) return gemm::describe_bf16_dma(p, env);
+    if (gemm::bf16_dma_applies(p, env)) return gemm::describe_bf16_dma(p, env);
     if (p.n <= 64)
         return gemm::tiled_shape<gemm::TileNarrow>(p, gemm::plan_for<gemm::TileNarrow>(p, env), SN_PATH_BF16_REGISTER);
     return gemm::tiled_shape<gemm::TileSquare>(p, gemm::plan_for<gemm::TileSquare>(p, env), SN_PATH_BF16_REGISTER);
@@ -187,7 +187,7 @@ LaunchShape describe_gemm_bf16(const Problem& p, const Env& env) {
 hipError_t launch_gemm_bf16(const Problem& p, const Env& env, hipStream_t stream) {
     if (gemm::bf16_wide_applies(p, env)) return gemm::launch_gemm_bf16_wide(p, env, stream);
     if (gemm::bf16_staged_applies(p, env)) return gemm::launch_gemm_bf16_staged(p, env, stream);
-    if (gemm::bf16_dma_applies(p)) return gemm::launch_gemm_bf16_dma(p, env, stream);
+    if (gemm::bf16_dma_applies(p, env)) return gemm::launch_gemm_bf16_dma(p, env, stream);
     if (p.n <= 64) return gemm::dispatch_layout_bf16<gemm::TileNarrow>(p, env, stream);
     return gemm::dispatch_layout_bf16<gemm::TileSquare>(p, env, stream);
 }

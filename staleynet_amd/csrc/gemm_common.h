@@ -715,7 +715,7 @@ LaunchShape describe_f32_dma(const Problem& p, const Env& env);
 hipError_t launch_gemm_f32_dma(const Problem& p, const Env& env, hipStream_t stream);
 // The bf16 variant of the direct-to-LDS kernel: whether it serves `p`, its
 // launch shape (with the split-K workspace it uses) and its launcher.
-bool bf16_dma_applies(const Problem& p);
+bool bf16_dma_applies(const Problem& p, const Env& env);
 LaunchShape describe_bf16_dma(const Problem& p, const Env& env);
 hipError_t launch_gemm_bf16_dma(const Problem& p, const Env& env, hipStream_t stream);
 // The 256 x 256 bf16 kernel that rounds fp32 operands as it loads them

@@ -698,9 +698,18 @@ auto with_f32_dma_config(const Problem& p, const Env& env, F&& f) {
     return workgroups < std::max(env.cu_count, 1) ? f(DmaSmall{}) : f(DmaSquare{});
 }
 
+// Small bf16 products (fewer 128 x 128 tiles than CUs: config 0's) skip
+// the staging pass, whose two extra launches they cannot amortise, and take
+// 64 x 64 tiles that round fp32 fragments as they are read: config 0's bf16
+// set 60 -> 80 TFLOP/s, 2048 x 768 x 256 54 -> 74, 2048 x 1024 x 256 74 -> 108.
+bool small_bf16(const Problem& p, const Env& env) {
+    return ((p.m + 127) / 128) * ((p.n + 127) / 128) * p.batch < std::max(env.cu_count, 1);
+}
+
 template <class F>
-auto with_bf16_dma_config(const Problem& p, F&& f) {
+auto with_bf16_dma_config(const Problem& p, const Env& env, F&& f) {
     if (p.n <= 64) return f(Bf16Narrow{});
+    if (small_bf16(p, env)) return f(DmaSmall{});
     if (p.n >= kBf16WideColumns) return f(Bf16Wide{});
     return f(Bf16Square{});
 }
@@ -714,8 +723,8 @@ bool dma_applies(const Problem& p, const Env& env) {
     return with_f32_dma_config(p, env, [&](auto c) { return config_applies<decltype(c)>(p); });
 }
 
-bool bf16_dma_applies(const Problem& p) {
-    return with_bf16_dma_config(p, [&](auto c) { return config_applies<decltype(c)>(p); });
+bool bf16_dma_applies(const Problem& p, const Env& env) {
+    return with_bf16_dma_config(p, env, [&](auto c) { return config_applies<decltype(c)>(p); });
 }
 
 LaunchShape describe_f32_dma(const Problem& p, const Env& env) {
@@ -726,7 +735,7 @@ LaunchShape describe_f32_dma(const Problem& p, const Env& env) {
 }
 
 LaunchShape describe_bf16_dma(const Problem& p, const Env& env) {
-    return with_bf16_dma_config(p, [&](auto c) {
+    return with_bf16_dma_config(p, env, [&](auto c) {
         using C = decltype(c);
         return tiled_shape<typename C::T>(p, dma_plan<C, kFeedRound>(p, env), SN_PATH_BF16_DIRECT);
     });
@@ -737,7 +746,7 @@ hipError_t launch_gemm_f32_dma(const Problem& p, const Env& env, hipStream_t str
 }
 
 hipError_t launch_gemm_bf16_dma(const Problem& p, const Env& env, hipStream_t stream) {
-    return with_bf16_dma_config(p, [&](auto c) { return launch_dma_layout<decltype(c), kFeedRound>(p, env, stream); });
+    return with_bf16_dma_config(p, env, [&](auto c) { return launch_dma_layout<decltype(c), kFeedRound>(p, env, stream); });
 }
 
 // ---- The weight-gradient product with Linear's bias gradient -------------
@@ -861,7 +870,8 @@ bool bf16_staged_applies(const Problem& p, const Env& env) {
     // Unmasked (the masked products keep their in-stage masking), operands
     // that the direct-to-LDS loads could read, n above the narrow tile, and
     // room for both staged operands.
-    if (p.mask != SN_MASK_NONE || p.n <= 64 || p.k < 1 || env.workspace == nullptr || !bf16_dma_applies(p))
+    if (p.mask != SN_MASK_NONE || p.n <= 64 || p.k < 1 || env.workspace == nullptr || !bf16_dma_applies(p, env) ||
+        small_bf16(p, env))
         return false;
     if (p.batch > 65535) return false;
     const Staging st = staging_for(p);

@@ -156,12 +156,16 @@ def test_configs_take_the_expected_kernel_families():
     long_k = gemm.plan(MatmulSpec.new(256, 640, 500_000).left_transposed().with_precision(Precision.Bf16),
                        workspace_bytes=1 << 40)
     assert long_k.workspace_bytes == long_k.splits * 256 * 640 * 4 + 256 * 500_000 * 2  # x^T staged
-    # Too small for the wide tiles: operands staged as bf16 for the 128-wide kernels.
-    assert gemm.plan(MatmulSpec.new(96, 2304, 768).with_precision(Precision.Bf16)).path == gemm.PATH_BF16_STAGED
+    # Too small for the wide tiles, and fewer 128 x 128 tiles than CUs: no staging pass, 64 x 64 tiles
+    # rounding fp32 fragments as they are read.
+    tiny = gemm.plan(MatmulSpec.new(96, 2304, 768).with_precision(Precision.Bf16))
+    assert tiny.path == gemm.PATH_BF16_DIRECT and (tiny.tile_rows, tiny.tile_cols) == (64, 64)
     # 256 x 256 tiles that would leave more than half the CUs idle (config 0's 2048 x 768 x 256: 24 of
     # them) also go to the 128-wide kernels; 128 tiles are enough.
     small = gemm.plan(MatmulSpec.new(2048, 768, 256).with_precision(Precision.Bf16))
-    assert small.path == gemm.PATH_BF16_STAGED and (small.tile_rows, small.tile_cols) == (128, 128)
+    assert small.path == gemm.PATH_BF16_DIRECT and (small.tile_rows, small.tile_cols) == (64, 64)
+    mid = gemm.plan(MatmulSpec.new(4096, 4096, 256).with_precision(Precision.Bf16), cu_count=1024)
+    assert mid.path == gemm.PATH_BF16_STAGED and (mid.tile_rows, mid.tile_cols) == (128, 256)
     assert gemm.plan(MatmulSpec.new(2048, 4096, 256).with_precision(Precision.Bf16)).path == gemm.PATH_BF16_WIDE
     assert gemm.plan(MatmulSpec.new(2048, 768, 256).with_precision(Precision.Bf16), cu_count=32).path == \
         gemm.PATH_BF16_WIDE

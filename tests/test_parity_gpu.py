@@ -19,6 +19,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle
+from staleynet_amd import gemm
 from staleynet_amd.gemm import (BatchStrides, MatmulKernel, MatmulPanic, MatmulSpec, Precision, Shape, SN_ERR_ALIASING,
                                 SN_ERR_EMPTY_BATCH, SN_ERR_LEFT_TOO_SMALL, SN_ERR_OUTPUT_TOO_SMALL)
 
@@ -351,41 +352,54 @@ def test_bf16_is_exact_on_bf16_representable_integers(gpu, variant):
     assert np.array_equal(expected, actual)
 
 
-@pytest.mark.parametrize("k", [16, 128])  # 16: the narrow tile; 128: operands staged as bf16 first
-def test_bf16_inputs_round_to_nearest_even(gpu, k):
-    # A times the identity returns A rounded to bf16 (7 stored mantissa bits).
-    # Expected values follow from IEEE roundTiesToEven by hand:
-    u = 2.0 ** -7  # bf16 ulp in [1, 2)
-    cases = [
-        (1.0, 1.0),
-        (1 + 2.0 ** -8, 1.0),                      # halfway, 1.0 is even
-        (1 + 3 * 2.0 ** -8, 1 + 2 * u),            # halfway between 1+u (odd) and 1+2u (even)
-        (1 + 2.0 ** -8 + 2.0 ** -20, 1 + u),       # just above halfway
-        (1 + 2.0 ** -8 - 2.0 ** -20, 1.0),         # just below halfway
-        (-(1 + 3 * 2.0 ** -8), -(1 + 2 * u)),
-        (3.0, 3.0),
-        (1.0 / 3.0, 0.333984375),                  # 0x3EAB: 0.01010101 01010101... rounds up
-        (float(np.finfo(np.float32).max), float("inf")),
-        (2.0 ** -100 * 1.5, 2.0 ** -100 * 1.5),    # exact, small exponent
-        (0.0, 0.0),
-    ]
-    a = np.zeros((len(cases), k), np.float32)
-    a[:, 0] = [c[0] for c in cases]
-    eye = np.eye(k, dtype=np.float32)
-    spec = MatmulSpec.new(len(cases), k, k)
-    out = run_gpu(gpu, spec, a.ravel(), eye.ravel(), np.zeros(len(cases) * k, np.float32), MatmulKernel.MfmaBf16)
-    got = out.reshape(len(cases), k)[:, 0]
-    assert got.tolist() == [np.float32(c[1]) for c in cases]
+# Rounding to nearest even, hand-derived (IEEE roundTiesToEven), where each path rounds: k = 16 the
+# narrow tile and k = 128 the 64 x 64 tile, both rounding fp32 fragments as they are read; "staged",
+# a right operand of 256 identity blocks side by side (fewer rows than a 256 x 256 tile, as many
+# 128 x 128 tiles as CUs), whose operands are first rounded into the workspace by the staging kernels.
+BF16_RNE_CASES = [
+    (1.0, 1.0),
+    (1 + 2.0 ** -8, 1.0),                      # halfway, 1.0 is even
+    (1 + 3 * 2.0 ** -8, 1 + 2 * 2.0 ** -7),    # halfway between 1+u (odd) and 1+2u (even), u = 2^-7
+    (1 + 2.0 ** -8 + 2.0 ** -20, 1 + 2.0 ** -7),  # just above halfway
+    (1 + 2.0 ** -8 - 2.0 ** -20, 1.0),         # just below halfway
+    (-(1 + 3 * 2.0 ** -8), -(1 + 2 * 2.0 ** -7)),
+    (3.0, 3.0),
+    (1.0 / 3.0, 0.333984375),                  # 0x3EAB: 0.01010101 01010101... rounds up
+    (float(np.finfo(np.float32).max), float("inf")),
+    (2.0 ** -100 * 1.5, 2.0 ** -100 * 1.5),    # exact, small exponent
+    (0.0, 0.0),
+]
 
 
-# Unmasked aligned bf16 products with more than 64 columns first round both operands to
-# bf16, K-contiguous, in the context's workspace (zeros pad K to a multiple of 8), then
-# multiply; exact integer inputs pin every layout, padding, batch and shared-operand case.
+@pytest.mark.parametrize("case", ["k16", "k128", "staged"])
+def test_bf16_inputs_round_to_nearest_even(gpu, case):
+    # A times the identity (or identity blocks) returns A rounded to bf16 (7 stored mantissa bits).
+    k = 16 if case == "k16" else 128
+    blocks = 256 if case == "staged" else 1
+    rows = len(BF16_RNE_CASES)
+    a = np.zeros((rows, k), np.float32)
+    a[:, 0] = [c[0] for c in BF16_RNE_CASES]
+    right = np.tile(np.eye(k, dtype=np.float32), (1, blocks))
+    spec = MatmulSpec.new(rows, k * blocks, k)
+    plan = gemm.plan(spec.with_precision(Precision.Bf16))
+    assert plan.path == {"k16": gemm.PATH_BF16_DIRECT, "k128": gemm.PATH_BF16_DIRECT,
+                         "staged": gemm.PATH_BF16_STAGED}[case], f"path {plan.path}"
+    out = run_gpu(gpu, spec, a.ravel(), right.ravel(), np.zeros(rows * k * blocks, np.float32),
+                  MatmulKernel.MfmaBf16).reshape(rows, k * blocks)
+    expected = [np.float32(c[1]) for c in BF16_RNE_CASES]
+    assert out[:, 0].tolist() == expected
+    assert out[:, k * (blocks - 1)].tolist() == expected  # the last identity block
+
+
+# Unmasked aligned bf16 products with more than 64 columns, too small for the 256 x 256 kernel but
+# with at least as many 128 x 128 tiles as CUs, first round both operands to bf16, K-contiguous, in
+# the context's workspace (zeros pad K to a multiple of 8), then multiply; exact integer inputs pin
+# every layout, padding, batch and shared-operand case. Each case checks that the plan stages.
 @pytest.mark.parametrize("variant,rows,cols,inner", [
-    ("TN", 96, 160, 203),    # both operands transposed while staged, K padded to 208
-    ("TT", 68, 132, 36),     # A transposed, B K-contiguous
-    ("NT", 100, 72, 1000),   # both K-contiguous
-    ("NN", 260, 2052, 96),   # the 128x256 tile, partial tiles on both edges
+    ("TN", 96, 32800, 203),   # both operands transposed while staged, K padded to 208
+    ("TT", 68, 32900, 36),    # A transposed, B K-contiguous
+    ("NT", 32800, 100, 1000), # both K-contiguous
+    ("NN", 1030, 4100, 96),   # the 128x256 tile, partial tiles on both edges
 ])
 def test_bf16_staged_operands_are_exact_on_integers(gpu, variant, rows, cols, inner):
     rng = np.random.default_rng(rows + cols + inner)
@@ -396,15 +410,18 @@ def test_bf16_staged_operands_are_exact_on_integers(gpu, variant, rows, cols, in
         spec = spec.left_transposed()
     if variant[1] == "T":
         spec = spec.right_transposed()
+    spec = spec.accumulate()
+    assert gemm.plan(spec.with_precision(Precision.Bf16)).path == gemm.PATH_BF16_STAGED
     initial = rng.integers(-8, 9, size=rows * cols).astype(np.float32)
-    expected = expected_for(spec.accumulate(), left, right, initial)
-    actual = run_gpu(gpu, spec.accumulate(), left, right, initial, MatmulKernel.MfmaBf16)
+    expected = initial.copy()
+    oracle.matmul_parallel(to_product(spec), left, right, expected)
+    actual = run_gpu(gpu, spec, left, right, initial, MatmulKernel.MfmaBf16)
     assert np.array_equal(expected, actual)
 
 
 @pytest.mark.parametrize("shared", ["none", "left", "right"])
 def test_bf16_staged_batches_and_shared_operands(gpu, shared):
-    batches, rows, cols, inner = 3, 72, 136, 64
+    batches, rows, cols, inner = 3, 72, 11000, 64
     rng = np.random.default_rng(5)
     left_stride = 0 if shared == "left" else rows * inner
     right_stride = 0 if shared == "right" else inner * cols
@@ -412,8 +429,10 @@ def test_bf16_staged_batches_and_shared_operands(gpu, shared):
     right = rng.integers(-16, 17, size=max(right_stride, inner * cols) * (1 if shared == "right" else batches))
     spec = MatmulSpec.new(rows, cols, inner).right_transposed().batched(
         BatchStrides(batches, left_stride, right_stride, rows * cols))
+    assert gemm.plan(spec.with_precision(Precision.Bf16)).path == gemm.PATH_BF16_STAGED
     initial = np.zeros(batches * rows * cols, np.float32)
-    expected = expected_for(spec, left.astype(np.float32), right.astype(np.float32), initial)
+    expected = initial.copy()
+    oracle.matmul_parallel(to_product(spec), left.astype(np.float32), right.astype(np.float32), expected)
     actual = run_gpu(gpu, spec, left.astype(np.float32), right.astype(np.float32), initial, MatmulKernel.MfmaBf16)
     assert np.array_equal(expected, actual)
 
