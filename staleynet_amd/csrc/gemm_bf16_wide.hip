@@ -324,7 +324,7 @@ size_t round256(size_t bytes) { return (bytes + 255) / 256 * 256; }
 // products) when it has at most half the other's elements and fits beside
 // the partial sums: rounding it once costs 6 bytes an element, while every
 // tile row (or column) that reads it then fetches 2 bytes an element
-// instead of 4. Measured on c2's set (596 TFLOP/s against 558 with nothing
+// instead of 4. Measured on the 111.5M model's set (596 TFLOP/s against 558 with nothing
 // staged): a quarter as the bound 595, any smaller operand 592 (the square
 // weight gradients then pay the staging for no gain).
 constexpr int kStageRatio = 2;
@@ -398,15 +398,15 @@ hipError_t launch_wide(const Problem& p, const Env& env, const Plan& plan, hipSt
 
 // Unmasked products with 128-bit-loadable operands (buffers_ok) whose output
 // fills at least a quarter of a 256 x 256 tile each way, and room for the
-// partial sums. Measured on c2's products against staging both operands as
+// partial sums. Measured on the 111.5M model's products against staging both operands as
 // bf16 for the 128 x 256 kernel (gemm_dma.hip): weight gradients (TN)
 // 310-549 -> 394-755 TFLOP/s, input gradients (NT) 464-616 -> 517-826,
 // forward (NN) 430-601 -> 496-693.
 //
-// Products whose 256 x 256 plan leaves more than half the CUs idle (config 0's
+// Products whose 256 x 256 plan leaves more than half the CUs idle (the 7.1M model's
 // products: 2048 x 768 x 256 is 24 tiles) take the 128-wide kernels instead:
-// config 0's bf16 set 52.0 -> 59.4 TFLOP/s, 2048 x 768 x 256 47 -> 55
-// (a whole-device threshold cost config 2's set 7 %).
+// the 7.1M model's bf16 set 52.0 -> 59.4 TFLOP/s, 2048 x 768 x 256 47 -> 55
+// (a whole-device threshold cost the 111.5M model's set 7 %).
 bool bf16_wide_applies(const Problem& p, const Env& env) {
     if (p.mask != SN_MASK_NONE || p.m < 128 || p.n < 128 || !buffers_ok<WideTile>(p)) return false;
     const WideStaging st = wide_staging(p, env);

@@ -618,7 +618,7 @@ struct SplitCost {
 // Products whose output tiles cannot fill every CU four times over (the
 // K = 32768 weight gradients: 36 to 768 tiles of 128x128) split K into
 // BK-aligned slices of at least 8 steps, as far as the workspace allows. The
-// count is the cheapest under a model of the launch, measured on c2's
+// count is the cheapest under a model of the launch, measured on the 111.5M model's
 // weight gradients:
 //  * workgroups are dealt evenly over the CUs; the busiest CU runs
 //    ceil(tiles x slices / CUs) of them, workgroups_per_cu at a time, and

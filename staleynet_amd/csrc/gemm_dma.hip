@@ -682,11 +682,11 @@ bool config_applies(const Problem& p) {
 // through these).
 // Products whose 128x128 plan (split K included) has fewer workgroups than
 // the device has CUs take 64x64 tiles (four waves of 32x32, five workgroups
-// per CU by LDS): config 0's products and the reference's published shapes
-// (2048 x 768 x 256: 96 tiles of 128 x 128 on 256 CUs). Measured: config 0's
+// per CU by LDS): the 7.1M model's products and the reference's published shapes
+// (2048 x 768 x 256: 96 tiles of 128 x 128 on 256 CUs). Measured: the 7.1M model's
 // set 43.6 -> 56.1 TFLOP/s, 2048 x 768 x 256 34 -> 54, 2048 x 1024 x 256
-// 45 -> 68; configs 1 and 2, whose plans fill the CUs, keep 128 x 128 (a
-// 128 x 64 tile below 256 tiles lost 6 % on config 2's 768 x 768 weight
+// 45 -> 68; the 42.9M and 111.5M models, whose plans fill the CUs, keep 128 x 128 (a
+// 128 x 64 tile below 256 tiles lost 6 % on the 111.5M model's 768 x 768 weight
 // gradient).
 using DmaSmall = DmaConfig<Tile<64, 64, 32, 2, 2>, 2>;
 
@@ -698,9 +698,9 @@ auto with_f32_dma_config(const Problem& p, const Env& env, F&& f) {
     return workgroups < std::max(env.cu_count, 1) ? f(DmaSmall{}) : f(DmaSquare{});
 }
 
-// Small bf16 products (fewer 128 x 128 tiles than CUs: config 0's) skip
+// Small bf16 products (fewer 128 x 128 tiles than CUs: the 7.1M model's) skip
 // the staging pass, whose two extra launches they cannot amortise, and take
-// 64 x 64 tiles that round fp32 fragments as they are read: config 0's bf16
+// 64 x 64 tiles that round fp32 fragments as they are read: the 7.1M model's bf16
 // set 60 -> 80 TFLOP/s, 2048 x 768 x 256 54 -> 74, 2048 x 1024 x 256 74 -> 108.
 bool small_bf16(const Problem& p, const Env& env) {
     return ((p.m + 127) / 128) * ((p.n + 127) / 128) * p.batch < std::max(env.cu_count, 1);
