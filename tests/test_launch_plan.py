@@ -248,3 +248,85 @@ def test_tile_map_rejects_bad_arguments():
         gemm.tile_map(0, 1, 1, 1)
     with pytest.raises(gemm.GpuError):
         gemm.plan(MatmulSpec.new(2, 3, 4).batched(BatchStrides(0, 0, 0, 0)))
+
+
+# ---- randomized plans ------------------------------------------------------------------
+
+from hypothesis import HealthCheck, given, settings  # noqa: E402
+from hypothesis import strategies as st  # noqa: E402
+
+TILE_SIZES = {gemm.PATH_F32_DIRECT: {(128, 128), (128, 64), (64, 64)},
+              gemm.PATH_F32_DIRECT_SUMS: {(128, 128), (128, 64), (64, 64)},
+              gemm.PATH_BF16_WIDE: {(256, 256)},
+              gemm.PATH_BF16_STAGED: {(128, 128), (128, 256), (128, 64)},
+              gemm.PATH_BF16_DIRECT: {(128, 128), (128, 256), (128, 64), (64, 64)}}
+
+
+@settings(max_examples=300, deadline=None, suppress_health_check=[HealthCheck.too_slow])
+@given(m=st.integers(1, 5000), n=st.integers(1, 5000), k=st.integers(1, 40000),
+       left_t=st.booleans(), right_t=st.booleans(), batch=st.sampled_from([1, 1, 1, 2, 3, 12]),
+       bf16=st.booleans(), cus=st.sampled_from([32, 80, 256, 304]),
+       workspace=st.sampled_from([0, 1 << 20, 64 << 20, 1536 << 20]), align4=st.booleans())
+def test_random_plans_cover_the_product_once(m, n, k, left_t, right_t, batch, bf16, cus, workspace, align4):
+    # Shapes with 16-byte rows take the direct-to-LDS kernels, the rest the register-staged ones; any CU
+    # count and workspace. Whatever the plan, its slices cover K, its tiles cover the output, the
+    # workspace it asks for holds its partial sums, and the workgroup map visits each tile once.
+    if align4:
+        m, n, k = (max(4, x // 4 * 4) for x in (m, n, k))
+    spec = MatmulSpec.new(m, n, k)
+    if left_t:
+        spec = spec.left_transposed()
+    if right_t:
+        spec = spec.right_transposed()
+    if batch > 1:
+        spec = spec.batched(BatchStrides(batch, m * k, k * n, m * n))
+    if bf16:
+        spec = spec.with_precision(Precision.Bf16)
+    try:
+        plan = gemm.plan(spec, cu_count=cus, workspace_bytes=workspace)
+    except gemm.GpuError as err:
+        assert err.status == gemm.SN_ERR_WORKSPACE
+        return
+    assert (plan.splits - 1) * plan.k_per_split < k <= plan.splits * plan.k_per_split
+    if plan.path in TILE_SIZES:
+        assert (plan.tile_rows, plan.tile_cols) in TILE_SIZES[plan.path], plan.path
+    if plan.path in gemm.TILED_PATHS:
+        assert plan.tiles_m == -(-m // plan.tile_rows) and plan.tiles_n == -(-n // plan.tile_cols)
+        if plan.splits > 1:
+            assert plan.workspace_bytes >= plan.splits * m * n * 4
+        if plan.workgroups <= 1 << 16:
+            check_tiled_cover(plan)
+    # The 256 x 256 bf16 tiles only where they keep half the CUs busy.
+    if plan.path == gemm.PATH_BF16_WIDE:
+        assert 2 * plan.tiles_m * plan.tiles_n * plan.splits * batch >= cus
+    assert plan.workspace_bytes <= workspace
+
+
+@settings(max_examples=200, deadline=None)
+@given(inputs=st.integers(1, 4000), outputs=st.integers(1, 4000), rows=st.integers(1, 70000),
+       cus=st.sampled_from([80, 256]), workspace=st.sampled_from([0, 1 << 20, 1536 << 20]), bf16=st.booleans())
+def test_random_column_sum_plans_keep_the_product_plan(inputs, outputs, rows, cus, workspace, bf16):
+    # The weight-gradient spec of linear.rs:54-56: fused or not, the product's tiles and slices are
+    # sn_matmul's; fused, the workspace adds N floats per slice.
+    spec = MatmulSpec.new(inputs, outputs, rows).left_transposed().accumulate()
+    if bf16:
+        spec = spec.with_precision(Precision.Bf16)
+    try:
+        product = gemm.plan(spec, cu_count=cus, workspace_bytes=workspace)
+    except gemm.GpuError:
+        product = None
+    try:
+        fused = gemm.plan_column_sums(spec, cu_count=cus, workspace_bytes=workspace)
+    except gemm.GpuError as err:
+        assert err.status == gemm.SN_ERR_WORKSPACE
+        return
+    assert fused.workspace_bytes <= workspace
+    if fused.path == gemm.PATH_F32_DIRECT_SUMS:
+        assert not bf16 and outputs % 4 == 0 and inputs % 4 == 0
+        if fused.splits > 1:
+            assert fused.workspace_bytes == fused.splits * (inputs * outputs + outputs) * 4
+        if fused.workgroups <= 1 << 16:
+            check_tiled_cover(fused)
+    elif product is not None:
+        assert (fused.path, fused.tiles_m, fused.tiles_n, fused.splits) == \
+            (product.path, product.tiles_m, product.tiles_n, product.splits)
