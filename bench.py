@@ -1187,6 +1187,10 @@ def main() -> int:
     parser.add_argument("--one-product", nargs=2, metavar=("LAYOUT", "PRECISION"),
                         help="run only config 2's qkv product (NN, TN or NT; f32 or bf16) 1 + 5 times and exit: "
                              "the workload of the per-kernel counter profiles")
+    parser.add_argument("--one-linear", action="store_true",
+                        help="run only config 2's Linear bias measurements (block 0's four layers and the head: "
+                             "forward with and without the fused bias, weight and bias gradients as two calls "
+                             "and fused) and exit: the workload of the fused bias-gradient trace")
     args = parser.parse_args()
 
     if args.summarize_trace:
@@ -1218,6 +1222,15 @@ def main() -> int:
     events = HipEvents()
     if args.one_attention:
         print(json.dumps(run_one_attention(gpu, events, args.one_attention)))
+        gpu.close()
+        return 0
+    if args.one_linear:
+        model = MODEL_111M
+        buffers = [LinearBuffers(gpu, model["tokens"], inputs, outputs, 16 * index)
+                   if label.startswith("b0.") or label == "head" else None
+                   for index, (label, inputs, outputs) in enumerate(training_set(model))]
+        gpu.synchronize()
+        print(json.dumps({"linear_bias": measure_linear(gpu, events, buffers)}))
         gpu.close()
         return 0
     if args.one_product:
