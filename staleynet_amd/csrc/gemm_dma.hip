@@ -560,8 +560,9 @@ struct DmaConfig {
 };
 
 // LDS (the stages) caps a CU's workgroups; registers are held to the same
-// number of waves per SIMD (two for every tile here: 256 registers a lane),
-// so that the register file never lowers it further.
+// number of waves per SIMD (dma_waves_per_eu: two for the 128 x 128 tile,
+// 256 registers a lane; three for 128 x 64; four for 64 x 64), so that the
+// register file never lowers it further.
 template <class C, bool A_K, bool B_K>
 __global__ __launch_bounds__(C::T::THREADS)
 __attribute__((amdgpu_waves_per_eu(dma_waves_per_eu<typename C::T, C::STAGES>(),
