@@ -244,11 +244,13 @@ int sn_matmul_bias(sn_context *context, const sn_matmul_spec *spec, const float 
  * sums_len must equal spec->cols (SN_ERR_LENGTH_MISMATCH); sums must not
  * overlap the output or the operands (SN_ERR_ALIASING). fp32 products the
  * direct-to-LDS kernel serves add the column sums while the right operand's
- * tiles pass through LDS (the first tile row of each K slice; the sums
- * are fixed-order, the same on every run, within the fp32 tolerance of the
- * row-order sum), which saves a second read of the right operand; other
- * products run as the two calls. The product's bits are sn_matmul's either
- * way. */
+ * tiles pass through LDS, and bf16 products the 256 x 256 kernel serves while
+ * its fp32 values pass through the registers before rounding (unless the
+ * right operand is the one staged as bf16): the first tile row of each K
+ * slice sums them, in a fixed order, the same on every run, within the fp32
+ * tolerance of the row-order sum. That saves a second read of the right
+ * operand; other products run as the two calls. The product's bits are
+ * sn_matmul's either way. */
 int sn_matmul_column_sums(sn_context *context, const sn_matmul_spec *spec, const float *left, size_t left_len,
                           const float *right, size_t right_len, float *output, size_t output_len, float *sums,
                           size_t sums_len);
@@ -466,6 +468,7 @@ int sn_matmul_noalloc(const sn_matmul_spec *spec, const float *left, size_t left
 #define SN_PATH_BF16_REGISTER 8u   /* bf16: register-staged (unaligned) operands */
 #define SN_PATH_BF16_WIDE 9u       /* bf16: 256x256 tiles rounding fp32 operands as they load */
 #define SN_PATH_F32_DIRECT_SUMS 10u /* SN_PATH_F32_DIRECT adding the right operand's column sums */
+#define SN_PATH_BF16_WIDE_SUMS 11u  /* SN_PATH_BF16_WIDE adding the right operand's column sums */
 
 /* How one product is launched: the role of the reference's launch geometry
  * (`launch::matmul_tiles` / `matmul_blocks`, crates/staleynet-cuda/src/
@@ -499,11 +502,12 @@ typedef struct sn_launch_plan {
  * sufficient; SN_ERR_WORKSPACE when the product would not fit. */
 int sn_plan_matmul(const sn_matmul_spec *spec, uint32_t kernel, const float *left, const float *right,
                    const float *output, uint32_t cu_count, size_t workspace_bytes, sn_launch_plan *plan);
-/* The same for sn_matmul_column_sums: path SN_PATH_F32_DIRECT_SUMS when the
- * column sums are fused into the product (the workspace then holds N more
- * floats per K slice), else the product's plan with the workspace the
- * larger of the product's and sn_accumulate_column_sums'. SN_ERR_UNSUPPORTED
- * for what sn_matmul_column_sums rejects as unsupported. */
+/* The same for sn_matmul_column_sums: path SN_PATH_F32_DIRECT_SUMS or
+ * SN_PATH_BF16_WIDE_SUMS when the column sums are fused into the product (the
+ * workspace then holds N more floats per K slice), else the product's plan
+ * with the workspace the larger of the product's and
+ * sn_accumulate_column_sums'. SN_ERR_UNSUPPORTED for what
+ * sn_matmul_column_sums rejects as unsupported. */
 int sn_plan_matmul_column_sums(const sn_matmul_spec *spec, uint32_t kernel, const float *left, const float *right,
                                const float *output, uint32_t cu_count, size_t workspace_bytes,
                                sn_launch_plan *plan);

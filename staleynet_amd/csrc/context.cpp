@@ -398,7 +398,11 @@ int plan_of(const sn_matmul_spec* spec, uint32_t kernel, const float* left, cons
         // non-null: any aligned stand-in will do.
         p.column_sums = reinterpret_cast<float*>(uintptr_t(1) << 46);
         s = sn::describe_matmul_column_sums(p, k, env);
-        if (sn::f32_column_sums_fused(p, k, env)) s.path = SN_PATH_F32_DIRECT_SUMS;
+        switch (sn::column_sums_fusion(p, k, env)) {
+            case sn::ColumnSumsFusion::F32Direct: s.path = SN_PATH_F32_DIRECT_SUMS; break;
+            case sn::ColumnSumsFusion::Bf16Wide: s.path = SN_PATH_BF16_WIDE_SUMS; break;
+            case sn::ColumnSumsFusion::None: break;
+        }
     } else {
         s = sn::describe_matmul(p, k, env);
     }

@@ -161,7 +161,9 @@ constexpr int loads_per_step() {
     return sizeof(L::reg) / sizeof(f32x4);
 }
 
-template <bool A_K, bool B_K, int SIDE>
+// COLSUM: the first tile row also adds the right operand's column sums over
+// K (row-contiguous fp32, not staged), from the fp32 values as loaded.
+template <bool A_K, bool B_K, int SIDE, bool COLSUM = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_bf16_wide_kernel(Args args) {
     using T = WideTile;
     using LA = OperandLoader<A_K, SIDE == kStageLeft, T::BM, T::BK, T::THREADS>;
@@ -169,6 +171,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     using OA = OctetPlanes<T::BM, T::BK, LA::BF16_PAD>;
     using OB = OctetPlanes<T::BN, T::BK, LB::BF16_PAD>;
     constexpr int kSetLoads = loads_per_step<LA>() + loads_per_step<LB>();
+    if constexpr (COLSUM)
+        static_assert(!B_K && SIDE != kStageRight && LB::PER_THREAD == 1 && LB::GROUPS == 8,
+                      "column sums of a row-contiguous fp32 right operand, one 4-column block per thread");
     __shared__ __attribute__((aligned(16))) uint16_t lds_a[2][8 * OA::SLOTS];
     __shared__ __attribute__((aligned(16))) uint16_t lds_b[2][8 * OB::SLOTS];
 
@@ -219,10 +224,24 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         la[S].load(a, args.lda, m0, args.m, k0, k_end, tid);
         lb[S].load(b, args.ldb, n0, args.n, k0, k_end, tid);
     };
+    // Column sums (COLSUM, first tile row): thread t holds columns 4 (t / 8)
+    // .. + 3 at k = 4 (t % 8) .. + 3 of every step, added here in k order as
+    // each step is staged; the 8 threads of a column block are added at the
+    // end in a fixed butterfly order.
+    const bool colsum_tile = COLSUM && tm == 0;  // uniform over the workgroup
+    float colsum[4] = {0.f, 0.f, 0.f, 0.f};
     // Rounds register set S into LDS stage L.
     auto stage = [&](auto set, auto lds) __attribute__((always_inline)) {
         constexpr int S = decltype(set)::value;
         constexpr int L = decltype(lds)::value;
+        if constexpr (COLSUM) {
+            if (colsum_tile) {
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) colsum[e] = colsum[e] + lb[S].reg[0][kk][e];
+            }
+        }
         la[S].store_bf16(lds_a[L], tid);
         lb[S].store_bf16(lds_b[L], tid);
     };
@@ -290,6 +309,26 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 
     const bool partial = args.splits > 1;
+    if constexpr (COLSUM) {
+        if (colsum_tile) {
+#pragma unroll
+            for (int mask = 1; mask < 8; mask *= 2)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) colsum[e] = colsum[e] + __shfl_xor(colsum[e], mask);
+            if ((tid & 7) == 0) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int64_t c = n0 + 4 * (tid / 8) + e;
+                    if (c < args.n) {
+                        if (partial)
+                            args.ws[int64_t(args.splits) * args.m * args.n + int64_t(split) * args.n + c] = colsum[e];
+                        else
+                            args.column_sums[c] = args.column_sums[c] + colsum[e];
+                    }
+                }
+            }
+        }
+    }
     float* c_batch = args.c + batch * args.stride_c;
     float* out = partial ? args.ws + ((batch_local * int64_t(args.splits) + split) * args.m) * args.n : c_batch;
     write_tile<T, true>(args, acc, out, m0, n0, wave_m, wave_n, lane, partial);
@@ -375,7 +414,7 @@ WideStaging wide_staging(const Problem& p, const Env& env) {
     return st;
 }
 
-template <bool A_K, bool B_K, int SIDE>
+template <bool A_K, bool B_K, int SIDE, bool COLSUM = false>
 hipError_t launch_wide(const Problem& p, const Env& env, const Plan& plan, hipStream_t stream) {
     const LaunchShape shape = tiled_shape<WideTile>(p, plan, SN_PATH_BF16_WIDE);
     if (shape.batches_per_launch < 1) return hipErrorInvalidConfiguration;
@@ -385,7 +424,7 @@ hipError_t launch_wide(const Problem& p, const Env& env, const Plan& plan, hipSt
     for (int64_t first = 0; first < p.batch; first += chunk) {
         const int64_t count = std::min<int64_t>(chunk, p.batch - first);
         args.batch_base = first;
-        hipLaunchKernelGGL((gemm_bf16_wide_kernel<A_K, B_K, SIDE>), dim3(unsigned(count * per_batch)),
+        hipLaunchKernelGGL((gemm_bf16_wide_kernel<A_K, B_K, SIDE, COLSUM>), dim3(unsigned(count * per_batch)),
                            dim3(WideTile::THREADS), 0, stream, args);
         hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
@@ -446,6 +485,62 @@ hipError_t launch_gemm_bf16_wide(const Problem& p, const Env& env, hipStream_t s
     if (p.a_k_contiguous) return launch_wide<true, false, kStageNone>(p, env, plan, stream);
     if (p.b_k_contiguous) return launch_wide<false, true, kStageNone>(p, env, plan, stream);
     return launch_wide<false, false, kStageNone>(p, env, plan, stream);
+}
+
+// ---- The weight-gradient product with Linear's bias gradient -------------
+//
+// dY, the right operand of dW += x^T dY, is row-contiguous fp32; unless it is
+// the operand staged as bf16 (when it has at most half x's columns), every
+// 256 x 32 slab of it passes through the registers as fp32 before rounding,
+// and the first tile row sums its columns there. Each K slice also leaves N
+// partial column sums after the product's partials, so the split count is
+// chosen as if the workspace left after staging were M / (M + 1) of its size.
+
+namespace {
+
+Plan wide_column_sums_plan(const WideStaging& st, const Problem& p) {
+    Env e = st.rest;
+    e.workspace_bytes = st.rest.workspace_bytes / size_t(p.m + 1) * size_t(p.m);
+    return wide_plan(st.q, e);
+}
+
+}  // namespace
+
+bool bf16_wide_column_sums_applies(const Problem& p, const Env& env) {
+    if (p.batch != 1 || p.m < 1 || p.k < 1 || p.b_k_contiguous || p.bias != nullptr || !bf16_wide_applies(p, env))
+        return false;
+    const WideStaging st = wide_staging(p, env);
+    if (st.side == kStageRight) return false;  // dY reaches the kernel as bf16 only
+    const Plan plan = wide_column_sums_plan(st, p);
+    return plan.splits == 1 ||
+           size_t(plan.splits) * (size_t(p.m) * size_t(p.n) + size_t(p.n)) * sizeof(float) <= st.rest.workspace_bytes;
+}
+
+LaunchShape describe_bf16_wide_column_sums(const Problem& p, const Env& env) {
+    const WideStaging st = wide_staging(p, env);
+    const Plan plan = wide_column_sums_plan(st, p);
+    LaunchShape shape = tiled_shape<WideTile>(st.q, plan, SN_PATH_BF16_WIDE);
+    shape.workspace_bytes += st.bytes;
+    if (plan.splits > 1) shape.workspace_bytes += size_t(plan.splits) * size_t(p.n) * sizeof(float);
+    return shape;
+}
+
+hipError_t launch_gemm_bf16_wide_column_sums(const Problem& p, const Env& env, hipStream_t stream) {
+    const WideStaging st = wide_staging(p, env);
+    const Problem& q = st.q;
+    const Plan plan = wide_column_sums_plan(st, p);
+    hipError_t err = hipSuccess;
+    if (st.side == kStageLeft) {
+        err = launch_stage_bf16(p.a, p.a_k_contiguous, p.lda, p.m, p.k, st.kp, st.copies, p.stride_a,
+                                reinterpret_cast<uint16_t*>(env.workspace), stream);
+        if (err == hipSuccess) err = launch_wide<true, false, kStageLeft, true>(q, st.rest, plan, stream);
+    } else {
+        err = p.a_k_contiguous ? launch_wide<true, false, kStageNone, true>(p, env, plan, stream)
+                               : launch_wide<false, false, kStageNone, true>(p, env, plan, stream);
+    }
+    if (err != hipSuccess || plan.splits == 1) return err;
+    return launch_column_sums_finish(st.rest.workspace + int64_t(plan.splits) * p.m * p.n, plan.splits, p.n,
+                                     p.column_sums, stream);
 }
 
 }  // namespace gemm

@@ -731,6 +731,13 @@ hipError_t launch_gemm_bf16_wide(const Problem& p, const Env& env, hipStream_t s
 bool f32_column_sums_applies(const Problem& p, const Env& env);
 LaunchShape describe_f32_column_sums(const Problem& p, const Env& env);
 hipError_t launch_gemm_f32_column_sums(const Problem& p, const Env& env, hipStream_t stream);
+// The bf16 wide product that also adds the right operand's column sums into
+// p.column_sums (gemm_bf16_wide.hip): whether it serves `p` (batch 1, no
+// bias, right operand row-contiguous fp32 and not the one staged), its
+// launch shape and launcher.
+bool bf16_wide_column_sums_applies(const Problem& p, const Env& env);
+LaunchShape describe_bf16_wide_column_sums(const Problem& p, const Env& env);
+hipError_t launch_gemm_bf16_wide_column_sums(const Problem& p, const Env& env, hipStream_t stream);
 // bf16 with both operands first staged as bf16 in the workspace (gemm_dma.hip):
 // whether it serves `p` (unmasked, aligned, staged operands fit), its
 // launch shape (workspace: staged operands and partial sums) and launcher.

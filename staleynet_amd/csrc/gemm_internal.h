@@ -204,10 +204,12 @@ hipError_t launch_column_sums_finish(const float* partial, int64_t slices, int64
 
 // The weight-gradient product with the bias gradient (sn_matmul_column_sums):
 // p.column_sums[c] += the sum over K of the right operand's column c, beside
-// the product. Fused into the fp32 direct-to-LDS kernel where that serves `p`
-// (see f32_column_sums_fused), else the product and then launch_column_sums.
-// The workspace bytes are the larger of the two steps'.
-bool f32_column_sums_fused(const Problem& p, uint32_t kernel, const Env& env);
+// the product. Fused into the fp32 direct-to-LDS kernel or the bf16 wide
+// kernel where that serves `p` (column_sums_fusion), else the product and
+// then launch_column_sums; the workspace bytes are then the larger of the
+// two steps'.
+enum class ColumnSumsFusion { None, F32Direct, Bf16Wide };
+ColumnSumsFusion column_sums_fusion(const Problem& p, uint32_t kernel, const Env& env);
 LaunchShape describe_matmul_column_sums(const Problem& p, uint32_t kernel, const Env& env);
 hipError_t launch_matmul_column_sums(const Problem& p, uint32_t kernel, const Env& env, hipStream_t stream);
 

@@ -48,14 +48,21 @@ hipError_t launch_matmul(const Problem& p, uint32_t kernel, const Env& env, hipS
     return kernel == SN_KERNEL_MFMA_BF16 ? launch_gemm_bf16(p, env, stream) : launch_gemm_f32(p, env, stream);
 }
 
-bool f32_column_sums_fused(const Problem& p, uint32_t kernel, const Env& env) {
-    return kernel == SN_KERNEL_MFMA_F32 && family_of(p, kernel, env) == Family::Tiled &&
-           gemm::f32_column_sums_applies(p, env);
+ColumnSumsFusion column_sums_fusion(const Problem& p, uint32_t kernel, const Env& env) {
+    if (family_of(p, kernel, env) != Family::Tiled) return ColumnSumsFusion::None;
+    if (kernel == SN_KERNEL_MFMA_F32 && gemm::f32_column_sums_applies(p, env)) return ColumnSumsFusion::F32Direct;
+    if (kernel == SN_KERNEL_MFMA_BF16 && gemm::bf16_wide_column_sums_applies(p, env))
+        return ColumnSumsFusion::Bf16Wide;
+    return ColumnSumsFusion::None;
 }
 
 LaunchShape describe_matmul_column_sums(const Problem& p, uint32_t kernel, const Env& env) {
     if (p.n == 0) return LaunchShape{};
-    if (f32_column_sums_fused(p, kernel, env)) return gemm::describe_f32_column_sums(p, env);
+    switch (column_sums_fusion(p, kernel, env)) {
+        case ColumnSumsFusion::F32Direct: return gemm::describe_f32_column_sums(p, env);
+        case ColumnSumsFusion::Bf16Wide: return gemm::describe_bf16_wide_column_sums(p, env);
+        case ColumnSumsFusion::None: break;
+    }
     Problem product = p;
     product.column_sums = nullptr;
     LaunchShape s = describe_matmul(product, kernel, env);
@@ -65,7 +72,11 @@ LaunchShape describe_matmul_column_sums(const Problem& p, uint32_t kernel, const
 
 hipError_t launch_matmul_column_sums(const Problem& p, uint32_t kernel, const Env& env, hipStream_t stream) {
     if (p.n == 0) return hipSuccess;
-    if (f32_column_sums_fused(p, kernel, env)) return gemm::launch_gemm_f32_column_sums(p, env, stream);
+    switch (column_sums_fusion(p, kernel, env)) {
+        case ColumnSumsFusion::F32Direct: return gemm::launch_gemm_f32_column_sums(p, env, stream);
+        case ColumnSumsFusion::Bf16Wide: return gemm::launch_gemm_bf16_wide_column_sums(p, env, stream);
+        case ColumnSumsFusion::None: break;
+    }
     Problem product = p;
     product.column_sums = nullptr;
     hipError_t err = launch_matmul(product, kernel, env, stream);

@@ -217,9 +217,9 @@ class CLaunchPlan(ctypes.Structure):
 # sn_launch_plan.path values (include/staleynet_gemm.h).
 PATH_NONE, PATH_REFERENCE_ORDER, PATH_FEW_ROWS, PATH_FEW_ROWS_NT = 0, 1, 2, 3
 PATH_F32_DIRECT, PATH_F32_REGISTER, PATH_BF16_STAGED, PATH_BF16_DIRECT, PATH_BF16_REGISTER = 4, 5, 6, 7, 8
-PATH_BF16_WIDE, PATH_F32_DIRECT_SUMS = 9, 10
+PATH_BF16_WIDE, PATH_F32_DIRECT_SUMS, PATH_BF16_WIDE_SUMS = 9, 10, 11
 TILED_PATHS = (PATH_F32_DIRECT, PATH_F32_REGISTER, PATH_BF16_STAGED, PATH_BF16_DIRECT, PATH_BF16_REGISTER,
-               PATH_BF16_WIDE, PATH_F32_DIRECT_SUMS)
+               PATH_BF16_WIDE, PATH_F32_DIRECT_SUMS, PATH_BF16_WIDE_SUMS)
 
 
 class CAttentionShape(ctypes.Structure):
@@ -424,7 +424,8 @@ def plan_column_sums(spec: MatmulSpec, kernel: int = 0, cu_count: int = 256, wor
                      left: int = ALIGNED_ADDRESS, right: int = 2 * ALIGNED_ADDRESS,
                      output: int = 3 * ALIGNED_ADDRESS) -> CLaunchPlan:
     """``sn_plan_matmul_column_sums``: the launch ``Gpu.matmul_column_sums`` would make (host only);
-    path ``PATH_F32_DIRECT_SUMS`` when the column sums ride in the product's kernel."""
+    path ``PATH_F32_DIRECT_SUMS`` or ``PATH_BF16_WIDE_SUMS`` when the column sums ride in the product's
+    kernel."""
     c = spec.to_c()
     out = CLaunchPlan()
     rc = _library().sn_plan_matmul_column_sums(ctypes.byref(c), kernel, left, right, output, cu_count,
@@ -618,8 +619,8 @@ class Gpu:
     def matmul_column_sums(self, spec: MatmulSpec, left: Tensor, right: Tensor, output: Tensor, sums: Tensor) -> None:
         """``Linear::backward``'s weight-gradient ``matmul`` then ``accumulate_column_sums`` of the same
         output gradient (linear.rs:54-59) in one call (``sn_matmul_column_sums``): the product as ``matmul``
-        computes it and ``sums[c] += Σ_k right[k, c]``, the sums taken while the right operand's tiles pass
-        through LDS where the fp32 direct-to-LDS kernel serves the product."""
+        computes it and ``sums[c] += Σ_k right[k, c]``, the sums taken inside the product where the fp32
+        direct-to-LDS kernel or the bf16 256 x 256 kernel serves it."""
         c = spec.to_c()
         rc = _library().sn_matmul_column_sums(self._ctx, ctypes.byref(c), ctypes.c_void_p(left.pointer), len(left),
                                               ctypes.c_void_p(right.pointer), len(right),

@@ -124,11 +124,19 @@ def test_weight_gradients_take_the_column_sums_into_the_product():
     tight = gemm.plan_column_sums(spec, workspace_bytes=product.workspace_bytes)
     assert tight.path == gemm.PATH_F32_DIRECT_SUMS and tight.splits < product.splits
     assert tight.workspace_bytes <= product.workspace_bytes
-    # bf16, a right operand whose rows are not 16-byte multiples: the product, then the column sums,
-    # with the larger of the two workspaces.
-    bf16 = spec.with_precision(Precision.Bf16)
-    assert gemm.plan_column_sums(bf16).path == gemm.PATH_BF16_WIDE
-    assert gemm.plan_column_sums(bf16).workspace_bytes == gemm.plan(bf16).workspace_bytes
+    # bf16 on the 256 x 256 kernel: the sums ride in it where dY reaches it as fp32 (x^T staged or
+    # nothing staged), N floats more per slice; the down projection's dY is the operand staged as bf16,
+    # so it runs as the product, then the column sums, with the larger of the two workspaces.
+    for inputs, outputs in ((768, 2304), (768, 768), (768, 3072), (768, 16384)):
+        bf16 = MatmulSpec.new(inputs, outputs, 32768).left_transposed().accumulate().with_precision(Precision.Bf16)
+        product, fused = gemm.plan(bf16), gemm.plan_column_sums(bf16)
+        assert product.path == gemm.PATH_BF16_WIDE and fused.path == gemm.PATH_BF16_WIDE_SUMS
+        assert (fused.splits, fused.tiles_m, fused.tiles_n) == (product.splits, product.tiles_m, product.tiles_n)
+        extra = fused.splits * outputs * 4 if fused.splits > 1 else 0
+        assert fused.workspace_bytes == product.workspace_bytes + extra
+    down = MatmulSpec.new(3072, 768, 32768).left_transposed().accumulate().with_precision(Precision.Bf16)
+    assert gemm.plan_column_sums(down).path == gemm.PATH_BF16_WIDE
+    assert gemm.plan_column_sums(down).workspace_bytes == gemm.plan(down).workspace_bytes
     odd = MatmulSpec.new(96, 50, 300).left_transposed()
     assert gemm.plan_column_sums(odd).path == gemm.PATH_F32_REGISTER
     # The unsupported forms are rejected by the planner as by the call.
@@ -321,10 +329,10 @@ def test_random_column_sum_plans_keep_the_product_plan(inputs, outputs, rows, cu
         assert err.status == gemm.SN_ERR_WORKSPACE
         return
     assert fused.workspace_bytes <= workspace
-    if fused.path == gemm.PATH_F32_DIRECT_SUMS:
-        assert not bf16 and outputs % 4 == 0 and inputs % 4 == 0
+    if fused.path in (gemm.PATH_F32_DIRECT_SUMS, gemm.PATH_BF16_WIDE_SUMS):
+        assert bf16 == (fused.path == gemm.PATH_BF16_WIDE_SUMS) and outputs % 4 == 0 and inputs % 4 == 0
         if fused.splits > 1:
-            assert fused.workspace_bytes == fused.splits * (inputs * outputs + outputs) * 4
+            assert fused.workspace_bytes >= fused.splits * (inputs * outputs + outputs) * 4
         if fused.workgroups <= 1 << 16:
             check_tiled_cover(fused)
     elif product is not None:

@@ -11,8 +11,10 @@ right operand's tiles sit in LDS.
 * Random inputs: the sums within the reference's fp32 tolerance (1e-5,
   kernels_match_reference.rs:12) of the oracle's, no further from an f64 sum than the oracle is
   (plus 1e-6 of the largest sum), and the same bits on every run.
-* Products the fused kernel does not serve (bf16, right operand columns not a multiple of 4) run as
-  the two calls and must give their bits.
+* bf16 products on the 256 x 256 kernel take the sums from dY's fp32 values before rounding: exact on
+  integers, the product bit-identical to sn_matmul's, the sums within the fp32 tolerance on random data.
+* Products no fused kernel serves (small bf16 products, bf16 with dY the staged operand, right operand
+  columns not a multiple of 4) run as the two calls and must give their bits.
 Each fused case first checks, through the host-only planner, that the fused path is the one taken.
 """
 import numpy as np
@@ -151,19 +153,70 @@ def test_weight_gradient_at_config_2_scale(gpu):
     assert error < TOLERANCE
 
 
-@pytest.mark.parametrize("case", ["bf16", "columns_not_multiple_of_4", "empty_rows"])
+# bf16 on the 256 x 256 kernel: dY's fp32 values are summed in the registers before they are rounded.
+# Integers of magnitude <= 2 (exact in bf16; every product sum and column sum stays below 2^24) make the
+# product exact in any order: it is compared in full with the exact integer product (float64
+# arithmetic), and the sums with the oracle's row-order sums, bit for bit.
+@pytest.mark.parametrize("inputs,outputs,rows", [
+    (768, 2304, 32768),   # the qkv weight gradient: x^T staged as bf16, 9 K slices
+    (768, 768, 32768),    # the out projection's: nothing staged, 28 slices
+    (772, 2312, 20010),   # ragged tiles both ways, a K tail
+])
+def test_bf16_fused_sums_are_exact_on_integers(gpu, inputs, outputs, rows):
+    print(f"bf16 column sums {inputs}x{outputs}x{rows}", flush=True)
+    rng = np.random.default_rng(inputs + outputs + rows)
+    left = rng.integers(-2, 3, size=inputs * rows).astype(np.float32)
+    right = rng.integers(-2, 3, size=rows * outputs).astype(np.float32)
+    initial = rng.integers(-8, 9, size=inputs * outputs).astype(np.float32)
+    sums0 = rng.integers(-8, 9, size=outputs).astype(np.float32)
+    spec = weight_grad_spec(inputs, outputs, rows)
+    assert gemm.plan_column_sums(spec, int(MatmulKernel.MfmaBf16)).path == gemm.PATH_BF16_WIDE_SUMS
+    out, sums = fused(gpu, spec, left, right, initial, sums0, MatmulKernel.MfmaBf16)
+    x = left.reshape(rows, inputs).astype(np.float64)
+    dy = right.reshape(rows, outputs).astype(np.float64)
+    want_out = (initial.astype(np.float64) + (x.T @ dy).ravel()).astype(np.float32)
+    want_sums = sums0.copy()
+    oracle.accumulate_column_sums(right, outputs, want_sums)
+    assert np.array_equal(sums, want_sums)
+    assert np.array_equal(out, want_out)
+
+
+def test_bf16_fused_product_is_sn_matmul_and_sums_within_tolerance(gpu):
+    inputs, outputs, rows = 768, 2304, 32768
+    left = oracle.random_values(inputs * rows, 71)
+    right = oracle.random_values(rows * outputs, 72)
+    initial = oracle.random_values(inputs * outputs, 73)
+    sums0 = oracle.random_values(outputs, 74)
+    spec = weight_grad_spec(inputs, outputs, rows)
+    assert gemm.plan_column_sums(spec, int(MatmulKernel.MfmaBf16)).path == gemm.PATH_BF16_WIDE_SUMS
+    out, sums = fused(gpu, spec, left, right, initial, sums0, MatmulKernel.MfmaBf16)
+    out2, sums2 = fused(gpu, spec, left, right, initial, sums0, MatmulKernel.MfmaBf16)
+    sep_out, _ = separate(gpu, spec, left, right, initial, sums0, MatmulKernel.MfmaBf16)
+    assert np.array_equal(out, sep_out), "the product's bits differ from sn_matmul's"
+    assert np.array_equal(out, out2) and np.array_equal(sums, sums2), "results differ between two runs"
+    expected = sums0.copy()
+    oracle.accumulate_column_sums(right, outputs, expected)
+    assert oracle.relative_error(expected, sums) < TOLERANCE
+    truth = oracle.column_sums_f64(right, outputs, sums0)
+    assert np.max(np.abs(sums - truth)) <= np.max(np.abs(expected - truth)) + 1e-6 * np.max(np.abs(truth))
+
+
+@pytest.mark.parametrize("case", ["bf16", "bf16_dy_staged", "columns_not_multiple_of_4", "empty_rows"])
 def test_unfused_products_run_as_the_two_calls(gpu, case):
     inputs, outputs, rows = 96, 80, 300
     kernel = MatmulKernel.MfmaF32
     if case == "bf16":
         inputs, outputs, rows = 256, 512, 256
         kernel = MatmulKernel.MfmaBf16
+    elif case == "bf16_dy_staged":  # the down projection's shape: dY is the operand rounded into the workspace
+        inputs, outputs, rows = 3072, 768, 4096
+        kernel = MatmulKernel.MfmaBf16
     elif case == "columns_not_multiple_of_4":
         outputs = 50
     else:
         inputs = 0
     spec = weight_grad_spec(inputs, outputs, rows)
-    assert gemm.plan_column_sums(spec, int(kernel)).path != gemm.PATH_F32_DIRECT_SUMS
+    assert gemm.plan_column_sums(spec, int(kernel)).path not in (gemm.PATH_F32_DIRECT_SUMS, gemm.PATH_BF16_WIDE_SUMS)
     left = oracle.random_values(max(inputs * rows, 1), 51)
     right = oracle.random_values(rows * outputs, 52)
     initial = oracle.random_values(max(inputs * outputs, 1), 53)
