@@ -31,6 +31,9 @@ The printed JSON line is the driver's contract plus:
 - ``published``: the reference's own published products (the only GEMM numbers it publishes, on
   Jetsons) with its timing method, fp32 and bf16; configs 0 and 1 as whole training sets; config 2's
   two weakest products.
+
+``--vendor`` prints, instead, the same set through torch.mm (hipBLASLt / rocBLAS) beside this build's,
+one decode token through torch.mm, and the shader clock under each set's load.
 """
 from __future__ import annotations
 
@@ -772,6 +775,144 @@ def measure_published(gpu: Gpu, events: HipEvents, set_per_shape: dict):
     return result
 
 
+# ---- the vendor library on the same set, and the clock under load (context) -------------
+
+def _sclk_mhz():
+    """The shader clock rocm-smi reports now, or None where the tool is absent."""
+    try:
+        text = subprocess.run(["rocm-smi", "--showclocks"], capture_output=True, text=True, timeout=10).stdout
+    except (OSError, subprocess.SubprocessError):
+        return None
+    for line in text.splitlines():
+        if "sclk" in line and "Mhz" in line:
+            return int(line.rsplit("(", 1)[1].split("Mhz")[0])
+    return None
+
+
+def clocks_under_load(gpu: Gpu, calls, precision, seconds: float = 4.0):
+    """Steps of the set run back to back for `seconds` while the shader clock is sampled."""
+    import threading
+    samples, stop = [], threading.Event()
+
+    def sample():
+        while not stop.is_set():
+            mhz = _sclk_mhz()
+            if mhz is not None:
+                samples.append(mhz)
+            time.sleep(0.3)
+
+    run_step(gpu, calls, precision)
+    gpu.synchronize()
+    thread = threading.Thread(target=sample)
+    thread.start()
+    start, steps = time.time(), 0
+    while time.time() - start < seconds:
+        run_step(gpu, calls, precision)
+        gpu.synchronize()
+        steps += 1
+    stop.set()
+    thread.join()
+    steady = samples[2:] or samples
+    return {"steps": steps, "sclk_mhz_median": int(np.median(steady)) if steady else None,
+            "samples": len(samples)}
+
+
+def measure_vendor(gpu: Gpu, events: HipEvents, calls, repeats: int = 5):
+    """Config 2's set through torch.mm (hipBLASLt / rocBLAS) on the same shapes and layouts: fp32
+    (TF32 off); bf16 with the fp32 operands rounded inside the timed call, as this build's bf16
+    contract does; and bf16 with the operands already bf16 in HBM (half the bytes, bf16 output).
+    Each of the 15 distinct products is timed on torch's stream and weighted by its count in the
+    set. Beside it, this build's own set in the same process, and the shader clock during each."""
+    import torch
+    torch.backends.cuda.matmul.allow_tf32 = False
+    dev = torch.device("cuda", 0)
+
+    def ms_of(fn):
+        fn()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(repeats):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / repeats
+
+    counts = {}
+    for label, _, _, _ in calls[::3]:
+        name = label.split(".")[-1]
+        counts[name] = counts.get(name, 0) + 1
+    d, f, heads, m = MODEL_111M["width"], MODEL_111M["ffn"], MODEL_111M["heads_width"], MODEL_111M["tokens"]
+    layers = {"qkv": (d, 3 * d), "out": (d, d), "up": (d, f), "down": (f, d), "head": (d, heads)}
+    per_shape, totals, set_flops = {}, {"f32": 0.0, "bf16_from_f32": 0.0, "bf16_inputs": 0.0}, 0.0
+    gen = torch.Generator(device=dev).manual_seed(SEED)
+    for name, (i, o) in layers.items():
+        x = torch.randn(m, i, device=dev, generator=gen)
+        w = torch.randn(i, o, device=dev, generator=gen) * 0.02
+        dy = torch.randn(m, o, device=dev, generator=gen)
+        y, dx, dw = torch.empty(m, o, device=dev), torch.empty(m, i, device=dev), torch.zeros(i, o, device=dev)
+        xb, wb, dyb, dwb = x.bfloat16(), w.bfloat16(), dy.bfloat16(), dw.bfloat16()
+        # Two-dimensional products only (no batched bf16 calls).
+        variants = {
+            "NN": (lambda: torch.mm(x, w, out=y), lambda: torch.mm(x.bfloat16(), w.bfloat16()).float(),
+                   lambda: torch.mm(xb, wb), (m, o, i)),
+            "TN": (lambda: dw.addmm_(x.t(), dy), lambda: dw.add_(torch.mm(x.bfloat16().t(), dy.bfloat16()).float()),
+                   lambda: dwb.addmm_(xb.t(), dyb), (i, o, m)),
+            "NT": (lambda: torch.mm(dy, w.t(), out=dx), lambda: torch.mm(dy.bfloat16(), w.bfloat16().t()).float(),
+                   lambda: torch.mm(dyb, wb.t()), (m, i, o)),
+        }
+        flops = 2.0 * m * i * o
+        for layout, (f32, from_f32, inputs, (r, c, k)) in variants.items():
+            t = {"f32": ms_of(f32), "bf16_from_f32": ms_of(from_f32), "bf16_inputs": ms_of(inputs)}
+            per_shape[f"{layout} {r}x{c}x{k}"] = {key: round(flops / (v * 1e-3) / 1e12, 1) for key, v in t.items()}
+            for key, v in t.items():
+                totals[key] += v * counts[name]
+            set_flops += flops * counts[name]
+        del x, w, dy, y, dx, dw, xb, wb, dyb, dwb
+        torch.cuda.empty_cache()
+
+    # One decode token (M = 1, 49 distinct weights, 390 MB > the Infinity Cache) through torch.mm,
+    # captured in one graph as this build's token is, checked against the same calls run eagerly.
+    layers = [(k, n) for _ in range(12) for _, k, n in DECODE_SHAPES[:4]] + [DECODE_SHAPES[4][1:]]
+    token = [(torch.randn(1, k, device=dev, generator=gen), torch.randn(k, n, device=dev, generator=gen) * 0.02,
+              torch.empty(1, n, device=dev)) for k, n in layers]
+    for x, w, y in token:
+        torch.mm(x, w, out=y)
+    eager = [y.clone() for _, _, y in token]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for x, w, y in token:
+            torch.mm(x, w, out=y)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for x, w, y in token:
+            torch.mm(x, w, out=y)
+    token_ms = ms_of(graph.replay)
+    replay_matches = all(torch.equal(e, y) for e, (_, _, y) in zip(eager, token))
+    token_bytes = sum(decode_bytes(1, k, n) for k, n in layers)
+    del graph, token, eager
+    torch.cuda.empty_cache()
+
+    own_ms, _ = measure_set(gpu, events, calls, 3, 1)
+    own_bf16_ms, _ = measure_set(gpu, events, calls, 3, 1, Precision.Bf16)
+    return {
+        "decode_token": {"us_per_token": round(token_ms * 1e3, 1), "gbs": round(token_bytes / (token_ms * 1e-3) / 1e9, 1),
+                         "replay_matches_eager": replay_matches,
+                         "method": "49 torch.mm (M = 1) captured in one graph, mean of replays"},
+        "library": f"torch {torch.__version__} (HIP {torch.version.hip}) torch.mm / addmm_",
+        "method": f"mean of {repeats} calls after 1 warm-up per product, weighted by the product's count in the set",
+        "set_tflops": {key: round(set_flops / (v * 1e-3) / 1e12, 1) for key, v in totals.items()},
+        "this_build_set_tflops": {"f32": round(set_flops / (own_ms * 1e-3) / 1e12, 1),
+                                  "bf16": round(set_flops / (own_bf16_ms * 1e-3) / 1e12, 1)},
+        "per_shape_tflops": per_shape,
+        "clocks": {"f32_set": clocks_under_load(gpu, calls, Precision.Default),
+                   "bf16_set": clocks_under_load(gpu, calls, Precision.Bf16),
+                   "idle_sclk_mhz": _sclk_mhz()},
+    }
+
+
 # ---- Linear's bias kernels (the steps either side of the NN and TN products) -----------
 
 def measure_linear(gpu: Gpu, events: HipEvents, buffers, repeats: int = 5):
@@ -1197,6 +1338,9 @@ def main() -> int:
     parser.add_argument("--one-product", nargs=2, metavar=("LAYOUT", "PRECISION"),
                         help="run only config 2's qkv product (NN, TN or NT; f32 or bf16) 1 + 5 times and exit: "
                              "the workload of the per-kernel counter profiles")
+    parser.add_argument("--vendor", action="store_true",
+                        help="run only the vendor-library comparison on config 2's set (torch.mm fp32 and bf16 "
+                             "beside this build's set, and the shader clock under each set's load) and exit")
     parser.add_argument("--one-linear", action="store_true",
                         help="run only config 2's Linear bias measurements (block 0's four layers and the head: "
                              "forward with and without the fused bias, weight and bias gradients as two calls "
@@ -1232,6 +1376,11 @@ def main() -> int:
     events = HipEvents()
     if args.one_attention:
         print(json.dumps(run_one_attention(gpu, events, args.one_attention)))
+        gpu.close()
+        return 0
+    if args.vendor:
+        calls, _buffers = build_set(gpu)
+        print(json.dumps({"vendor": measure_vendor(gpu, events, calls)}))
         gpu.close()
         return 0
     if args.one_linear:
