@@ -369,6 +369,7 @@ def _library() -> ctypes.CDLL:
         lib.sn_causal_attention_backward.argtypes = [ctx, ctypes.POINTER(CAttentionShape)] + [ctypes.c_void_p, size] * 9
         lib.sn_plan_matmul.argtypes = [ctypes.POINTER(CMatmulSpec), ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p,
                                        ctypes.c_void_p, ctypes.c_uint32, size, ctypes.POINTER(CLaunchPlan)]
+        lib.sn_plan_matmul_column_sums.argtypes = lib.sn_plan_matmul.argtypes
         lib.sn_matmul_noalloc.argtypes = [ctypes.POINTER(CMatmulSpec), ctypes.c_void_p, size, ctypes.c_void_p, size,
                                           ctypes.c_void_p, size, ctypes.c_void_p]
         u32p = ctypes.POINTER(ctypes.c_uint32)

@@ -36,6 +36,17 @@ def test_library_exports_every_declared_entry_point():
         assert hasattr(lib, name), f"{name} is declared in include/ but not exported"
 
 
+def test_every_bound_entry_point_declares_its_argument_types():
+    # Without argtypes ctypes passes a Python int as a 32-bit C int: a size_t or pointer parameter
+    # then holds whatever the register's upper half held (the planner once read a negative
+    # workspace size that way and declined to split K).
+    lib = gemm.library()
+    bound = sorted(set(re.findall(r'"(sn_[a-z0-9_]+)"', open(gemm.__file__).read())) & set(declared_functions()))
+    assert "sn_plan_matmul_column_sums" in bound and len(bound) >= 20
+    for name in bound:
+        assert getattr(lib, name).argtypes is not None, f"{name} has no argtypes"
+
+
 def test_spec_new_matches_the_reference_defaults():
     # MatmulSpec::new (ops/matmul.rs:86-97; test :178-188).
     spec = gemm.library().sn_matmul_spec_new(2, 3, 4)
