@@ -30,7 +30,8 @@ The printed JSON line is the driver's contract plus:
 - ``head_cross_entropy``: the head's 16 per-codebook cross-entropy calls at config 2;
 - ``published``: the reference's own published products (the only GEMM numbers it publishes, on
   Jetsons) with its timing method, fp32 and bf16; configs 0 and 1 as whole training sets; config 2's
-  two weakest products.
+  two weakest products;
+- ``shard_of_8``: config 2's set at one GPU's share when its tokens are split over 8 GPUs (M = 4096).
 
 ``--vendor`` prints, instead, the same set through torch.mm (hipBLASLt / rocBLAS) beside this build's,
 one decode token through torch.mm, and the shader clock under each set's load.
@@ -763,16 +764,36 @@ def measure_published(gpu: Gpu, events: HipEvents, set_per_shape: dict):
         calls, buffers = build_set(gpu, model)
         flops = sum(spec.flops() for _, _, spec, _ in calls)
         ms, per_call = measure_set(gpu, events, calls, 3, 1)
-        _, per_layout, _ = summarize_set(calls, per_call, PEAK_FP32_TFLOPS)
+        _, per_layout, per_shape = summarize_set(calls, per_call, PEAK_FP32_TFLOPS)
         result[key] = {"tflops": round(flops / (ms * 1e-3) / 1e12, 2), "ms_per_step": round(ms, 3),
                        "frac_fp32_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 4),
-                       "gemms": len(calls), "tflop": round(flops / 1e12, 4), "per_layout": per_layout}
+                       "gemms": len(calls), "tflop": round(flops / 1e12, 4), "per_layout": per_layout,
+                       "per_shape_tflops": per_shape}
         for buf in buffers:
             for t in (buf.x, buf.w, buf.dy, buf.y, buf.dx, buf.dw):
                 t.free()
     result["config2_weakest"] = {k: {"tflops": v, "frac_fp32_peak": round(v / PEAK_FP32_TFLOPS, 4)}
                                  for k, v in sorted(set_per_shape.items(), key=lambda kv: kv[1])[:2]}
     return result
+
+
+# ---- one GPU's share of config 2 sharded over 8 GPUs -----------------------------------
+
+def measure_shard_share(gpu: Gpu, events: HipEvents, shards: int = 8):
+    """Config 2's set at the shape one GPU runs when the tokens are split over `shards` GPUs (the
+    Linear products shard along M with no exchange; the weight gradients then sum over the shards,
+    which this one-GPU run does not do): M = 32768 / shards, weight-gradient K the same."""
+    model = dict(MODEL_111M, name=f"111.5M / {shards}", tokens=MODEL_111M["tokens"] // shards)
+    calls, buffers = build_set(gpu, model)
+    flops = sum(spec.flops() for _, _, spec, _ in calls)
+    ms, per_call = measure_set(gpu, events, calls, 3, 1)
+    _, per_layout, per_shape = summarize_set(calls, per_call, PEAK_FP32_TFLOPS)
+    for buf in buffers:
+        for t in (buf.x, buf.w, buf.dy, buf.y, buf.dx, buf.dw):
+            t.free()
+    return {"shards": shards, "per_shape_tflops": per_shape, "tokens": model["tokens"], "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+            "frac_fp32_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 4),
+            "ms_per_step": round(ms, 3), "per_layout": per_layout}
 
 
 # ---- the vendor library on the same set, and the clock under load (context) -------------
@@ -1484,6 +1505,7 @@ def main() -> int:
         result["attention"] = measure_attention(gpu, events)
         result["decode"] = measure_decode(gpu, events)
         result["published"] = measure_published(gpu, events, per_shape)
+        result["shard_of_8"] = measure_shard_share(gpu, events)
 
     if not args.no_cpu:
         projected_s, sampled_flops, sampled_s, samples = cpu_baseline(gpu, calls, args.cpu_budget)

@@ -691,12 +691,26 @@ bool config_applies(const Problem& p) {
 // gradient).
 using DmaSmall = DmaConfig<Tile<64, 64, 32, 2, 2>, 2>;
 
+// Products whose 128x128 plan leaves CU slots empty (under two workgroups
+// per CU) with under 24 K-steps per workgroup take 64x64 tiles as well: the
+// 128x128 plan there splits an already short K (or runs one workgroup per
+// CU), and each workgroup's start-up and epilogue weigh on a few K-steps;
+// four 64x64 workgroups per CU fill the device without splitting. Measured
+// (fp32, one GPU's share of config 2 over 8 GPUs, M = 4096): NN and NT
+// 4096 x 768 x 768 74-76 -> 104-107 TFLOP/s, TN 768 x 768 x 4096 83 -> 89;
+// the 42.9M model's NN and NT 8192 x 512 x 512 99-103 -> 102-105. Longer
+// slices keep 128x128 (the 111.5M model's 768 x 768 x 32768 weight
+// gradient, 74 K-steps a workgroup: 127 TFLOP/s against 119 on 64x64).
+constexpr int64_t kSmallTileMaxK = 768;
+
 template <class F>
 auto with_f32_dma_config(const Problem& p, const Env& env, F&& f) {
     if (p.n <= 64) return f(DmaNarrow{});
     const Plan square = dma_plan<DmaSquare, kFeedF32>(p, env);
     const int64_t workgroups = int64_t(square.tiles_m) * square.tiles_n * square.splits * p.batch;
-    return workgroups < std::max(env.cu_count, 1) ? f(DmaSmall{}) : f(DmaSquare{});
+    const int64_t cus = std::max(env.cu_count, 1);
+    const bool short_slices = workgroups < 2 * cus && square.k_per_split < kSmallTileMaxK;
+    return workgroups < cus || short_slices ? f(DmaSmall{}) : f(DmaSquare{});
 }
 
 // Small bf16 products (fewer 128 x 128 tiles than CUs: the 7.1M model's) skip

@@ -180,8 +180,16 @@ def test_configs_take_the_expected_kernel_families():
     # fp32: 64 x 64 tiles when the 128 x 128 plan has fewer workgroups than CUs.
     f32_small = gemm.plan(MatmulSpec.new(2048, 768, 256))
     assert f32_small.path == gemm.PATH_F32_DIRECT and (f32_small.tile_rows, f32_small.tile_cols) == (64, 64)
-    assert (gemm.plan(MatmulSpec.new(2048, 768, 256), cu_count=64).tile_rows,
+    assert (gemm.plan(MatmulSpec.new(2048, 768, 256), cu_count=32).tile_rows,
             gemm.plan(MatmulSpec.new(2048, 4096, 256)).tile_rows) == (128, 128)
+    # ... and when it has fewer than two per CU with under 24 K-steps each (one GPU's share of config 2
+    # over 8 GPUs; the 42.9M model's 512-wide products), but not on longer slices.
+    for spec in (MatmulSpec.new(4096, 768, 768), MatmulSpec.new(4096, 768, 768).right_transposed(),
+                 MatmulSpec.new(768, 768, 4096).left_transposed().accumulate(), MatmulSpec.new(8192, 512, 512)):
+        assert gemm.plan(spec).tile_rows == 64, spec
+    for spec in (MatmulSpec.new(768, 768, 32768).left_transposed().accumulate(),
+                 MatmulSpec.new(512, 1536, 8192).left_transposed().accumulate(), MatmulSpec.new(32768, 768, 768)):
+        assert gemm.plan(spec).tile_rows == 128, spec
     # Too narrow for a quarter tile: the staged kernels keep it.
     assert gemm.plan(MatmulSpec.new(32768, 64, 768).right_transposed().with_precision(Precision.Bf16)).path != \
         gemm.PATH_BF16_WIDE
