@@ -1,4 +1,5 @@
-"""A seeded random sweep of products across the planner's choices, against the exact product.
+"""Seeded random sweeps of products across the planner's choices, against the exact product; then the
+fused Linear entry points (product + bias, weight gradient + bias gradient) the same way.
 
 Each case draws a layout (NN / NT / TN / TT), sizes from 1 to a few thousand (so that aligned, ragged,
 unaligned, few-row, split-K, small-tile, 256 x 256 bf16 and staged bf16 plans all come up), a batch of 1 to 3
@@ -95,3 +96,75 @@ def test_random_products_are_exact_across_the_planners_choices(gpu):
     wanted = {gemm.PATH_F32_DIRECT, gemm.PATH_F32_REGISTER, gemm.PATH_FEW_ROWS, gemm.PATH_BF16_WIDE,
               gemm.PATH_BF16_DIRECT, gemm.PATH_BF16_REGISTER, gemm.PATH_BF16_STAGED}
     assert wanted <= paths, f"the sweep reached {sorted(paths)}"
+
+
+def upload_case(gpu, rng, spec):
+    left_len = (spec.batch.count - 1) * spec.batch.left + spec.rows * spec.inner
+    right_len = (spec.batch.count - 1) * spec.batch.right + spec.inner * spec.cols
+    out_len = spec.batch.count * spec.rows * spec.cols
+    left = rng.integers(-4, 5, size=left_len).astype(np.float32)
+    right = rng.integers(-4, 5, size=right_len).astype(np.float32)
+    initial = rng.integers(-8, 9, size=out_len).astype(np.float32)
+    tensors = (gpu.upload(Shape.vector(left_len), left), gpu.upload(Shape.vector(right_len), right),
+               gpu.upload(Shape.vector(out_len), initial))
+    return (left, right, initial), tensors
+
+
+def test_random_products_with_the_fused_bias_are_exact(gpu):
+    # sn_matmul_bias: Linear::forward's matmul then add_row_bias (linear.rs:46-47), the bias added to
+    # every output matrix of the batch after the combine, as its own rounded add.
+    rng = np.random.default_rng(7)
+    for case in range(48):
+        layout, spec = draw(rng)
+        print(f"bias case {case}: {layout} {spec.rows}x{spec.cols}x{spec.inner} batch {spec.batch.count} "
+              f"accumulate {bool(spec.write)} precision {int(spec.precision)}", flush=True)
+        (left, right, initial), (lt, rt, ot) = upload_case(gpu, rng, spec)
+        bias = rng.integers(-8, 9, size=spec.cols).astype(np.float32)
+        bt = gpu.upload(Shape.vector(spec.cols), bias)
+        gpu.matmul_bias(spec, lt, rt, bt, ot)
+        got = gpu.download(ot)
+        for t in (lt, rt, ot, bt):
+            t.free()
+        want = exact(spec, left, right, initial) + np.tile(bias, spec.batch.count * spec.rows)
+        bad = np.flatnonzero(got != want)
+        assert bad.size == 0, f"case {case}: {bad.size} outputs differ"
+
+
+def test_random_weight_gradients_with_fused_column_sums_are_exact(gpu):
+    # sn_matmul_column_sums: Linear::backward's weight gradient dW (+)= X^T dY and the bias gradient
+    # accumulate_column_sums(dY) (linear.rs:54-59), over weight shapes from tiny to config 2's and
+    # token counts up to 4096 (left stored as X, or already transposed).
+    rng = np.random.default_rng(11)
+    paths = set()
+    for case in range(48):
+        def size(hi):
+            return int(np.exp(rng.uniform(0.0, np.log(hi))))
+
+        big = rng.random() < 0.3
+        inputs = int(rng.integers(512, 3073)) if big else 1 + size(1024)
+        outputs = int(rng.integers(512, 3073)) if big else 1 + size(1024)
+        tokens = int(rng.integers(2048, 4097)) if big else 1 + size(4096)
+        if big or rng.random() < 0.5:
+            inputs, outputs, tokens = (4 * ((v + 3) // 4) for v in (inputs, outputs, tokens))
+        spec = MatmulSpec.new(inputs, outputs, tokens)
+        if rng.random() < 0.8:
+            spec = spec.left_transposed()
+        spec = spec.scaled(float(rng.choice([1.0, 0.5]))).accumulate()
+        if rng.random() < 0.4:
+            spec = spec.with_precision(Precision.Bf16)
+        kernel = MatmulKernel.MfmaBf16 if spec.precision == Precision.Bf16 else MatmulKernel.MfmaF32
+        plan = gemm.plan_column_sums(spec, int(kernel))
+        paths.add(plan.path)
+        print(f"column sums case {case}: {inputs}x{outputs}x{tokens} left transposed {bool(spec.left)} "
+              f"precision {int(spec.precision)} path {plan.path} splits {plan.splits}", flush=True)
+        (left, right, initial), (lt, rt, ot) = upload_case(gpu, rng, spec)
+        sums0 = rng.integers(-8, 9, size=outputs).astype(np.float32)
+        st = gpu.upload(Shape.vector(outputs), sums0)
+        gpu.matmul_column_sums(spec, lt, rt, ot, st)
+        got, sums = gpu.download(ot), gpu.download(st)
+        for t in (lt, rt, ot, st):
+            t.free()
+        assert np.array_equal(got, exact(spec, left, right, initial)), f"case {case}: product"
+        want_sums = (sums0.astype(np.float64) + right.astype(np.float64).reshape(tokens, outputs).sum(axis=0))
+        assert np.array_equal(sums, want_sums.astype(np.float32)), f"case {case}: column sums"
+    assert {gemm.PATH_F32_DIRECT_SUMS, gemm.PATH_BF16_WIDE_SUMS} <= paths, f"the sweep reached {sorted(paths)}"
