@@ -100,6 +100,23 @@ def test_backward_without_probabilities_matches_the_reference_calls(gpu, heads, 
     assert not np.any(got["dv"].reshape(heads, keys, h)[:, seen:])
 
 
+def test_random_shapes_match_the_reference_calls(gpu):
+    # A seeded sweep: 1-3 heads, 1-300 queries, 1-600 keys, head dims 32 / 64 / 128, offsets 0-300.
+    rng = np.random.default_rng(23)
+    for case in range(16):
+        heads, queries, keys = int(rng.integers(1, 4)), int(rng.integers(1, 301)), int(rng.integers(1, 601))
+        h = int(rng.choice([32, 64, 128]))
+        offset, scale = int(rng.integers(0, 301)), float(rng.choice([0.125, 0.17, 0.09]))
+        print(f"backward case {case}: {heads} heads, {queries} queries, {keys} keys, h {h}, offset {offset}",
+              flush=True)
+        inputs, got = run(gpu, heads, queries, keys, h, scale, offset, seed=100 + case)
+        out, _, dq, dk, dv = reference(*inputs, heads, queries, keys, h, scale, offset)
+        for name, expected in (("out", out), ("dq", dq), ("dk", dk), ("dv", dv)):
+            assert np.all(np.isfinite(got[name])), (case, name)
+            error = oracle.relative_error(expected, got[name])
+            assert error < TOLERANCE, f"case {case} {name}: relative error {error}"
+
+
 def test_forward_with_stats_gives_the_same_output(gpu):
     # The statistics are an extra output of the same kernel: O is bit for bit sn_causal_attention's.
     heads, t, h = 2, 300, 64

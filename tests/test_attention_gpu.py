@@ -75,6 +75,23 @@ def test_fused_attention_matches_the_three_calls(gpu, heads, queries, keys, h, o
         assert not np.any(p[:, r, visible:])
 
 
+def test_random_shapes_match_the_three_calls(gpu):
+    # A seeded sweep: 1-4 heads, 1-300 queries, 1-600 keys (fewer, as many, or more than the queries'
+    # horizon reaches), head dims 32 / 64 / 128, query offsets 0-300, with and without probabilities.
+    rng = np.random.default_rng(17)
+    for case in range(24):
+        heads, queries, keys = int(rng.integers(1, 5)), int(rng.integers(1, 301)), int(rng.integers(1, 601))
+        h = int(rng.choice([32, 64, 128]))
+        offset, scale = int(rng.integers(0, 301)), float(rng.choice([0.125, 0.17, 0.09]))
+        with_p = bool(rng.random() < 0.5)
+        print(f"attention case {case}: {heads} heads, {queries} queries, {keys} keys, h {h}, offset {offset}, "
+              f"probabilities {with_p}", flush=True)
+        eo, go, ep, gp = run(gpu, heads, queries, keys, h, scale, offset, seed=case, with_p=with_p)
+        assert np.all(np.isfinite(go)) and oracle.relative_error(eo, go) < TOLERANCE, f"case {case}"
+        if with_p:
+            assert oracle.relative_error(ep, gp) < TOLERANCE, f"case {case}"
+
+
 def test_large_logits(gpu):
     # Q and K ~ N(0, 9): scaled scores with a spread of about 9 and row maxima near 30, so the
     # differences from the maximum reach -60 or so. The exponential of a rounded difference d is
