@@ -245,12 +245,13 @@ int sn_matmul_bias(sn_context *context, const sn_matmul_spec *spec, const float 
  * overlap the output or the operands (SN_ERR_ALIASING). fp32 products the
  * direct-to-LDS kernel serves add the column sums while the right operand's
  * tiles pass through LDS, and bf16 products the 256 x 256 kernel serves while
- * its fp32 values pass through the registers before rounding (unless the
- * right operand is the one staged as bf16): the first tile row of each K
- * slice sums them, in a fixed order, the same on every run, within the fp32
- * tolerance of the row-order sum. That saves a second read of the right
- * operand; other products run as the two calls. The product's bits are
- * sn_matmul's either way. */
+ * its fp32 values pass through the registers before rounding: the first tile
+ * row of each K slice sums them (or, where the right operand is the one
+ * staged as bf16, the staging pass sums each 64 k as it reads them), in a
+ * fixed order, the same on every run, within the fp32 tolerance of the
+ * row-order sum. That saves a second read of the right operand; other
+ * products run as the two calls. The product's bits are sn_matmul's either
+ * way. */
 int sn_matmul_column_sums(sn_context *context, const sn_matmul_spec *spec, const float *left, size_t left_len,
                           const float *right, size_t right_len, float *output, size_t output_len, float *sums,
                           size_t sums_len);

@@ -12,6 +12,9 @@
 //    tiles transposed through LDS. Loads read 64 consecutive rows of each k
 //    (16 bytes a lane); 8 consecutive lanes then write one row's 64 k (128
 //    bytes). The LDS pitch of 65 floats keeps both sides conflict-free.
+//    Optionally (SUMS) each tile also leaves its 64 rows' fp32 sums over its
+//    64 k, in k order (Linear's bias gradient of a dY staged for the weight
+//    gradient: the rows here are dY's columns).
 //
 // HBM-bound: 4 bytes read and 2 written per element.
 #include <hip/hip_runtime.h>
@@ -65,11 +68,12 @@ __global__ __launch_bounds__(kThreads) void stage_rows_kernel(const float* __res
     *reinterpret_cast<bf16x8*>(dst + (batch * rows + r) * kp + k0) = round8(v);
 }
 
-template <bool VECTOR>
+template <bool VECTOR, bool SUMS>
 __global__ __launch_bounds__(kThreads) void stage_transposed_kernel(const float* __restrict__ src, int64_t ld,
                                                                     int64_t rows, int64_t k, int64_t kp,
                                                                     int64_t src_stride,
-                                                                    uint16_t* __restrict__ dst) {
+                                                                    uint16_t* __restrict__ dst,
+                                                                    float* __restrict__ sums) {
     __shared__ float tile[kTile * kPitch];  // [k][row]
     const int tid = threadIdx.x;
     const int64_t k_base = int64_t(blockIdx.x) * kTile;
@@ -101,6 +105,22 @@ __global__ __launch_bounds__(kThreads) void stage_transposed_kernel(const float*
     }
     __syncthreads();
 
+    // Sums (one batch): thread t adds row r_base + t % 64 over k 16 (t / 64)
+    // .. + 15 of the tile in order (k past K hold 0), and the four quarters
+    // are added in order; partial [k tile][row].
+    if constexpr (SUMS) {
+        __shared__ float quarter_sums[4][kTile];
+        const int row = tid % kTile, quarter = tid / kTile;
+        float part = 0.f;
+#pragma unroll
+        for (int kk = 16 * quarter; kk < 16 * quarter + 16; ++kk) part = part + tile[kk * kPitch + row];
+        quarter_sums[quarter][row] = part;
+        __syncthreads();
+        if (tid < kTile && r_base + tid < rows)
+            sums[int64_t(blockIdx.x) * rows + r_base + tid] =
+                ((quarter_sums[0][tid] + quarter_sums[1][tid]) + quarter_sums[2][tid]) + quarter_sums[3][tid];
+    }
+
     // Stores: 8 lanes per row, lane l of a group writing k 8 (l % 8) .. +7.
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -122,10 +142,14 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 }  // namespace
 
+int64_t stage_sum_tiles(int64_t kp) { return (kp + kTile - 1) / kTile; }
+
 hipError_t launch_stage_bf16(const float* src, bool k_contiguous, int64_t ld, int64_t rows, int64_t k, int64_t kp,
-                             int64_t batch, int64_t src_stride, uint16_t* dst, hipStream_t stream) {
+                             int64_t batch, int64_t src_stride, uint16_t* dst, hipStream_t stream,
+                             float* row_sums) {
     if (rows == 0 || kp == 0 || batch == 0) return hipSuccess;
     if (batch > 65535 || kp % 8 != 0 || kp < k) return hipErrorInvalidValue;
+    if (row_sums != nullptr && (k_contiguous || batch != 1)) return hipErrorInvalidValue;
     const bool vector = ld % 4 == 0 && src_stride % 4 == 0 && aligned16(src);
     if (k_contiguous) {
         const int64_t work = rows * (kp / 8);
@@ -142,12 +166,20 @@ hipError_t launch_stage_bf16(const float* src, bool k_contiguous, int64_t ld, in
         const int64_t tiles_r = (rows + kTile - 1) / kTile;
         if (tiles_r > 65535) return hipErrorInvalidValue;
         const dim3 grid{unsigned(tiles_k), unsigned(tiles_r), unsigned(batch)};
-        if (vector)
-            hipLaunchKernelGGL(stage_transposed_kernel<true>, grid, dim3(kThreads), 0, stream, src, ld, rows, k, kp,
-                               src_stride, dst);
-        else
-            hipLaunchKernelGGL(stage_transposed_kernel<false>, grid, dim3(kThreads), 0, stream, src, ld, rows, k,
-                               kp, src_stride, dst);
+        if (row_sums != nullptr) {
+            if (vector)
+                hipLaunchKernelGGL((stage_transposed_kernel<true, true>), grid, dim3(kThreads), 0, stream, src, ld,
+                                   rows, k, kp, src_stride, dst, row_sums);
+            else
+                hipLaunchKernelGGL((stage_transposed_kernel<false, true>), grid, dim3(kThreads), 0, stream, src, ld,
+                                   rows, k, kp, src_stride, dst, row_sums);
+        } else if (vector) {
+            hipLaunchKernelGGL((stage_transposed_kernel<true, false>), grid, dim3(kThreads), 0, stream, src, ld, rows,
+                               k, kp, src_stride, dst, nullptr);
+        } else {
+            hipLaunchKernelGGL((stage_transposed_kernel<false, false>), grid, dim3(kThreads), 0, stream, src, ld,
+                               rows, k, kp, src_stride, dst, nullptr);
+        }
     }
     return hipGetLastError();
 }

@@ -126,30 +126,41 @@ __global__ __launch_bounds__(kThreads) void column_slice_sums_kernel(const float
     }
 }
 
-// sums[c] += the slices' sums: slice s goes to accumulator s % 8 (so eight
-// loads are in flight), the accumulators are added in order, then the
-// total is added to sums[c]. A fixed order.
+// sums[c] += the slices' sums. A workgroup takes 32 columns; its 8 groups
+// of 32 threads take slices g, g + 8, g + 16, ... of them (up to 16 loads in
+// flight a thread, added in slice order), and the 8 group sums are then
+// added in group order: a fixed order. Split-K leaves 2-32 slices; the bf16
+// staging pass of a 32768-deep dY, 512.
+constexpr int kFinishCols = 32;
+constexpr int kFinishGroups = kThreads / kFinishCols;
 __global__ __launch_bounds__(kThreads) void column_sums_finish_kernel(const float* __restrict__ partial,
                                                                       int64_t slices, int64_t cols,
                                                                       float* __restrict__ sums) {
-    const int64_t c = blockIdx.x * int64_t(kThreads) + threadIdx.x;
-    if (c >= cols) return;
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    int64_t s = 0;
-    for (; s + 8 <= slices; s += 8) {
-        float v[8];
+    __shared__ float group_sums[kFinishGroups][kFinishCols];
+    const int lane_col = threadIdx.x % kFinishCols;
+    const int group = threadIdx.x / kFinishCols;
+    const int64_t c = blockIdx.x * int64_t(kFinishCols) + lane_col;
+    float acc = 0.f;
+    if (c < cols) {
+        constexpr int kInFlight = 16;
+        int64_t s = group;
+        for (; s + (kInFlight - 1) * kFinishGroups < slices; s += kInFlight * kFinishGroups) {
+            float v[kInFlight];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = partial[(s + j) * cols + c];
+            for (int j = 0; j < kInFlight; ++j) v[j] = partial[(s + j * kFinishGroups) * cols + c];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] = acc[j] + v[j];
+            for (int j = 0; j < kInFlight; ++j) acc = acc + v[j];
+        }
+        for (; s < slices; s += kFinishGroups) acc = acc + partial[s * cols + c];
     }
+    group_sums[group][lane_col] = acc;
+    __syncthreads();
+    if (group == 0 && c < cols) {
+        float total = group_sums[0][lane_col];
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-        if (s + j < slices) acc[j] = acc[j] + partial[(s + j) * cols + c];
-    float total = acc[0];
-#pragma unroll
-    for (int j = 1; j < 8; ++j) total = total + acc[j];
-    sums[c] = sums[c] + total;
+        for (int q = 1; q < kFinishGroups; ++q) total = total + group_sums[q][lane_col];
+        sums[c] = sums[c] + total;
+    }
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -208,8 +219,8 @@ hipError_t launch_column_sums(const float* in, int64_t rows, int64_t cols, float
 
 hipError_t launch_column_sums_finish(const float* partial, int64_t slices, int64_t cols, float* sums,
                                      hipStream_t stream) {
-    hipLaunchKernelGGL(column_sums_finish_kernel, dim3(unsigned((cols + kThreads - 1) / kThreads)), dim3(kThreads), 0,
-                       stream, partial, slices, cols, sums);
+    hipLaunchKernelGGL(column_sums_finish_kernel, dim3(unsigned((cols + kFinishCols - 1) / kFinishCols)),
+                       dim3(kThreads), 0, stream, partial, slices, cols, sums);
     return hipGetLastError();
 }
 

@@ -489,19 +489,43 @@ hipError_t launch_gemm_bf16_wide(const Problem& p, const Env& env, hipStream_t s
 
 // ---- The weight-gradient product with Linear's bias gradient -------------
 //
-// dY, the right operand of dW += x^T dY, is row-contiguous fp32; unless it is
+// dY, the right operand of dW += x^T dY, is row-contiguous fp32. Unless it is
 // the operand staged as bf16 (when it has at most half x's columns), every
 // 256 x 32 slab of it passes through the registers as fp32 before rounding,
 // and the first tile row sums its columns there. Each K slice also leaves N
 // partial column sums after the product's partials, so the split count is
 // chosen as if the workspace left after staging were M / (M + 1) of its size.
+// When dY is the staged operand (the down projection: N <= M / 2), the
+// staging pass, which reads all of dY as fp32 once, takes the sums instead:
+// one partial per 64 k and column (stage_sum_tiles x N floats after the
+// product's partials), added in k order by the finish kernel.
 
 namespace {
 
+size_t staged_sum_bytes(const WideStaging& st, const Problem& p) {
+    return size_t(stage_sum_tiles(st.kp)) * size_t(p.n) * sizeof(float);
+}
+
 Plan wide_column_sums_plan(const WideStaging& st, const Problem& p) {
     Env e = st.rest;
-    e.workspace_bytes = st.rest.workspace_bytes / size_t(p.m + 1) * size_t(p.m);
+    if (st.side == kStageRight) {
+        const size_t sums = staged_sum_bytes(st, p);
+        e.workspace_bytes = st.rest.workspace_bytes > sums ? st.rest.workspace_bytes - sums : 0;
+    } else {
+        e.workspace_bytes = st.rest.workspace_bytes / size_t(p.m + 1) * size_t(p.m);
+    }
     return wide_plan(st.q, e);
+}
+
+// Workspace after the staged operand: the product's split partials, then the
+// column sums' partials (per K slice, or per 64 k of the staging pass).
+size_t product_partial_bytes(const Plan& plan, const Problem& p) {
+    return plan.splits > 1 ? size_t(plan.splits) * size_t(p.m) * size_t(p.n) * sizeof(float) : 0;
+}
+
+size_t column_partial_bytes(const WideStaging& st, const Plan& plan, const Problem& p) {
+    if (st.side == kStageRight) return staged_sum_bytes(st, p);
+    return plan.splits > 1 ? size_t(plan.splits) * size_t(p.n) * sizeof(float) : 0;
 }
 
 }  // namespace
@@ -510,18 +534,15 @@ bool bf16_wide_column_sums_applies(const Problem& p, const Env& env) {
     if (p.batch != 1 || p.m < 1 || p.k < 1 || p.b_k_contiguous || p.bias != nullptr || !bf16_wide_applies(p, env))
         return false;
     const WideStaging st = wide_staging(p, env);
-    if (st.side == kStageRight) return false;  // dY reaches the kernel as bf16 only
     const Plan plan = wide_column_sums_plan(st, p);
-    return plan.splits == 1 ||
-           size_t(plan.splits) * (size_t(p.m) * size_t(p.n) + size_t(p.n)) * sizeof(float) <= st.rest.workspace_bytes;
+    return product_partial_bytes(plan, p) + column_partial_bytes(st, plan, p) <= st.rest.workspace_bytes;
 }
 
 LaunchShape describe_bf16_wide_column_sums(const Problem& p, const Env& env) {
     const WideStaging st = wide_staging(p, env);
     const Plan plan = wide_column_sums_plan(st, p);
     LaunchShape shape = tiled_shape<WideTile>(st.q, plan, SN_PATH_BF16_WIDE);
-    shape.workspace_bytes += st.bytes;
-    if (plan.splits > 1) shape.workspace_bytes += size_t(plan.splits) * size_t(p.n) * sizeof(float);
+    shape.workspace_bytes += st.bytes + column_partial_bytes(st, plan, p);
     return shape;
 }
 
@@ -530,6 +551,16 @@ hipError_t launch_gemm_bf16_wide_column_sums(const Problem& p, const Env& env, h
     const Problem& q = st.q;
     const Plan plan = wide_column_sums_plan(st, p);
     hipError_t err = hipSuccess;
+    if (st.side == kStageRight) {
+        float* sums = st.rest.workspace + product_partial_bytes(plan, p) / sizeof(float);
+        err = launch_stage_bf16(p.b, false, p.ldb, p.n, p.k, st.kp, 1, p.stride_b,
+                                reinterpret_cast<uint16_t*>(env.workspace), stream, sums);
+        if (err == hipSuccess)
+            err = q.a_k_contiguous ? launch_wide<true, true, kStageRight>(q, st.rest, plan, stream)
+                                   : launch_wide<false, true, kStageRight>(q, st.rest, plan, stream);
+        if (err != hipSuccess) return err;
+        return launch_column_sums_finish(sums, stage_sum_tiles(st.kp), p.n, p.column_sums, stream);
+    }
     if (st.side == kStageLeft) {
         err = launch_stage_bf16(p.a, p.a_k_contiguous, p.lda, p.m, p.k, st.kp, st.copies, p.stride_a,
                                 reinterpret_cast<uint16_t*>(env.workspace), stream);

@@ -181,8 +181,13 @@ bool attention_backward_supported(const AttentionBackwardArgs& args);
 // K-contiguous, zeros for k in [k, kp) (bf16_stage.hip). Element (r, k) of
 // the source is src[r * ld + k] when k_contiguous, else src[k * ld + r];
 // batches are src_stride floats apart. kp must be a multiple of 8 and >= k.
+// row_sums (a row-contiguous source, one batch): also the fp32 sums of each
+// row over K, left as stage_sum_tiles(kp) partials, row_sums[tile][row],
+// each over 64 consecutive k in order, for launch_column_sums_finish.
 hipError_t launch_stage_bf16(const float* src, bool k_contiguous, int64_t ld, int64_t rows, int64_t k, int64_t kp,
-                             int64_t batch, int64_t src_stride, uint16_t* dst, hipStream_t stream);
+                             int64_t batch, int64_t src_stride, uint16_t* dst, hipStream_t stream,
+                             float* row_sums = nullptr);
+int64_t stage_sum_tiles(int64_t kp);
 
 // Bytes of workspace launch_gemm_* would use for `p` (0 = none): split-K
 // partial sums, and for bf16 the staged operands.

@@ -126,7 +126,7 @@ def test_weight_gradients_take_the_column_sums_into_the_product():
     assert tight.workspace_bytes <= product.workspace_bytes
     # bf16 on the 256 x 256 kernel: the sums ride in it where dY reaches it as fp32 (x^T staged or
     # nothing staged), N floats more per slice; the down projection's dY is the operand staged as bf16,
-    # so it runs as the product, then the column sums, with the larger of the two workspaces.
+    # and the staging pass takes the sums, one partial per 64 k and column.
     for inputs, outputs in ((768, 2304), (768, 768), (768, 3072), (768, 16384)):
         bf16 = MatmulSpec.new(inputs, outputs, 32768).left_transposed().accumulate().with_precision(Precision.Bf16)
         product, fused = gemm.plan(bf16), gemm.plan_column_sums(bf16)
@@ -135,8 +135,10 @@ def test_weight_gradients_take_the_column_sums_into_the_product():
         extra = fused.splits * outputs * 4 if fused.splits > 1 else 0
         assert fused.workspace_bytes == product.workspace_bytes + extra
     down = MatmulSpec.new(3072, 768, 32768).left_transposed().accumulate().with_precision(Precision.Bf16)
-    assert gemm.plan_column_sums(down).path == gemm.PATH_BF16_WIDE
-    assert gemm.plan_column_sums(down).workspace_bytes == gemm.plan(down).workspace_bytes
+    product, fused = gemm.plan(down), gemm.plan_column_sums(down)
+    assert fused.path == gemm.PATH_BF16_WIDE_SUMS
+    assert (fused.splits, fused.tiles_m, fused.tiles_n) == (product.splits, product.tiles_m, product.tiles_n)
+    assert fused.workspace_bytes == product.workspace_bytes + (32768 // 64) * 768 * 4
     odd = MatmulSpec.new(96, 50, 300).left_transposed()
     assert gemm.plan_column_sums(odd).path == gemm.PATH_F32_REGISTER
     # The unsupported forms are rejected by the planner as by the call.

@@ -153,7 +153,8 @@ def test_weight_gradient_at_config_2_scale(gpu):
     assert error < TOLERANCE
 
 
-# bf16 on the 256 x 256 kernel: dY's fp32 values are summed in the registers before they are rounded.
+# bf16 on the 256 x 256 kernel: dY's fp32 values are summed in the registers before they are rounded,
+# or, where dY is the operand staged as bf16, by the staging pass as it reads them.
 # Integers of magnitude <= 2 (exact in bf16; every product sum and column sum stays below 2^24) make the
 # product exact in any order: it is compared in full with the exact integer product (float64
 # arithmetic), and the sums with the oracle's row-order sums, bit for bit.
@@ -161,6 +162,8 @@ def test_weight_gradient_at_config_2_scale(gpu):
     (768, 2304, 32768),   # the qkv weight gradient: x^T staged as bf16, 9 K slices
     (768, 768, 32768),    # the out projection's: nothing staged, 28 slices
     (772, 2312, 20010),   # ragged tiles both ways, a K tail
+    (3072, 768, 32768),   # the down projection's: dY staged as bf16, the staging pass takes the sums
+    (3080, 772, 20010),   # dY staged, ragged: a partial last 64-k tile and column block
 ])
 def test_bf16_fused_sums_are_exact_on_integers(gpu, inputs, outputs, rows):
     print(f"bf16 column sums {inputs}x{outputs}x{rows}", flush=True)
@@ -181,8 +184,10 @@ def test_bf16_fused_sums_are_exact_on_integers(gpu, inputs, outputs, rows):
     assert np.array_equal(out, want_out)
 
 
-def test_bf16_fused_product_is_sn_matmul_and_sums_within_tolerance(gpu):
-    inputs, outputs, rows = 768, 2304, 32768
+@pytest.mark.parametrize("inputs,outputs", [(768, 2304), (3072, 768)])  # x^T staged; dY staged
+def test_bf16_fused_product_is_sn_matmul_and_sums_within_tolerance(gpu, inputs, outputs):
+    rows = 32768
+    print(f"bf16 column sums random {inputs}x{outputs}x{rows}", flush=True)
     left = oracle.random_values(inputs * rows, 71)
     right = oracle.random_values(rows * outputs, 72)
     initial = oracle.random_values(inputs * outputs, 73)
@@ -201,15 +206,12 @@ def test_bf16_fused_product_is_sn_matmul_and_sums_within_tolerance(gpu):
     assert np.max(np.abs(sums - truth)) <= np.max(np.abs(expected - truth)) + 1e-6 * np.max(np.abs(truth))
 
 
-@pytest.mark.parametrize("case", ["bf16", "bf16_dy_staged", "columns_not_multiple_of_4", "empty_rows"])
+@pytest.mark.parametrize("case", ["bf16", "columns_not_multiple_of_4", "empty_rows"])
 def test_unfused_products_run_as_the_two_calls(gpu, case):
     inputs, outputs, rows = 96, 80, 300
     kernel = MatmulKernel.MfmaF32
     if case == "bf16":
         inputs, outputs, rows = 256, 512, 256
-        kernel = MatmulKernel.MfmaBf16
-    elif case == "bf16_dy_staged":  # the down projection's shape: dY is the operand rounded into the workspace
-        inputs, outputs, rows = 3072, 768, 4096
         kernel = MatmulKernel.MfmaBf16
     elif case == "columns_not_multiple_of_4":
         outputs = 50
