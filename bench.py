@@ -942,8 +942,8 @@ def measure_linear(gpu: Gpu, events: HipEvents, buffers, repeats: int = 5):
     the bias gradient (accumulate_column_sums, linear.rs:59), with the bias kernels' HBM rates
     (add_row_bias: 8 bytes per output element; column sums: 4 bytes per input element); and the
     weight and bias gradients as the reference calls them (matmul, then accumulate_column_sums;
-    linear.rs:54-59) against sn_matmul_column_sums, the sums taken inside the product, in fp32 and at
-    bf16 precision."""
+    linear.rs:54-59) against sn_matmul_column_sums, the sums taken inside the product; forward and
+    gradients in fp32 and at bf16 precision."""
     layers = [b for b, (label, _, _) in zip(buffers, training_set()) if label.startswith("b0.") or label == "head"]
     names = ["qkv", "out", "up", "down", "head"]
     result = {}
@@ -969,6 +969,11 @@ def measure_linear(gpu: Gpu, events: HipEvents, buffers, repeats: int = 5):
                                                              gpu.accumulate_column_sums(buf.dy, sums)), repeats)
         grads_fused = timed(events, gpu.stream, lambda: gpu.matmul_column_sums(grad, buf.x, buf.dy, buf.dw, sums),
                             repeats)
+        spec16 = spec.with_precision(Precision.Bf16)
+        gpu.matmul_bias(spec16, buf.x, buf.w, bias, buf.y)
+        separate16 = timed(events, gpu.stream, lambda: (gpu.matmul(spec16, buf.x, buf.w, buf.y),
+                                                         gpu.add_row_bias(buf.y, bias)), repeats)
+        fused16 = timed(events, gpu.stream, lambda: gpu.matmul_bias(spec16, buf.x, buf.w, bias, buf.y), repeats)
         grad16 = grad.with_precision(Precision.Bf16)
         gpu.matmul_column_sums(grad16, buf.x, buf.dy, buf.dw, sums)
         grads16_separate = timed(events, gpu.stream, lambda: (gpu.matmul(grad16, buf.x, buf.dy, buf.dw),
@@ -984,6 +989,8 @@ def measure_linear(gpu: Gpu, events: HipEvents, buffers, repeats: int = 5):
             "weight_bias_grads_separate_ms": round(grads_separate, 4),
             "weight_bias_grads_fused_ms": round(grads_fused, 4),
             "grads_fused_saving_pct": round(100 * (1 - grads_fused / grads_separate), 1),
+            "bf16_forward_separate_ms": round(separate16, 4), "bf16_forward_fused_ms": round(fused16, 4),
+            "bf16_fused_saving_pct": round(100 * (1 - fused16 / separate16), 1),
             "bf16_weight_bias_grads_separate_ms": round(grads16_separate, 4),
             "bf16_weight_bias_grads_fused_ms": round(grads16_fused, 4),
             "bf16_grads_fused_saving_pct": round(100 * (1 - grads16_fused / grads16_separate), 1)}
