@@ -10,8 +10,12 @@
 // One wave per row, as the softmax kernels: the head's logits held in
 // registers (16-byte loads) when they are at most 4096 aligned columns,
 // else three passes; the row's max and sum are reduced by a butterfly (a
-// fixed order). exp and log are the device's expf and logf; differences and
-// products are rounded separately, as the reference rounds them. A target
+// fixed order). Differences and products are rounded separately, as the
+// reference rounds them; e^d of a rounded difference d is 2^(d log2 e) on the
+// transcendental unit (v_exp_f32, about 1 ulp): rounding d log2 e adds at
+// most |d| 2^-24 to the exponent, a relative error under 2e-6 for every term
+// above e^-20 (the library expf took about 12 instructions, and two per
+// element made the kernel compute-bound); the log is logf. A target
 // outside the head (neither a class nor empty) gives a NaN loss and no
 // onehot term. HBM-bound: 8 bytes per head element (read the logits, write
 // the gradient).
@@ -30,6 +34,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 4;
 constexpr uint32_t kEmptyToken = 0xFFFFFFFFu;
+
+constexpr float kLog2e = 1.44269504088896340736f;
+__device__ __forceinline__ float exp_of(float d) { return __builtin_amdgcn_exp2f(d * kLog2e); }
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -77,7 +84,7 @@ __global__ __launch_bounds__(64 * kWaves) void cross_entropy_vector_kernel(Cross
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const float shifted = v[i][j] - maximum;
-                total = total + expf(shifted);
+                total = total + exp_of(shifted);
             }
         }
     total = wave_sum(total);
@@ -92,7 +99,7 @@ __global__ __launch_bounds__(64 * kWaves) void cross_entropy_vector_kernel(Cross
             for (int j = 0; j < 4; ++j) {
                 const float shifted = v[i][j] - log_partition;
                 const float one_hot = c + j == int64_t(target) ? 1.f : 0.f;
-                const float difference = expf(shifted) - one_hot;
+                const float difference = exp_of(shifted) - one_hot;
                 out[j] = difference * a.grad_scale;
             }
             g4[lane + 64 * i] = out;
@@ -119,7 +126,7 @@ __global__ __launch_bounds__(64 * kWaves) void cross_entropy_loop_kernel(CrossEn
     float total = 0.f;
     for (int64_t c = lane; c < a.classes; c += 64) {
         const float shifted = z[c] - maximum;
-        total = total + expf(shifted);
+        total = total + exp_of(shifted);
     }
     total = wave_sum(total);
     const float log_partition = maximum + logf(total);
@@ -127,7 +134,7 @@ __global__ __launch_bounds__(64 * kWaves) void cross_entropy_loop_kernel(CrossEn
     for (int64_t c = lane; c < a.classes; c += 64) {
         const float shifted = z[c] - log_partition;
         const float one_hot = c == int64_t(target) ? 1.f : 0.f;
-        const float difference = expf(shifted) - one_hot;
+        const float difference = exp_of(shifted) - one_hot;
         g[c] = difference * a.grad_scale;
     }
 }
