@@ -1504,9 +1504,10 @@ def main() -> int:
                           "frac_bf16_peak": round(bf16_tflops / PEAK_BF16_TFLOPS, 4),
                           "roofline_min_peak_or_ai_x_hbm": round(attainable, 1),
                           "frac_roofline": round(bf16_tflops / attainable, 4), "per_layout": bf16_layout,
-                          "inputs": "fp32 in HBM; each call first rounds both operands to bf16 (nearest-even), "
-                                    "K-contiguous, in the context's workspace (timed with the product), then "
-                                    "multiplies bf16 LDS stages with fp32 accumulation"}
+                          "inputs": "fp32 in HBM; the 256x256 kernel rounds fp32 operand fragments to bf16 "
+                                    "(nearest-even) as it loads them into LDS; an operand at most half the size "
+                                    "of the other is first rounded into the context's workspace (timed with "
+                                    "the product); bf16 matrix-core products with fp32 accumulation"}
         result["linear_bias"] = measure_linear(gpu, events, _buffers)
         result["head_cross_entropy"] = measure_loss(gpu, events, _buffers)
         result["attention"] = measure_attention(gpu, events)
