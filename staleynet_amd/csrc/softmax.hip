@@ -32,7 +32,10 @@ namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kWaves = 4;  // rows per workgroup
+// Rows (one wave each) per workgroup. Two measured 3-5 % faster than four on
+// 192 x 2048 x 2048 scores: causal softmax 0.92-0.94 ms against 0.95-0.97,
+// its backward 1.72-1.75 against 1.80-1.84.
+constexpr int kWaves = 2;
 constexpr int kMaxVectors = 16;
 
 __device__ __forceinline__ float wave_max(float v) {
