@@ -438,16 +438,17 @@ int sn_free_tokens(sn_context *context, uint32_t *buffer);
 #define SN_NOALLOC_WORKSPACE_BYTES ((size_t)64 << 20)
 
 /* sn_matmul without a context and without allocating anything. It has no
- * counterpart in the reference (whose Gpu::matmul, ops/matmul.rs:146-171,
- * needs no scratch); it is for callers that cannot allocate device memory:
- * code under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc. The product runs on the calling thread's current device, on
- * `stream` (a hipStream_t; null is the default stream), with the kernel the
- * spec's precision names (default and F32: fp32 matrix cores; BF16: bf16
- * inputs). Its scratch is a device array of the library's, one per device,
- * held from the library's load until the process ends: 64 KiB of arrival
- * counters (cleared on the first call on each device) and
- * SN_NOALLOC_WORKSPACE_BYTES for partial sums. A product that would need
+ * counterpart in the reference; it is for callers that cannot allocate
+ * device memory: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc. The product runs on the calling thread's
+ * current device, on `stream` (a hipStream_t; null is the default stream),
+ * with the kernel the spec's precision names (default and F32: fp32 matrix
+ * cores; BF16: bf16 inputs). Its scratch is a device array of the
+ * library's, one per device, held from the library's load until the process
+ * ends: 64 KiB of arrival counters (zero from the load; each kernel resets
+ * what it counts) and SN_NOALLOC_WORKSPACE_BYTES for partial sums. The first
+ * call on a device only looks up that array's address and enqueues nothing
+ * else, so it may itself be under stream capture. A product that would need
  * more partial sums than that splits K into fewer slices (within the fp32
  * tolerance of sn_matmul's result; bit-identical when both plans agree);
  * one that cannot fit returns SN_ERR_WORKSPACE. The same checks and codes as

@@ -92,11 +92,18 @@ __global__ __launch_bounds__(256) void attention_rows_kernel(RowsArgs a) {
     }
 #pragma unroll
     for (int o = 1; o < 16; o <<= 1) d = d + __shfl_xor(d, o);
+    float* planes = a.rows + head * 3 * plane_of(a.queries) + q;
     if (li == 0) {
-        float* planes = a.rows + head * 3 * plane_of(a.queries) + q;
         planes[0] = a.stats[2 * g];
         planes[plane_of(a.queries)] = 1.f / a.stats[2 * g + 1];
         planes[2 * plane_of(a.queries)] = d;
+    } else if (li < 4 && q == a.queries - 1 && q + li < plane_of(a.queries)) {
+        // The last query's group also zeroes its head's padding slots (up to
+        // three per plane), so the key kernels' whole 16-byte record loads
+        // never bring in what the workspace held before.
+        planes[li] = 0.f;
+        planes[plane_of(a.queries) + li] = 0.f;
+        planes[2 * plane_of(a.queries) + li] = 0.f;
     }
 }
 
@@ -354,14 +361,20 @@ void attention_key_grad_kernel(KeyGradArgs a) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const float shifted = s[4 * g + j] * a.scale - m4[j];
-                float pr = exp_of(shifted) * il4[j];
-                if (MASKED) {
-                    const int64_t query = sub0 + 8 * g + 4 * half + j;
-                    pr = key_ok && query < a.queries && key <= query + a.query_offset ? pr : 0.f;
-                }
-                p[j] = pr;
+                const float pr = exp_of(shifted) * il4[j];
                 const float difference = dp[4 * g + j] - d4[j];
-                gr[j] = pr * difference;
+                const float grad = pr * difference;
+                if (MASKED) {
+                    // Both terms are selected, not scaled by a zero p: a record
+                    // slot past the last query may hold any bits, Inf and NaN included.
+                    const int64_t query = sub0 + 8 * g + 4 * half + j;
+                    const bool visible = key_ok && query < a.queries && key <= query + a.query_offset;
+                    p[j] = visible ? pr : 0.f;
+                    gr[j] = visible ? grad : 0.f;
+                } else {
+                    p[j] = pr;
+                    gr[j] = grad;
+                }
             }
 #pragma unroll
             for (int b = 0; b < G::OBLOCKS; ++b)
@@ -565,14 +578,20 @@ void attention_key_grad_lds_kernel(KeyGradArgs a) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const float shifted = s[4 * g + j] * a.scale - m4[j];
-                float pr = exp_of(shifted) * il4[j];
-                if (MASKED) {
-                    const int64_t query = sub0 + 8 * g + 4 * half + j;
-                    pr = key_ok && query < a.queries && key <= query + a.query_offset ? pr : 0.f;
-                }
-                p[j] = pr;
+                const float pr = exp_of(shifted) * il4[j];
                 const float difference = dp[4 * g + j] - d4[j];
-                gr[j] = pr * difference;
+                const float grad = pr * difference;
+                if (MASKED) {
+                    // Both terms are selected, not scaled by a zero p: a record
+                    // slot past the last query may hold any bits, Inf and NaN included.
+                    const int64_t query = sub0 + 8 * g + 4 * half + j;
+                    const bool visible = key_ok && query < a.queries && key <= query + a.query_offset;
+                    p[j] = visible ? pr : 0.f;
+                    gr[j] = visible ? grad : 0.f;
+                } else {
+                    p[j] = pr;
+                    gr[j] = grad;
+                }
             }
 #pragma unroll
             for (int b = 0; b < G::OBLOCKS; ++b)
@@ -784,13 +803,15 @@ void attention_query_grad_kernel(QueryGradArgs a) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const float shifted = s[4 * g + j] * a.scale - rec[0];
-                float pr = exp_of(shifted) * rec[1];
+                const float pr = exp_of(shifted) * rec[1];
+                const float difference = dp[4 * g + j] - rec[2];
+                const float grad = pr * difference;
                 if (MASKED) {
                     const int64_t key = sub0 + 8 * g + 4 * half + j;
-                    pr = row_ok && key < a.keys && key <= q + a.query_offset ? pr : 0.f;
+                    gr[j] = row_ok && key < a.keys && key <= q + a.query_offset ? grad : 0.f;
+                } else {
+                    gr[j] = grad;
                 }
-                const float difference = dp[4 * g + j] - rec[2];
-                gr[j] = pr * difference;
             }
 #pragma unroll
             for (int b = 0; b < G::OBLOCKS; ++b)

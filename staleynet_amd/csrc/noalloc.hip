@@ -1,19 +1,20 @@
 // sn_matmul_noalloc: sn_matmul for callers that cannot allocate device
 // memory (code under HIP graph capture, tight serving loops, harnesses that
-// forbid hipMalloc). It has no counterpart in the reference, whose
-// Gpu::matmul (crates/staleynet-cuda/src/ops/matmul.rs:146-171) needs no
-// scratch. Here the kernels' scratch, split-K partial sums (and bf16 staged
-// operands) and the decode kernels' arrival counters, lives in a file-scope
-// device array instead of a context's workspace:
+// forbid hipMalloc). It has no counterpart in the reference. Here the
+// kernels' scratch, split-K partial sums (and bf16 staged operands) and the
+// decode kernels' arrival counters, lives in a file-scope device array
+// instead of a context's workspace:
 //  * every device the library runs on holds its own copy of the array from
 //    the moment the code object loads until the process ends;
 //  * on the first call on a device (with that device current) its address
 //    is looked up with hipGetSymbolAddress and kept per device; the array's
-//    name in host code is only a stand-in, never a device address;
-//  * the counters must be zero between calls: they are cleared once, by a
-//    kernel on that first call's stream, and every kernel that increments a
-//    counter resets it before it ends; the partial sums are written before
-//    they are read within each call;
+//    name in host code is only a stand-in, never a device address. That
+//    set-up puts no work on any stream, so a first call made under stream
+//    capture records only the product's own kernels;
+//  * the counters must be zero between calls: the array has static storage
+//    and no initializer, so the code object's loader zero-fills it, and
+//    every kernel that increments a counter resets it before it ends; the
+//    partial sums are written before they are read within each call;
 //  * every call on a device shares that device's array, so calls that
 //    overlap on one device (two streams, two threads) race.
 // Products whose plan would split K into more partial sums than the array
@@ -44,25 +45,16 @@ struct DeviceScratch {
 
 DeviceScratch g_devices[kMaxDevices];
 
-__global__ __launch_bounds__(256) void clear_counters(uint32_t* counters, uint32_t count) {
-    for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < count; i += gridDim.x * 256u) counters[i] = 0u;
-}
-
 // Set-up of `device` (current on the calling thread), once: the device
-// address of its `scratch`, its compute-unit count, and the counters cleared
-// on `stream`. A failure is kept and returned by every later call.
-DeviceScratch& scratch_of(int device, hipStream_t stream) {
+// address of its `scratch` and its compute-unit count. Nothing is enqueued.
+// A failure is kept and returned by every later call.
+DeviceScratch& scratch_of(int device) {
     DeviceScratch& d = g_devices[device];
     std::call_once(d.once, [&] {
         void* ptr = nullptr;
         hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
         int cus = 0;
         if (err == hipSuccess) err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
-        if (err == hipSuccess) {
-            hipLaunchKernelGGL(clear_counters, dim3(16), dim3(256), 0, stream, static_cast<uint32_t*>(ptr),
-                               uint32_t(kScratchCounters));
-            err = hipGetLastError();
-        }
         if (err == hipSuccess) {
             d.ptr = static_cast<unsigned char*>(ptr);
             d.cu_count = cus > 0 ? cus : 256;
@@ -84,7 +76,7 @@ extern "C" int sn_matmul_noalloc(const sn_matmul_spec* spec, const float* left, 
     if (err != hipSuccess) return int(err);
     if (device < 0 || device >= kMaxDevices) return SN_ERR_NO_DEVICE;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    DeviceScratch& d = scratch_of(device, s);
+    DeviceScratch& d = scratch_of(device);
     if (d.status != hipSuccess) return int(d.status);
     sn::Env env;
     env.counters = reinterpret_cast<uint32_t*>(d.ptr);

@@ -5,7 +5,8 @@ CausalSelfAttention::forward and ::backward (crates/staleynet-model/src/layers/a
 the scores product, causal_softmax (reference.rs:100-119), the dP and dV products, softmax_backward
 (reference.rs:121-137) and the dQ and dK products (reference.rs:19-38), at the reference's fp32
 tolerance. Cases: ragged blocks, query offsets, more or fewer keys than queries, head dims 32 / 64 /
-128, config 3's size, reruns bit-identical, and the entry point's checks."""
+128, config 3's whole 192-head launch (eight heads across it compared in full, statistics included),
+reruns bit-identical, a workspace left holding NaN, and the entry point's checks."""
 import numpy as np
 import pytest
 
@@ -141,6 +142,79 @@ def test_config_3_heads_at_full_size_and_determinism(gpu):
     _, again = run(gpu, heads, t, t, h, 0.125, 0, seed=31)
     for name in ("dq", "dk", "dv"):
         assert np.array_equal(got[name], again[name]), name
+
+
+# Config 3's whole launch: 16 sequences x 12 heads = 192 head matrices of T = 2048, h = 64. A
+# workgroup's head is its index mod 192 and workgroup i runs on XCD i mod 8, so head % 8 names the XCD
+# group: these eight heads are the first, the last and one on every XCD.
+CONFIG_3_HEADS, CONFIG_3_T, CONFIG_3_H = 192, 2048, 64
+CHECKED_HEADS = [0, 25, 50, 75, 100, 125, 150, 191]
+
+
+def test_config_3_full_launch_matches_the_reference_calls_on_heads_across_it(gpu):
+    heads, t, h, scale = CONFIG_3_HEADS, CONFIG_3_T, CONFIG_3_H, 0.125
+    assert sorted(x % 8 for x in CHECKED_HEADS) == list(range(8))
+    print(f"config 3 full launch: {heads} heads, T {t}, h {h}", flush=True)
+    inputs, got = run(gpu, heads, t, t, h, scale, 0, seed=3)
+    # The reference's calls on the checked heads only (each head is independent).
+    picked = [x.reshape(heads, t * h)[CHECKED_HEADS].ravel() for x in inputs]
+    n = len(CHECKED_HEADS)
+    out, row_max, dq, dk, dv = reference(*picked, n, t, t, h, scale, 0)
+    errors = {}
+    for name, expected in (("out", out), ("dq", dq), ("dk", dk), ("dv", dv)):
+        mine = got[name].reshape(heads, t * h)[CHECKED_HEADS]
+        assert np.all(np.isfinite(got[name])), name
+        errors[name] = max(oracle.relative_error(e, a) for e, a in zip(expected.reshape(n, t * h), mine))
+    # The statistics in full: m against the largest scaled visible score, l against the f64 sum of
+    # e^(x - m) over the visible keys (both from the oracle's scores product).
+    stats = got["stats"].reshape(heads, t, 2)[CHECKED_HEADS]
+    errors["m"] = oracle.relative_error(row_max.ravel(), stats[..., 0].ravel())
+    q, k = picked[0].reshape(n, t, h), picked[1].reshape(n, t, h)
+    scores = np.zeros(n * t * t, np.float32)
+    oracle.matmul_parallel(product(t, t, h, rt=True, batch=(n, t * h, t * h, t * t)), q.ravel(), k.ravel(), scores)
+    scaled = scores.reshape(n, t, t).astype(np.float64) * scale
+    visible = np.tril(np.ones((t, t), bool))
+    l_expected = np.where(visible[None], np.exp(scaled - stats[..., 0:1].astype(np.float64)), 0.0).sum(axis=2)
+    errors["l"] = float(np.max(np.abs(stats[..., 1] - l_expected) / l_expected))
+    print(" ".join(f"{k} {e:.2e}" for k, e in errors.items()))
+    assert all(e < TOLERANCE for e in errors.values()), errors
+    # Every head's gradients are finite, and a rerun of the whole launch gives the same bits.
+    _, again = run(gpu, heads, t, t, h, scale, 0, seed=3)
+    for name in ("out", "stats", "dq", "dk", "dv"):
+        assert np.array_equal(got[name], again[name]), name
+
+
+def poison_workspace(gpu):
+    """Leaves NaN in the context workspace's first bytes: a split-K weight-gradient product whose
+    left operand is all Inf stores non-finite partial sums there (Inf times values of both signs)."""
+    from staleynet_amd.gemm import MatmulSpec, plan
+
+    m, n, k = 256, 256, 32768
+    spec = MatmulSpec.new(m, n, k).left_transposed()
+    assert plan(spec).splits > 1
+    left = gpu.upload(Shape.vector(k * m), np.full(k * m, np.inf, np.float32))
+    right = gpu.upload(Shape.vector(k * n), np.random.default_rng(5).normal(0, 1, k * n).astype(np.float32))
+    out = gpu.zeros(Shape(m, n))
+    gpu.matmul(spec, left, right, out)
+    assert np.all(np.isnan(gpu.download(out)))
+    for buf in (left, right, out):
+        buf.free()
+
+
+@pytest.mark.parametrize("queries,h", [(37, 64), (299, 64), (37, 128), (301, 32)])
+def test_record_padding_never_reaches_the_gradients(gpu, queries, h):
+    # The row records are planes of queries rounded up to 4; the key kernels load the last 16-byte
+    # chunk whole, so a query count that is not a multiple of 4 reads padding slots. Whatever the
+    # workspace held there before (here NaN), the gradients stay finite and equal the reference's.
+    heads, keys, scale = 2, queries, 0.125
+    print(f"padding: heads={heads} queries={queries} h={h} after a NaN workspace", flush=True)
+    poison_workspace(gpu)
+    inputs, got = run(gpu, heads, queries, keys, h, scale, 0, seed=queries + h)
+    out, _, dq, dk, dv = reference(*inputs, heads, queries, keys, h, scale, 0)
+    for name, expected in (("out", out), ("dq", dq), ("dk", dk), ("dv", dv)):
+        assert np.all(np.isfinite(got[name])), name
+        error = oracle.relative_error(expected, got[name])
+        assert error < TOLERANCE, f"{name}: relative error {error}"
 
 
 def test_entry_point_checks(gpu):

@@ -5,12 +5,14 @@ and Linear::forward / backward (layers/linear.rs:43-63); and one cached decode s
 (forward_cached, attention.rs:274-320) against the last row of the full causal forward, the check
 of the reference's model_is_trainable.rs:161-213.
 
-Two call sequences run on the GPU:
+Three call sequences run on the GPU:
 * ``reference``: the reference's calls one for one (dense scores and mix products, causal_softmax,
   softmax_backward, four backward products, separate bias calls);
 * ``fused``: what a caller of this library would issue instead (the bias in the product's
   epilogue, the fused attention forward with probabilities, the fused probability and query
-  gradient, the causal-left value and key gradients).
+  gradient, the causal-left value and key gradients);
+* ``no_probabilities``: the same Linears around the training attention that keeps no [T, T]
+  matrix (the forward with per-query statistics, then the backward that rebuilds P from them).
 Every activation and gradient is compared, in the reference test's metric, at the fp32 tolerance.
 Weights and inputs come from the reference test's LCG (kernels_match_reference.rs:26-38)."""
 import math
@@ -115,8 +117,11 @@ def oracle_layer(L: Layer, backward=True):
     return r
 
 
-def gpu_layer(gpu, L: Layer, fused: bool):
-    """The same layer through the library: the reference's calls one for one, or fused."""
+def gpu_layer(gpu, L: Layer, mode: str):
+    """The same layer through the library: the reference's calls one for one (``reference_calls``),
+    fused with the probabilities kept (``fused``), or the training attention that keeps none
+    (``no_probabilities``: the forward with row statistics and the backward that rebuilds P)."""
+    fused = mode != "reference_calls"
     B, T, d, H, h = L.batch, L.time, L.width, L.heads, L.head_dim
     rows, BH = B * T, B * L.heads
     hb, sb = T * h, T * T
@@ -147,7 +152,10 @@ def gpu_layer(gpu, L: Layer, fused: bool):
     for i, t in enumerate((q, k, v)):
         gpu.split_heads(qkv, t, layout(3 * d, i * d))
     p, ctx_heads = matrix(BH * T, T), zeros(BH * hb)
-    if fused:
+    stats = zeros(2 * BH * T)
+    if mode == "no_probabilities":
+        gpu.causal_attention_with_stats(q, k, v, ctx_heads, stats, BH, T, T, h, float(L.scale))
+    elif fused:
         gpu.causal_attention(q, k, v, ctx_heads, BH, T, T, h, float(L.scale), probabilities=p)
     else:
         gpu.matmul(MatmulSpec.new(T, T, h).right_transposed().batched(per_head(hb, hb, sb)), q, k, p)
@@ -164,7 +172,9 @@ def gpu_layer(gpu, L: Layer, fused: bool):
     gpu.split_heads(dctx, do, layout(d, 0))
     ds, dq, dk, dv = matrix(BH * T, T), zeros(BH * hb), zeros(BH * hb), zeros(BH * hb)
     mix_t = MatmulSpec.new(T, h, T).left_transposed().batched(per_head(sb, hb, hb))
-    if fused:
+    if mode == "no_probabilities":
+        gpu.causal_attention_backward(q, k, v, ctx_heads, do, stats, dq, dk, dv, BH, T, T, h, float(L.scale))
+    elif fused:
         gpu.causal_attention_score_grad(do, v, ctx_heads, p, ds, BH, T, T, h, k=k, q_grad=dq, scale=float(L.scale))
         gpu.matmul(mix_t.causal_left(), p, do, dv)
         gpu.matmul(mix_t.scaled(float(L.scale)).causal_left(), ds, q, dk)
@@ -181,22 +191,25 @@ def gpu_layer(gpu, L: Layer, fused: bool):
     linear_backward_gpu(x, w_qkv, dqkv, dw_qkv, db_qkv, dx, d, 3 * d)
     out = {"qkv": qkv, "p": p, "context_heads": ctx_heads, "y": y, "dw_out": dw_out, "db_out": db_out, "ds": ds,
            "dq": dq, "dk": dk, "dv": dv, "dw_qkv": dw_qkv, "db_qkv": db_qkv, "dx": dx}
+    if mode == "no_probabilities":  # P and dS never exist on this path
+        del out["p"], out["ds"]
     return {name: gpu.download(t) for name, t in out.items()}
 
 
-@pytest.mark.parametrize("fused", [False, True], ids=["reference_calls", "fused"])
+@pytest.mark.parametrize("mode", ["reference_calls", "fused", "no_probabilities"])
 @pytest.mark.parametrize("batch,time,width,heads", [
     (2, 512, 256, 8),   # config 0's layer (d = 256, 8 heads of 32), two sequences of 512
     (2, 300, 256, 4),   # head dim 64 (configs 2 and 3), a ragged sequence length
+    (1, 301, 128, 2),   # head dim 64, a sequence length that is not a multiple of 4
 ])
-def test_attention_layer_forward_and_backward(gpu, batch, time, width, heads, fused):
+def test_attention_layer_forward_and_backward(gpu, batch, time, width, heads, mode):
     L = Layer(batch, time, width, heads, seed=time + heads)
-    print(f"layer B={batch} T={time} d={width} heads={heads} fused={fused}", flush=True)
+    print(f"layer B={batch} T={time} d={width} heads={heads} mode={mode}", flush=True)
     expected = oracle_layer(L)
-    got = gpu_layer(gpu, L, fused)
+    got = gpu_layer(gpu, L, mode)
     errors = {}
-    for name, e in expected.items():
-        a = got[name]
+    for name, a in got.items():
+        e = expected[name]
         assert np.all(np.isfinite(a)), name
         errors[name] = oracle.relative_error(e, a)
     print(" ".join(f"{k} {v:.1e}" for k, v in errors.items()))
