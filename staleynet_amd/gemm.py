@@ -270,9 +270,9 @@ class TokenBuffer:
         return self._count
 
     def free(self) -> None:
-        if self.pointer:
-            _library().sn_free_tokens(self._gpu._ctx, ctypes.c_void_p(self.pointer))
-            self.pointer = 0
+        if self.pointer and self._gpu._ctx:  # as Tensor.free: a closed Gpu has no context to free through
+            self._gpu._check(_library().sn_free_tokens(self._gpu._ctx, ctypes.c_void_p(self.pointer)), "free_tokens")
+        self.pointer = 0
 
     def __del__(self):
         try:
