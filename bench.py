@@ -493,6 +493,25 @@ def measure_decode(gpu: Gpu, events: HipEvents, pool_bytes: int = 640 << 20, rep
         w.free()
     sums.free()
     result["stream_read_head_size_gbs"] = round(best, 1)
+    # A plain streaming read of each weight, one launch per weight of the same kind of pool: the
+    # ceiling a single launch reading that many bytes reaches here (best of three grid sizes).
+    result["read_same_weight_us"] = {}
+    for name, k, n in DECODE_SHAPES:
+        copies = max(2, -(-pool_bytes // (4 * k * n)))
+        pool = [gpu.zeros(Shape(k, n)) for _ in range(copies)]
+        best_ms = None
+        for blocks in (256, 512, 1024):
+            part = gpu.zeros(Shape(blocks, 1))
+            graph = REPLAY(gpu.stream, lambda: [gpu.read_sum(w, part) for w in pool])
+            graph.launch()
+            ms = timed(events, gpu.stream, graph.launch, repeats) / copies
+            graph.close()
+            part.free()
+            best_ms = ms if best_ms is None else min(best_ms, ms)
+        for w in pool:
+            w.free()
+        result["read_same_weight_us"][f"{name} {k}x{n}"] = round(best_ms * 1e3, 2)
+    result["per_shape_us"] = {}
     for m in (1, 4, 16):
         for name, k, n in DECODE_SHAPES:
             copies = max(2, -(-pool_bytes // (4 * k * n)))
@@ -507,6 +526,7 @@ def measure_decode(gpu: Gpu, events: HipEvents, pool_bytes: int = 640 << 20, rep
             ms = timed(events, gpu.stream, graph.launch, repeats) / copies
             graph.close()
             result["per_shape_gbs"][f"M={m} {name} {k}x{n}"] = round(decode_bytes(m, k, n) / (ms * 1e-3) / 1e9, 1)
+            result["per_shape_us"][f"M={m} {name} {k}x{n}"] = round(ms * 1e3, 2)
             for w in pool:
                 w.free()
     # One decode token: every product of the 12 blocks and the head, each weight distinct.
@@ -549,6 +569,10 @@ def measure_decode(gpu: Gpu, events: HipEvents, pool_bytes: int = 640 << 20, rep
     result["head_m1_frac_hbm_peak"] = round(head / PEAK_HBM_GBS, 4)
     result["head_m1_frac_stream_read"] = round(head / result["stream_read_gbs"], 4)
     result["head_m1_frac_stream_read_head_size"] = round(head / result["stream_read_head_size_gbs"], 4)
+    result["m1_over_read_same_weight"] = {
+        f"{name} {k}x{n}": round(result["per_shape_us"][f"M=1 {name} {k}x{n}"]
+                                 / result["read_same_weight_us"][f"{name} {k}x{n}"], 2)
+        for name, k, n in DECODE_SHAPES}
     result["token_sequence"] = {"products": len(layers), "mb_per_token": round(token_bytes / 1e6, 1),
                                 "us_per_token": round(ms * 1e3, 1),
                                 "gbs": round(token_bytes / (ms * 1e-3) / 1e9, 1)}

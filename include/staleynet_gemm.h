@@ -434,7 +434,8 @@ int sn_free_tokens(sn_context *context, uint32_t *buffer);
 
 /* ---- the allocation-free variant ------------------------------------------ */
 /* The most scratch sn_matmul_noalloc's kernels use for split-K partial sums
- * (and bf16 staged operands); 64 KiB of arrival counters come on top. */
+ * (and bf16 staged operands); 64 KiB of arrival counters and 4 MiB of
+ * few-row hand-off slots come on top. */
 #define SN_NOALLOC_WORKSPACE_BYTES ((size_t)64 << 20)
 
 /* sn_matmul without a context and without allocating anything. It has no
@@ -445,8 +446,9 @@ int sn_free_tokens(sn_context *context, uint32_t *buffer);
  * with the kernel the spec's precision names (default and F32: fp32 matrix
  * cores; BF16: bf16 inputs). Its scratch is a device array of the
  * library's, one per device, held from the library's load until the process
- * ends: 64 KiB of arrival counters (zero from the load; each kernel resets
- * what it counts) and SN_NOALLOC_WORKSPACE_BYTES for partial sums. The first
+ * ends: 64 KiB of arrival counters and 4 MiB of hand-off slots (zero from
+ * the load; each kernel resets what it touched) and
+ * SN_NOALLOC_WORKSPACE_BYTES for partial sums. The first
  * call on a device only looks up that array's address and enqueues nothing
  * else, so it may itself be under stream capture. A product that would need
  * more partial sums than that splits K into fewer slices (within the fp32

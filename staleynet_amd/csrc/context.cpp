@@ -126,12 +126,16 @@ int sn_context_create_with_workspace(int ordinal, size_t workspace_bytes, sn_con
     if (err == hipSuccess && prop.multiProcessorCount > 0) ctx->env.cu_count = prop.multiProcessorCount;
     if (err == hipSuccess) err = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     if (err == hipSuccess) {
+        // The arrival counters and the hand-off slots: one allocation, zeroed once.
         void* counters = nullptr;
-        err = hipMalloc(&counters, kCounterCount * sizeof(uint32_t));
+        const size_t words = kCounterCount + sn::kHandoffWords;
+        err = hipMalloc(&counters, words * sizeof(uint32_t));
         if (err == hipSuccess) {
             ctx->env.counters = static_cast<uint32_t*>(counters);
             ctx->env.counter_count = kCounterCount;
-            err = hipMemsetAsync(counters, 0, kCounterCount * sizeof(uint32_t), ctx->stream);
+            ctx->env.handoff = ctx->env.counters + kCounterCount;
+            ctx->env.handoff_words = sn::kHandoffWords;
+            err = hipMemsetAsync(counters, 0, words * sizeof(uint32_t), ctx->stream);
             if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);
         }
     }
@@ -391,6 +395,8 @@ int plan_of(const sn_matmul_spec* spec, uint32_t kernel, const float* left, cons
     env.workspace = workspace_bytes > 0 ? reinterpret_cast<float*>(uintptr_t(1) << 44) : nullptr;
     env.counters = reinterpret_cast<uint32_t*>(uintptr_t(1) << 45);
     env.counter_count = kCounterCount;
+    env.handoff = env.counters + kCounterCount;
+    env.handoff_words = sn::kHandoffWords;
     const uint32_t k = sn::kernel_for(kernel, spec->precision);
     sn::LaunchShape s;
     if (column_sums) {

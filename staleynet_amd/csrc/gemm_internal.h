@@ -39,14 +39,23 @@ struct Problem {
 
 // What a launch may use beyond its operands: the context's split-K scratch,
 // its arrival counters (zero between calls; a kernel that increments one
-// resets it before it ends) and the device's compute-unit count.
+// resets it before it ends), the decode kernel's hand-off slots (zero
+// between calls; the kernel that fills a slot clears it before it ends) and
+// the device's compute-unit count.
 struct Env {
     float* workspace = nullptr;
     size_t workspace_bytes = 0;
     uint32_t* counters = nullptr;
     size_t counter_count = 0;
+    uint32_t* handoff = nullptr;
+    size_t handoff_words = 0;
     int cu_count = 256;
 };
+
+// Words of hand-off slots a context (and the allocation-free scratch)
+// holds: 4 MiB, above the most any few-row plan needs (its slices number at
+// most about 448 over all column blocks, each M x 64 words, M <= 16).
+constexpr size_t kHandoffWords = size_t(1) << 20;
 
 // How a product is launched (sn_launch_plan's fields): the kernel family,
 // its tiles, K slices and grid. Each launcher below computes its grid with

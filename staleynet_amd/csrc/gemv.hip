@@ -31,16 +31,20 @@
 //  * With a slab per CU or more (the 16-codebook head: 256 slabs), each slab
 //    streams the whole of K. Narrower weights (768 to 3072 columns: 12 to 48
 //    slabs) split K into slices of whole 16-row groups, for 128-192
-//    workgroups. Each slice writes its partial sums with
-//    device-coherent stores (agent-scope: written through to where every XCD
-//    reads them), waits for them to complete and increments its slab's
-//    arrival counter; the workgroup that arrives last reads the partials with
-//    device-coherent loads, adds them in slice order, applies the
-//    reference's combine and resets the counter. No workgroup waits for
-//    another, the summation order is fixed, and no L2 write-back or
-//    invalidate (a cost of ~100 us per launch here) is needed; the hand-off
-//    costs three device-wide round trips, less than streaming a weight
-//    through a tenth of the CUs would.
+//    workgroups. Every slice but the last of a slab writes its partial sums
+//    into zeroed slots with device-coherent stores (agent scope: written
+//    through to where every XCD reads them) and ends. The last slice, the
+//    slab's highest workgroup id and so the last dispatched, polls the slots
+//    with device-coherent loads until all are written, adds them in slice
+//    order with its own, applies the reference's combine and zeroes the
+//    slots. The summation order is fixed, no L2 write-back or invalidate (a
+//    cost of ~100 us per launch here) is needed, and the hand-off costs one
+//    store's flight and one polling round trip. (An arrival counter, read
+//    by whichever slice finishes last, cost a store acknowledgement, an
+//    atomic and a load round trip: about half of a layer product's time.)
+//    The grid is far smaller than what the device holds at once, so every
+//    slice a last slice waits for is resident or done; the polling still
+//    ends at a deadline, so every wave exits whatever happens.
 #include "gemm_common.h"
 
 namespace sn {
@@ -96,12 +100,37 @@ constexpr int waves_for() { return uses_mfma<MT>() ? 8 : 4; }
 template <int MT, int LPR, int LOADS>
 constexpr int pass_rows() { return waves_for<MT>() * LOADS * (64 / LPR); }
 
+// The hand-off's encoding of a partial sum in a slot word: the bitwise NOT
+// of its bits, with every NaN first made the canonical quiet NaN. The only
+// bits that encode to 0 (an empty slot) are 0xFFFFFFFF, a NaN, which never
+// gets stored, so an empty slot and a written one cannot be confused. (The
+// whole vector is reinterpreted at once: clang's __builtin_bit_cast of an
+// ext_vector element reads element 0, whatever the subscript.)
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ f32x4 handoff_encode(f32x4 v) {
+    u32x4 bits = __builtin_bit_cast(u32x4, v);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float x = v[j];
+        if (x != x) bits[j] = 0x7FC00000u;
+    }
+    return __builtin_bit_cast(f32x4, ~bits);
+}
+__device__ __forceinline__ bool handoff_filled(f32x4 v) {
+    const u32x4 bits = __builtin_bit_cast(u32x4, v);
+    return bits[0] != 0u && bits[1] != 0u && bits[2] != 0u && bits[3] != 0u;
+}
+__device__ __forceinline__ f32x4 handoff_decode(f32x4 v) { return __builtin_bit_cast(f32x4, ~__builtin_bit_cast(u32x4, v)); }
+// Slices polled per batch of loads, and the polling deadline in ticks of
+// the 100 MHz clock s_memrealtime reads (0.5 s).
+constexpr int kHandoffBatch = 16;
+constexpr uint64_t kHandoffDeadlineTicks = 50000000ull;
+
 struct GemvArgs {
     const float* x;
     const float* w;
     float* y;
-    float* ws;
-    uint32_t* counters;
+    uint32_t* handoff;  // zero-initialized slots, (splits - 1) x m x 64 words per column block and batch
     int64_t m, n, k;
     int64_t k_limit;       // keys actually multiplied: k, or the last row's horizon + 1 (causal left)
     int64_t query_offset;  // causal left: x[m][k] counts only for k <= m + query_offset
@@ -131,7 +160,6 @@ __global__ __launch_bounds__(64 * waves_for<MT>()) void gemv_kernel(GemvArgs arg
     constexpr int kXStride = MT == 1 ? 1 : MT + 1;
     __shared__ __attribute__((aligned(16))) float x_pass[2][kPassRows][kXStride];
     __shared__ f32x4 partial[kWaves][MT][LPR];
-    __shared__ int arrived_last;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -327,49 +355,72 @@ __global__ __launch_bounds__(64 * waves_for<MT>()) void gemv_kernel(GemvArgs arg
         return;
     }
 
-    // Partial sums of this slice, written device-coherently; offsets from the
-    // slab's origin in this slice's workspace matrix.
-    const int64_t per_matrix = args.m * args.n;
-    const __amdgpu_buffer_rsrc_t mine =
-        gemm::buffer_of(args.ws + (batch * args.splits + split) * per_matrix + n0);
-    if (owner)
-        gemm::buffer_store4_coherent(mine, out_ok ? int32_t((om * args.n + 4 * oc) * 4) : gemm::kOutOfRange,
-                                     slab_sum);
-    __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are complete device-wide
-    __syncthreads();
-    uint32_t* counter = args.counters + batch * args.column_blocks + blockIdx.x;
-    if (tid == 0)
-        arrived_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                       uint32_t(args.splits - 1);
-    __syncthreads();
-    if (!arrived_last) return;
-
-    // Last to arrive: every slice's partials are complete; add them in slice
-    // order (device-coherent loads, up to 16 slices' in flight at once: the
-    // decode products split K into 3 to 16 slices, and each round trip is
-    // most of a microsecond) and apply the combine.
-    if (out_ok) {
-        constexpr int kBatch = 16;
-        const __amdgpu_buffer_rsrc_t all = gemm::buffer_of(args.ws + batch * args.splits * per_matrix + n0);
-        f32x4 sum = {0.f, 0.f, 0.f, 0.f};
-        for (int s0 = 0; s0 < args.splits; s0 += kBatch) {
-            f32x4 part[kBatch];
+    // Split K: the slices hand their partial sums to the column block's last
+    // slice, the highest workgroup id of the block (so the last dispatched,
+    // after every slice it waits for). Slots are M x 64 words per slice,
+    // zero between calls; a slice writes its encoded partials device-
+    // coherently and ends, and the last slice polls them (device-coherent
+    // loads) until every word is non-zero, adds them in slice order with its
+    // own last, applies the combine and clears the slots. One one-way store
+    // and one polling round trip, where an arrival counter costs a store
+    // acknowledgement, an atomic and a load round trip.
+    const int last = args.splits - 1;
+    const int64_t slice_words = args.m * kColumns;
+    uint32_t* slots = args.handoff + (batch * args.column_blocks + blockIdx.x) * int64_t(last) * slice_words;
+    const int32_t chunk = int32_t((om * kColumns + 4 * oc) * 4);  // this owner's 16 bytes within a slice's slot
+    if (split < last) {
+        if (owner && om < args.m)  // every column of the slab, zeros past n: each slot word gets written
+            gemm::buffer_store4_coherent(gemm::buffer_of(reinterpret_cast<float*>(slots + split * slice_words)), chunk,
+                                         handoff_encode(slab_sum));
+        return;
+    }
+    if (!(owner && om < args.m)) return;
+    const __amdgpu_buffer_rsrc_t all = gemm::buffer_of(reinterpret_cast<float*>(slots));
+    const int32_t slice_bytes = int32_t(slice_words * 4);
+    // Polling ends at a deadline (0.5 s of the 100 MHz real-time clock, far
+    // past any slice's arrival) so that every wave exits whatever happens; a
+    // slot still empty then reads as a NaN partial.
+    const uint64_t deadline = __builtin_amdgcn_s_memrealtime() + kHandoffDeadlineTicks;
+    f32x4 sum = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < last; s0 += kHandoffBatch) {
+        f32x4 part[kHandoffBatch];
+        uint32_t pending = 0;
 #pragma unroll
-            for (int u = 0; u < kBatch; ++u) {
-                const int s = s0 + u;
-                part[u] = gemm::buffer_load4_coherent(
-                    all, s < args.splits ? int32_t((s * per_matrix + om * args.n + 4 * oc) * 4) : gemm::kOutOfRange);
-            }
-#pragma unroll
-            for (int u = 0; u < kBatch; ++u)
-                if (s0 + u < args.splits) sum += part[u];
+        for (int u = 0; u < kHandoffBatch; ++u) {
+            part[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (s0 + u < last) pending |= 1u << u;
         }
+        while (pending != 0) {
+            // Every pending slot's load in flight at once, then the checks.
+            f32x4 got[kHandoffBatch];
+#pragma unroll
+            for (int u = 0; u < kHandoffBatch; ++u)
+                got[u] = gemm::buffer_load4_coherent(
+                    all, (pending >> u) & 1u ? (s0 + u) * slice_bytes + chunk : gemm::kOutOfRange);
+#pragma unroll
+            for (int u = 0; u < kHandoffBatch; ++u) {
+                if (((pending >> u) & 1u) && handoff_filled(got[u])) {
+                    part[u] = got[u];
+                    pending &= ~(1u << u);
+                }
+            }
+            if (pending != 0 && __builtin_amdgcn_s_memrealtime() > deadline) break;
+        }
+#pragma unroll
+        for (int u = 0; u < kHandoffBatch; ++u) {
+            if (s0 + u < last) {
+                sum += handoff_decode(part[u]);
+                gemm::buffer_store4_coherent(all, (s0 + u) * slice_bytes + chunk, f32x4{0.f, 0.f, 0.f, 0.f});
+            }
+        }
+    }
+    sum += slab_sum;
+    if (out_ok) {
         float* dst = args.y + batch * args.stride_y + om * args.n + out_col;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             gemm::write_output(dst + j, sum[j], args.scale, args.accumulate != 0, args.bias, out_col + j);
     }
-    if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 struct GemvPlan {
@@ -426,14 +477,17 @@ GemvPlan gemv_plan(const Problem& p) {
     return plan;
 }
 
+size_t handoff_words(const Problem& p, const GemvPlan& plan) {
+    return size_t(p.batch) * size_t(plan.column_blocks) * size_t(plan.splits - 1) * size_t(p.m) * 64;
+}
+
 template <int MT, int LPR, int LOADS>
 hipError_t launch_rows(const Problem& p, const Env& env, const GemvPlan& plan, hipStream_t stream) {
     GemvArgs args;
     args.x = p.a;
     args.w = p.b;
     args.y = p.c;
-    args.ws = env.workspace;
-    args.counters = env.counters;
+    args.handoff = env.handoff;
     args.m = p.m;
     args.n = p.n;
     args.k = p.k;
@@ -561,7 +615,7 @@ __global__ __launch_bounds__(256) void gemv_nt_kernel(GemvNtArgs a) {
 bool gemv_applies(const Problem& p, const Env& env) {
     // Row-major x (K-contiguous) and row-major W (N-contiguous), aligned for
     // 16-byte loads; no mask or a causal left mask; few rows; grid
-    // dimensions, counters and the split-K workspace large enough; a pass's
+    // dimensions and the hand-off slots large enough; a pass's
     // offsets within 31 bits.
     if (!(p.m >= 1 && p.m <= kMaxRows && p.k >= 1 && (p.mask == SN_MASK_NONE || p.mask == SN_MASK_CAUSAL_LEFT) &&
           p.a_k_contiguous &&
@@ -572,11 +626,10 @@ bool gemv_applies(const Problem& p, const Env& env) {
     if ((plan.pass_rows * p.n + 64) * 4 >= gemm::kMaxBufferOffset) return false;
     if (p.m * p.k * 4 >= gemm::kMaxBufferOffset) return false;  // x's offsets
     if (plan.splits == 1) return true;
-    // Workspace offsets of one batch's partials must fit the 31-bit range.
-    if (int64_t(plan.splits) * p.m * p.n * 4 >= gemm::kMaxBufferOffset) return false;
-    const size_t partials = size_t(plan.splits) * size_t(p.batch) * size_t(p.m) * size_t(p.n) * sizeof(float);
-    return plan.splits <= 65535 && partials <= env.workspace_bytes &&
-           size_t(p.batch) * size_t(plan.column_blocks) <= env.counter_count;
+    // The hand-off slots (splits - 1 slices of m x 64 words per column block
+    // and batch) must fit the environment's; their byte offsets then stay
+    // within 31 bits.
+    return plan.splits <= 65535 && env.handoff != nullptr && handoff_words(p, plan) <= env.handoff_words;
 }
 
 bool gemv_nt_applies(const Problem& p) {
@@ -632,7 +685,7 @@ LaunchShape describe_gemv(const Problem& p) {
     s.batches_per_launch = p.batch;
     s.workgroups = int64_t(plan.column_blocks) * plan.splits * p.batch;
     s.launches = 1;
-    s.workspace_bytes = plan.splits > 1 ? size_t(plan.splits) * size_t(p.batch) * size_t(p.m) * size_t(p.n) * 4 : 0;
+    s.workspace_bytes = 0;  // the split hand-off uses its own zeroed slots, not the workspace
     return s;
 }
 

@@ -1,9 +1,9 @@
 // sn_matmul_noalloc: sn_matmul for callers that cannot allocate device
 // memory (code under HIP graph capture, tight serving loops, harnesses that
 // forbid hipMalloc). It has no counterpart in the reference. Here the
-// kernels' scratch, split-K partial sums (and bf16 staged operands) and the
-// decode kernels' arrival counters, lives in a file-scope device array
-// instead of a context's workspace:
+// kernels' scratch (split-K partial sums and bf16 staged operands, arrival
+// counters, and the decode kernel's hand-off slots) lives in a file-scope
+// device array instead of a context's workspace:
 //  * every device the library runs on holds its own copy of the array from
 //    the moment the code object loads until the process ends;
 //  * on the first call on a device (with that device current) its address
@@ -11,10 +11,11 @@
 //    name in host code is only a stand-in, never a device address. That
 //    set-up puts no work on any stream, so a first call made under stream
 //    capture records only the product's own kernels;
-//  * the counters must be zero between calls: the array has static storage
-//    and no initializer, so the code object's loader zero-fills it, and
-//    every kernel that increments a counter resets it before it ends; the
-//    partial sums are written before they are read within each call;
+//  * the counters and hand-off slots must be zero between calls: the array
+//    has static storage and no initializer, so the code object's loader
+//    zero-fills it, and every kernel that increments a counter or fills a
+//    slot resets it before it ends; the partial sums are written before
+//    they are read within each call;
 //  * every call on a device shares that device's array, so calls that
 //    overlap on one device (two streams, two threads) race.
 // Products whose plan would split K into more partial sums than the array
@@ -29,10 +30,12 @@ namespace {
 
 constexpr size_t kScratchCounters = 16384;                              // as a context has
 constexpr size_t kScratchCounterBytes = kScratchCounters * sizeof(uint32_t);  // 64 KiB
+constexpr size_t kScratchHandoffBytes = sn::kHandoffWords * sizeof(uint32_t);  // 4 MiB
 constexpr size_t kScratchWorkspaceBytes = SN_NOALLOC_WORKSPACE_BYTES;   // 64 MiB
-static_assert(kScratchCounterBytes % 256 == 0, "the workspace part stays 256-byte aligned");
+static_assert((kScratchCounterBytes + kScratchHandoffBytes) % 256 == 0, "the workspace part stays 256-byte aligned");
 
-static __device__ __align__(256) unsigned char scratch[kScratchCounterBytes + kScratchWorkspaceBytes];
+static __device__ __align__(256)
+    unsigned char scratch[kScratchCounterBytes + kScratchHandoffBytes + kScratchWorkspaceBytes];
 
 constexpr int kMaxDevices = 64;
 
@@ -81,7 +84,9 @@ extern "C" int sn_matmul_noalloc(const sn_matmul_spec* spec, const float* left, 
     sn::Env env;
     env.counters = reinterpret_cast<uint32_t*>(d.ptr);
     env.counter_count = kScratchCounters;
-    env.workspace = reinterpret_cast<float*>(d.ptr + kScratchCounterBytes);
+    env.handoff = reinterpret_cast<uint32_t*>(d.ptr + kScratchCounterBytes);
+    env.handoff_words = sn::kHandoffWords;
+    env.workspace = reinterpret_cast<float*>(d.ptr + kScratchCounterBytes + kScratchHandoffBytes);
     env.workspace_bytes = kScratchWorkspaceBytes;
     env.cu_count = d.cu_count;
     const sn::Problem p = sn::problem_of(spec, left, right, output, nullptr);

@@ -348,3 +348,33 @@ def test_random_column_sum_plans_keep_the_product_plan(inputs, outputs, rows, cu
     elif product is not None:
         assert (fused.path, fused.tiles_m, fused.tiles_n, fused.splits) == \
             (product.path, product.tiles_m, product.tiles_n, product.splits)
+
+
+# The few-row kernel's split hand-off uses its own zeroed slots (4 Mi words per context and in the
+# allocation-free scratch): (splits - 1) slices of rows x 64 words per column block and matrix.
+HANDOFF_WORDS = 1 << 20
+
+
+@settings(max_examples=300, deadline=None)
+@given(m=st.integers(1, 16), n=st.integers(1, 20000), k=st.integers(1, 200000),
+       batch=st.sampled_from([1, 1, 2, 3, 12, 200]), cus=st.sampled_from([80, 256, 304]))
+def test_few_row_split_plans_fit_the_handoff_slots(m, n, k, batch, cus):
+    n = max(4, n // 4 * 4)
+    spec = MatmulSpec.new(m, n, k)
+    if batch > 1:
+        spec = spec.batched(BatchStrides(batch, m * k, k * n, m * n))
+    plan = gemm.plan(spec, cu_count=cus)
+    if plan.path != gemm.PATH_FEW_ROWS:
+        return
+    assert plan.workspace_bytes == 0  # the hand-off never touches the workspace
+    assert plan.tiles_n == -(-n // 64) and plan.workgroups == plan.tiles_n * plan.splits * batch
+    assert batch * plan.tiles_n * (plan.splits - 1) * m * 64 <= HANDOFF_WORDS
+
+
+def test_decode_products_keep_the_few_row_path():
+    # Every config-4 product (M = 1, 4, 16 against the 111.5M model's weights and the head).
+    for m in (1, 4, 16):
+        for k, n in ((768, 2304), (768, 768), (768, 3072), (3072, 768), (768, 16384)):
+            plan = gemm.plan(MatmulSpec.new(m, n, k))
+            assert plan.path == gemm.PATH_FEW_ROWS, (m, k, n, plan.path)
+            assert plan.splits == 1 or plan.splits * plan.tiles_n <= 448
