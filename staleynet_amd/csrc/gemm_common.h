@@ -451,17 +451,44 @@ __device__ __forceinline__ void write_output(float* dst, float sum, float scale,
     *dst = value;
 }
 
-// Writes a wave's accumulators: 32x32 blocks, element r of a block at row
-// 8(r/4) + 4*half + r%4 and column lane%32. `partial` writes raw sums to the
-// split-K workspace; otherwise the reference's combine, with causal-masked
-// outputs written 0 (overwrite) or left alone (accumulate).
-template <class T, bool BUF>
+// Where a wave's accumulators sit in its WTM x WTN sub-tile. Element r of
+// 32x32 block (i, j) in lane l is MFMA row q = 8(r/4) + 4(l/32) + r%4 and
+// MFMA column l%32. Normally block i covers rows 32i .. 32i + 31 (row 32i +
+// q) and block j columns 32j + l%32. A paired side (two blocks whose
+// fragments a lane reads as adjacent rows of a row-contiguous operand, one
+// 8-byte LDS read per k) interleaves them instead: block i covers rows
+// 2q + i, block j columns 2(l%32) + j.
+template <bool PAIR_M, bool PAIR_N>
+struct TileMap {
+    // Row within the wave's sub-tile: a per-lane part (half = l/32) and a
+    // part per (block, element) that does not depend on the lane.
+    __device__ __forceinline__ static constexpr int row_lane(int half) { return PAIR_M ? 8 * half : 4 * half; }
+    __device__ __forceinline__ static constexpr int row_elem(int i, int r) {
+        return PAIR_M ? 2 * (8 * (r / 4) + (r % 4)) + i : 32 * i + 8 * (r / 4) + (r % 4);
+    }
+    __device__ __forceinline__ static constexpr int col_lane(int col_in_block) {
+        return PAIR_N ? 2 * col_in_block : col_in_block;
+    }
+    __device__ __forceinline__ static constexpr int col_elem(int j) { return PAIR_N ? j : 32 * j; }
+};
+
+// Writes a wave's accumulators (TileMap gives each element's place).
+// `partial` writes raw sums to the split-K workspace; otherwise the
+// reference's combine, with causal-masked outputs written 0 (overwrite) or
+// left alone (accumulate).
+template <class T, bool BUF, bool PAIR_M = false, bool PAIR_N = false>
 __device__ __forceinline__ void write_tile(const Args& args, const f32x16 (&acc)[T::FM][T::FN], float* out,
                                            int64_t m0, int64_t n0, int wave_m, int wave_n, int lane, bool partial) {
+    using Map = TileMap<PAIR_M, PAIR_N>;
+    static_assert(!PAIR_M || T::FM == 2, "pairs of row blocks");
+    static_assert(!PAIR_N || T::FN == 2, "pairs of column blocks");
     const int col_in_block = lane & 31;
     const int half = lane >> 5;
     const bool accumulate = args.accumulate != 0;
     const bool output_causal = args.mask == int(SN_MASK_CAUSAL_OUTPUT);
+    // The lane's first row and column within the tile.
+    const int lane_row = wave_m * T::WTM + Map::row_lane(half);
+    const int lane_col = wave_n * T::WTN + Map::col_lane(col_in_block);
     if constexpr (BUF) {
         // Offsets from the tile origin; kOutOfRange drops stores outside the matrix.
         const __amdgpu_buffer_rsrc_t rsrc = buffer_of(out + m0 * args.n + n0);
@@ -481,29 +508,43 @@ __device__ __forceinline__ void write_tile(const Args& args, const f32x16 (&acc)
             const bool add_bias = !partial && args.bias != nullptr;
             float bias_value[T::FN];
 #pragma unroll
-            for (int j = 0; j < T::FN; ++j)
-                bias_value[j] = add_bias ? args.bias[n0 + wave_n * T::WTN + 32 * j + col_in_block] : 0.f;
+            for (int j = 0; j < T::FN; ++j) bias_value[j] = add_bias ? args.bias[n0 + lane_col + Map::col_elem(j)] : 0.f;
             // col - row - offset of the lane's element at block (0, 0), r = 0.
             // (Clamped to 32 bits: beyond +-2^30 every element is on the same side.)
-            const int64_t diagonal64 = n0 + wave_n * T::WTN + col_in_block - (m0 + wave_m * T::WTM + 4 * half) -
-                                       args.query_offset;
+            const int64_t diagonal64 = n0 + lane_col - (m0 + lane_row) - args.query_offset;
             const int diagonal = int(max(min(diagonal64, int64_t(1) << 30), -(int64_t(1) << 30)));
-#pragma unroll
-            for (int j = 0; j < T::FN; ++j) {
-                const int32_t column_offset =
-                    int32_t(((wave_m * T::WTM + 4 * half) * args.n + wave_n * T::WTN + 32 * j + col_in_block) * 4);
+            auto value_of = [&](int i, int j, int r) __attribute__((always_inline)) {
+                float value = scale * acc[i][j][r];
+                if (any_masked) value = diagonal + Map::col_elem(j) - Map::row_elem(i, r) > 0 ? 0.f : value;
+                if (add_bias) value = value + bias_value[j];
+                return value;
+            };
+            if constexpr (PAIR_N) {
+                // The lane's two columns are adjacent: one 8-byte store per element pair.
+                typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+                const int32_t column_offset = int32_t((lane_row * args.n + lane_col) * 4);
 #pragma unroll
                 for (int i = 0; i < T::FM; ++i)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
-                        const int row = 32 * i + 8 * (r / 4) + (r % 4);
-                        const int32_t row_offset = int32_t(row * args.n * 4);
-                        float value = scale * acc[i][j][r];
-                        if (any_masked) value = diagonal + 32 * j - row > 0 ? 0.f : value;
-                        if (add_bias) value = value + bias_value[j];
-                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, value), rsrc, column_offset,
-                                                              row_offset, 0);
+                        const int32_t row_offset = int32_t(Map::row_elem(i, r) * args.n * 4);
+                        const u32x2_t pair = {__builtin_bit_cast(uint32_t, value_of(i, 0, r)),
+                                              __builtin_bit_cast(uint32_t, value_of(i, 1, r))};
+                        __builtin_amdgcn_raw_buffer_store_b64(pair, rsrc, column_offset, row_offset, 0);
                     }
+            } else {
+#pragma unroll
+                for (int j = 0; j < T::FN; ++j) {
+                    const int32_t column_offset = int32_t((lane_row * args.n + lane_col + Map::col_elem(j)) * 4);
+#pragma unroll
+                    for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            const int32_t row_offset = int32_t(Map::row_elem(i, r) * args.n * 4);
+                            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, value_of(i, j, r)), rsrc,
+                                                                  column_offset, row_offset, 0);
+                        }
+                }
             }
             return;
         }
@@ -513,8 +554,8 @@ __device__ __forceinline__ void write_tile(const Args& args, const f32x16 (&acc)
             for (int j = 0; j < T::FN; ++j)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int row = wave_m * T::WTM + 32 * i + 8 * (r / 4) + 4 * half + (r % 4);
-                    const int col = wave_n * T::WTN + 32 * j + col_in_block;
+                    const int row = lane_row + Map::row_elem(i, r);
+                    const int col = lane_col + Map::col_elem(j);
                     const bool inside = m0 + row < args.m && n0 + col < args.n;
                     const int32_t offset = inside ? int32_t((row * args.n + col) * 4) : kOutOfRange;
                     const float sum = acc[i][j][r];
@@ -537,8 +578,8 @@ __device__ __forceinline__ void write_tile(const Args& args, const f32x16 (&acc)
             for (int j = 0; j < T::FN; ++j)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int64_t row = m0 + wave_m * T::WTM + 32 * i + 8 * (r / 4) + 4 * half + (r % 4);
-                    const int64_t col = n0 + wave_n * T::WTN + 32 * j + col_in_block;
+                    const int64_t row = m0 + lane_row + Map::row_elem(i, r);
+                    const int64_t col = n0 + lane_col + Map::col_elem(j);
                     if (row < args.m && col < args.n) {
                         float* dst = out + row * args.n + col;
                         if (partial) {
