@@ -13,7 +13,9 @@
 //  * A workgroup of 4 waves (8 on the matrix-core path) owns a slab of 64
 //    columns; a lane owns 4
 //    consecutive columns, 16 lanes read one 256-byte row piece and one wave
-//    load covers 4 rows. A pass is 16 (8 for 3-4 rows of x) 16-byte
+//    load covers 4 rows. A single row of x against a weight that K is split
+//    for takes 32-column slabs instead (8 lanes per 128-byte piece, 8 rows
+//    per wave load): twice the workgroups per slice. A pass is 16 (8 for 3-4 rows of x) 16-byte
 //    loads in flight per lane, rows dealt to the waves in groups of 4; the
 //    next pass's loads are issued before the current one is multiplied (two
 //    register sets, loads issued unconditionally so that the compiler's
@@ -76,6 +78,17 @@ constexpr int kSplitTargetFewRowsNarrow = 96;
 constexpr int kNarrowSlabs = 16;
 constexpr int kSplitTargetManyRows = 192;
 constexpr int kMinSliceGroups = 8;
+// One row of x against one weight that K gets split for (the layer products
+// of a decode step): 32-column slabs, 8 lanes per 128-byte row piece, so
+// twice the workgroups stream a slice of the same length. On the c4 layer
+// weights at M = 1 (graph replay) the products took 4.9 / 5.6 / 6.2 / 6.8 us
+// (out / qkv / up / down) against 5.3 / 6.2 / 6.4 / 7.6 with 64 columns;
+// 16-column slabs were slower for each. Split from fewer than 96 such slabs
+// (the 3072-wide up product, 96 slabs, took 6.2 us whole against 6.4 in two
+// slices) into slices for about 192 workgroups.
+constexpr int kNarrowLanes = 8;
+constexpr int kUnsplitNarrowSlabs = 96;
+constexpr int kSplitTargetNarrow = 192;
 
 // Rows of x from which the products go to the matrix cores: 16 output rows
 // cost one v_mfma_f32_16x16x4f32 per 4 rows x 16 columns of W, where the
@@ -357,7 +370,7 @@ __global__ __launch_bounds__(64 * waves_for<MT>()) void gemv_kernel(GemvArgs arg
 
     // Split K: the slices hand their partial sums to the column block's last
     // slice, the highest workgroup id of the block (so the last dispatched,
-    // after every slice it waits for). Slots are M x 64 words per slice,
+    // after every slice it waits for). Slots are M x (slab width) words per slice,
     // zero between calls; a slice writes its encoded partials device-
     // coherently and ends, and the last slice polls them (device-coherent
     // loads) until every word is non-zero, adds them in slice order with its
@@ -424,7 +437,8 @@ __global__ __launch_bounds__(64 * waves_for<MT>()) void gemv_kernel(GemvArgs arg
 }
 
 struct GemvPlan {
-    int lanes_per_row;  // lanes per 256-byte row piece: 64-column slabs
+    int lanes_per_row;  // lanes per row piece: 16 (64-column slabs) or kNarrowLanes
+    int narrow_loads;   // loads in flight per lane on the 32-column slabs
     int column_blocks;
     int splits;
     int64_t k_per_split;
@@ -454,16 +468,22 @@ GemvPlan gemv_plan(const Problem& p) {
     GemvPlan plan;
     plan.lanes_per_row = 16;
     plan.column_blocks = int((p.n + 63) / 64);
+    if (p.m == 1 && p.batch == 1 && plan.column_blocks < kUnsplitSlabs) {
+        plan.lanes_per_row = kNarrowLanes;
+        plan.column_blocks = int((p.n + 4 * kNarrowLanes - 1) / (4 * kNarrowLanes));
+    }
+    const bool narrow = plan.lanes_per_row == kNarrowLanes;
     const int64_t slabs = int64_t(plan.column_blocks) * p.batch;
     int64_t rows_per_split = std::max<int64_t>(k, 1);
-    if (slabs < kUnsplitSlabs) {
+    if (slabs < (narrow ? kUnsplitNarrowSlabs : kUnsplitSlabs)) {
         // Enough slices for about `target` workgroups, each a whole
         // number of 16-row groups (4 waves x 4 rows; on the 8-wave path a
         // slice's last group may leave waves idle).
         const int64_t groups = (std::max<int64_t>(k, 1) + 15) / 16;
         // Narrow weights (16 column blocks or fewer: the 768-wide out and down
         // products) do better with fewer, longer slices when there are few rows.
-        const int64_t target = p.m > 4 ? kSplitTargetManyRows
+        const int64_t target = narrow ? kSplitTargetNarrow
+                               : p.m > 4 ? kSplitTargetManyRows
                                : slabs <= kNarrowSlabs ? kSplitTargetFewRowsNarrow : kSplitTargetFewRows;
         // Slices of at least 8 groups (128 rows): the 768-deep out product
         // took 5-11 % less time in 6 slices than in 8 (M = 1) or 16 (M = 16).
@@ -473,12 +493,18 @@ GemvPlan gemv_plan(const Problem& p) {
     }
     plan.k_per_split = rows_per_split;
     plan.splits = int((std::max<int64_t>(k, 1) + rows_per_split - 1) / rows_per_split);
-    plan.pass_rows = pass_rows_for<16>(p.m, plan.splits > 1);
+    // A pass no longer than a slice: 8 loads (256 rows) from 256-row slices,
+    // else 4 (the 128-row slices of the out product: 4.9 us against 5.1+).
+    plan.narrow_loads = rows_per_split >= 256 ? 8 : 4;
+    plan.pass_rows = !narrow                  ? pass_rows_for<16>(p.m, plan.splits > 1)
+                     : plan.narrow_loads == 8 ? pass_rows<1, kNarrowLanes, 8>()
+                                              : pass_rows<1, kNarrowLanes, 4>();
     return plan;
 }
 
 size_t handoff_words(const Problem& p, const GemvPlan& plan) {
-    return size_t(p.batch) * size_t(plan.column_blocks) * size_t(plan.splits - 1) * size_t(p.m) * 64;
+    return size_t(p.batch) * size_t(plan.column_blocks) * size_t(plan.splits - 1) * size_t(p.m) * 4 *
+           size_t(plan.lanes_per_row);
 }
 
 template <int MT, int LPR, int LOADS>
@@ -626,7 +652,7 @@ bool gemv_applies(const Problem& p, const Env& env) {
     if ((plan.pass_rows * p.n + 64) * 4 >= gemm::kMaxBufferOffset) return false;
     if (p.m * p.k * 4 >= gemm::kMaxBufferOffset) return false;  // x's offsets
     if (plan.splits == 1) return true;
-    // The hand-off slots (splits - 1 slices of m x 64 words per column block
+    // The hand-off slots (splits - 1 slices of m x (slab width) words per column block
     // and batch) must fit the environment's; their byte offsets then stay
     // within 31 bits.
     return plan.splits <= 65535 && env.handoff != nullptr && handoff_words(p, plan) <= env.handoff_words;
@@ -708,6 +734,9 @@ LaunchShape describe_gemv_nt(const Problem& p) {
 hipError_t launch_gemv(const Problem& p, const Env& env, hipStream_t stream) {
     if (!gemv_applies(p, env)) return hipErrorNotSupported;
     const GemvPlan plan = gemv_plan(p);
+    if (plan.lanes_per_row == kNarrowLanes)
+        return plan.narrow_loads == 8 ? launch_rows<1, kNarrowLanes, 8>(p, env, plan, stream)
+                                      : launch_rows<1, kNarrowLanes, 4>(p, env, plan, stream);
     return launch_width<16>(p, env, plan, stream);
 }
 

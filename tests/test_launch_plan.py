@@ -99,7 +99,9 @@ def test_every_tile_and_slice_is_launched_once(label, spec, kernel):
             assert plan.k_per_split % step == 0
         check_tiled_cover(plan)
     elif plan.path == gemm.PATH_FEW_ROWS:
-        assert spec.rows <= 16 and plan.tiles_n == -(-spec.cols // 64) and plan.k_per_split % 16 == 0
+        width = few_row_slab_width(spec.rows, spec.cols, spec.batch.count)
+        assert plan.tile_cols == width and plan.tiles_n == -(-spec.cols // width)
+        assert spec.rows <= 16 and plan.k_per_split % 16 == 0
         assert plan.workgroups == plan.tiles_n * plan.splits * spec.batch.count
     else:
         assert plan.path == gemm.PATH_FEW_ROWS_NT and spec.rows <= 4 and plan.splits == 1
@@ -351,8 +353,14 @@ def test_random_column_sum_plans_keep_the_product_plan(inputs, outputs, rows, cu
 
 
 # The few-row kernel's split hand-off uses its own zeroed slots (4 Mi words per context and in the
-# allocation-free scratch): (splits - 1) slices of rows x 64 words per column block and matrix.
+# allocation-free scratch): (splits - 1) slices of rows x (slab width) words per column block and matrix.
 HANDOFF_WORDS = 1 << 20
+
+
+def few_row_slab_width(m, n, batch):
+    """Columns per workgroup of the few-row kernel: 32 for one row of x against one weight narrower
+    than 256 64-column slabs (a weight K is split for), else 64."""
+    return 32 if m == 1 and batch == 1 and -(-n // 64) < 256 else 64
 
 
 @settings(max_examples=300, deadline=None)
@@ -367,8 +375,10 @@ def test_few_row_split_plans_fit_the_handoff_slots(m, n, k, batch, cus):
     if plan.path != gemm.PATH_FEW_ROWS:
         return
     assert plan.workspace_bytes == 0  # the hand-off never touches the workspace
-    assert plan.tiles_n == -(-n // 64) and plan.workgroups == plan.tiles_n * plan.splits * batch
-    assert batch * plan.tiles_n * (plan.splits - 1) * m * 64 <= HANDOFF_WORDS
+    width = few_row_slab_width(m, n, batch)
+    assert plan.tile_cols == width and plan.tiles_n == -(-n // width)
+    assert plan.workgroups == plan.tiles_n * plan.splits * batch
+    assert batch * plan.tiles_n * (plan.splits - 1) * m * width <= HANDOFF_WORDS
 
 
 def test_decode_products_keep_the_few_row_path():
@@ -378,3 +388,16 @@ def test_decode_products_keep_the_few_row_path():
             plan = gemm.plan(MatmulSpec.new(m, n, k))
             assert plan.path == gemm.PATH_FEW_ROWS, (m, k, n, plan.path)
             assert plan.splits == 1 or plan.splits * plan.tiles_n <= 448
+
+
+def test_single_row_layer_products_take_the_measured_slabs_and_slices():
+    # M = 1 against the config-4 weights: 32-column slabs for the layer products, in the slices that
+    # measured fastest (qkv 3, out 6, up whole; down 8, as fast as 6), and 64-column slabs for the head
+    # (256 of them).
+    for k, n, width, splits in ((768, 2304, 32, 3), (768, 768, 32, 6), (768, 3072, 32, 1), (3072, 768, 32, 8),
+                                (768, 16384, 64, 1)):
+        plan = gemm.plan(MatmulSpec.new(1, n, k))
+        assert (plan.tile_cols, plan.splits) == (width, splits), (k, n, plan.tile_cols, plan.splits)
+    # Two rows, or a batch of matrices, keep the 64-column slabs.
+    assert gemm.plan(MatmulSpec.new(2, 768, 768)).tile_cols == 64
+    assert gemm.plan(MatmulSpec.new(1, 64, 1408).batched(BatchStrides(12, 1408, 1408 * 64, 64))).tile_cols == 64
