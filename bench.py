@@ -270,6 +270,17 @@ def measure_set(gpu: Gpu, events: HipEvents, calls, steps: int, warmup: int, pre
     return ms_per_step, per_call
 
 
+def replayed_step_ms(gpu: Gpu, events: HipEvents, calls, steps: int, precision=Precision.Default) -> float:
+    """Milliseconds per step with the step's calls captured once into a HIP graph and replayed:
+    the kernels back to back without the host's per-call cost (ctypes, and the events that
+    measure_set records between launches), which sets the rate of sets of short products."""
+    graph = REPLAY(gpu.stream, lambda: run_step(gpu, calls, precision))
+    try:
+        return timed(events, gpu.stream, graph.launch, steps)
+    finally:
+        graph.close()
+
+
 def summarize_set(calls, per_call_ms, peak):
     layouts, shapes = {}, {}
     for i, (_, layout, spec, _) in enumerate(calls):
@@ -789,8 +800,13 @@ def measure_published(gpu: Gpu, events: HipEvents, set_per_shape: dict):
         flops = sum(spec.flops() for _, _, spec, _ in calls)
         ms, per_call = measure_set(gpu, events, calls, 3, 1)
         _, per_layout, per_shape = summarize_set(calls, per_call, PEAK_FP32_TFLOPS)
+        replay_ms = replayed_step_ms(gpu, events, calls, 5)
         result[key] = {"tflops": round(flops / (ms * 1e-3) / 1e12, 2), "ms_per_step": round(ms, 3),
                        "frac_fp32_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 4),
+                       "graph_replay": {"tflops": round(flops / (replay_ms * 1e-3) / 1e12, 2),
+                                        "ms_per_step": round(replay_ms, 3),
+                                        "frac_fp32_peak": round(flops / (replay_ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS,
+                                                                4)},
                        "gemms": len(calls), "tflop": round(flops / 1e12, 4), "per_layout": per_layout,
                        "per_shape_tflops": per_shape}
         for buf in buffers:
@@ -812,12 +828,15 @@ def measure_shard_share(gpu: Gpu, events: HipEvents, shards: int = 8):
     flops = sum(spec.flops() for _, _, spec, _ in calls)
     ms, per_call = measure_set(gpu, events, calls, 3, 1)
     _, per_layout, per_shape = summarize_set(calls, per_call, PEAK_FP32_TFLOPS)
+    replay_ms = replayed_step_ms(gpu, events, calls, 3)
     for buf in buffers:
         for t in (buf.x, buf.w, buf.dy, buf.y, buf.dx, buf.dw):
             t.free()
     return {"shards": shards, "per_shape_tflops": per_shape, "tokens": model["tokens"], "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
             "frac_fp32_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 4),
-            "ms_per_step": round(ms, 3), "per_layout": per_layout}
+            "ms_per_step": round(ms, 3), "per_layout": per_layout,
+            "graph_replay": {"tflops": round(flops / (replay_ms * 1e-3) / 1e12, 2), "ms_per_step": round(replay_ms, 3),
+                             "frac_fp32_peak": round(flops / (replay_ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 4)}}
 
 
 # ---- the vendor library on the same set, and the clock under load (context) -------------

@@ -419,6 +419,7 @@ int plan_of(const sn_matmul_spec* spec, uint32_t kernel, const float* left, cons
     plan->tiles_m = uint32_t(s.tiles_m);
     plan->tiles_n = uint32_t(s.tiles_n);
     plan->splits = uint32_t(s.splits);
+    plan->persistent_grid = uint32_t(s.persistent_grid);
     plan->k_per_split = uint64_t(s.k_per_split);
     plan->batches_per_launch = uint64_t(s.batches_per_launch);
     plan->workgroups = uint64_t(s.workgroups);

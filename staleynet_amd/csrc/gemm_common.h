@@ -113,6 +113,7 @@ struct Args {
     const float* bias;  // null, or one value per column added after the combine
     float* column_sums; // null, or the right operand's column sums over K, accumulated (see Problem)
     int32_t streaming_output;  // nonzero: the output tiles go out with kStreaming stores
+    int32_t persistent_items;  // persistent kernels: the work items the grid loops over
 };
 
 template <int BM_, int BN_, int BK_, int WAVES_M_, int WAVES_N_>
@@ -486,7 +487,10 @@ struct TileMap {
 // `partial` writes raw sums to the split-K workspace; otherwise the
 // reference's combine, with causal-masked outputs written 0 (overwrite) or
 // left alone (accumulate). POLICY: the buffer stores' cache policy.
-template <class T, bool BUF, bool PAIR_M = false, bool PAIR_N = false, int32_t POLICY = 0>
+// INTERIOR_ONLY: the caller guarantees an interior tile that reads nothing
+// back (partial, or overwrite), so only that path is compiled.
+template <class T, bool BUF, bool PAIR_M = false, bool PAIR_N = false, int32_t POLICY = 0,
+          bool INTERIOR_ONLY = false>
 __device__ __forceinline__ void write_tile(const Args& args, const f32x16 (&acc)[T::FM][T::FN], float* out,
                                            int64_t m0, int64_t n0, int wave_m, int wave_n, int lane, bool partial) {
     using Map = TileMap<PAIR_M, PAIR_N>;
@@ -507,8 +511,8 @@ __device__ __forceinline__ void write_tile(const Args& args, const f32x16 (&acc)
         // each element's row in a scalar offset, no per-element selects or
         // branches. The general path below costs ~20 instructions per element,
         // which at K = 64 outweighed the tile's MFMAs.
-        const bool interior = m0 + T::BM <= args.m && n0 + T::BN <= args.n;
-        if (interior && (partial || !accumulate)) {
+        const bool interior = INTERIOR_ONLY || (m0 + T::BM <= args.m && n0 + T::BN <= args.n);
+        if (INTERIOR_ONLY || (interior && (partial || !accumulate))) {
             // Split-K partials are raw sums: scale 1, which is exact. Tiles
             // that cross the causal diagonal write 0 where masked (a compare
             // and a select per element, still no branch).
@@ -558,6 +562,7 @@ __device__ __forceinline__ void write_tile(const Args& args, const f32x16 (&acc)
             }
             return;
         }
+        if constexpr (INTERIOR_ONLY) return;
 #pragma unroll
         for (int i = 0; i < T::FM; ++i)
 #pragma unroll
@@ -757,6 +762,7 @@ Args make_args(const Problem& p, const Env& env, const Plan& plan) {
     args.bias = p.bias;
     args.column_sums = p.column_sums;
     args.streaming_output = 0;
+    args.persistent_items = 0;
     return args;
 }
 

@@ -593,6 +593,183 @@ __device__ __forceinline__ void dma_tile(const Args& args) {
         write_tile<T, true, PM, PN>(args, acc, out, m0, n0, wave_m, wave_n, lane, partial);
 }
 
+// The fp32 tile schedule of dma_tile (two LDS stages, one barrier per K-step
+// between its chunks) as a persistent loop: each workgroup takes work items
+// blockIdx.x, blockIdx.x + gridDim.x, ... (a work item is a matrix, K slice
+// and tile, mapped by tile_coordinates as the one-tile kernels map their
+// workgroups) for unmasked products whose every tile has an even number of
+// K-steps. The two loads a tile would issue past its last K-step (zeros, in
+// dma_tile) fetch the next item's first two K-steps instead, so when a tile's
+// last MFMAs are issued the next one's first stage is in LDS and its second
+// in flight. Its output stores then go out behind those loads, and the next
+// tile's first barrier waits for the loads only: load and store completions
+// are counted in issue order (vmcnt), so waiting until at most as many
+// operations are outstanding as the epilogue issued means every load before
+// it has landed. The stores then drain under the next tile's first K-step,
+// where the one-tile kernel ended the workgroup and started the next one's
+// loads only after them.
+template <class T, bool A_K, bool B_K>
+__device__ __forceinline__ void dma_persistent(const Args& args) {
+    constexpr int FEED = kFeedF32;
+    constexpr int WAVES = T::THREADS / 64;
+    constexpr int A_SLOTS = T::BM * T::BK / 4;
+    constexpr int B_SLOTS = T::BN * T::BK / 4;
+    __shared__ f32x4 a0[A_SLOTS], b0[B_SLOTS], a1[A_SLOTS], b1[B_SLOTS];
+    f32x4* const stage_a[2] = {a0, a1};
+    f32x4* const stage_b[2] = {b0, b1};
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wave_m = wave / T::WAVES_N;
+    const int wave_n = wave % T::WAVES_N;
+    const int items = args.persistent_items;
+    const int stride = int(gridDim.x);
+
+    // A work item's tile row and column, matrix and K slice.
+    struct Item {
+        int tm, tn, batch_local, split;
+    };
+    auto item_of = [&](int w) {
+        Item it;
+        tile_coordinates(w, items, args.tiles_m, args.tiles_n, args.splits, it.batch_local, it.split, it.tm, it.tn);
+        return it;
+    };
+    auto k_begin_of = [&](const Item& it) { return int64_t(it.split) * args.k_per_split; };
+    auto k_end_of = [&](const Item& it) { return min(args.k, k_begin_of(it) + args.k_per_split); };
+    auto a_of = [&](const Item& it) {
+        const int64_t m0 = int64_t(it.tm) * T::BM;
+        return args.a + (args.batch_base + it.batch_local) * args.stride_a + (A_K ? m0 * args.lda : m0);
+    };
+    auto b_of = [&](const Item& it) {
+        const int64_t n0 = int64_t(it.tn) * T::BN;
+        return args.b + (args.batch_base + it.batch_local) * args.stride_b + (B_K ? n0 * args.ldb : n0);
+    };
+
+    int w = int(blockIdx.x);
+    if (w >= items) return;
+    Item cur = item_of(w);
+    // The item whose loads are being issued: tile origins and K end.
+    const float* ld_a = a_of(cur);
+    const float* ld_b = b_of(cur);
+    int64_t ld_end = k_end_of(cur);
+    OperandFor<A_K, T::BM, WAVES> oa;
+    OperandFor<B_K, T::BN, WAVES> ob;
+    // Every tile is interior (checked on the host), so the row bounds of the
+    // loaders' offsets are the same for every item.
+    oa.init(args.lda, 0, T::BM, lane, wave);
+    ob.init(args.ldb, 0, T::BN, lane, wave);
+    auto issue = [&](const f32x4* sa, const f32x4* sb, int64_t k0) {
+        if constexpr (A_K) oa.issue(sa, ld_a, k0, ld_end, wave);
+        else oa.issue(sa, ld_a, args.lda, k0, ld_end, wave);
+        if constexpr (B_K) ob.issue(sb, ld_b, k0, ld_end, wave);
+        else ob.issue(sb, ld_b, args.ldb, k0, ld_end, wave);
+    };
+
+    constexpr int LOADS_PER_STEP = (T::BM + T::BN) / (8 * WAVES);
+    constexpr int DS = (A_K ? 2 * T::FM : paired<T, A_K, true>() ? 4 : 4 * T::FM) +
+                       (B_K ? 2 * T::FN : paired<T, B_K, false>() ? 4 : 4 * T::FN);
+    constexpr bool PM = paired<T, A_K, true>(), PN = paired<T, B_K, false>();
+    // Store instructions of write_tile's interior path, capped at what the
+    // 6-bit count can hold (then at least the loads before them are done).
+    constexpr int STORES = (PN ? 1 : T::FN) * T::FM * 16;
+    constexpr int AFTER_STORES = STORES < 63 ? STORES : 63;
+    Chunk<T> f0, f1;
+    f32x16 acc[T::FM][T::FN];
+    auto first_half = [&](auto stage) {
+        constexpr int S = decltype(stage)::value;
+        __builtin_amdgcn_sched_barrier(0);
+        read_chunk<T, A_K, B_K>(oa, ob, stage_a[S], stage_b[S], 1, f1, lane, wave_m, wave_n);
+        multiply_chunk<T, FEED>(f0, acc);
+        interleave<T, FEED, 0, DS>();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto sync = [&] {
+        wait_loads<0>();
+        lds_barrier();
+    };
+    // READ_NEXT: also read the next stage's chunk 0 (not for a tile's last
+    // half: the next tile's first fragments are read after the epilogue, so
+    // that they are not held in registers across it).
+    auto second_half = [&](auto stage, int64_t k_load, auto read_next) {
+        constexpr int S = decltype(stage)::value;
+        constexpr int N = (S + 1) % 2;
+        constexpr bool READ_NEXT = decltype(read_next)::value;
+        __builtin_amdgcn_sched_barrier(0);
+        issue(stage_a[S], stage_b[S], k_load);
+        if constexpr (READ_NEXT) read_chunk<T, A_K, B_K>(oa, ob, stage_a[N], stage_b[N], 0, f0, lane, wave_m, wave_n);
+        multiply_chunk<T, FEED>(f1, acc);
+        interleave<T, FEED, LOADS_PER_STEP, READ_NEXT ? DS : DS / 2>();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using Read = std::true_type;
+    using NoRead = std::false_type;
+
+    {
+        const int64_t k_begin = k_begin_of(cur);
+        issue(a0, b0, k_begin);
+        issue(a1, b1, k_begin + T::BK);
+    }
+    wait_loads<LOADS_PER_STEP>();
+    lds_barrier();
+    bool first = true;
+    for (;;) {
+        read_chunk<T, A_K, B_K>(oa, ob, a0, b0, 0, f0, lane, wave_m, wave_n);
+#pragma unroll
+        for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+            for (int j = 0; j < T::FN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+        // Step 0's first half; then its second stage is waited for (issued
+        // before the previous tile's stores, which may stay in flight).
+        first_half(I0{});
+        if (first) wait_loads<0>();
+        else wait_loads<AFTER_STORES>();
+        lds_barrier();
+        const int64_t k_begin = k_begin_of(cur);
+        const int steps = int((k_end_of(cur) - k_begin + T::BK - 1) / T::BK);
+        int s = 0;
+        for (; s + 2 < steps; s += 2) {
+            const int64_t k0 = k_begin + int64_t(s) * T::BK;
+            second_half(I0{}, k0 + 2 * T::BK, Read{});
+            first_half(I1{});
+            sync();
+            second_half(I1{}, k0 + 3 * T::BK, Read{});
+            first_half(I0{});
+            sync();
+        }
+        // The tile's last two K-steps load the next item's first two (or,
+        // for the workgroup's last item, nothing: offsets past the K end).
+        const bool has_next = w + stride < items;
+        int64_t k_next = ld_end;
+        if (has_next) {
+            const Item next = item_of(w + stride);
+            ld_a = a_of(next);
+            ld_b = b_of(next);
+            ld_end = k_end_of(next);
+            k_next = k_begin_of(next);
+        }
+        second_half(I0{}, k_next, Read{});
+        first_half(I1{});
+        sync();
+        second_half(I1{}, has_next ? k_next + T::BK : k_next, NoRead{});
+
+        const bool partial = args.splits > 1;
+        float* out = partial ? args.ws + ((cur.batch_local * int64_t(args.splits) + cur.split) * args.m) * args.n
+                             : args.c + (args.batch_base + cur.batch_local) * args.stride_c;
+        write_tile<T, true, PM, PN, 0, true>(args, acc, out, int64_t(cur.tm) * T::BM, int64_t(cur.tn) * T::BN, wave_m,
+                                            wave_n, lane, partial);
+        if (!has_next) break;
+        w += stride;
+        cur = item_of(w);
+        first = false;
+    }
+    wait_loads<0>();
+}
+
 // A tile shape with its number of LDS stages.
 template <class T_, int STAGES_>
 struct DmaConfig {
@@ -610,6 +787,15 @@ __attribute__((amdgpu_waves_per_eu(dma_waves_per_eu<typename C::T, C::STAGES>(),
                                    dma_waves_per_eu<typename C::T, C::STAGES>())))
 void gemm_f32_dma_kernel(Args args) {
     dma_tile<typename C::T, C::STAGES, A_K, B_K, kFeedF32>(args);
+}
+
+// The persistent form of the 128 x 128 fp32 tile (dma_persistent).
+template <class C, bool A_K, bool B_K>
+__global__ __launch_bounds__(C::T::THREADS)
+__attribute__((amdgpu_waves_per_eu(dma_waves_per_eu<typename C::T, C::STAGES>(),
+                                   dma_waves_per_eu<typename C::T, C::STAGES>())))
+void gemm_f32_persistent_kernel(Args args) {
+    dma_persistent<typename C::T, A_K, B_K>(args);
 }
 
 // The fp32 product with the right operand's column sums over K (Linear's
@@ -665,6 +851,28 @@ Plan dma_plan(const Problem& p, const Env& env) {
 
 constexpr int64_t kStreamingMaxK = 128;
 
+// The grid of the persistent fp32 kernel for `p` (a multiple of the XCD
+// count, so that a workgroup's items stay on its XCD), or 0 when the product
+// takes the one-tile kernel: masked products, several launches, tiles with an
+// odd number of K-steps, or under two items per workgroup slot.
+template <class C>
+int64_t persistent_grid(const Problem& p, const Env& env, const Plan& plan, const LaunchShape& shape) {
+    using T = typename C::T;
+    if constexpr (C::STAGES != 2 || T::BM != 128 || T::BN != 128) return 0;
+    // Interior tiles that read nothing back: write_tile's one store path.
+    if (p.mask != SN_MASK_NONE || shape.batches_per_launch < p.batch || p.k <= kStreamingMaxK ||
+        p.m % T::BM != 0 || p.n % T::BN != 0 || (plan.splits == 1 && p.accumulate))
+        return 0;
+    const int64_t items = int64_t(plan.tiles_m) * plan.tiles_n * plan.splits * p.batch;
+    const int64_t per_cu = std::max(1, dma_waves_per_eu<T, C::STAGES>() * 4 / (T::THREADS / 64));
+    const int64_t slots = int64_t(std::max(env.cu_count, 1)) * per_cu / kXcds * kXcds;
+    if (slots < kXcds || items < 2 * slots || items > 0x7FFFFFFF) return 0;
+    const int64_t steps = (plan.k_per_split + T::BK - 1) / T::BK;
+    const int64_t last_steps = (p.k - int64_t(plan.splits - 1) * plan.k_per_split + T::BK - 1) / T::BK;
+    if (steps % 2 != 0 || last_steps % 2 != 0 || last_steps < 2) return 0;
+    return slots;
+}
+
 template <class C, bool A_K, bool B_K, int FEED>
 hipError_t launch_dma_tiles(const Problem& p, const Env& env, hipStream_t stream) {
     using T = typename C::T;
@@ -678,6 +886,18 @@ hipError_t launch_dma_tiles(const Problem& p, const Env& env, hipStream_t stream
     // 64): 1.38-1.44 -> 1.25 ms and 1.31-1.32 -> 1.17-1.19 ms; at K = 768
     // (the Linear products) streaming stores changed nothing beyond noise.
     args.streaming_output = p.mask == SN_MASK_NONE && plan.splits == 1 && p.k <= kStreamingMaxK ? 1 : 0;
+    if constexpr (FEED == kFeedF32 && C::STAGES == 2 && T::BM == 128 && T::BN == 128) {
+        const int64_t grid = persistent_grid<C>(p, env, plan, shape);  // describe_f32_dma's choice
+        if (grid > 0) {
+            args.persistent_items = int32_t(int64_t(plan.tiles_m) * plan.tiles_n * plan.splits * p.batch);
+            hipLaunchKernelGGL((gemm_f32_persistent_kernel<C, A_K, B_K>), dim3(unsigned(grid)), dim3(T::THREADS), 0,
+                               stream, args);
+            hipError_t err = hipGetLastError();
+            if (err != hipSuccess) return err;
+            if (plan.splits > 1) return launch_splitk_reduce(p, env, plan.splits, stream);
+            return hipSuccess;
+        }
+    }
     const int64_t per_batch = int64_t(plan.tiles_m) * plan.tiles_n * plan.splits;
     const int64_t chunk = shape.batches_per_launch;
     for (int64_t first = 0; first < p.batch; first += chunk) {
@@ -794,7 +1014,11 @@ bool bf16_dma_applies(const Problem& p, const Env& env) {
 LaunchShape describe_f32_dma(const Problem& p, const Env& env) {
     return with_f32_dma_config(p, env, [&](auto c) {
         using C = decltype(c);
-        return tiled_shape<typename C::T>(p, dma_plan<C, kFeedF32>(p, env), SN_PATH_F32_DIRECT);
+        const Plan plan = dma_plan<C, kFeedF32>(p, env);
+        LaunchShape s = tiled_shape<typename C::T>(p, plan, SN_PATH_F32_DIRECT);
+        s.persistent_grid = persistent_grid<C>(p, env, plan, s);
+        if (s.persistent_grid > 0) s.path = SN_PATH_F32_PERSISTENT;
+        return s;
     });
 }
 

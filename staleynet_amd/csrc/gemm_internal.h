@@ -70,6 +70,7 @@ struct LaunchShape {
     int64_t workgroups = 0;
     int64_t launches = 0;
     size_t workspace_bytes = 0;
+    int64_t persistent_grid = 0;  // SN_PATH_F32_PERSISTENT: workgroups launched, looping over `workgroups` items
 };
 LaunchShape describe_gemm_f32(const Problem& p, const Env& env);
 LaunchShape describe_gemm_bf16(const Problem& p, const Env& env);

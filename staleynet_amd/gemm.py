@@ -209,7 +209,7 @@ class CLaunchPlan(ctypes.Structure):
     """``sn_launch_plan``: how one product is launched (the role of launch.rs:28-48)."""
     _fields_ = [("path", ctypes.c_uint32), ("threads", ctypes.c_uint32), ("tile_rows", ctypes.c_uint32),
                 ("tile_cols", ctypes.c_uint32), ("tiles_m", ctypes.c_uint32), ("tiles_n", ctypes.c_uint32),
-                ("splits", ctypes.c_uint32), ("reserved", ctypes.c_uint32), ("k_per_split", ctypes.c_uint64),
+                ("splits", ctypes.c_uint32), ("persistent_grid", ctypes.c_uint32), ("k_per_split", ctypes.c_uint64),
                 ("batches_per_launch", ctypes.c_uint64), ("workgroups", ctypes.c_uint64),
                 ("launches", ctypes.c_uint64), ("workspace_bytes", ctypes.c_uint64)]
 
@@ -217,9 +217,9 @@ class CLaunchPlan(ctypes.Structure):
 # sn_launch_plan.path values (include/staleynet_gemm.h).
 PATH_NONE, PATH_REFERENCE_ORDER, PATH_FEW_ROWS, PATH_FEW_ROWS_NT = 0, 1, 2, 3
 PATH_F32_DIRECT, PATH_F32_REGISTER, PATH_BF16_STAGED, PATH_BF16_DIRECT, PATH_BF16_REGISTER = 4, 5, 6, 7, 8
-PATH_BF16_WIDE, PATH_F32_DIRECT_SUMS, PATH_BF16_WIDE_SUMS = 9, 10, 11
+PATH_BF16_WIDE, PATH_F32_DIRECT_SUMS, PATH_BF16_WIDE_SUMS, PATH_F32_PERSISTENT = 9, 10, 11, 12
 TILED_PATHS = (PATH_F32_DIRECT, PATH_F32_REGISTER, PATH_BF16_STAGED, PATH_BF16_DIRECT, PATH_BF16_REGISTER,
-               PATH_BF16_WIDE, PATH_F32_DIRECT_SUMS, PATH_BF16_WIDE_SUMS)
+               PATH_BF16_WIDE, PATH_F32_DIRECT_SUMS, PATH_BF16_WIDE_SUMS, PATH_F32_PERSISTENT)
 
 
 class CAttentionShape(ctypes.Structure):

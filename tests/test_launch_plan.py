@@ -114,7 +114,8 @@ def test_weight_gradients_take_the_column_sums_into_the_product():
         spec = MatmulSpec.new(inputs, outputs, 32768).left_transposed().accumulate()
         product = gemm.plan(spec)
         fused = gemm.plan_column_sums(spec)
-        assert product.path == gemm.PATH_F32_DIRECT and fused.path == gemm.PATH_F32_DIRECT_SUMS
+        assert product.path in (gemm.PATH_F32_DIRECT, gemm.PATH_F32_PERSISTENT)
+        assert fused.path == gemm.PATH_F32_DIRECT_SUMS
         assert (fused.splits, fused.k_per_split, fused.tiles_m, fused.tiles_n) == \
             (product.splits, product.k_per_split, product.tiles_m, product.tiles_n)
         extra = fused.splits * outputs * 4 if fused.splits > 1 else 0
@@ -150,7 +151,7 @@ def test_weight_gradients_take_the_column_sums_into_the_product():
 
 
 def test_configs_take_the_expected_kernel_families():
-    assert gemm.plan(MatmulSpec.new(32768, 2304, 768)).path == gemm.PATH_F32_DIRECT
+    assert gemm.plan(MatmulSpec.new(32768, 2304, 768)).path == gemm.PATH_F32_PERSISTENT
     # Large bf16 products round their fp32 operands as they load them, 256 x 256 tiles; the forward
     # and input-gradient products first round the (smaller) weight into the workspace.
     forward = gemm.plan(MatmulSpec.new(32768, 2304, 768).with_precision(Precision.Bf16))
@@ -207,6 +208,54 @@ def test_configs_take_the_expected_kernel_families():
     assert gemm.plan(MatmulSpec.new(256, 256, 256), left=gemm.ALIGNED_ADDRESS + 4).path == gemm.PATH_F32_REGISTER
     assert gemm.plan(MatmulSpec.new(2, 3, 4), int(MatmulKernel.Simple)).path == gemm.PATH_REFERENCE_ORDER
     assert gemm.plan(MatmulSpec.new(0, 3, 4)).path == gemm.PATH_NONE
+
+
+def check_persistent_rules(spec, plan, cus):
+    """The persistent fp32 grid: two workgroups per CU, rounded down to whole XCDs, at least two work
+    items each; whole 128 x 128 tiles that read nothing back; every slice an even number of 32-deep
+    K-steps; one launch; no mask; K above the streaming-store range."""
+    if plan.path != gemm.PATH_F32_PERSISTENT:
+        assert plan.persistent_grid == 0
+        return
+    grid = plan.persistent_grid
+    assert grid == 2 * cus // 8 * 8 and plan.workgroups >= 2 * grid
+    assert (plan.tile_rows, plan.tile_cols) == (128, 128)
+    assert spec.rows % 128 == 0 and spec.cols % 128 == 0 and spec.mask == gemm.Mask.None_
+    assert plan.splits > 1 or not spec.write
+    assert plan.launches == 1 and spec.inner > 128
+    last = spec.inner - (plan.splits - 1) * plan.k_per_split
+    assert plan.k_per_split % 64 == 0 and -(-last // 32) % 2 == 0
+
+
+def test_persistent_products():
+    # Config 2's forward and input-gradient products, its qkv and head weight gradients (split K, even
+    # slices) and one GPU's share of the head run persistent; so does an NT product with an odd step
+    # count's neighbour ruled out: every one of these plans obeys the rules above.
+    persistent = [MatmulSpec.new(32768, 2304, 768), MatmulSpec.new(32768, 768, 768),
+                  MatmulSpec.new(32768, 768, 2304).right_transposed(), MatmulSpec.new(32768, 768, 16384).right_transposed(),
+                  MatmulSpec.new(768, 2304, 32768).left_transposed().accumulate(),
+                  MatmulSpec.new(768, 16384, 32768).left_transposed().accumulate(),
+                  MatmulSpec.new(4096, 16384, 768)]
+    for spec in persistent:
+        plan = gemm.plan(spec)
+        assert plan.path == gemm.PATH_F32_PERSISTENT, (spec, plan.path)
+        check_persistent_rules(spec, plan, 256)
+        check_tiled_cover(plan)
+    # Not persistent: masked, ragged, accumulating without a split, odd slices, one item per slot, K
+    # in the streaming-store range, bf16.
+    others = [MatmulSpec.new(2048, 2048, 64).right_transposed().batched(BatchStrides(192, 2048 * 64, 2048 * 64,
+                                                                                   2048 * 2048)).causal_output(),
+              MatmulSpec.new(32768, 2300, 768), MatmulSpec.new(32768, 2304, 768).accumulate(),
+              MatmulSpec.new(768, 3072, 32768).left_transposed().accumulate(),
+              MatmulSpec.new(8192, 1024, 768),
+              MatmulSpec.new(2048, 2048, 64).right_transposed().batched(BatchStrides(192, 2048 * 64, 2048 * 64,
+                                                                                   2048 * 2048)),
+              MatmulSpec.new(32768, 2304, 768).with_precision(Precision.Bf16)]
+    for spec in others:
+        plan = gemm.plan(spec)
+        assert plan.path != gemm.PATH_F32_PERSISTENT and plan.persistent_grid == 0, (spec, plan.path)
+    # The grid follows the CU count.
+    assert gemm.plan(MatmulSpec.new(32768, 2304, 768), cu_count=80).persistent_grid == 160
 
 
 def test_tiles_round_up_and_keep_the_batch_axis():
@@ -276,6 +325,7 @@ from hypothesis import HealthCheck, given, settings  # noqa: E402
 from hypothesis import strategies as st  # noqa: E402
 
 TILE_SIZES = {gemm.PATH_F32_DIRECT: {(128, 128), (128, 64), (64, 64)},
+              gemm.PATH_F32_PERSISTENT: {(128, 128)},
               gemm.PATH_F32_DIRECT_SUMS: {(128, 128), (128, 64), (64, 64)},
               gemm.PATH_BF16_WIDE: {(256, 256)},
               gemm.PATH_BF16_STAGED: {(128, 128), (128, 256), (128, 64)},
@@ -316,6 +366,7 @@ def test_random_plans_cover_the_product_once(m, n, k, left_t, right_t, batch, bf
             assert plan.workspace_bytes >= plan.splits * m * n * 4
         if plan.workgroups <= 1 << 16:
             check_tiled_cover(plan)
+    check_persistent_rules(spec, plan, cus)
     # The 256 x 256 bf16 tiles only where they keep half the CUs busy.
     if plan.path == gemm.PATH_BF16_WIDE:
         assert 2 * plan.tiles_m * plan.tiles_n * plan.splits * batch >= cus
