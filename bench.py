@@ -1175,8 +1175,10 @@ def _cpu_model() -> str:
 
 # ---- rocprofv3 summaries ----------------------------------------------------------------
 
-# The roofline kernel: the direct-to-LDS fp32 MFMA kernel, 128x128 tile, A K-contiguous, B N-contiguous.
-NN_KERNEL_KEY = "gemm_f32_dma_kernel<sn::gemm::(anonymous namespace)::DmaConfig<sn::gemm::Tile<128, 128, 32, 2, 2>, 2>, true, false>"
+# The roofline kernel: the persistent direct-to-LDS fp32 MFMA kernel, 128x128 tile, A K-contiguous, B
+# N-contiguous (every forward NN product of config 2's set).
+NN_KERNEL_KEY = ("gemm_f32_persistent_kernel<sn::gemm::(anonymous namespace)::DmaConfig<sn::gemm::Tile<128, 128, 32, "
+                 "2, 2>, 2>, true, false>")
 COPY_KERNEL_KEY = "copy_kernel("
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "gemm_f32_nn_111M_hbm_traffic.txt")
 
@@ -1343,9 +1345,9 @@ def summarize_trace(stats_csv: str, bench_json: str = "") -> str:
     import csv
     with open(stats_csv, newline="") as f:
         rows = list(csv.DictReader(f))
-    lines = [f"{'kernel':<78} {'calls':>6} {'avg us':>9} {'min us':>9} {'max us':>9} {'total ms':>9} {'%':>6}"]
+    lines = [f"{'kernel':<92} {'calls':>6} {'avg us':>9} {'min us':>9} {'max us':>9} {'total ms':>9} {'%':>6}"]
     for r in rows:
-        lines.append(f"{_short(r['Name'])[:78]:<78} {int(r['Calls']):>6} {float(r['AverageNs']) / 1e3:>9.1f} "
+        lines.append(f"{_short(r['Name'])[:92]:<92} {int(r['Calls']):>6} {float(r['AverageNs']) / 1e3:>9.1f} "
                      f"{float(r['MinNs']) / 1e3:>9.1f} {float(r['MaxNs']) / 1e3:>9.1f} "
                      f"{float(r['TotalDurationNs']) / 1e6:>9.2f} {float(r['Percentage']):>6.2f}")
     nn = next((r for r in rows if NN_KERNEL_KEY in r["Name"]), None)
@@ -1502,8 +1504,8 @@ def main() -> int:
     nn_flops_per_launch = nn["flops"] / nn["launches"]
     nn_ms_per_launch = nn["ms"] / nn["launches"]
     achieved = nn_flops_per_launch / (nn_ms_per_launch * 1e-3) / 1e12
-    roofline = {"kernel": "gemm_f32_dma_kernel<DmaConfig<Tile<128,128,32,2,2>, 2 stages>, A K-contiguous, B N-contiguous> "
-                          "(every forward NN product of the set)",
+    roofline = {"kernel": "gemm_f32_persistent_kernel<DmaConfig<Tile<128,128,32,2,2>, 2 stages>, A K-contiguous, "
+                          "B N-contiguous> (every forward NN product of the set)",
                 "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "traffic": load_traffic(),
                 "launch_ms_mean": round(nn_ms_per_launch, 4), "flops_per_launch": nn_flops_per_launch,
