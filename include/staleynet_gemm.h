@@ -473,7 +473,7 @@ int sn_matmul_noalloc(const sn_matmul_spec *spec, const float *left, size_t left
 #define SN_PATH_BF16_WIDE 9u       /* bf16: 256x256 tiles rounding fp32 operands as they load */
 #define SN_PATH_F32_DIRECT_SUMS 10u /* SN_PATH_F32_DIRECT adding the right operand's column sums */
 #define SN_PATH_BF16_WIDE_SUMS 11u  /* SN_PATH_BF16_WIDE adding the right operand's column sums */
-#define SN_PATH_F32_PERSISTENT 12u  /* SN_PATH_F32_DIRECT's tiles, looped over by persistent_grid workgroups */
+#define SN_PATH_F32_PERSISTENT 12u  /* SN_PATH_F32_DIRECT's 128x128 tiles, looped over by persistent_grid workgroups */
 
 /* How one product is launched: the role of the reference's launch geometry
  * (`launch::matmul_tiles` / `matmul_blocks`, crates/staleynet-cuda/src/
@@ -490,8 +490,10 @@ typedef struct sn_launch_plan {
     uint32_t tile_rows, tile_cols;
     uint32_t tiles_m, tiles_n;
     uint32_t splits;
-    uint32_t persistent_grid;     /* SN_PATH_F32_PERSISTENT: the workgroups launched, each taking work items
-                                   * g, g + persistent_grid, ... of the `workgroups`; otherwise 0 */
+    uint32_t persistent_grid;     /* nonzero for a persistent launch (SN_PATH_F32_PERSISTENT always,
+                                   * SN_PATH_BF16_WIDE(_SUMS) when its tiles allow): the workgroups
+                                   * launched, workgroup g taking work items g, g + persistent_grid, ...
+                                   * of the `workgroups`; otherwise 0 */
     uint64_t k_per_split;
     uint64_t batches_per_launch;
     uint64_t workgroups;          /* of one launch holding batches_per_launch matrices (persistent

@@ -339,6 +339,196 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         write_tile<T, true, false, false, kStreaming>(args, acc, out, m0, n0, wave_m, wave_n, lane, partial);
 }
 
+// The same product as a persistent loop: each workgroup takes work items
+// blockIdx.x, blockIdx.x + gridDim.x, ... (a matrix, K slice and 256 x 256
+// tile, mapped by tile_coordinates as the one-tile launch maps its
+// workgroups), for products whose tiles are all whole, read nothing back
+// and have an even number of K-steps. The three loads a tile would issue
+// past its last K-step (zeros, in the one-tile kernel) fetch the next item's
+// first three K-steps instead, and its last step rounds the next item's
+// first into LDS, so the next tile starts from data already in LDS and in
+// registers. The tile's (streaming) output stores go out after those loads:
+// load and store completions are counted in issue order (vmcnt), so the next
+// tile's first two steps wait for their register sets with at most 63
+// operations outstanding, which the 128 stores after them always exceed, and
+// the stores drain under those two steps instead of ending the workgroup.
+template <bool A_K, bool B_K, int SIDE>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_bf16_wide_persistent_kernel(
+    Args args) {
+    using T = WideTile;
+    using LA = OperandLoader<A_K, SIDE == kStageLeft, T::BM, T::BK, T::THREADS>;
+    using LB = OperandLoader<B_K, SIDE == kStageRight, T::BN, T::BK, T::THREADS>;
+    using OA = OctetPlanes<T::BM, T::BK, LA::BF16_PAD>;
+    using OB = OctetPlanes<T::BN, T::BK, LB::BF16_PAD>;
+    constexpr int kSetLoads = loads_per_step<LA>() + loads_per_step<LB>();
+    // Store instructions of the interior epilogue (one per accumulator).
+    constexpr int kStores = T::FM * T::FN * 16;
+    static_assert(kStores + kSetLoads >= 63, "enough operations after a set for a wait at 63 to cover it");
+    __shared__ __attribute__((aligned(16))) uint16_t lds_a[2][8 * OA::SLOTS];
+    __shared__ __attribute__((aligned(16))) uint16_t lds_b[2][8 * OB::SLOTS];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wave_m = wave / T::WAVES_N;
+    const int wave_n = wave % T::WAVES_N;
+    const int row = lane & 31;
+    const int half = lane >> 5;
+    const int items = args.persistent_items;
+    const int stride = int(gridDim.x);
+
+    struct Item {
+        int tm, tn, batch_local, split;
+    };
+    auto item_of = [&](int w) {
+        Item it;
+        tile_coordinates(w, items, args.tiles_m, args.tiles_n, args.splits, it.batch_local, it.split, it.tm, it.tn);
+        return it;
+    };
+    int w = int(blockIdx.x);
+    if (w >= items) return;
+    Item cur = item_of(w);
+
+    constexpr int NSETS = 2;
+    LA la[NSETS];
+    LB lb[NSETS];
+    // Whole tiles only (checked on the host): the loaders' offsets are the
+    // same for every item.
+#pragma unroll
+    for (int j = 0; j < NSETS; ++j) {
+        la[j].init(args.lda, 0, T::BM, tid);
+        lb[j].init(args.ldb, 0, T::BN, tid);
+    }
+    // The item whose loads are being issued.
+    const float* ld_a = args.a + (args.batch_base + cur.batch_local) * args.stride_a;
+    const float* ld_b = args.b + (args.batch_base + cur.batch_local) * args.stride_b;
+    int64_t ld_m0 = int64_t(cur.tm) * T::BM, ld_n0 = int64_t(cur.tn) * T::BN;
+    int64_t ld_begin = int64_t(cur.split) * args.k_per_split;
+    int64_t ld_end = min(args.k, ld_begin + args.k_per_split);
+    auto switch_loads = [&](const Item& it) __attribute__((always_inline)) {
+        ld_a = args.a + (args.batch_base + it.batch_local) * args.stride_a;
+        ld_b = args.b + (args.batch_base + it.batch_local) * args.stride_b;
+        ld_m0 = int64_t(it.tm) * T::BM;
+        ld_n0 = int64_t(it.tn) * T::BN;
+        ld_begin = int64_t(it.split) * args.k_per_split;
+        ld_end = min(args.k, ld_begin + args.k_per_split);
+    };
+
+    f32x16 acc[T::FM][T::FN];
+    // Loads of K-step `step` of the load item into register set S (past its
+    // end: out of range, zeros).
+    auto issue = [&](auto set, int step) __attribute__((always_inline)) {
+        constexpr int S = decltype(set)::value;
+        const int64_t k0 = ld_begin + int64_t(step) * T::BK;
+        la[S].load(ld_a, args.lda, ld_m0, args.m, k0, ld_end, tid);
+        lb[S].load(ld_b, args.ldb, ld_n0, args.n, k0, ld_end, tid);
+    };
+    auto stage = [&](auto set, auto lds) __attribute__((always_inline)) {
+        constexpr int S = decltype(set)::value;
+        constexpr int L = decltype(lds)::value;
+        la[S].store_bf16(lds_a[L], tid);
+        lb[S].store_bf16(lds_b[L], tid);
+    };
+    auto read_chunk = [&](auto set, int c, bf16x8 (&fa)[T::FM], bf16x8 (&fb)[T::FN]) __attribute__((always_inline)) {
+        constexpr int S = decltype(set)::value;
+        const int octet = 2 * c + half;
+#pragma unroll
+        for (int i = 0; i < T::FM; ++i)
+            fa[i] = *reinterpret_cast<const bf16x8*>(lds_a[S] + 8 * (octet * OA::PLANE + wave_m * T::WTM + 32 * i + row));
+#pragma unroll
+        for (int j = 0; j < T::FN; ++j)
+            fb[j] = *reinterpret_cast<const bf16x8*>(lds_b[S] + 8 * (octet * OB::PLANE + wave_n * T::WTN + 32 * j + row));
+    };
+    auto multiply_chunk = [&](const bf16x8 (&fa)[T::FM], const bf16x8 (&fb)[T::FN]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+            for (int j = 0; j < T::FN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    };
+    auto step_from = [&](auto set, auto between) __attribute__((always_inline)) {
+        bf16x8 fa0[T::FM], fb0[T::FN], fa1[T::FM], fb1[T::FN];
+        read_chunk(set, 0, fa0, fb0);
+        multiply_chunk(fa0, fb0);
+        between();
+        read_chunk(set, 1, fa1, fb1);
+        multiply_chunk(fa1, fb1);
+    };
+    // Step s (s % 2 == J) computes from LDS stage J while register set
+    // (J + 1) % 2 (step s + 1 of the tile, or the next item's) is waited for,
+    // rounded into the other stage and reloaded with `load_step` of the load
+    // item. AFTER_STORES: the first two steps after an epilogue, whose sets
+    // were issued before its stores.
+    auto do_step = [&](auto j, int load_step, auto after_stores) __attribute__((always_inline)) {
+        constexpr int J = decltype(j)::value;
+        using Stage = std::integral_constant<int, J>;
+        using NextSet = std::integral_constant<int, (J + 1) % NSETS>;
+        using NextStage = std::integral_constant<int, (J + 1) % 2>;
+        step_from(Stage{}, [&]() __attribute__((always_inline)) {
+            if constexpr (decltype(after_stores)::value) wait_vector_loads<63>();
+            else wait_vector_loads<(NSETS - 1) * kSetLoads>();
+            stage(NextSet{}, NextStage{});
+            issue(NextSet{}, load_step);
+        });
+        stage_barrier();
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using Plain = std::false_type;
+    using AfterStores = std::true_type;
+
+    issue(I0{}, 0);
+    issue(I1{}, 1);
+    wait_vector_loads<(NSETS - 1) * kSetLoads>();  // set 0 (step 0) is in
+    stage(I0{}, I0{});
+    issue(I0{}, NSETS);
+    stage_barrier();
+    bool first = true;
+    for (;;) {
+#pragma unroll
+        for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+            for (int j = 0; j < T::FN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+        const int64_t k_begin = int64_t(cur.split) * args.k_per_split;
+        const int steps = int((min(args.k, k_begin + args.k_per_split) - k_begin + T::BK - 1) / T::BK);
+        const bool has_next = w + stride < items;
+        const Item next = has_next ? item_of(w + stride) : cur;
+        // Step s loads step s + 3: the tile's own while s + 3 < steps, then
+        // the next item's 0, 1 and 2 (a load cursor switched once).
+        auto load_step = [&](int s) __attribute__((always_inline)) {
+            const int target = s + 1 + NSETS;
+            if (target == steps && has_next) switch_loads(next);
+            return target >= steps && has_next ? target - steps : target;
+        };
+        int s = 0;
+        if (!first) {
+            do_step(I0{}, load_step(0), AfterStores{});
+            do_step(I1{}, load_step(1), AfterStores{});
+            s = 2;
+        }
+        for (; s < steps; s += 2) {
+            do_step(I0{}, load_step(s), Plain{});
+            do_step(I1{}, load_step(s + 1), Plain{});
+        }
+        const bool partial = args.splits > 1;
+        float* out = partial ? args.ws + ((cur.batch_local * int64_t(args.splits) + cur.split) * args.m) * args.n
+                             : args.c + (args.batch_base + cur.batch_local) * args.stride_c;
+        const int64_t m0 = int64_t(cur.tm) * T::BM, n0 = int64_t(cur.tn) * T::BN;
+        if (partial)
+            write_tile<T, true, false, false, 0, true>(args, acc, out, m0, n0, wave_m, wave_n, lane, partial);
+        else
+            write_tile<T, true, false, false, kStreaming, true>(args, acc, out, m0, n0, wave_m, wave_n, lane,
+                                                                 partial);
+        if (!has_next) break;
+        w += stride;
+        cur = next;
+        first = false;
+    }
+    wait_vector_loads<0>();
+}
+
 // Split-K under the launch model of plan_for: one workgroup per CU, and the
 // per-CU rate the split counts were measured with.
 Plan wide_plan(const Problem& p, const Env& env) {
@@ -419,11 +609,53 @@ WideStaging wide_staging(const Problem& p, const Env& env) {
     return st;
 }
 
+// The grid of the persistent kernel for `p` (the product as the kernel sees
+// it, with any staged operand), or 0 for the one-tile kernel: one launch,
+// whole tiles that read nothing back, slices of an even number (at least
+// four) of K-steps, and either two work items per CU or more, or more than
+// one with tiles of at most kWidePersistentShortSteps K-steps (where the
+// output write is a large share of a tile). One workgroup per CU, rounded
+// down to whole XCDs. Measured on config 2's bf16 products against the
+// one-tile kernel: NN qkv / up / head (K = 768, 4.5 to 32 tiles per CU)
+// 664-668 -> 698-716, 736-746 -> 806-807, 760-770 -> 826-843 TFLOP/s; NT
+// down (6 per CU) 752-765 -> 816-822; NN out (1.5 per CU, 24 K-steps)
+// 537-567 -> 589-591; the 1.5-per-CU products with 72 to 512 K-steps
+// (NN down, NT qkv / up / head) unchanged to 3 % slower, so they keep the
+// one-tile kernel.
+constexpr int64_t kWidePersistentShortSteps = 32;
+
+int64_t wide_persistent_grid(const Problem& p, const Env& env, const Plan& plan, const LaunchShape& shape) {
+    using T = WideTile;
+    if (shape.batches_per_launch < p.batch || p.m % T::BM != 0 || p.n % T::BN != 0 ||
+        (plan.splits == 1 && p.accumulate))
+        return 0;
+    const int64_t items = int64_t(plan.tiles_m) * plan.tiles_n * plan.splits * p.batch;
+    const int64_t slots = int64_t(std::max(env.cu_count, 1)) / kXcds * kXcds;
+    if (slots < kXcds || items <= slots || items > 0x7FFFFFFF) return 0;
+    const int64_t steps = (plan.k_per_split + T::BK - 1) / T::BK;
+    const int64_t last_steps = (p.k - int64_t(plan.splits - 1) * plan.k_per_split + T::BK - 1) / T::BK;
+    if (steps % 2 != 0 || last_steps % 2 != 0 || last_steps < 4) return 0;
+    if (items < 2 * slots && steps > kWidePersistentShortSteps) return 0;
+    return slots;
+}
+
 template <bool A_K, bool B_K, int SIDE, bool COLSUM = false>
 hipError_t launch_wide(const Problem& p, const Env& env, const Plan& plan, hipStream_t stream) {
     const LaunchShape shape = tiled_shape<WideTile>(p, plan, SN_PATH_BF16_WIDE);
     if (shape.batches_per_launch < 1) return hipErrorInvalidConfiguration;
     Args args = make_args<WideTile>(p, env, plan);
+    if constexpr (!COLSUM) {
+        const int64_t grid = wide_persistent_grid(p, env, plan, shape);
+        if (grid > 0) {
+            args.persistent_items = int32_t(int64_t(plan.tiles_m) * plan.tiles_n * plan.splits * p.batch);
+            hipLaunchKernelGGL((gemm_bf16_wide_persistent_kernel<A_K, B_K, SIDE>), dim3(unsigned(grid)),
+                               dim3(WideTile::THREADS), 0, stream, args);
+            hipError_t err = hipGetLastError();
+            if (err != hipSuccess) return err;
+            if (plan.splits > 1) return launch_splitk_reduce(p, env, plan.splits, stream);
+            return hipSuccess;
+        }
+    }
     const int64_t per_batch = int64_t(plan.tiles_m) * plan.tiles_n * plan.splits;
     const int64_t chunk = shape.batches_per_launch;
     for (int64_t first = 0; first < p.batch; first += chunk) {
@@ -463,7 +695,9 @@ bool bf16_wide_applies(const Problem& p, const Env& env) {
 
 LaunchShape describe_bf16_wide(const Problem& p, const Env& env) {
     const WideStaging st = wide_staging(p, env);
-    LaunchShape shape = tiled_shape<WideTile>(st.q, wide_plan(st.q, st.rest), SN_PATH_BF16_WIDE);
+    const Plan plan = wide_plan(st.q, st.rest);
+    LaunchShape shape = tiled_shape<WideTile>(st.q, plan, SN_PATH_BF16_WIDE);
+    shape.persistent_grid = wide_persistent_grid(st.q, st.rest, plan, shape);
     shape.workspace_bytes += st.bytes;
     return shape;
 }
@@ -547,6 +781,9 @@ LaunchShape describe_bf16_wide_column_sums(const Problem& p, const Env& env) {
     const WideStaging st = wide_staging(p, env);
     const Plan plan = wide_column_sums_plan(st, p);
     LaunchShape shape = tiled_shape<WideTile>(st.q, plan, SN_PATH_BF16_WIDE);
+    // With dY staged, the staging pass takes the sums and the product runs
+    // as launch_gemm_bf16_wide's (persistent where its tiles allow).
+    if (st.side == kStageRight) shape.persistent_grid = wide_persistent_grid(st.q, st.rest, plan, shape);
     shape.workspace_bytes += st.bytes + column_partial_bytes(st, plan, p);
     return shape;
 }

@@ -213,7 +213,18 @@ def test_configs_take_the_expected_kernel_families():
 def check_persistent_rules(spec, plan, cus):
     """The persistent fp32 grid: two workgroups per CU, rounded down to whole XCDs, at least two work
     items each; whole 128 x 128 tiles that read nothing back; every slice an even number of 32-deep
-    K-steps; one launch; no mask; K above the streaming-store range."""
+    K-steps; one launch; no mask; K above the streaming-store range. The persistent bf16 256 x 256
+    grid: one workgroup per CU, whole tiles that read nothing back, slices of an even number (at least
+    4) of K-steps, more items than workgroups: two each, or tiles of at most 32 K-steps."""
+    if plan.path in (gemm.PATH_BF16_WIDE, gemm.PATH_BF16_WIDE_SUMS) and plan.persistent_grid:
+        grid = plan.persistent_grid
+        assert grid == cus // 8 * 8 and plan.workgroups > grid and plan.launches == 1
+        assert spec.rows % 256 == 0 and spec.cols % 256 == 0 and (plan.splits > 1 or not spec.write)
+        steps = -(-plan.k_per_split // 32)
+        last = -(-(spec.inner - (plan.splits - 1) * plan.k_per_split) // 32)
+        assert steps % 2 == 0 and last % 2 == 0 and last >= 4
+        assert plan.workgroups >= 2 * grid or steps <= 32
+        return
     if plan.path != gemm.PATH_F32_PERSISTENT:
         assert plan.persistent_grid == 0
         return
@@ -241,8 +252,8 @@ def test_persistent_products():
         assert plan.path == gemm.PATH_F32_PERSISTENT, (spec, plan.path)
         check_persistent_rules(spec, plan, 256)
         check_tiled_cover(plan)
-    # Not persistent: masked, ragged, accumulating without a split, odd slices, one item per slot, K
-    # in the streaming-store range, bf16.
+    # Not persistent fp32: masked, ragged, accumulating without a split, odd slices, one item per slot,
+    # K in the streaming-store range; bf16 takes its own kernels.
     others = [MatmulSpec.new(2048, 2048, 64).right_transposed().batched(BatchStrides(192, 2048 * 64, 2048 * 64,
                                                                                    2048 * 2048)).causal_output(),
               MatmulSpec.new(32768, 2300, 768), MatmulSpec.new(32768, 2304, 768).accumulate(),
@@ -253,9 +264,24 @@ def test_persistent_products():
               MatmulSpec.new(32768, 2304, 768).with_precision(Precision.Bf16)]
     for spec in others:
         plan = gemm.plan(spec)
-        assert plan.path != gemm.PATH_F32_PERSISTENT and plan.persistent_grid == 0, (spec, plan.path)
+        assert plan.path != gemm.PATH_F32_PERSISTENT, (spec, plan.path)
+        assert plan.persistent_grid == 0 or plan.path == gemm.PATH_BF16_WIDE, (spec, plan.path)
     # The grid follows the CU count.
     assert gemm.plan(MatmulSpec.new(32768, 2304, 768), cu_count=80).persistent_grid == 160
+    # bf16 on the 256 x 256 kernel: config 2's forward products and the wide input gradient loop over
+    # their tiles; the 768-wide products with long K keep the one-tile launch.
+    bf16 = Precision.Bf16
+    for spec in (MatmulSpec.new(32768, 2304, 768), MatmulSpec.new(32768, 768, 768), MatmulSpec.new(32768, 16384, 768),
+                 MatmulSpec.new(32768, 3072, 768).right_transposed(),
+                 MatmulSpec.new(768, 16384, 32768).left_transposed().accumulate()):
+        plan = gemm.plan(spec.with_precision(bf16))
+        assert plan.path == gemm.PATH_BF16_WIDE and plan.persistent_grid == 256, spec
+        check_persistent_rules(spec, plan, 256)
+        check_tiled_cover(plan)
+    for spec in (MatmulSpec.new(32768, 768, 3072), MatmulSpec.new(32768, 768, 2304).right_transposed(),
+                 MatmulSpec.new(768, 2304, 32768).left_transposed().accumulate(), MatmulSpec.new(8192, 1024, 768)):
+        plan = gemm.plan(spec.with_precision(bf16))
+        assert plan.path == gemm.PATH_BF16_WIDE and plan.persistent_grid == 0, spec
 
 
 def test_tiles_round_up_and_keep_the_batch_axis():

@@ -1,4 +1,5 @@
-"""The persistent fp32 kernel (SN_PATH_F32_PERSISTENT, gemm_dma.hip's dma_persistent).
+"""The persistent kernels: fp32 128 x 128 tiles (SN_PATH_F32_PERSISTENT, gemm_dma.hip's dma_persistent) and
+bf16 256 x 256 tiles (SN_PATH_BF16_WIDE with a persistent grid, gemm_bf16_wide_persistent_kernel).
 
 Each of its workgroups loops over work items (matrix, K slice, tile) and loads the next item's first two
 K-steps under the current tile's last two, so the tile's output stores go out behind those loads. Per tile it
@@ -7,19 +8,20 @@ bit the one-tile kernel's. A product that runs persistent is therefore compared 
 computed by calls too small to run persistent (row blocks, or single matrices of a batch: each output
 element's sum is the same one); split-K weight gradients run on integer operands, where every summation
 order is exact, against the exact product; a sample of rows goes through the oracle (the reference's loop,
-reference.rs:10-38) at the fp32 tolerance; and reruns must give the same bits. The device is an MI355X
-(256 CUs), whose plans these are."""
+reference.rs:10-38) at the fp32 tolerance (2e-2 for bf16 inputs); and reruns must give the same bits. The
+device is an MI355X (256 CUs), whose plans these are."""
 import numpy as np
 import pytest
 
 from oracle import oracle
 from staleynet_amd import gemm
-from staleynet_amd.gemm import BatchStrides, MatmulSpec, Shape
+from staleynet_amd.gemm import BatchStrides, MatmulSpec, Precision, Shape
 
 pytestmark = pytest.mark.gpu
 
 CUS = 256
 TOLERANCE = 1e-5
+BF16_TOLERANCE = 2e-2
 
 
 def upload(gpu, values):
@@ -28,34 +30,42 @@ def upload(gpu, values):
 
 def assert_persistent(spec, expected=True):
     plan = gemm.plan(spec, cu_count=CUS)
-    assert (plan.path == gemm.PATH_F32_PERSISTENT) == expected, (spec, plan.path)
+    if spec.precision == Precision.Bf16:
+        assert plan.path == gemm.PATH_BF16_WIDE and (plan.persistent_grid > 0) == expected, (spec, plan.path)
+    else:
+        assert (plan.path == gemm.PATH_F32_PERSISTENT) == expected, (spec, plan.path)
     return plan
 
 
 def sample_rows_against_oracle(spec, left, right, out, rows):
     """The oracle's full-precision loop on a few output rows (NN / NT storage, unbatched)."""
     m, n, k = spec.rows, spec.cols, spec.inner
+    tolerance = BF16_TOLERANCE if spec.precision == Precision.Bf16 else TOLERANCE
     for row in rows:
         product = oracle.Product(1, n, k, False, bool(spec.right), 1, 0, 0, 0, spec.scale, False)
         expected = np.zeros(n, np.float32)
         oracle.matmul(product, left[row * k:(row + 1) * k], right, expected)
         error = oracle.relative_error(expected, out[row * n:(row + 1) * n])
-        assert error < TOLERANCE, f"row {row}: relative error {error}"
+        assert error < tolerance, f"row {row}: relative error {error}"
 
 
-@pytest.mark.parametrize("layout,m,n,k,parts", [("NN", 4096, 4096, 768, 2), ("NT", 8192, 2048, 512, 2),
-                                                ("NN", 4096, 16384, 256, 8)])
-def test_persistent_matches_the_one_tile_kernel_bit_for_bit(gpu, layout, m, n, k, parts):
-    print(f"persistent {layout} {m}x{n}x{k} against {parts} row blocks", flush=True)
-    spec = MatmulSpec.new(m, n, k)
+@pytest.mark.parametrize("layout,m,n,k,parts,precision", [
+    ("NN", 4096, 4096, 768, 2, Precision.F32), ("NT", 8192, 2048, 512, 2, Precision.F32),
+    ("NN", 4096, 16384, 256, 8, Precision.F32),
+    # bf16, 256 x 256 tiles (the weight staged as bf16 in both): 512 work items against blocks of 128.
+    ("NN", 32768, 1024, 768, 4, Precision.Bf16), ("NT", 32768, 1024, 768, 4, Precision.Bf16)])
+def test_persistent_matches_the_one_tile_kernel_bit_for_bit(gpu, layout, m, n, k, parts, precision):
+    print(f"persistent {layout} {m}x{n}x{k} {precision.name} against {parts} row blocks", flush=True)
+    spec = MatmulSpec.new(m, n, k).with_precision(precision)
     if layout == "NT":
         spec = spec.right_transposed()
     assert_persistent(spec)
-    block = MatmulSpec.new(m // parts, n, k)
+    block = MatmulSpec.new(m // parts, n, k).with_precision(precision)
     if layout == "NT":
         block = block.right_transposed()
     block_plan = assert_persistent(block, expected=False)
-    assert (block_plan.tile_rows, block_plan.tile_cols, block_plan.splits) == (128, 128, 1)
+    tile = 256 if precision == Precision.Bf16 else 128
+    assert (block_plan.tile_rows, block_plan.tile_cols, block_plan.splits) == (tile, tile, 1)
     left = oracle.random_values(m * k, 11)
     right = oracle.random_values(k * n, 12) * np.float32(0.02)
     lt, rt = upload(gpu, left), upload(gpu, right)
@@ -147,13 +157,14 @@ def test_persistent_forward_with_bias_matches_the_one_tile_kernel(gpu):
         t.free()
 
 
-@pytest.mark.parametrize("inputs,outputs", [(768, 2304), (768, 4096)])
-def test_persistent_split_weight_gradients_are_exact_on_integers(gpu, inputs, outputs):
-    # dW += x^T dY at config 2's qkv shape and a wider one (K = 32768, split into even slices), on integer
-    # operands of magnitude <= 2: every partial sum is an integer below 2^24, so any summation order
-    # gives the exact result.
-    tokens = 32768
-    spec = MatmulSpec.new(inputs, outputs, tokens).left_transposed().accumulate()
+@pytest.mark.parametrize("inputs,outputs,tokens,precision", [(768, 2304, 32768, Precision.F32),
+                                                              (768, 4096, 32768, Precision.F32),
+                                                              (768, 16384, 8192, Precision.Bf16)])
+def test_persistent_split_weight_gradients_are_exact_on_integers(gpu, inputs, outputs, tokens, precision):
+    # dW += x^T dY at config 2's qkv shape and wider ones (K split into even slices), on integer operands
+    # of magnitude <= 2 (exact in bf16 too): every partial sum is an integer below 2^24, so any summation
+    # order gives the exact result.
+    spec = MatmulSpec.new(inputs, outputs, tokens).left_transposed().accumulate().with_precision(precision)
     plan = assert_persistent(spec)
     assert plan.splits > 1
     print(f"persistent TN {inputs}x{outputs}x{tokens}: {plan.splits} slices of {plan.k_per_split}", flush=True)
