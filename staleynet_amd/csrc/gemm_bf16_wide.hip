@@ -55,15 +55,41 @@ __device__ __forceinline__ void stage_barrier() {
 // instead of being precomputed per vector and held across the loop.
 __device__ __forceinline__ void launder(int& x) { asm volatile("" : "+v"(x)); }
 
+// The right operand's stage rows in QUAD order (write_tile's QUAD_N map):
+// LDS position p of each 128-row group (a wave's columns) holds the logical
+// row quad_row(p), so that block j's fragment rows, positions 32 j + (0..31),
+// are the rows 4 (0..31) + j whose outputs the epilogue stores side by side.
+// The fragment reads are unchanged; the loaders place each row at
+// quad_position of it (the inverse).
+__host__ __device__ constexpr int quad_row(int p) { return (p / 128) * 128 + 4 * (p % 32) + (p % 128) / 32; }
+__host__ __device__ constexpr int quad_position(int r) { return (r / 128) * 128 + 32 * (r % 4) + (r % 128) / 4; }
+static_assert(quad_position(quad_row(37)) == 37 && quad_row(quad_position(201)) == 201, "inverse maps");
+
 // The fp32 loaders (gemm_common.h) with the bf16 LDS write addressed from one
 // per-lane base: vector v of a K-contiguous loader is row tid / 8 + v x
 // (THREADS / 8), 16 x THREADS / 8 bytes further into the octet plane; block
 // v of a row-contiguous loader is rows 4 (tid / 8 + v x THREADS / 8) .. + 3.
-template <int ROWS, int BK, int THREADS>
+// QUAD: the rows in quad order (a K-contiguous loader loads, for the same
+// LDS slots, the rows quad_row of them; a row-contiguous one writes each of
+// its four rows at quad_position of it).
+template <int ROWS, int BK, int THREADS, bool QUAD = false>
 struct WideKLoader : KContiguousBufferLoader<ROWS, BK, THREADS> {
     using Base = KContiguousBufferLoader<ROWS, BK, THREADS>;
     using Base::reg;
     static_assert(Base::TOTAL % THREADS == 0 && THREADS % Base::GROUPS == 0, "whole vectors per thread");
+    static_assert(!QUAD || ROWS % 128 == 0, "whole 128-row groups");
+    __device__ __forceinline__ void init(int64_t ld, int64_t row0, int64_t rows, int tid) {
+        if constexpr (!QUAD) {
+            Base::init(ld, row0, rows, tid);
+        } else {
+#pragma unroll
+            for (int v = 0; v < Base::PER_THREAD; ++v) {
+                const int idx = tid + v * THREADS;
+                const int r = quad_row(idx / Base::GROUPS);
+                Base::offset[v] = row0 + r < rows ? int32_t((r * ld + (idx % Base::GROUPS) * 4) * 4) : kOutOfRange;
+            }
+        }
+    }
     __device__ __forceinline__ void store_bf16(uint16_t* lds, int tid) const {
         using O = OctetPlanes<ROWS, BK, Base::BF16_PAD>;
         const int g = tid % Base::GROUPS;
@@ -76,15 +102,20 @@ struct WideKLoader : KContiguousBufferLoader<ROWS, BK, THREADS> {
     }
 };
 
-template <int ROWS, int BK, int THREADS>
+template <int ROWS, int BK, int THREADS, bool QUAD = false>
 struct WideRowLoader : RowContiguousBufferLoader<ROWS, BK, THREADS> {
     using Base = RowContiguousBufferLoader<ROWS, BK, THREADS>;
     using Base::reg;
     static_assert(Base::TOTAL % THREADS == 0 && THREADS % Base::GROUPS == 0, "whole blocks per thread");
+    // Blocks v of a thread are 4 THREADS / GROUPS rows apart: whole 128-row
+    // groups, so block v's quad positions are block 0's plus 4 v THREADS /
+    // GROUPS (immediate offsets from one base).
+    static_assert(!QUAD || ((4 * THREADS / Base::GROUPS) % 128 == 0 && ROWS % 128 == 0), "whole 128-row groups");
     __device__ __forceinline__ void store_bf16(uint16_t* lds, int tid) const {
         using O = OctetPlanes<ROWS, BK, Base::BF16_PAD>;
         const int g = tid % Base::GROUPS;
-        int base = ((g / 2) * O::PLANE + 4 * (tid / Base::GROUPS)) * 16 + 8 * (g % 2);
+        const int c = tid / Base::GROUPS;  // this thread's rows 4 c .. 4 c + 3 of block 0
+        int base = ((g / 2) * O::PLANE + (QUAD ? quad_position(4 * c) : 4 * c)) * 16 + 8 * (g % 2);
         launder(base);
         char* p = reinterpret_cast<char*>(lds) + base;
 #pragma unroll
@@ -92,14 +123,16 @@ struct WideRowLoader : RowContiguousBufferLoader<ROWS, BK, THREADS> {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const f32x4 t = {reg[v][0][e], reg[v][1][e], reg[v][2][e], reg[v][3][e]};
-                *reinterpret_cast<u32x2*>(p + (4 * v * (THREADS / Base::GROUPS) + e) * 16) = pack_bf16(t);
+                // quad_position(4 c + e) = quad_position(4 c) + 32 e for e < 4.
+                const int row = 4 * v * (THREADS / Base::GROUPS) + (QUAD ? 32 * e : e);
+                *reinterpret_cast<u32x2*>(p + row * 16) = pack_bf16(t);
             }
     }
 };
 
-template <bool K_CONTIGUOUS, int ROWS, int BK, int THREADS>
-using WideLoaderFor = typename std::conditional<K_CONTIGUOUS, WideKLoader<ROWS, BK, THREADS>,
-                                                WideRowLoader<ROWS, BK, THREADS>>::type;
+template <bool K_CONTIGUOUS, int ROWS, int BK, int THREADS, bool QUAD = false>
+using WideLoaderFor = typename std::conditional<K_CONTIGUOUS, WideKLoader<ROWS, BK, THREADS, QUAD>,
+                                                WideRowLoader<ROWS, BK, THREADS, QUAD>>::type;
 
 // An operand already rounded to bf16 and laid out K-contiguous in the
 // workspace (launch_stage_bf16: [rows][kp], kp = K rounded up to 8, zeros
@@ -108,7 +141,7 @@ using WideLoaderFor = typename std::conditional<K_CONTIGUOUS, WideKLoader<ROWS, 
 // contiguous bytes) and each writes its octet's LDS slot as it came. `ld` is
 // kp, in bf16 elements; `base` points at the operand (batch offsets in
 // floats, kp being even).
-template <int ROWS, int BK, int THREADS>
+template <int ROWS, int BK, int THREADS, bool QUAD = false>
 struct StagedLoader {
     static constexpr int OCTETS = BK / 8;
     static constexpr int PER_THREAD = ROWS * OCTETS / THREADS;
@@ -121,10 +154,15 @@ struct StagedLoader {
     f32x4 reg[PER_THREAD];  // 8 bf16 each, as loaded
     int32_t offset[PER_THREAD];
 
+    static_assert(!QUAD || ROWS % 128 == 0, "whole 128-row groups");
+
+    // QUAD: the rows whose slots these are in quad order (the slots, and so
+    // the LDS writes, stay where they are).
     __device__ __forceinline__ void init(int64_t ld, int64_t row0, int64_t rows, int tid) {
 #pragma unroll
         for (int v = 0; v < PER_THREAD; ++v) {
-            const int r = tid / OCTETS + v * (THREADS / OCTETS);
+            const int slot_row = tid / OCTETS + v * (THREADS / OCTETS);
+            const int r = QUAD ? quad_row(slot_row) : slot_row;
             offset[v] = row0 + r < rows ? int32_t((r * ld + 8 * (tid % OCTETS)) * 2) : kOutOfRange;
         }
     }
@@ -151,9 +189,9 @@ struct StagedLoader {
 // Which operand the workspace holds as bf16: none, the left or the right.
 enum StagedSide { kStageNone = 0, kStageLeft = 1, kStageRight = 2 };
 
-template <bool K_CONTIGUOUS, bool STAGED, int ROWS, int BK, int THREADS>
-using OperandLoader = typename std::conditional<STAGED, StagedLoader<ROWS, BK, THREADS>,
-                                                WideLoaderFor<K_CONTIGUOUS, ROWS, BK, THREADS>>::type;
+template <bool K_CONTIGUOUS, bool STAGED, int ROWS, int BK, int THREADS, bool QUAD = false>
+using OperandLoader = typename std::conditional<STAGED, StagedLoader<ROWS, BK, THREADS, QUAD>,
+                                                WideLoaderFor<K_CONTIGUOUS, ROWS, BK, THREADS, QUAD>>::type;
 
 // Vector-memory instructions one loader issues per step.
 template <class L>
@@ -167,7 +205,7 @@ template <bool A_K, bool B_K, int SIDE, bool COLSUM = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_bf16_wide_kernel(Args args) {
     using T = WideTile;
     using LA = OperandLoader<A_K, SIDE == kStageLeft, T::BM, T::BK, T::THREADS>;
-    using LB = OperandLoader<B_K, SIDE == kStageRight, T::BN, T::BK, T::THREADS>;
+    using LB = OperandLoader<B_K, SIDE == kStageRight, T::BN, T::BK, T::THREADS, true>;
     using OA = OctetPlanes<T::BM, T::BK, LA::BF16_PAD>;
     using OB = OctetPlanes<T::BN, T::BK, LB::BF16_PAD>;
     constexpr int kSetLoads = loads_per_step<LA>() + loads_per_step<LB>();
@@ -334,9 +372,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // The product goes out with streaming stores; split-K partials, which the
     // reduce reads back, with ordinary ones (measured 1 % faster over the set).
     if (partial)
-        write_tile<T, true>(args, acc, out, m0, n0, wave_m, wave_n, lane, partial);
+        write_tile<T, true, false, false, 0, false, true>(args, acc, out, m0, n0, wave_m, wave_n, lane, partial);
     else
-        write_tile<T, true, false, false, kStreaming>(args, acc, out, m0, n0, wave_m, wave_n, lane, partial);
+        write_tile<T, true, false, false, kStreaming, false, true>(args, acc, out, m0, n0, wave_m, wave_n, lane,
+                                                                    partial);
 }
 
 // The same product as a persistent loop: each workgroup takes work items
@@ -349,21 +388,27 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // first into LDS, so the next tile starts from data already in LDS and in
 // registers. The tile's (streaming) output stores go out after those loads:
 // load and store completions are counted in issue order (vmcnt), so the next
-// tile's first two steps wait for their register sets with at most 63
-// operations outstanding, which the 128 stores after them always exceed, and
-// the stores drain under those two steps instead of ending the workgroup.
+// tile's first two steps wait for their register sets with as many
+// operations outstanding as were issued after them (the other set and the
+// stores), and the stores drain under those two steps instead of ending the
+// workgroup.
 template <bool A_K, bool B_K, int SIDE>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_bf16_wide_persistent_kernel(
     Args args) {
     using T = WideTile;
     using LA = OperandLoader<A_K, SIDE == kStageLeft, T::BM, T::BK, T::THREADS>;
-    using LB = OperandLoader<B_K, SIDE == kStageRight, T::BN, T::BK, T::THREADS>;
+    using LB = OperandLoader<B_K, SIDE == kStageRight, T::BN, T::BK, T::THREADS, true>;
     using OA = OctetPlanes<T::BM, T::BK, LA::BF16_PAD>;
     using OB = OctetPlanes<T::BN, T::BK, LB::BF16_PAD>;
     constexpr int kSetLoads = loads_per_step<LA>() + loads_per_step<LB>();
-    // Store instructions of the interior epilogue (one per accumulator).
-    constexpr int kStores = T::FM * T::FN * 16;
-    static_assert(kStores + kSetLoads >= 63, "enough operations after a set for a wait at 63 to cover it");
+    // Store instructions of the interior epilogue (one 16-byte store per row
+    // of a lane's four adjacent columns), and the count the first two steps
+    // of a tile wait down to: a set issued before the previous epilogue has
+    // at least these many operations after it (the other set's loads and the
+    // stores; a fused bias adds loads before the stores).
+    constexpr int kStores = T::FM * 16;
+    constexpr int kAfterEpilogue = kSetLoads + kStores;
+    static_assert(kAfterEpilogue < 64, "vmcnt is 6 bits");
     __shared__ __attribute__((aligned(16))) uint16_t lds_a[2][8 * OA::SLOTS];
     __shared__ __attribute__((aligned(16))) uint16_t lds_b[2][8 * OB::SLOTS];
 
@@ -465,7 +510,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         using NextSet = std::integral_constant<int, (J + 1) % NSETS>;
         using NextStage = std::integral_constant<int, (J + 1) % 2>;
         step_from(Stage{}, [&]() __attribute__((always_inline)) {
-            if constexpr (decltype(after_stores)::value) wait_vector_loads<63>();
+            if constexpr (decltype(after_stores)::value) wait_vector_loads<kAfterEpilogue>();
             else wait_vector_loads<(NSETS - 1) * kSetLoads>();
             stage(NextSet{}, NextStage{});
             issue(NextSet{}, load_step);
@@ -517,10 +562,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                              : args.c + (args.batch_base + cur.batch_local) * args.stride_c;
         const int64_t m0 = int64_t(cur.tm) * T::BM, n0 = int64_t(cur.tn) * T::BN;
         if (partial)
-            write_tile<T, true, false, false, 0, true>(args, acc, out, m0, n0, wave_m, wave_n, lane, partial);
+            write_tile<T, true, false, false, 0, true, true>(args, acc, out, m0, n0, wave_m, wave_n, lane, partial);
         else
-            write_tile<T, true, false, false, kStreaming, true>(args, acc, out, m0, n0, wave_m, wave_n, lane,
-                                                                 partial);
+            write_tile<T, true, false, false, kStreaming, true, true>(args, acc, out, m0, n0, wave_m, wave_n, lane,
+                                                                       partial);
         if (!has_next) break;
         w += stride;
         cur = next;

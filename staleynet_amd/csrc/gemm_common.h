@@ -469,7 +469,11 @@ __device__ __forceinline__ void write_output(float* dst, float sum, float scale,
 // fragments a lane reads as adjacent rows of a row-contiguous operand, one
 // 8-byte LDS read per k) interleaves them instead: block i covers rows
 // 2q + i, block j columns 2(l%32) + j.
-template <bool PAIR_M, bool PAIR_N>
+// QUAD_N: four column blocks whose columns interleave in fours instead
+// (block j covers columns 4(l%32) + j of the wave's 128), so a lane's four
+// outputs of a row are adjacent (one 16-byte store); the operand side reads
+// its rows permuted to match (the wide bf16 kernel's right-operand stages).
+template <bool PAIR_M, bool PAIR_N, bool QUAD_N = false>
 struct TileMap {
     // Row within the wave's sub-tile: a per-lane part (half = l/32) and a
     // part per (block, element) that does not depend on the lane.
@@ -478,9 +482,9 @@ struct TileMap {
         return PAIR_M ? 2 * (8 * (r / 4) + (r % 4)) + i : 32 * i + 8 * (r / 4) + (r % 4);
     }
     __device__ __forceinline__ static constexpr int col_lane(int col_in_block) {
-        return PAIR_N ? 2 * col_in_block : col_in_block;
+        return QUAD_N ? 4 * col_in_block : PAIR_N ? 2 * col_in_block : col_in_block;
     }
-    __device__ __forceinline__ static constexpr int col_elem(int j) { return PAIR_N ? j : 32 * j; }
+    __device__ __forceinline__ static constexpr int col_elem(int j) { return PAIR_N || QUAD_N ? j : 32 * j; }
 };
 
 // Writes a wave's accumulators (TileMap gives each element's place).
@@ -488,14 +492,16 @@ struct TileMap {
 // reference's combine, with causal-masked outputs written 0 (overwrite) or
 // left alone (accumulate). POLICY: the buffer stores' cache policy.
 // INTERIOR_ONLY: the caller guarantees an interior tile that reads nothing
-// back (partial, or overwrite), so only that path is compiled.
+// back (partial, or overwrite), so only that path is compiled. QUAD_N: see
+// TileMap.
 template <class T, bool BUF, bool PAIR_M = false, bool PAIR_N = false, int32_t POLICY = 0,
-          bool INTERIOR_ONLY = false>
+          bool INTERIOR_ONLY = false, bool QUAD_N = false>
 __device__ __forceinline__ void write_tile(const Args& args, const f32x16 (&acc)[T::FM][T::FN], float* out,
                                            int64_t m0, int64_t n0, int wave_m, int wave_n, int lane, bool partial) {
-    using Map = TileMap<PAIR_M, PAIR_N>;
+    using Map = TileMap<PAIR_M, PAIR_N, QUAD_N>;
     static_assert(!PAIR_M || T::FM == 2, "pairs of row blocks");
     static_assert(!PAIR_N || T::FN == 2, "pairs of column blocks");
+    static_assert(!QUAD_N || (T::FN == 4 && T::WTN == 128 && !PAIR_N), "fours of column blocks");
     const int col_in_block = lane & 31;
     const int half = lane >> 5;
     const bool accumulate = args.accumulate != 0;
@@ -533,7 +539,28 @@ __device__ __forceinline__ void write_tile(const Args& args, const f32x16 (&acc)
                 if (add_bias) value = value + bias_value[j];
                 return value;
             };
-            if constexpr (PAIR_N) {
+            if constexpr (QUAD_N) {
+                // The lane's four columns are adjacent: one 16-byte store per
+                // row. The row goes into the vector offset, with a constant
+                // scalar offset: with the row in an SGPR offset, a store's
+                // data registers were rewritten by the next VALU instruction
+                // before the store read them (the next row's values came out
+                // in some lanes), a wait the compiler keeps only for stores
+                // without a register scalar offset.
+                typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+                const int32_t column_offset = int32_t((lane_row * args.n + lane_col) * 4);
+#pragma unroll
+                for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int32_t row_offset = int32_t(Map::row_elem(i, r) * args.n * 4);
+                        const u32x4_t quad = {__builtin_bit_cast(uint32_t, value_of(i, 0, r)),
+                                              __builtin_bit_cast(uint32_t, value_of(i, 1, r)),
+                                              __builtin_bit_cast(uint32_t, value_of(i, 2, r)),
+                                              __builtin_bit_cast(uint32_t, value_of(i, 3, r))};
+                        __builtin_amdgcn_raw_buffer_store_b128(quad, rsrc, column_offset + row_offset, 0, POLICY);
+                    }
+            } else if constexpr (PAIR_N) {
                 // The lane's two columns are adjacent: one 8-byte store per element pair.
                 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
                 const int32_t column_offset = int32_t((lane_row * args.n + lane_col) * 4);
