@@ -111,10 +111,31 @@ struct WideRowLoader : RowContiguousBufferLoader<ROWS, BK, THREADS> {
     // groups, so block v's quad positions are block 0's plus 4 v THREADS /
     // GROUPS (immediate offsets from one base).
     static_assert(!QUAD || ((4 * THREADS / Base::GROUPS) % 128 == 0 && ROWS % 128 == 0), "whole 128-row groups");
+    // The row quad (rows 4 c .. 4 c + 3) a thread's block 0 holds. In quad
+    // order the four rows of quad c land at positions 32 e + c, so two quads
+    // written in the same 16-lane phase must be 4 apart for their 8-byte
+    // writes to take distinct banks: quad index bits 0 and 2 are swapped
+    // (the lanes of a wave still read the same 128-byte row pieces). The
+    // LDS-bank counters showed the unswapped order conflicting.
+    __device__ __forceinline__ static constexpr int quad_of(int q) {
+        return QUAD ? (q & ~5) | ((q & 1) << 2) | ((q >> 2) & 1) : q;
+    }
+    __device__ __forceinline__ void init(int64_t ld, int64_t row0, int64_t rows, int tid) {
+#pragma unroll
+        for (int v = 0; v < Base::PER_THREAD; ++v) {
+            const int idx = tid + v * THREADS;
+            const int r = 4 * quad_of(idx / Base::GROUPS);
+            const bool valid = row0 + r < rows;
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk)
+                Base::offset[v][kk] =
+                    valid ? int32_t((((idx % Base::GROUPS) * 4 + kk) * ld + r) * 4) : kOutOfRange;
+        }
+    }
     __device__ __forceinline__ void store_bf16(uint16_t* lds, int tid) const {
         using O = OctetPlanes<ROWS, BK, Base::BF16_PAD>;
         const int g = tid % Base::GROUPS;
-        const int c = tid / Base::GROUPS;  // this thread's rows 4 c .. 4 c + 3 of block 0
+        const int c = quad_of(tid / Base::GROUPS);  // this thread's rows 4 c .. 4 c + 3 of block 0
         int base = ((g / 2) * O::PLANE + (QUAD ? quad_position(4 * c) : 4 * c)) * 16 + 8 * (g % 2);
         launder(base);
         char* p = reinterpret_cast<char*>(lds) + base;
@@ -129,6 +150,10 @@ struct WideRowLoader : RowContiguousBufferLoader<ROWS, BK, THREADS> {
             }
     }
 };
+
+static_assert(WideRowLoader<256, 32, 512, true>::quad_of(5) == 5 && WideRowLoader<256, 32, 512, true>::quad_of(1) == 4 &&
+                  WideRowLoader<256, 32, 512, true>::quad_of(68) == 65,
+              "quad index bits 0 and 2 swapped");
 
 template <bool K_CONTIGUOUS, int ROWS, int BK, int THREADS, bool QUAD = false>
 using WideLoaderFor = typename std::conditional<K_CONTIGUOUS, WideKLoader<ROWS, BK, THREADS, QUAD>,
@@ -262,8 +287,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         la[S].load(a, args.lda, m0, args.m, k0, k_end, tid);
         lb[S].load(b, args.ldb, n0, args.n, k0, k_end, tid);
     };
-    // Column sums (COLSUM, first tile row): thread t holds columns 4 (t / 8)
-    // .. + 3 at k = 4 (t % 8) .. + 3 of every step, added here in k order as
+    // Column sums (COLSUM, first tile row): thread t holds columns 4 q .. +3
+    // (q = LB::quad_of(t / 8)) at k = 4 (t % 8) .. + 3 of every step, added here in k order as
     // each step is staged; the 8 threads of a column block are added at the
     // end in a fixed butterfly order.
     const bool colsum_tile = COLSUM && tm == 0;  // uniform over the workgroup
@@ -356,7 +381,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             if ((tid & 7) == 0) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const int64_t c = n0 + 4 * (tid / 8) + e;
+                    const int64_t c = n0 + 4 * LB::quad_of(tid / 8) + e;
                     if (c < args.n) {
                         if (partial)
                             args.ws[int64_t(args.splits) * args.m * args.n + int64_t(split) * args.n + c] = colsum[e];
