@@ -235,7 +235,7 @@ def check_persistent_rules(spec, plan, cus):
     assert plan.splits > 1 or not spec.write
     assert plan.launches == 1 and spec.inner > 128
     last = spec.inner - (plan.splits - 1) * plan.k_per_split
-    assert plan.k_per_split % 64 == 0 and -(-last // 32) % 2 == 0
+    assert -(-plan.k_per_split // 32) % 2 == 0 and -(-last // 32) % 2 == 0
 
 
 def test_persistent_products():

@@ -52,6 +52,8 @@ def sample_rows_against_oracle(spec, left, right, out, rows):
 @pytest.mark.parametrize("layout,m,n,k,parts,precision", [
     ("NN", 4096, 4096, 768, 2, Precision.F32), ("NT", 8192, 2048, 512, 2, Precision.F32),
     ("NN", 4096, 16384, 256, 8, Precision.F32),
+    # K not a whole number of 32-deep steps (six steps, the last 4 deep): the loads past K read zeros.
+    ("NN", 4096, 4096, 164, 2, Precision.F32), ("NT", 4096, 4096, 164, 2, Precision.F32),
     # bf16, 256 x 256 tiles (the weight staged as bf16 in both): 512 work items against blocks of 128.
     ("NN", 32768, 1024, 768, 4, Precision.Bf16), ("NT", 32768, 1024, 768, 4, Precision.Bf16)])
 def test_persistent_matches_the_one_tile_kernel_bit_for_bit(gpu, layout, m, n, k, parts, precision):
