@@ -389,9 +389,15 @@ int sn_causal_attention_with_stats(sn_context *context, const sn_attention_shape
  * [heads][keys][head_dim], all dense, with dS = P * (dO V^T - D) and D per
  * query = sum over h of dO * O (softmax_backward's projection, since O =
  * P V). Within the fp32 tolerance of the reference's calls; deterministic
- * (no atomics). Uses 12 bytes of the context's workspace per query
- * (SN_ERR_WORKSPACE); the same shape codes as sn_causal_attention; an
- * output overlapping an input or another output is SN_ERR_ALIASING. */
+ * (no atomics). Needs 12 bytes of the context's workspace per query
+ * (SN_ERR_WORKSPACE). For head dims 32 and 64 it also keeps dQ's partial
+ * sums per 128-key block there when they fit (256 or 128 bytes per query
+ * and block whose keys the query's 64-query stage reaches: 855 MB at 192
+ * heads of 2048), for all heads or in runs of heads, and then skips the
+ * second recomputation of S and dP; the two ways sum dQ in different orders,
+ * so its bits depend on the workspace size (dK and dV's do not). The same
+ * shape codes as sn_causal_attention; an output overlapping an input or
+ * another output is SN_ERR_ALIASING. */
 int sn_causal_attention_backward(sn_context *context, const sn_attention_shape *shape, const float *q, size_t q_len,
                                  const float *k, size_t k_len, const float *v, size_t v_len, const float *out,
                                  size_t out_len, const float *d_out, size_t d_out_len, const float *stats,

@@ -13,24 +13,30 @@
 // with D per query = sum over h of dO * O (equal to softmax_backward's
 // projection sum over keys of dP * P, since O = P V).
 //
-// Three launches, each output element summed by one wave in a fixed order
-// (no atomics; reruns give the same bits):
-//  * rows: per query {m, 1 / l, D} into the workspace (16 bytes);
+// Three launches, every sum taken in a fixed order (no atomics; reruns give
+// the same bits):
+//  * rows: per query {m, 1 / l, D} into the workspace (12 bytes);
 //  * key blocks: a workgroup owns 128 keys of a head, a wave 32, with K and V
-//    of its keys in registers; Q, dO and the rows stream through LDS in
-//    64-query stages, from the first query that sees the block to the last.
-//    A wave computes S = Q K^T and dP = dO V^T for 32 queries against its 32
-//    keys: in the 32x32 accumulator lane l holds column l % 32, its key, so
-//    P and dS are already laid out as the B operands of dV^T += dO^T P and
-//    dK^T += Q^T dS (the forward's O^T += V^T P^T, transposed roles);
-//  * query blocks: the layout of the forward and the probability gradient
-//    (a lane owns a query): S^T = K Q^T and dP^T = V dO^T against staged K
-//    and V, then dQ^T += K^T dS^T.
-// Per 32 x 32 block of (query, key) pairs the key kernel issues four
-// products' MFMAs and the query kernel three; blocks wholly past a wave's
-// causal horizon are skipped, and only those that cross it test each pair.
+//    of its keys in LDS (head dims 32, 64) or registers (128); Q, dO and the
+//    rows stream through LDS in 64-query stages, from the first query that
+//    sees the block to the last. A wave computes S = Q K^T and dP = dO V^T
+//    for 32 queries against its 32 keys: in the 32x32 accumulator lane l
+//    holds column l % 32, its key, so P and dS are already laid out as the B
+//    operands of dV^T += dO^T P and dK^T += Q^T dS (the forward's O^T +=
+//    V^T P^T, transposed roles);
+//  * dQ, one of two ways. Where the workspace holds them (head dims 32 and
+//    64), the key kernel also writes each stage's dS to LDS and multiplies it
+//    by the block's K, leaving per key block partial sums of dQ that a third
+//    kernel adds up in block order: five products' MFMAs per pair in all.
+//    Otherwise query blocks recompute S and dP in the layout of the forward
+//    and the probability gradient (a lane owns a query): S^T = K Q^T and
+//    dP^T = V dO^T against staged K and V, then dQ^T += K^T dS^T: seven
+//    products' MFMAs per pair.
+// Blocks wholly past a wave's causal horizon are skipped, and only those that
+// cross it test each pair.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <type_traits>
@@ -107,6 +113,27 @@ __global__ __launch_bounds__(256) void attention_rows_kernel(RowsArgs a) {
     }
 }
 
+// The first query of the first stage of key block `block`: the first query
+// that sees the block's first key, rounded down to a whole stage.
+__host__ __device__ constexpr int64_t stage_begin(int64_t block, int64_t query_offset) {
+    return (block * kKeyBlock - query_offset > 0 ? block * kKeyBlock - query_offset : 0) / kKeys * kKeys;
+}
+
+// The queries a key block's stages cover (from stage_begin to the last).
+__host__ __device__ constexpr int64_t block_queries(int64_t block, int64_t queries, int64_t query_offset) {
+    return stage_begin(block, query_offset) < queries ? queries - stage_begin(block, query_offset) : 0;
+}
+
+// dQ partial sums, when the key kernel computes them: per head, for each key
+// block in order, one row of H floats per query its stages cover (the
+// block's dS times its K rows, summed over its keys); block b's rows start
+// after those of blocks 0 .. b - 1. Rows per head:
+__host__ __device__ inline int64_t partial_rows(int64_t queries, int64_t keys, int64_t query_offset) {
+    int64_t rows = 0;
+    for (int64_t b = 0; b * kKeyBlock < keys; ++b) rows += block_queries(b, queries, query_offset);
+    return rows;
+}
+
 struct KeyGradArgs {
     const float* q;
     const float* k;
@@ -120,6 +147,8 @@ struct KeyGradArgs {
     int64_t query_offset;
     int64_t heads;
     float scale;
+    float* partials;       // dQ partial sums (the LDS kernel's dQ form), else unused
+    int64_t partial_rows;  // partial_rows() of the shape: rows per head
 };
 
 // Element (row, h = 32 b + col) of a stage whose 16-byte chunks are
@@ -449,9 +478,29 @@ void attention_key_grad_kernel(KeyGradArgs a) {
 // dV^T and dK^T meet in LDS and are added in a fixed order (half 0, then
 // half 1): deterministic. (K, V and the stages of h = 128 exceed the LDS, so
 // that head dim keeps the register kernel above.)
+//
+// With DQ the kernel also computes dQ, as partial sums per key block that
+// attention_dq_sum_kernel adds up in block order, so that no query kernel has
+// to recompute S and dP (five products' MFMAs per pair instead of seven). Each
+// stage then ends in two more steps: the waves write their dS blocks to LDS,
+// as the stage's [64 queries][128 keys], over the stage's own Q and dO rows
+// (h = 64; h = 32 has LDS to spare for a buffer of its own); then wave w
+// multiplies queries 16 (w % 4) .. + 15 of it by h columns (w / 4) H / 2 ..
+// + H / 2 - 1 of the block's K (16 x 16 x 4 MFMAs over the 128 keys, in key
+// order) and stores that part of the block's partial sums. The next stage's
+// loads are issued after the stage's first barrier, into the buffer the stage
+// before has finished with.
 constexpr int kLdsKeyWaves = 8;
 
-template <int H>
+// The dS rows of a stage in LDS: row q holds the block's 128 keys, its 16-byte
+// chunk c stored at c ^ ds_swizzle(q). Bijective on the low four bits of c for
+// any 16 consecutive rows (the dQ step's reads, 16 rows at a time, cover all
+// banks), and rows q and q + 4 (the two lane halves of a write) differ in bit 3
+// (they fill opposite halves of the banks).
+__device__ __forceinline__ int ds_swizzle(int q) { return (q & 15) ^ ((q & 4) << 1); }
+constexpr int kDsRow = kKeyBlock;  // floats per dS row
+
+template <int H, bool DQ = false>
 __global__ __launch_bounds__(64 * kLdsKeyWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attention_key_grad_lds_kernel(KeyGradArgs a) {
 #pragma clang fp contract(off)
@@ -462,17 +511,32 @@ void attention_key_grad_lds_kernel(KeyGradArgs a) {
     constexpr int KV_LOADS = KV_SLOTS / (64 * W);
     static_assert(H <= 64 && G::STAGE_SLOTS % (64 * W) == 0 && KV_SLOTS % (64 * W) == 0, "whole loads per wave");
     // Partial sums handed over at the end: 2 x OBLOCKS accumulators per lane
-    // of the four half-1 waves, in the stages' space.
-    constexpr int HANDOFF_FLOATS = 4 * 2 * G::OBLOCKS * 16 * 64;
-    static_assert(HANDOFF_FLOATS <= 4 * G::STAGE_SLOTS * 4, "the hand-off fits in the stages");
+    // of the four half-1 waves, group g's in stage buffer g.
+    constexpr int HANDOFF_FLOATS = 2 * G::OBLOCKS * 16 * 64;
+    static_assert(HANDOFF_FLOATS <= G::STAGE_SLOTS * 4, "a group's hand-off fits in a stage buffer");
+    // A stage's dS: 64 rows of the block's keys, over the stage's Q and dO
+    // rows when those are large enough (h = 64), else in a buffer of its own.
+    constexpr int DS_FLOATS = kKeys * kDsRow;
+    constexpr bool DS_OVER_STAGE = 2 * G::STAGE_SLOTS * 4 >= DS_FLOATS;
+    constexpr int DS_OWN = DQ && !DS_OVER_STAGE ? DS_FLOATS / 4 : 1;
+    // Each stage's Q and dO rows are one LDS object, apart from the other
+    // stage's: the compiler tracks the direct-to-LDS loads in flight per
+    // object, so the reads of one stage do not wait for the loads into the
+    // other (with one array for both stages it made every stage's first
+    // read wait for the next stage's loads).
     __shared__ f32x4 kv_lds[2][KV_SLOTS];
-    __shared__ f32x4 stages[4][G::STAGE_SLOTS];  // Q stage 0, Q stage 1, dO stage 0, dO stage 1
+    __shared__ f32x4 stage0[2][G::STAGE_SLOTS], stage1[2][G::STAGE_SLOTS];  // [Q, dO]
     __shared__ f32x4 r_stage0[W][64], r_stage1[W][64];
+    __shared__ f32x4 ds_own[DS_OWN];
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
-    auto q_of = [&](auto stage) __attribute__((always_inline)) -> f32x4* { return stages[decltype(stage)::value]; };
+    auto q_of = [&](auto stage) __attribute__((always_inline)) -> f32x4* {
+        if constexpr (decltype(stage)::value == 0) return stage0[0];
+        else return stage1[0];
+    };
     auto d_of = [&](auto stage) __attribute__((always_inline)) -> f32x4* {
-        return stages[2 + decltype(stage)::value];
+        if constexpr (decltype(stage)::value == 0) return stage0[1];
+        else return stage1[1];
     };
     auto r_of = [&](auto stage) __attribute__((always_inline)) -> f32x4* {
         if constexpr (decltype(stage)::value == 0) return r_stage0[0];
@@ -554,8 +618,9 @@ void attention_key_grad_lds_kernel(KeyGradArgs a) {
         }
 
     // This wave's block of a stage: queries sub0 .. + 31 (rows 32 qh ..)
-    // against its 32 keys, as the register kernel's block_grad.
-    auto block_grad = [&](auto stage, auto masked, int64_t sub0) __attribute__((always_inline)) {
+    // against its 32 keys, as the register kernel's block_grad; dS of row
+    // 8 g + 4 half + j of the block into ds_out[4 g + j].
+    auto block_grad = [&](auto stage, auto masked, int64_t sub0, float (&ds_out)[16]) __attribute__((always_inline)) {
         constexpr bool MASKED = decltype(masked)::value;
         const f32x4* qs = q_of(stage);
         const f32x4* ds = d_of(stage);
@@ -600,45 +665,151 @@ void attention_key_grad_lds_kernel(KeyGradArgs a) {
                     dv[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(columns.read(ds, qh, g, j, b), p[j], dv[b], 0, 0, 0);
                     dk[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(columns.read(qs, qh, g, j, b), gr[j], dk[b], 0, 0, 0);
                 }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) ds_out[4 * g + j] = gr[j];
         }
         __builtin_amdgcn_sched_barrier(0);
     };
     using Masked = std::true_type;
     using Whole = std::false_type;
-    auto compute = [&](auto stage, int64_t q0) __attribute__((always_inline)) {
+    // The wave's block of the stage; dS stays 0 for a skipped block.
+    auto compute = [&](auto stage, int64_t q0, float (&ds_out)[16]) __attribute__((always_inline)) {
         const int64_t sub0 = q0 + 32 * qh;
         // Wave-uniform: skipped when none of the block's queries sees the wave's first key.
         if (sub0 < a.queries && sub0 + 31 + a.query_offset >= k_wave && k_wave < a.keys) {
             if (sub0 + a.query_offset >= k_wave + 31 && sub0 + 32 <= a.queries && k_wave + 32 <= a.keys)
-                block_grad(stage, Whole{}, sub0);
+                block_grad(stage, Whole{}, sub0, ds_out);
             else
-                block_grad(stage, Masked{}, sub0);
+                block_grad(stage, Masked{}, sub0, ds_out);
         }
     };
-    // K and V go first, so the first wait (all but one stage's loads)
-    // covers them too.
-    constexpr int kStageLoads = 2 * LOADS + 1;
-    issue(I0{}, q_begin);
-    issue(I1{}, q_begin + kKeys);
-    for (int st = 0; st < stages_total; st += 2) {
-        const int64_t q0 = q_begin + int64_t(st) * kKeys;
-        wait_loads<kStageLoads>();
-        lds_barrier();
-        compute(I0{}, q0);
-        lds_barrier();
-        issue(I0{}, q0 + 2 * kKeys);
-        wait_loads<kStageLoads>();
-        lds_barrier();
-        if (st + 1 < stages_total) compute(I1{}, q0 + kKeys);
-        lds_barrier();
-        issue(I1{}, q0 + 3 * kKeys);
+    if constexpr (DQ) {
+        // The dQ step's share of wave w: stage rows 16 (w % 4) + (lane % 16)
+        // (B operand: dS[q][keys]) against h columns (w / 4) H / 2 + 16 t +
+        // (lane % 16) of K (A operand), t < H / 32; MFMA 4 u + e pairs the
+        // keys 16 u + 4 (lane / 16) + e. The 16 x 16 result in lane l:
+        // h = 4 (l / 16) + r, query l % 16, four consecutive h per lane.
+        constexpr int HT = H / 32;
+        const int h_base = (wave / 4) * (H / 2);
+        // Partial sums of this block: rows from its first stage's first query.
+        int64_t rows_before = 0;
+        for (int64_t b = 0; b < block / a.heads; ++b) rows_before += block_queries(b, a.queries, a.query_offset);
+        const __amdgpu_buffer_rsrc_t p_rsrc =
+            buffer_of(a.partials + (head * a.partial_rows + rows_before) * H);
+        constexpr int STORES = HT;  // partial-sum stores per wave per stage
+        auto dq_step = [&](auto stage, int64_t q0, const float (&ds_in)[16]) __attribute__((always_inline)) {
+            float* dsm = DS_OVER_STAGE ? reinterpret_cast<float*>(q_of(stage)) : reinterpret_cast<float*>(ds_own);
+            if constexpr (DS_OVER_STAGE) lds_barrier();  // every wave is done with the stage's Q and dO
+            // dS row 32 qh + 8 g + 4 half + j, key 32 group + col.
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int q = 32 * qh + 8 * g + 4 * half + j, kl = 32 * group + col;
+                    dsm[q * kDsRow + 4 * ((kl / 4) ^ ds_swizzle(q)) + (kl & 3)] = ds_in[4 * g + j];
+                }
+            lds_barrier();  // the stage's dS is whole
+            // Byte offsets of the A reads (K row 4 lg + e of each 16-key step,
+            // column h_base + 16 t + lq) and of the B reads (chunk 4 (u % 4) +
+            // lg of dS row dq_row); u / 4 and the steps add immediates. Formed
+            // here, from a laundered lane, rather than held through the stage.
+            int l = lane;
+            launder(l);
+            const int lq = l % 16, lg = l / 16;
+            const int dq_row = 16 * (wave % 4) + lq;  // stage row
+            int k_off[4][HT], d_off[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+#pragma unroll
+                for (int t = 0; t < HT; ++t) {
+                    const int row = 4 * lg + e, h = h_base + 16 * t + lq;
+                    k_off[e][t] = (row * H + 4 * ((h / 4) ^ (row & G::SWIZZLE)) + (h & 3)) * 4;
+                }
+                d_off[e] = (dq_row * kDsRow + 4 * ((4 * e + lg) ^ ds_swizzle(dq_row))) * 4;
+            }
+            f32x4 acc[HT];
+#pragma unroll
+            for (int t = 0; t < HT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+            const char* kb = reinterpret_cast<const char*>(kv_lds[0]);
+            const char* db = reinterpret_cast<const char*>(dsm);
+#pragma unroll
+            for (int u = 0; u < kDsRow / 16; ++u) {
+                const f32x4 d4 = *reinterpret_cast<const f32x4*>(db + d_off[u % 4] + (u / 4) * 256);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+#pragma unroll
+                    for (int t = 0; t < HT; ++t) {
+                        const float kv = *reinterpret_cast<const float*>(kb + k_off[e][t] + u * 16 * H * 4);
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv, d4[e], acc[t], 0, 0, 0);
+                    }
+            }
+            // Rows past the last query are dropped (out-of-range offsets).
+            const int64_t q = q0 + dq_row;
+            typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+            for (int t = 0; t < HT; ++t) {
+                const int32_t off = q < a.queries ? int32_t(((q - q_begin) * H + h_base + 16 * t + 4 * lg) * 4)
+                                                  : kOutOfRange;
+                // The row offset rides in the vector offset, soffset 0: with a
+                // scalar soffset the compiler may let the next VALU overwrite
+                // the data registers before this 4-dword store has read them.
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[t]), p_rsrc, off, 0, 0);
+            }
+        };
+        auto stage_dq = [&](auto stage, int64_t q0) __attribute__((always_inline)) {
+            float dsv[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) dsv[i] = 0.f;
+            compute(stage, q0, dsv);
+            dq_step(stage, q0, dsv);
+        };
+        // Each stage starts once every wave is done with the stage before,
+        // whose buffer then takes the next stage's loads (past the last query
+        // they read zeros); it ends waiting for those loads, which leaves this
+        // wave's partial-sum stores in flight. The waits and loads are
+        // unconditional, so the compiler's count of the loads in flight stays
+        // exact and it adds no waits of its own.
+        issue(I0{}, q_begin);
+        wait_loads<0>();  // K, V and the first stage
+        for (int st = 0; st < stages_total; st += 2) {
+            const int64_t q0 = q_begin + int64_t(st) * kKeys;
+            lds_barrier();
+            issue(I1{}, q0 + kKeys);
+            stage_dq(I0{}, q0);
+            wait_loads<STORES>();
+            if (st + 1 >= stages_total) break;
+            lds_barrier();
+            issue(I0{}, q0 + 2 * kKeys);
+            stage_dq(I1{}, q0 + kKeys);
+            wait_loads<STORES>();
+        }
+    } else {
+        // K and V go first, so the first wait (all but one stage's loads)
+        // covers them too.
+        constexpr int kStageLoads = 2 * LOADS + 1;
+        float unused[16];
+        issue(I0{}, q_begin);
+        issue(I1{}, q_begin + kKeys);
+        for (int st = 0; st < stages_total; st += 2) {
+            const int64_t q0 = q_begin + int64_t(st) * kKeys;
+            wait_loads<kStageLoads>();
+            lds_barrier();
+            compute(I0{}, q0, unused);
+            lds_barrier();
+            issue(I0{}, q0 + 2 * kKeys);
+            wait_loads<kStageLoads>();
+            lds_barrier();
+            if (st + 1 < stages_total) compute(I1{}, q0 + kKeys, unused);
+            lds_barrier();
+            issue(I1{}, q0 + 3 * kKeys);
+        }
     }
     wait_loads<0>();
     lds_barrier();  // every wave is done with the stages (and K, V)
 
     // Half 1 hands its partial sums to half 0 through the stages' space
     // (lane-consecutive, conflict-free); half 0 adds them and writes.
-    float* handoff = reinterpret_cast<float*>(stages[0]) + group * (2 * G::OBLOCKS * 16 * 64) + lane;
+    float* handoff = reinterpret_cast<float*>(group < 2 ? stage0[group] : stage1[group - 2]) + lane;
     if (qh == 1) {
 #pragma unroll
         for (int b = 0; b < G::OBLOCKS; ++b)
@@ -869,6 +1040,43 @@ void attention_query_grad_kernel(QueryGradArgs a) {
     }
 }
 
+struct DqSumArgs {
+    const float* partials;
+    float* q_grad;
+    int64_t heads, queries, keys, query_offset, partial_rows;
+    float scale;
+};
+
+// dQ = scale x the sum of the key blocks' partial sums, added in block order
+// (the blocks whose stages cover the query; those are 0 .. some b, since a
+// block's first stage starts no earlier than the block before's). One
+// thread per 4 h of a query.
+template <int H>
+__global__ __launch_bounds__(256) void attention_dq_sum_kernel(DqSumArgs a) {
+#pragma clang fp contract(off)
+    constexpr int C = H / 4;
+    const int64_t t = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (t >= a.heads * a.queries * C) return;
+    const int c = int(t % C);
+    const int64_t row = t / C;  // head * queries + query
+    const int64_t head = row / a.queries, q = row % a.queries;
+    const float* base = a.partials + head * a.partial_rows * H + 4 * c;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    int64_t before = 0;  // rows of the blocks before
+    for (int64_t b = 0; b * kKeyBlock < a.keys; ++b) {
+        const int64_t first = stage_begin(b, a.query_offset);
+        if (first > q) break;
+        const f32x4 x = *reinterpret_cast<const f32x4*>(base + (before + q - first) * H);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc[s] = acc[s] + x[s];
+        before += a.queries - first;
+    }
+    f32x4 out;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) out[s] = a.scale * acc[s];
+    *reinterpret_cast<f32x4*>(a.q_grad + row * H + 4 * c) = out;
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 template <int H>
@@ -881,8 +1089,48 @@ hipError_t launch_backward(const AttentionBackwardArgs& a, hipStream_t stream) {
     if (err != hipSuccess) return err;
 
     KeyGradArgs ka{a.q, a.k, a.v, a.d_out, rows, a.k_grad, a.v_grad, a.queries, a.keys, a.q_stride,
-                   a.kv_stride, a.query_offset, a.heads, a.scale};
+                   a.kv_stride, a.query_offset, a.heads, a.scale, nullptr, 0};
     const int64_t key_blocks = (a.keys + kKeyBlock - 1) / kKeyBlock;
+    if constexpr (H <= 64) {
+        // dQ from the key kernel's partial sums when the workspace holds them
+        // after the row records: for all heads at once, or in runs of heads
+        // that still fill the device (512 workgroups or more); else the query
+        // kernel recomputes S and dP for it.
+        const size_t record_bytes = size_t(a.heads) * 3 * size_t(plane_of(a.queries)) * 4;
+        const size_t partial_start = (record_bytes + 255) / 256 * 256;
+        const int64_t prows = partial_rows(a.queries, a.keys, a.query_offset);
+        const size_t per_head = size_t(prows) * H * 4;
+        const size_t room = a.workspace_bytes > partial_start ? a.workspace_bytes - partial_start : 0;
+        const int64_t run = per_head == 0 ? a.heads : int64_t(std::min(size_t(a.heads), room / per_head));
+        if (run > 0 && (run == a.heads || run * key_blocks >= 512)) {
+            float* partials = reinterpret_cast<float*>(reinterpret_cast<char*>(a.workspace) + partial_start);
+            for (int64_t h0 = 0; h0 < a.heads; h0 += run) {
+                const int64_t n = std::min(run, a.heads - h0);
+                KeyGradArgs ra_ = ka;
+                ra_.q = a.q + h0 * a.q_stride;
+                ra_.d_out = a.d_out + h0 * a.q_stride;
+                ra_.k = a.k + h0 * a.kv_stride;
+                ra_.v = a.v + h0 * a.kv_stride;
+                ra_.rows = rows + h0 * 3 * plane_of(a.queries);
+                ra_.k_grad = a.k_grad + h0 * a.keys * H;
+                ra_.v_grad = a.v_grad + h0 * a.keys * H;
+                ra_.heads = n;
+                ra_.partials = partials;
+                ra_.partial_rows = prows;
+                hipLaunchKernelGGL((attention_key_grad_lds_kernel<H, true>), dim3(unsigned(n * key_blocks)),
+                                   dim3(64 * kLdsKeyWaves), 0, stream, ra_);
+                err = hipGetLastError();
+                if (err != hipSuccess) return err;
+                DqSumArgs sa{partials, a.q_grad + h0 * a.queries * H, n, a.queries, a.keys, a.query_offset, prows,
+                             a.scale};
+                hipLaunchKernelGGL(attention_dq_sum_kernel<H>, dim3(unsigned((n * a.queries * (H / 4) + 255) / 256)),
+                                   dim3(256), 0, stream, sa);
+                err = hipGetLastError();
+                if (err != hipSuccess) return err;
+            }
+            return hipSuccess;
+        }
+    }
     if constexpr (H <= 64)
         hipLaunchKernelGGL(attention_key_grad_lds_kernel<H>, dim3(unsigned(a.heads * key_blocks)),
                            dim3(64 * kLdsKeyWaves), 0, stream, ka);

@@ -6,12 +6,15 @@ the scores product, causal_softmax (reference.rs:100-119), the dP and dV product
 (reference.rs:121-137) and the dQ and dK products (reference.rs:19-38), at the reference's fp32
 tolerance. Cases: ragged blocks, query offsets, more or fewer keys than queries, head dims 32 / 64 /
 128, config 3's whole 192-head launch (eight heads across it compared in full, statistics included),
-reruns bit-identical, a workspace left holding NaN, and the entry point's checks."""
+reruns bit-identical, a workspace left holding NaN, and the entry point's checks. For head dims 32 and
+64 dQ comes from the key kernel's partial sums per key block when the workspace holds them (all heads
+at once or in runs of heads), else from the query kernel; both ways are checked, and dK and dV must
+not depend on the way."""
 import numpy as np
 import pytest
 
 from oracle import oracle
-from staleynet_amd.gemm import GpuError, Shape
+from staleynet_amd.gemm import Gpu, GpuError, Shape
 
 pytestmark = pytest.mark.gpu
 
@@ -182,6 +185,66 @@ def test_config_3_full_launch_matches_the_reference_calls_on_heads_across_it(gpu
     _, again = run(gpu, heads, t, t, h, scale, 0, seed=3)
     for name in ("out", "stats", "dq", "dk", "dv"):
         assert np.array_equal(got[name], again[name]), name
+
+
+def record_bytes(heads, queries):
+    """The row records' share of the workspace: three planes of queries rounded up to 4 per head,
+    rounded up to 256 bytes (the partial sums start there)."""
+    return (heads * 3 * ((queries + 3) // 4 * 4) * 4 + 255) // 256 * 256
+
+
+def partial_bytes(heads, queries, keys, h, offset):
+    """dQ's partial sums: per head, h floats per query and 128-key block whose 64-query stages reach
+    the query (from the first query that sees the block's first key, rounded down to a stage)."""
+    rows = sum(max(0, queries - max(0, b * 128 - offset) // 64 * 64) for b in range((keys + 127) // 128))
+    return heads * rows * h * 4
+
+
+@pytest.mark.parametrize("heads,queries,keys,h,offset,scale", [CASES[1], CASES[2], CASES[3], CASES[9]])
+def test_query_kernel_path_without_room_for_the_partial_sums(gpu, heads, queries, keys, h, offset, scale):
+    # A workspace that holds the row records but not one head's partial sums: dQ comes from the query
+    # kernel, which recomputes S and dP. The reference's results either way; dK, dV and O bit for bit
+    # those of the partial-sum path (the shared context's large workspace).
+    room = record_bytes(heads, queries) + partial_bytes(1, queries, keys, h, offset) - 4
+    print(f"query path: heads={heads} queries={queries} keys={keys} h={h} workspace {room} bytes", flush=True)
+    small = Gpu(0, workspace_bytes=room)
+    try:
+        inputs, got = run(small, heads, queries, keys, h, scale, offset, seed=queries + keys + h)
+    finally:
+        small.close()
+    out, _, dq, dk, dv = reference(*inputs, heads, queries, keys, h, scale, offset)
+    for name, expected in (("out", out), ("dq", dq), ("dk", dk), ("dv", dv)):
+        assert np.all(np.isfinite(got[name])), name
+        error = oracle.relative_error(expected, got[name])
+        assert error < TOLERANCE, f"{name}: relative error {error}"
+    _, partial = run(gpu, heads, queries, keys, h, scale, offset, seed=queries + keys + h)
+    for name in ("out", "stats", "dk", "dv"):
+        assert np.array_equal(got[name], partial[name]), name
+    assert oracle.relative_error(partial["dq"], got["dq"]) < TOLERANCE
+
+
+def test_head_runs_give_the_bits_of_one_launch(gpu):
+    # 24 heads of T = 4096 (32 key blocks each). A workspace for 17 heads' partial sums splits the
+    # launch into runs of 17 and 7 heads (17 x 32 workgroups fill the device); every bit equals that
+    # of the one-launch result, and the last head (second run) matches the reference's calls.
+    heads, t, h, scale = 24, 4096, 64, 0.125
+    room = record_bytes(heads, t) + 17 * partial_bytes(1, t, t, h, 0) + 4
+    assert record_bytes(heads, t) + partial_bytes(heads, t, t, h, 0) <= 1536 << 20  # one launch by default
+    print(f"head runs: {heads} heads, T {t}, workspace {room} bytes", flush=True)
+    inputs, whole = run(gpu, heads, t, t, h, scale, 0, seed=77)
+    small = Gpu(0, workspace_bytes=room)
+    try:
+        _, runs = run(small, heads, t, t, h, scale, 0, seed=77)
+    finally:
+        small.close()
+    for name in ("out", "stats", "dq", "dk", "dv"):
+        assert np.array_equal(whole[name], runs[name]), name
+    picked = [x.reshape(heads, t * h)[heads - 1] for x in inputs]
+    _, _, dq, dk, dv = reference(*picked, 1, t, t, h, scale, 0)
+    for name, expected in (("dq", dq), ("dk", dk), ("dv", dv)):
+        mine = runs[name].reshape(heads, t * h)[heads - 1]
+        error = oracle.relative_error(expected, mine)
+        assert error < TOLERANCE, f"{name}: relative error {error}"
 
 
 def poison_workspace(gpu):
