@@ -308,6 +308,16 @@ def bf16_roofline_tflops(spec: MatmulSpec) -> float:
 
 # ---- config 3: causal attention ---------------------------------------------------------
 
+def backward_products(heads: int, t: int, h: int, workspace: int = 1536 << 20) -> int:
+    """Products' MFMAs per visible pair that sn_causal_attention_backward executes on a causal
+    [heads, t, t] problem with the default workspace: 5 when dQ's partial sums (h floats per query
+    and 128-key block that reaches it) fit after the 12-byte row records (head dims 32 and 64),
+    else 7 (the query kernel recomputes S and dP)."""
+    records = (heads * 3 * ((t + 3) // 4 * 4) * 4 + 255) // 256 * 256
+    rows = sum(t - b * 128 // 64 * 64 for b in range((t + 127) // 128))
+    return 5 if h <= 64 and records + heads * rows * h * 4 <= workspace else 7
+
+
 def measure_attention(gpu: Gpu, events: HipEvents, repeats: int = 3):
     """The six attention products of attention.rs:206-260 for 16 x 12 heads, T = 2048, h = 64,
     dense (the reference's calls) and with the causal-mask extension."""
@@ -406,9 +416,10 @@ def measure_attention(gpu: Gpu, events: HipEvents, repeats: int = 3):
         "fused_tflops_on_visible_work": round(2 * causal_flops / (fused_ms * 1e-3) / 1e12, 1)}
     # One layer's attention training kernels, two ways. Keeping P: the fused forward with the
     # probabilities, the fused score gradient with dQ, and the causal dV and dK products. Without
-    # P (sn_causal_attention_with_stats + sn_causal_attention_backward): the forward keeps 16
-    # bytes per query, the backward recomputes S and dP (7 products' MFMAs over the visible
-    # pairs against the reference's 4).
+    # P (sn_causal_attention_with_stats + sn_causal_attention_backward): the forward keeps 8
+    # bytes per query, the backward recomputes S and dP once (5 products' MFMAs over the visible
+    # pairs against the reference's 4) with dQ's partial sums per key block in the context's
+    # workspace (855 MB here, of 1.5 GiB), or twice (7) where they do not fit.
     keeping_p_ms = (fused_p_ms + fused_grad_q_ms + result["products"]["dV = P^T.dO"]["causal_ms"]
                     + result["products"]["dK = s.dS^T.Q"]["causal_ms"])
     stats = gpu.zeros(Shape.vector(2 * heads * t))
@@ -422,7 +433,8 @@ def measure_attention(gpu: Gpu, events: HipEvents, repeats: int = 3):
         "probability_free_ms": round(stats_ms + backward_p_free_ms, 3),
         "forward_with_stats_ms": round(stats_ms, 3), "backward_ms": round(backward_p_free_ms, 3),
         "backward_tflops_on_reference_work": round(4 * causal_flops / (backward_p_free_ms * 1e-3) / 1e12, 1),
-        "backward_tflops_executed": round(7 * causal_flops / (backward_p_free_ms * 1e-3) / 1e12, 1),
+        "backward_tflops_executed": round(backward_products(heads, t, h) * causal_flops / (backward_p_free_ms * 1e-3)
+                                          / 1e12, 1),
         "probability_bytes_not_kept": 4 * heads * t * t}
     return result
 

@@ -470,9 +470,9 @@ void attention_key_grad_kernel(KeyGradArgs a) {
     }
 }
 
-// Key blocks with K and V in LDS, for head dims 32 and 64: eight waves, wave
-// w taking key group w % 4 (32 keys) against query half w / 4 of every stage
-// (stage rows 32 (w / 4) .. + 31). No wave holds K or V in registers, so
+// Key blocks with K and V in LDS, for head dims 32 and 64: eight waves, each
+// taking a key group (32 keys) against a query half of every stage (wave w:
+// half w / 4, stage rows 32 (w / 4) .. + 31). No wave holds K or V in registers, so
 // two share each SIMD; the K and V rows are read from LDS by the same
 // swizzled chunk reads as the stage rows. At the end the two halves' partial
 // dV^T and dK^T meet in LDS and are added in a fixed order (half 0, then
@@ -546,8 +546,13 @@ void attention_key_grad_lds_kernel(KeyGradArgs a) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int group = wave % 4;  // key group
-    const int qh = wave / 4;     // query half of each stage
+    // Key group and query half. Waves w and w + 4 share a SIMD: pairing group
+    // g of half 0 with group 3 - g of half 1 spreads the blocks of the two
+    // stages on the diagonal, where only groups up to the queries' reach
+    // work, over the SIMDs (with group g in both halves, the first stage's
+    // blocks fell on SIMDs 0 and 1 only).
+    const int group = wave < 4 ? wave : 7 - wave;
+    const int qh = wave / 4;
     const int col = lane & 31;
     const int half = lane >> 5;
 
@@ -1061,15 +1066,26 @@ __global__ __launch_bounds__(256) void attention_dq_sum_kernel(DqSumArgs a) {
     const int64_t row = t / C;  // head * queries + query
     const int64_t head = row / a.queries, q = row % a.queries;
     const float* base = a.partials + head * a.partial_rows * H + 4 * c;
+    const int64_t blocks = (a.keys + kKeyBlock - 1) / kKeyBlock;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     int64_t before = 0;  // rows of the blocks before
-    for (int64_t b = 0; b * kKeyBlock < a.keys; ++b) {
-        const int64_t first = stage_begin(b, a.query_offset);
-        if (first > q) break;
-        const f32x4 x = *reinterpret_cast<const f32x4*>(base + (before + q - first) * H);
+    // Four blocks' loads in flight at a time, added in block order.
+    for (int64_t b = 0; b < blocks; b += 4) {
+        f32x4 x[4];
+        bool ok[4];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) acc[s] = acc[s] + x[s];
-        before += a.queries - first;
+        for (int u = 0; u < 4; ++u) {
+            const int64_t first = stage_begin(b + u, a.query_offset);
+            ok[u] = b + u < blocks && first <= q;
+            x[u] = ok[u] ? *reinterpret_cast<const f32x4*>(base + (before + q - first) * H) : f32x4{0.f, 0.f, 0.f, 0.f};
+            if (ok[u]) before += a.queries - first;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (ok[u])
+#pragma unroll
+                for (int s = 0; s < 4; ++s) acc[s] = acc[s] + x[u][s];
+        if (!ok[3]) break;
     }
     f32x4 out;
 #pragma unroll
