@@ -16,6 +16,12 @@
 //    64 k, in k order (Linear's bias gradient of a dY staged for the weight
 //    gradient: the rows here are dY's columns).
 //
+// The same rounding can also write the 256 x 256 bf16 kernel's blocked layout
+// (launch_stage_bf16_blocks): per 32-deep step of K, the operand's rows of 32
+// k one after another, rows padded to a multiple of 256 and, for the right
+// operand, in that kernel's quad order; a step's rows of one tile are then
+// one contiguous 16 KB run, which its loads read 1 KB per wave instruction.
+//
 // HBM-bound: 4 bytes read and 2 written per element.
 #include <hip/hip_runtime.h>
 
@@ -34,6 +40,21 @@ constexpr int kThreads = 256;
 constexpr int kTile = 64;
 constexpr int kPitch = kTile + 1;
 
+// Where a staged group of 8 k goes: the plain layout (rows_pad 0),
+// [batch][rows][kp], or the blocked one, [batch][kp / 32][slot][32] over
+// rows_pad rows, slot = row or quad_position(row).
+struct StageDst {
+    uint16_t* base;
+    int64_t rows, kp, rows_pad;
+    bool quad;
+    __device__ __forceinline__ int64_t rows_out() const { return rows_pad > 0 ? rows_pad : rows; }
+    __device__ __forceinline__ uint16_t* at(int64_t batch, int64_t r, int64_t k0) const {
+        if (rows_pad == 0) return base + (batch * rows + r) * kp + k0;
+        const int64_t slot = quad ? quad_position(r) : r;
+        return base + batch * rows_pad * kp + (k0 / 32) * (rows_pad * 32) + slot * 32 + k0 % 32;
+    }
+};
+
 __device__ __forceinline__ bf16x8 round8(const float (&v)[8]) {
     const f32x8 x = {v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]};
     return __builtin_convertvector(x, bf16x8);
@@ -44,16 +65,19 @@ __device__ __forceinline__ bf16x8 round8(const float (&v)[8]) {
 template <bool VECTOR>
 __global__ __launch_bounds__(kThreads) void stage_rows_kernel(const float* __restrict__ src, int64_t ld,
                                                               int64_t rows, int64_t k, int64_t kp,
-                                                              int64_t src_stride, uint16_t* __restrict__ dst) {
+                                                              int64_t src_stride, StageDst dst) {
     const int64_t groups = kp / 8;
     const int64_t g = int64_t(blockIdx.x) * kThreads + threadIdx.x;
-    if (g >= rows * groups) return;
+    if (g >= dst.rows_out() * groups) return;
     const int64_t batch = blockIdx.y;
     const int64_t r = g / groups;
     const int64_t k0 = (g - r * groups) * 8;
     const float* row = src + batch * src_stride + r * ld;
     float v[8];
-    if (VECTOR && k0 + 8 <= k) {
+    if (r >= rows) {  // the blocked layout's padding rows
+#pragma unroll
+        for (int s = 0; s < 8; ++s) v[s] = 0.f;
+    } else if (VECTOR && k0 + 8 <= k) {
         const f32x4 lo = *reinterpret_cast<const f32x4*>(row + k0);
         const f32x4 hi = *reinterpret_cast<const f32x4*>(row + k0 + 4);
 #pragma unroll
@@ -65,14 +89,13 @@ __global__ __launch_bounds__(kThreads) void stage_rows_kernel(const float* __res
 #pragma unroll
         for (int s = 0; s < 8; ++s) v[s] = k0 + s < k ? row[k0 + s] : 0.f;
     }
-    *reinterpret_cast<bf16x8*>(dst + (batch * rows + r) * kp + k0) = round8(v);
+    *reinterpret_cast<bf16x8*>(dst.at(batch, r, k0)) = round8(v);
 }
 
 template <bool VECTOR, bool SUMS>
 __global__ __launch_bounds__(kThreads) void stage_transposed_kernel(const float* __restrict__ src, int64_t ld,
                                                                     int64_t rows, int64_t k, int64_t kp,
-                                                                    int64_t src_stride,
-                                                                    uint16_t* __restrict__ dst,
+                                                                    int64_t src_stride, StageDst dst,
                                                                     float* __restrict__ sums) {
     __shared__ float tile[kTile * kPitch];  // [k][row]
     const int tid = threadIdx.x;
@@ -129,11 +152,11 @@ __global__ __launch_bounds__(kThreads) void stage_transposed_kernel(const float*
         const int rr = e / 8;
         const int64_t r = r_base + rr;
         const int64_t k0 = k_base + 8 * kgrp;
-        if (r < rows && k0 < kp) {
+        if (r < dst.rows_out() && k0 < kp) {
             float v[8];
 #pragma unroll
             for (int t = 0; t < 8; ++t) v[t] = tile[(8 * kgrp + t) * kPitch + rr];
-            *reinterpret_cast<bf16x8*>(dst + (batch * rows + r) * kp + k0) = round8(v);
+            *reinterpret_cast<bf16x8*>(dst.at(batch, r, k0)) = round8(v);
         }
     }
 }
@@ -144,15 +167,18 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 int64_t stage_sum_tiles(int64_t kp) { return (kp + kTile - 1) / kTile; }
 
-hipError_t launch_stage_bf16(const float* src, bool k_contiguous, int64_t ld, int64_t rows, int64_t k, int64_t kp,
-                             int64_t batch, int64_t src_stride, uint16_t* dst, hipStream_t stream,
-                             float* row_sums) {
+namespace {
+
+hipError_t launch_stage(const float* src, bool k_contiguous, int64_t ld, int64_t rows, int64_t k, int64_t kp,
+                        int64_t batch, int64_t src_stride, const StageDst& dst, hipStream_t stream,
+                        float* row_sums) {
     if (rows == 0 || kp == 0 || batch == 0) return hipSuccess;
     if (batch > 65535 || kp % 8 != 0 || kp < k) return hipErrorInvalidValue;
     if (row_sums != nullptr && (k_contiguous || batch != 1)) return hipErrorInvalidValue;
     const bool vector = ld % 4 == 0 && src_stride % 4 == 0 && aligned16(src);
+    const int64_t rows_out = dst.rows_pad > 0 ? dst.rows_pad : rows;
     if (k_contiguous) {
-        const int64_t work = rows * (kp / 8);
+        const int64_t work = rows_out * (kp / 8);
         if ((work + kThreads - 1) / kThreads > 0x7FFFFFFF) return hipErrorInvalidValue;
         const dim3 grid(unsigned((work + kThreads - 1) / kThreads), unsigned(batch));
         if (vector)
@@ -163,7 +189,7 @@ hipError_t launch_stage_bf16(const float* src, bool k_contiguous, int64_t ld, in
                                src_stride, dst);
     } else {
         const int64_t tiles_k = (kp + kTile - 1) / kTile;
-        const int64_t tiles_r = (rows + kTile - 1) / kTile;
+        const int64_t tiles_r = (rows_out + kTile - 1) / kTile;
         if (tiles_r > 65535) return hipErrorInvalidValue;
         const dim3 grid{unsigned(tiles_k), unsigned(tiles_r), unsigned(batch)};
         if (row_sums != nullptr) {
@@ -182,6 +208,24 @@ hipError_t launch_stage_bf16(const float* src, bool k_contiguous, int64_t ld, in
         }
     }
     return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_stage_bf16(const float* src, bool k_contiguous, int64_t ld, int64_t rows, int64_t k, int64_t kp,
+                             int64_t batch, int64_t src_stride, uint16_t* dst, hipStream_t stream,
+                             float* row_sums) {
+    return launch_stage(src, k_contiguous, ld, rows, k, kp, batch, src_stride, StageDst{dst, rows, kp, 0, false},
+                        stream, row_sums);
+}
+
+hipError_t launch_stage_bf16_blocks(const float* src, bool k_contiguous, int64_t ld, int64_t rows, int64_t k,
+                                    int64_t kp, int64_t rows_pad, bool quad, int64_t batch, int64_t src_stride,
+                                    uint16_t* dst, hipStream_t stream, float* row_sums) {
+    if (rows == 0 || kp == 0 || batch == 0) return hipSuccess;
+    if (kp % 32 != 0 || rows_pad % 256 != 0 || rows_pad < rows) return hipErrorInvalidValue;
+    return launch_stage(src, k_contiguous, ld, rows, k, kp, batch, src_stride, StageDst{dst, rows, kp, rows_pad, quad},
+                        stream, row_sums);
 }
 
 }  // namespace sn

@@ -61,8 +61,7 @@ __device__ __forceinline__ void launder(int& x) { asm volatile("" : "+v"(x)); }
 // are the rows 4 (0..31) + j whose outputs the epilogue stores side by side.
 // The fragment reads are unchanged; the loaders place each row at
 // quad_position of it (the inverse).
-__host__ __device__ constexpr int quad_row(int p) { return (p / 128) * 128 + 4 * (p % 32) + (p % 128) / 32; }
-__host__ __device__ constexpr int quad_position(int r) { return (r / 128) * 128 + 32 * (r % 4) + (r % 128) / 4; }
+// (quad_row and quad_position: gemm_internal.h.)
 static_assert(quad_position(quad_row(37)) == 37 && quad_row(quad_position(201)) == 201, "inverse maps");
 
 // The fp32 loaders (gemm_common.h) with the bf16 LDS write addressed from one
@@ -159,13 +158,14 @@ template <bool K_CONTIGUOUS, int ROWS, int BK, int THREADS, bool QUAD = false>
 using WideLoaderFor = typename std::conditional<K_CONTIGUOUS, WideKLoader<ROWS, BK, THREADS, QUAD>,
                                                 WideRowLoader<ROWS, BK, THREADS, QUAD>>::type;
 
-// An operand already rounded to bf16 and laid out K-contiguous in the
-// workspace (launch_stage_bf16: [rows][kp], kp = K rounded up to 8, zeros
-// past K): vector v of a thread is one 16-byte octet (8 consecutive k) of
-// row tid / 4 + v x THREADS / 4, so four lanes read a row's 32 k (64
-// contiguous bytes) and each writes its octet's LDS slot as it came. `ld` is
-// kp, in bf16 elements; `base` points at the operand (batch offsets in
-// floats, kp being even).
+// An operand already rounded to bf16 in the workspace, in the blocked layout
+// of launch_stage_bf16_blocks: per 32-deep step, `ld` (rows_pad) rows of 32 k
+// (64 bytes), in quad order when QUAD, zeros past the rows and K. Vector v of
+// a thread is one 16-byte octet (8 consecutive k) of slot row tid / 4 + v x
+// THREADS / 4, so a step's 256 rows of the tile are one contiguous 16 KB run
+// (1 KB per wave instruction, where the row-by-row layout took 16 separate
+// 64-byte pieces), and each lane writes its octet's LDS slot as it came.
+// `base` points at the operand (batch offsets in floats).
 template <int ROWS, int BK, int THREADS, bool QUAD = false>
 struct StagedLoader {
     static constexpr int OCTETS = BK / 8;
@@ -176,29 +176,24 @@ struct StagedLoader {
     // same banks; the counters showed it.)
     static constexpr int BF16_PAD = 2;
     static_assert(ROWS * OCTETS % THREADS == 0 && THREADS % OCTETS == 0, "whole slots per thread");
+    static_assert(BK == 32 && ROWS % 128 == 0, "the blocked layout's 32-deep steps and whole quad groups");
     f32x4 reg[PER_THREAD];  // 8 bf16 each, as loaded
-    int32_t offset[PER_THREAD];
 
-    static_assert(!QUAD || ROWS % 128 == 0, "whole 128-row groups");
+    // The layout is padded to whole tiles and already in quad order: every
+    // offset is the same for every tile and step.
+    __device__ __forceinline__ void init(int64_t, int64_t, int64_t, int) {}
 
-    // QUAD: the rows whose slots these are in quad order (the slots, and so
-    // the LDS writes, stay where they are).
-    __device__ __forceinline__ void init(int64_t ld, int64_t row0, int64_t rows, int tid) {
-#pragma unroll
-        for (int v = 0; v < PER_THREAD; ++v) {
-            const int slot_row = tid / OCTETS + v * (THREADS / OCTETS);
-            const int r = QUAD ? quad_row(slot_row) : slot_row;
-            offset[v] = row0 + r < rows ? int32_t((r * ld + 8 * (tid % OCTETS)) * 2) : kOutOfRange;
-        }
-    }
-
+    // A step past the slice's end reads zeros (out-of-range offsets), keeping
+    // the counts the waits assume; a step inside it is whole (K is padded to
+    // 32 with zeros and slices are whole steps).
     __device__ __forceinline__ void load(const float* __restrict__ base, int64_t ld, int64_t row0, int64_t,
                                          int64_t k0, int64_t k_end, int tid) {
-        const uint16_t* tile = reinterpret_cast<const uint16_t*>(base) + row0 * ld + k0;
+        const uint16_t* tile = reinterpret_cast<const uint16_t*>(base) + (k0 / BK) * (ld * BK) + row0 * BK;
         const __amdgpu_buffer_rsrc_t rsrc = buffer_of(reinterpret_cast<const float*>(tile));
-        const bool k_valid = k0 + 8 * (tid % OCTETS) < k_end;
+        const bool k_valid = k0 < k_end;
 #pragma unroll
-        for (int v = 0; v < PER_THREAD; ++v) reg[v] = buffer_load4(rsrc, k_valid ? offset[v] : kOutOfRange);
+        for (int v = 0; v < PER_THREAD; ++v)
+            reg[v] = buffer_load4(rsrc, k_valid ? int32_t((v * THREADS + tid) * 16) : kOutOfRange);
     }
 
     __device__ __forceinline__ void store_bf16(uint16_t* lds, int tid) const {
@@ -613,8 +608,9 @@ Plan wide_plan(const Problem& p, const Env& env) {
 // partial sums after it).
 struct WideStaging {
     int side = kStageNone;
-    int64_t kp = 0;
-    int64_t copies = 0;  // 1 when the operand is shared by the whole batch
+    int64_t kp = 0;        // K rounded up to a whole step
+    int64_t rows_pad = 0;  // the staged operand's rows rounded up to a whole tile
+    int64_t copies = 0;    // 1 when the operand is shared by the whole batch
     size_t bytes = 0;
     Problem q;
     Env rest;
@@ -645,23 +641,24 @@ WideStaging wide_staging(const Problem& p, const Env& env) {
     if (side == kStageNone || env.workspace == nullptr || p.batch > 65535) return st;
     const int64_t rows = side == kStageLeft ? p.m : p.n;
     const int64_t copies = side == kStageLeft ? a_copies : b_copies;
-    const int64_t kp = (p.k + 7) / 8 * 8;
-    // The staged loader's per-lane byte offsets span a tile's rows (32-bit).
-    if ((int64_t(WideTile::BM > WideTile::BN ? WideTile::BM : WideTile::BN) * kp + 64) * 2 >= kMaxBufferOffset)
-        return st;
-    const size_t bytes = round256(size_t(copies) * size_t(rows) * size_t(kp) * 2);
+    // The blocked layout (launch_stage_bf16_blocks): whole steps of K, whole
+    // tiles of rows; `ld` of the staged operand is its padded row count.
+    const int64_t kp = (p.k + WideTile::BK - 1) / WideTile::BK * WideTile::BK;
+    constexpr int64_t kTileRows = WideTile::BM > WideTile::BN ? WideTile::BM : WideTile::BN;
+    const int64_t rows_pad = (rows + kTileRows - 1) / kTileRows * kTileRows;
+    const size_t bytes = round256(size_t(copies) * size_t(rows_pad) * size_t(kp) * 2);
     if (bytes >= env.workspace_bytes) return st;
     Problem q = p;
     const float* staged = env.workspace;
     if (side == kStageLeft) {
         q.a = staged;
-        q.lda = kp;
-        q.stride_a = copies > 1 ? rows * kp / 2 : 0;
+        q.lda = rows_pad;
+        q.stride_a = copies > 1 ? rows_pad * kp / 2 : 0;
         q.a_k_contiguous = true;
     } else {
         q.b = staged;
-        q.ldb = kp;
-        q.stride_b = copies > 1 ? rows * kp / 2 : 0;
+        q.ldb = rows_pad;
+        q.stride_b = copies > 1 ? rows_pad * kp / 2 : 0;
         q.b_k_contiguous = true;
     }
     Env rest = env;
@@ -672,6 +669,7 @@ WideStaging wide_staging(const Problem& p, const Env& env) {
         return st;
     st.side = side;
     st.kp = kp;
+    st.rows_pad = rows_pad;
     st.copies = copies;
     st.bytes = bytes;
     st.q = q;
@@ -777,15 +775,17 @@ hipError_t launch_gemm_bf16_wide(const Problem& p, const Env& env, hipStream_t s
     const Problem& q = st.q;
     const Plan plan = wide_plan(q, st.rest);
     if (st.side == kStageLeft) {
-        hipError_t err = launch_stage_bf16(p.a, p.a_k_contiguous, p.lda, p.m, p.k, st.kp, st.copies, p.stride_a,
-                                           reinterpret_cast<uint16_t*>(env.workspace), stream);
+        hipError_t err = launch_stage_bf16_blocks(p.a, p.a_k_contiguous, p.lda, p.m, p.k, st.kp, st.rows_pad, false,
+                                                  st.copies, p.stride_a, reinterpret_cast<uint16_t*>(env.workspace),
+                                                  stream);
         if (err != hipSuccess) return err;
         if (q.b_k_contiguous) return launch_wide<true, true, kStageLeft>(q, st.rest, plan, stream);
         return launch_wide<true, false, kStageLeft>(q, st.rest, plan, stream);
     }
     if (st.side == kStageRight) {
-        hipError_t err = launch_stage_bf16(p.b, p.b_k_contiguous, p.ldb, p.n, p.k, st.kp, st.copies, p.stride_b,
-                                           reinterpret_cast<uint16_t*>(env.workspace), stream);
+        hipError_t err = launch_stage_bf16_blocks(p.b, p.b_k_contiguous, p.ldb, p.n, p.k, st.kp, st.rows_pad, true,
+                                                  st.copies, p.stride_b, reinterpret_cast<uint16_t*>(env.workspace),
+                                                  stream);
         if (err != hipSuccess) return err;
         if (q.a_k_contiguous) return launch_wide<true, true, kStageRight>(q, st.rest, plan, stream);
         return launch_wide<false, true, kStageRight>(q, st.rest, plan, stream);
@@ -865,8 +865,8 @@ hipError_t launch_gemm_bf16_wide_column_sums(const Problem& p, const Env& env, h
     hipError_t err = hipSuccess;
     if (st.side == kStageRight) {
         float* sums = st.rest.workspace + product_partial_bytes(plan, p) / sizeof(float);
-        err = launch_stage_bf16(p.b, false, p.ldb, p.n, p.k, st.kp, 1, p.stride_b,
-                                reinterpret_cast<uint16_t*>(env.workspace), stream, sums);
+        err = launch_stage_bf16_blocks(p.b, false, p.ldb, p.n, p.k, st.kp, st.rows_pad, true, 1, p.stride_b,
+                                       reinterpret_cast<uint16_t*>(env.workspace), stream, sums);
         if (err == hipSuccess)
             err = q.a_k_contiguous ? launch_wide<true, true, kStageRight>(q, st.rest, plan, stream)
                                    : launch_wide<false, true, kStageRight>(q, st.rest, plan, stream);
@@ -874,8 +874,8 @@ hipError_t launch_gemm_bf16_wide_column_sums(const Problem& p, const Env& env, h
         return launch_column_sums_finish(sums, stage_sum_tiles(st.kp), p.n, p.column_sums, stream);
     }
     if (st.side == kStageLeft) {
-        err = launch_stage_bf16(p.a, p.a_k_contiguous, p.lda, p.m, p.k, st.kp, st.copies, p.stride_a,
-                                reinterpret_cast<uint16_t*>(env.workspace), stream);
+        err = launch_stage_bf16_blocks(p.a, p.a_k_contiguous, p.lda, p.m, p.k, st.kp, st.rows_pad, false, st.copies,
+                                       p.stride_a, reinterpret_cast<uint16_t*>(env.workspace), stream);
         if (err == hipSuccess) err = launch_wide<true, false, kStageLeft, true>(q, st.rest, plan, stream);
     } else {
         err = p.a_k_contiguous ? launch_wide<true, false, kStageNone, true>(p, env, plan, stream)

@@ -199,6 +199,25 @@ hipError_t launch_stage_bf16(const float* src, bool k_contiguous, int64_t ld, in
                              float* row_sums = nullptr);
 int64_t stage_sum_tiles(int64_t kp);
 
+// The 256 x 256 bf16 kernel's right-operand rows in quad order: position p
+// of each 128-row group holds row quad_row(p), so that the rows a lane's four
+// adjacent outputs come from sit 32 positions apart (gemm_bf16_wide.hip);
+// quad_position is the inverse.
+__host__ __device__ constexpr int64_t quad_row(int64_t p) { return (p / 128) * 128 + 4 * (p % 32) + (p % 128) / 32; }
+__host__ __device__ constexpr int64_t quad_position(int64_t r) {
+    return (r / 128) * 128 + 32 * (r % 4) + (r % 128) / 4;
+}
+
+// The same rounding into the layout the 256 x 256 bf16 kernel loads: per
+// batch, per 32-deep step of K, the operand's rows_pad rows of 32 k,
+// dst[batch][k / 32][slot][k % 32] with slot = row (or quad_position(row)
+// when quad), so that a step's rows of one tile are one contiguous run of
+// 64-byte rows. rows_pad (a multiple of 256, >= rows) and kp (a multiple of
+// 32, >= k) are filled with zeros past rows and K. row_sums as above.
+hipError_t launch_stage_bf16_blocks(const float* src, bool k_contiguous, int64_t ld, int64_t rows, int64_t k,
+                                    int64_t kp, int64_t rows_pad, bool quad, int64_t batch, int64_t src_stride,
+                                    uint16_t* dst, hipStream_t stream, float* row_sums = nullptr);
+
 // Bytes of workspace launch_gemm_* would use for `p` (0 = none): split-K
 // partial sums, and for bf16 the staged operands.
 size_t gemm_workspace_bytes(const Problem& p, bool bf16, const Env& env);

@@ -161,14 +161,16 @@ def test_configs_take_the_expected_kernel_families():
     assert wgrad.path == gemm.PATH_BF16_WIDE and wgrad.splits > 1
     dgrad = gemm.plan(MatmulSpec.new(32768, 768, 2304).right_transposed().with_precision(Precision.Bf16))
     assert dgrad.path == gemm.PATH_BF16_WIDE and dgrad.workspace_bytes == 768 * 2304 * 2
-    # A staged operand keeps 32-bit offsets across a tile's rows: with K in the millions the weight
-    # gradient rounds both operands as they load instead (its workspace holds only partial sums).
+    # The staged operand is blocked by 32-deep steps (each step's tile rows one 16 KB run), so its
+    # loads need no offsets across K: with K in the millions the weight gradient still stages x^T
+    # (rows padded to 256, K to 32), beside the partial sums.
     huge = gemm.plan(MatmulSpec.new(256, 640, 5_000_000).left_transposed().with_precision(Precision.Bf16),
                      workspace_bytes=1 << 40)
-    assert huge.path == gemm.PATH_BF16_WIDE and huge.workspace_bytes == huge.splits * 256 * 640 * 4
-    long_k = gemm.plan(MatmulSpec.new(256, 640, 500_000).left_transposed().with_precision(Precision.Bf16),
+    assert huge.path == gemm.PATH_BF16_WIDE
+    assert huge.workspace_bytes == huge.splits * 256 * 640 * 4 + 256 * 5_000_000 * 2
+    long_k = gemm.plan(MatmulSpec.new(200, 640, 500_001).left_transposed().with_precision(Precision.Bf16),
                        workspace_bytes=1 << 40)
-    assert long_k.workspace_bytes == long_k.splits * 256 * 640 * 4 + 256 * 500_000 * 2  # x^T staged
+    assert long_k.workspace_bytes == long_k.splits * 200 * 640 * 4 + 256 * 500_032 * 2  # x^T staged, padded
     # Too small for the wide tiles, and fewer 128 x 128 tiles than CUs: no staging pass, 64 x 64 tiles
     # rounding fp32 fragments as they are read.
     tiny = gemm.plan(MatmulSpec.new(96, 2304, 768).with_precision(Precision.Bf16))
