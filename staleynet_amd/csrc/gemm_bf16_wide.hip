@@ -101,21 +101,35 @@ struct WideKLoader : KContiguousBufferLoader<ROWS, BK, THREADS> {
     }
 };
 
-template <int ROWS, int BK, int THREADS, bool QUAD = false>
+template <int ROWS, int BK, int THREADS, bool QUAD = false, bool RUNS = true>
 struct WideRowLoader : RowContiguousBufferLoader<ROWS, BK, THREADS> {
     using Base = RowContiguousBufferLoader<ROWS, BK, THREADS>;
     using Base::reg;
-    static_assert(Base::TOTAL % THREADS == 0 && THREADS % Base::GROUPS == 0, "whole blocks per thread");
-    // Blocks v of a thread are 4 THREADS / GROUPS rows apart: whole 128-row
-    // groups, so block v's quad positions are block 0's plus 4 v THREADS /
-    // GROUPS (immediate offsets from one base).
-    static_assert(!QUAD || ((4 * THREADS / Base::GROUPS) % 128 == 0 && ROWS % 128 == 0), "whole 128-row groups");
-    // The row quad (rows 4 c .. 4 c + 3) a thread's block 0 holds. In quad
-    // order the four rows of quad c land at positions 32 e + c, so two quads
-    // written in the same 16-lane phase must be 4 apart for their 8-byte
-    // writes to take distinct banks: quad index bits 0 and 2 are swapped
-    // (the lanes of a wave still read the same 128-byte row pieces). The
-    // LDS-bank counters showed the unswapped order conflicting.
+    static constexpr int GROUPS = Base::GROUPS;  // k-groups of 4 per step
+    static_assert(GROUPS == 8 && ROWS % 64 == 0 && THREADS % (16 * GROUPS) == 0 && Base::TOTAL % THREADS == 0,
+                  "whole 16-quad runs per k-group");
+    // RUNS: lanes 16 j .. 16 j + 15 of a thread block take one k-group and
+    // 16 consecutive row quads (256 contiguous bytes of each of that group's
+    // four k-rows), so a wave instruction reads 4 k-rows x 256 bytes, where
+    // 8 k-groups x 8 quads (thread i: k-group i % 8, quad i / 8; kept for the
+    // column sums, whose 8 threads of a quad must be lanes of one wave) read
+    // 8 rows' 128-byte pieces: the loads' cost follows the pieces more than
+    // the bytes. RUNS thread index i: k-group (i / 16) % 8, quad 16 (i / 128)
+    // + i % 16.
+    __device__ __forceinline__ static constexpr int group_of(int i) { return RUNS ? (i / 16) % GROUPS : i % GROUPS; }
+    __device__ __forceinline__ static constexpr int quad_index(int i) {
+        return RUNS ? 16 * (i / (16 * GROUPS)) + i % 16 : i / GROUPS;
+    }
+    // Blocks v of a thread are THREADS / (16 GROUPS) x 16 quads apart: whole
+    // 128-row groups, so block v's quad positions are block 0's plus a
+    // constant (immediate offsets from one base), and its k-group is block 0's.
+    static constexpr int QUADS_PER_BLOCK = THREADS / GROUPS;
+    static_assert(!QUAD || ((4 * QUADS_PER_BLOCK) % 128 == 0 && ROWS % 128 == 0), "whole 128-row groups");
+    // The row quad (rows 4 c .. 4 c + 3) a thread's block 0 holds, as placed
+    // in LDS. In quad order the four rows of quad c land at positions 32 e +
+    // c; quad index bits 0 and 2 are swapped, as the unswapped order's
+    // 16-lane write phases conflicted when a phase held 8 k-groups x 2 quads
+    // (the lanes of a wave still read the same row pieces).
     __device__ __forceinline__ static constexpr int quad_of(int q) {
         return QUAD ? (q & ~5) | ((q & 1) << 2) | ((q >> 2) & 1) : q;
     }
@@ -123,18 +137,29 @@ struct WideRowLoader : RowContiguousBufferLoader<ROWS, BK, THREADS> {
 #pragma unroll
         for (int v = 0; v < Base::PER_THREAD; ++v) {
             const int idx = tid + v * THREADS;
-            const int r = 4 * quad_of(idx / Base::GROUPS);
+            const int r = 4 * quad_of(quad_index(idx));
             const bool valid = row0 + r < rows;
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk)
-                Base::offset[v][kk] =
-                    valid ? int32_t((((idx % Base::GROUPS) * 4 + kk) * ld + r) * 4) : kOutOfRange;
+                Base::offset[v][kk] = valid ? int32_t(((group_of(idx) * 4 + kk) * ld + r) * 4) : kOutOfRange;
+        }
+    }
+    __device__ __forceinline__ void load(const float* __restrict__ base, int64_t ld, int64_t row0, int64_t,
+                                         int64_t k0, int64_t k_total, int tid) {
+        const __amdgpu_buffer_rsrc_t rsrc = buffer_of(base + k0 * ld + row0);
+        const int64_t k_first = k0 + group_of(tid) * 4;  // the same k-group for every v
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const bool k_valid = k_first + kk < k_total;
+#pragma unroll
+            for (int v = 0; v < Base::PER_THREAD; ++v)
+                reg[v][kk] = buffer_load4(rsrc, k_valid ? Base::offset[v][kk] : kOutOfRange);
         }
     }
     __device__ __forceinline__ void store_bf16(uint16_t* lds, int tid) const {
         using O = OctetPlanes<ROWS, BK, Base::BF16_PAD>;
-        const int g = tid % Base::GROUPS;
-        const int c = quad_of(tid / Base::GROUPS);  // this thread's rows 4 c .. 4 c + 3 of block 0
+        const int g = group_of(tid);
+        const int c = quad_of(quad_index(tid));  // this thread's rows 4 c .. 4 c + 3 of block 0
         int base = ((g / 2) * O::PLANE + (QUAD ? quad_position(4 * c) : 4 * c)) * 16 + 8 * (g % 2);
         launder(base);
         char* p = reinterpret_cast<char*>(lds) + base;
@@ -144,7 +169,7 @@ struct WideRowLoader : RowContiguousBufferLoader<ROWS, BK, THREADS> {
             for (int e = 0; e < 4; ++e) {
                 const f32x4 t = {reg[v][0][e], reg[v][1][e], reg[v][2][e], reg[v][3][e]};
                 // quad_position(4 c + e) = quad_position(4 c) + 32 e for e < 4.
-                const int row = 4 * v * (THREADS / Base::GROUPS) + (QUAD ? 32 * e : e);
+                const int row = 4 * v * QUADS_PER_BLOCK + (QUAD ? 32 * e : e);
                 *reinterpret_cast<u32x2*>(p + row * 16) = pack_bf16(t);
             }
     }
@@ -154,9 +179,9 @@ static_assert(WideRowLoader<256, 32, 512, true>::quad_of(5) == 5 && WideRowLoade
                   WideRowLoader<256, 32, 512, true>::quad_of(68) == 65,
               "quad index bits 0 and 2 swapped");
 
-template <bool K_CONTIGUOUS, int ROWS, int BK, int THREADS, bool QUAD = false>
+template <bool K_CONTIGUOUS, int ROWS, int BK, int THREADS, bool QUAD = false, bool RUNS = true>
 using WideLoaderFor = typename std::conditional<K_CONTIGUOUS, WideKLoader<ROWS, BK, THREADS, QUAD>,
-                                                WideRowLoader<ROWS, BK, THREADS, QUAD>>::type;
+                                                WideRowLoader<ROWS, BK, THREADS, QUAD, RUNS>>::type;
 
 // An operand already rounded to bf16 in the workspace, in the blocked layout
 // of launch_stage_bf16_blocks: per 32-deep step, `ld` (rows_pad) rows of 32 k
@@ -209,9 +234,9 @@ struct StagedLoader {
 // Which operand the workspace holds as bf16: none, the left or the right.
 enum StagedSide { kStageNone = 0, kStageLeft = 1, kStageRight = 2 };
 
-template <bool K_CONTIGUOUS, bool STAGED, int ROWS, int BK, int THREADS, bool QUAD = false>
+template <bool K_CONTIGUOUS, bool STAGED, int ROWS, int BK, int THREADS, bool QUAD = false, bool RUNS = true>
 using OperandLoader = typename std::conditional<STAGED, StagedLoader<ROWS, BK, THREADS, QUAD>,
-                                                WideLoaderFor<K_CONTIGUOUS, ROWS, BK, THREADS, QUAD>>::type;
+                                                WideLoaderFor<K_CONTIGUOUS, ROWS, BK, THREADS, QUAD, RUNS>>::type;
 
 // Vector-memory instructions one loader issues per step.
 template <class L>
@@ -225,7 +250,7 @@ template <bool A_K, bool B_K, int SIDE, bool COLSUM = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_bf16_wide_kernel(Args args) {
     using T = WideTile;
     using LA = OperandLoader<A_K, SIDE == kStageLeft, T::BM, T::BK, T::THREADS>;
-    using LB = OperandLoader<B_K, SIDE == kStageRight, T::BN, T::BK, T::THREADS, true>;
+    using LB = OperandLoader<B_K, SIDE == kStageRight, T::BN, T::BK, T::THREADS, true, !COLSUM>;
     using OA = OctetPlanes<T::BM, T::BK, LA::BF16_PAD>;
     using OB = OctetPlanes<T::BN, T::BK, LB::BF16_PAD>;
     constexpr int kSetLoads = loads_per_step<LA>() + loads_per_step<LB>();
