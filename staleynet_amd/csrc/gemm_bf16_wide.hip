@@ -75,6 +75,8 @@ template <int ROWS, int BK, int THREADS, bool QUAD = false>
 struct WideKLoader : KContiguousBufferLoader<ROWS, BK, THREADS> {
     using Base = KContiguousBufferLoader<ROWS, BK, THREADS>;
     using Base::reg;
+    // LDS slot of stage row r (the rows as they are).
+    __device__ __forceinline__ static constexpr int row_slot(int r) { return r; }
     static_assert(Base::TOTAL % THREADS == 0 && THREADS % Base::GROUPS == 0, "whole vectors per thread");
     static_assert(!QUAD || ROWS % 128 == 0, "whole 128-row groups");
     __device__ __forceinline__ void init(int64_t ld, int64_t row0, int64_t rows, int tid) {
@@ -133,6 +135,14 @@ struct WideRowLoader : RowContiguousBufferLoader<ROWS, BK, THREADS> {
     __device__ __forceinline__ static constexpr int quad_of(int q) {
         return QUAD ? (q & ~5) | ((q & 1) << 2) | ((q >> 2) & 1) : q;
     }
+    // Rows as they are (QUAD off), the RUNS mapping puts a write phase's 16
+    // lanes on rows 4 c + e of 16 consecutive quads, all on the same half of
+    // their slots: slots 4 apart, 8 lanes to a bank. Row r then goes to slot
+    // r ^ ((r / 8) % 4), which spreads those 16 rows over 8 bank pairs
+    // (2-way, as in quad order) and keeps 8 consecutive rows, what a 16-byte
+    // fragment read phase takes, on 8 distinct slots modulo 8 (no conflict).
+    static constexpr bool ROW_SWIZZLE = !QUAD && RUNS;
+    __device__ __forceinline__ static constexpr int row_slot(int r) { return ROW_SWIZZLE ? r ^ ((r >> 3) & 3) : r; }
     __device__ __forceinline__ void init(int64_t ld, int64_t row0, int64_t rows, int tid) {
 #pragma unroll
         for (int v = 0; v < Base::PER_THREAD; ++v) {
@@ -163,13 +173,17 @@ struct WideRowLoader : RowContiguousBufferLoader<ROWS, BK, THREADS> {
         int base = ((g / 2) * O::PLANE + (QUAD ? quad_position(4 * c) : 4 * c)) * 16 + 8 * (g % 2);
         launder(base);
         char* p = reinterpret_cast<char*>(lds) + base;
+        // ROW_SWIZZLE: row 4 c + e sits at slot 4 c + (e ^ x), x = (c / 2) % 4
+        // (blocks v are whole 128-row groups apart, which the swizzle keeps).
+        int x = ROW_SWIZZLE ? (c >> 1) & 3 : 0;
+        launder(x);
 #pragma unroll
         for (int v = 0; v < Base::PER_THREAD; ++v)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const f32x4 t = {reg[v][0][e], reg[v][1][e], reg[v][2][e], reg[v][3][e]};
                 // quad_position(4 c + e) = quad_position(4 c) + 32 e for e < 4.
-                const int row = 4 * v * QUADS_PER_BLOCK + (QUAD ? 32 * e : e);
+                const int row = 4 * v * QUADS_PER_BLOCK + (QUAD ? 32 * e : ROW_SWIZZLE ? (e ^ x) : e);
                 *reinterpret_cast<u32x2*>(p + row * 16) = pack_bf16(t);
             }
     }
@@ -203,6 +217,7 @@ struct StagedLoader {
     static_assert(ROWS * OCTETS % THREADS == 0 && THREADS % OCTETS == 0, "whole slots per thread");
     static_assert(BK == 32 && ROWS % 128 == 0, "the blocked layout's 32-deep steps and whole quad groups");
     f32x4 reg[PER_THREAD];  // 8 bf16 each, as loaded
+    __device__ __forceinline__ static constexpr int row_slot(int r) { return r; }
 
     // The layout is padded to whole tiles and already in quad order: every
     // offset is the same for every tile and step.
@@ -267,6 +282,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int wave_n = wave % T::WAVES_N;
     const int row = lane & 31;
     const int half = lane >> 5;
+    const int a_row = LA::row_slot(row);  // where the A operand's loader put this lane's row
 
     int batch_local, split, tm, tn;
     tile_coordinates(blockIdx.x, gridDim.x, args.tiles_m, args.tiles_n, args.splits, batch_local, split, tm, tn);
@@ -334,7 +350,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const int octet = 2 * c + half;
 #pragma unroll
         for (int i = 0; i < T::FM; ++i)
-            fa[i] = *reinterpret_cast<const bf16x8*>(lds_a[S] + 8 * (octet * OA::PLANE + wave_m * T::WTM + 32 * i + row));
+            fa[i] = *reinterpret_cast<const bf16x8*>(lds_a[S] + 8 * (octet * OA::PLANE + wave_m * T::WTM + 32 * i + a_row));
 #pragma unroll
         for (int j = 0; j < T::FN; ++j)
             fb[j] = *reinterpret_cast<const bf16x8*>(lds_b[S] + 8 * (octet * OB::PLANE + wave_n * T::WTN + 32 * j + row));
@@ -464,6 +480,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int wave_n = wave % T::WAVES_N;
     const int row = lane & 31;
     const int half = lane >> 5;
+    const int a_row = LA::row_slot(row);  // where the A operand's loader put this lane's row
     const int items = args.persistent_items;
     const int stride = int(gridDim.x);
 
@@ -524,7 +541,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const int octet = 2 * c + half;
 #pragma unroll
         for (int i = 0; i < T::FM; ++i)
-            fa[i] = *reinterpret_cast<const bf16x8*>(lds_a[S] + 8 * (octet * OA::PLANE + wave_m * T::WTM + 32 * i + row));
+            fa[i] = *reinterpret_cast<const bf16x8*>(lds_a[S] + 8 * (octet * OA::PLANE + wave_m * T::WTM + 32 * i + a_row));
 #pragma unroll
         for (int j = 0; j < T::FN; ++j)
             fb[j] = *reinterpret_cast<const bf16x8*>(lds_b[S] + 8 * (octet * OB::PLANE + wave_n * T::WTN + 32 * j + row));
