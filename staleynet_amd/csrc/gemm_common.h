@@ -649,10 +649,19 @@ __device__ __forceinline__ void zero_tile(const Args& args, float* c_batch, int6
         const __amdgpu_buffer_rsrc_t rsrc = buffer_of(c_batch + m0 * args.n + n0);
         const int32_t lane_offset = int32_t(((tid / kPerRow) * args.n + 4 * (tid % kPerRow)) * 4);
         typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        // A product whose output streams out writes its zero tiles the same way.
+        if (args.streaming_output) {
 #pragma unroll
-        for (int q = 0; q < T::BM / kRowsPerRound; ++q)
-            __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, rsrc, lane_offset,
-                                                   int32_t(q * kRowsPerRound * args.n * 4), 0);
+            for (int q = 0; q < T::BM / kRowsPerRound; ++q)
+                __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, rsrc,
+                                                       lane_offset + int32_t(q * kRowsPerRound * args.n * 4), 0,
+                                                       kStreaming);
+        } else {
+#pragma unroll
+            for (int q = 0; q < T::BM / kRowsPerRound; ++q)
+                __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, rsrc, lane_offset,
+                                                       int32_t(q * kRowsPerRound * args.n * 4), 0);
+        }
         return;
     }
     for (int e = tid; e < T::BM * T::BN; e += T::THREADS) {
