@@ -660,8 +660,6 @@ struct WideStaging {
 
 size_t round256(size_t bytes) { return (bytes + 255) / 256 * 256; }
 
-
-
 // Stages the operand with fewer elements (the weight, for the Linear
 // products) when it has at most half the other's elements and fits beside
 // the partial sums: rounding it once costs 6 bytes an element, while every
@@ -670,7 +668,19 @@ size_t round256(size_t bytes) { return (bytes + 255) / 256 * 256; }
 // staged): a quarter as the bound 595, any smaller operand 592 (the square
 // weight gradients then pay the staging for no gain).
 constexpr int kStageRatio = 2;
-WideStaging wide_staging(const Problem& p, const Env& env) {
+// ... and only when at least kStageMinReuse tiles of the other operand read
+// the staged copy (tiles across the other output dimension, times the
+// batches that share it). The weight of the forward and input-gradient
+// products (128 tile rows at M = 32768) and x^T of the head's weight
+// gradient (64 tile columns) repay their staging pass; x^T of the qkv and up
+// weight gradients (9 and 12 tile columns: 100 MB of fp32 read, 50 MB
+// written and read back, 33 us a pass) ran 5 % faster rounded as loaded
+// (qkv TN 598-634 -> 647-652 TFLOP/s, up 634-643 -> 663-677), the down
+// projection's dY (12 tile rows) the same either way. With STAGE_SUMS (the
+// fused bias gradient) a right operand is staged whatever its reuse, as
+// that pass also takes its column sums.
+constexpr int64_t kStageMinReuse = 32;
+WideStaging wide_staging(const Problem& p, const Env& env, bool stage_sums = false) {
     WideStaging st;
     st.q = p;
     st.rest = env;
@@ -683,6 +693,10 @@ WideStaging wide_staging(const Problem& p, const Env& env) {
     if (side == kStageNone || env.workspace == nullptr || p.batch > 65535) return st;
     const int64_t rows = side == kStageLeft ? p.m : p.n;
     const int64_t copies = side == kStageLeft ? a_copies : b_copies;
+    const int64_t reuse = (side == kStageLeft ? (p.n + WideTile::BN - 1) / WideTile::BN
+                                              : (p.m + WideTile::BM - 1) / WideTile::BM) *
+                          (copies == 1 ? p.batch : 1);
+    if (reuse < kStageMinReuse && !(stage_sums && side == kStageRight)) return st;
     // The blocked layout (launch_stage_bf16_blocks): whole steps of K, whole
     // tiles of rows; `ld` of the staged operand is its padded row count.
     const int64_t kp = (p.k + WideTile::BK - 1) / WideTile::BK * WideTile::BK;
@@ -884,13 +898,13 @@ size_t column_partial_bytes(const WideStaging& st, const Plan& plan, const Probl
 bool bf16_wide_column_sums_applies(const Problem& p, const Env& env) {
     if (p.batch != 1 || p.m < 1 || p.k < 1 || p.b_k_contiguous || p.bias != nullptr || !bf16_wide_applies(p, env))
         return false;
-    const WideStaging st = wide_staging(p, env);
+    const WideStaging st = wide_staging(p, env, true);
     const Plan plan = wide_column_sums_plan(st, p);
     return product_partial_bytes(plan, p) + column_partial_bytes(st, plan, p) <= st.rest.workspace_bytes;
 }
 
 LaunchShape describe_bf16_wide_column_sums(const Problem& p, const Env& env) {
-    const WideStaging st = wide_staging(p, env);
+    const WideStaging st = wide_staging(p, env, true);
     const Plan plan = wide_column_sums_plan(st, p);
     LaunchShape shape = tiled_shape<WideTile>(st.q, plan, SN_PATH_BF16_WIDE);
     // With dY staged, the staging pass takes the sums and the product runs
@@ -901,7 +915,7 @@ LaunchShape describe_bf16_wide_column_sums(const Problem& p, const Env& env) {
 }
 
 hipError_t launch_gemm_bf16_wide_column_sums(const Problem& p, const Env& env, hipStream_t stream) {
-    const WideStaging st = wide_staging(p, env);
+    const WideStaging st = wide_staging(p, env, true);
     const Problem& q = st.q;
     const Plan plan = wide_column_sums_plan(st, p);
     hipError_t err = hipSuccess;

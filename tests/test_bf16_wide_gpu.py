@@ -161,10 +161,11 @@ def test_wide_split_k_is_exact_on_integers(gpu):
     assert np.array_equal(want, sampled)
 
 
-# "left" and "right": the shared operand is the smaller one and is staged once for the batch.
+# "left" and "right": the shared operand is the smaller one and is staged once for the batch (read by
+# 3 x 12 tile columns or 3 x 11 tile rows, over the 32 tiles staging asks for).
 @pytest.mark.parametrize("shared", ["none", "left", "right"])
 def test_wide_batches_and_shared_operands(gpu, shared):
-    batches, rows, cols, inner = 3, 2560, 3000, 64
+    batches, rows, cols, inner = 3, 2816, 3000, 64
     rng = np.random.default_rng(9)
     left_stride = 0 if shared == "left" else rows * inner
     right_stride = 0 if shared == "right" else inner * cols

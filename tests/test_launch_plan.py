@@ -127,9 +127,9 @@ def test_weight_gradients_take_the_column_sums_into_the_product():
     tight = gemm.plan_column_sums(spec, workspace_bytes=product.workspace_bytes)
     assert tight.path == gemm.PATH_F32_DIRECT_SUMS and tight.splits < product.splits
     assert tight.workspace_bytes <= product.workspace_bytes
-    # bf16 on the 256 x 256 kernel: the sums ride in it where dY reaches it as fp32 (x^T staged or
-    # nothing staged), N floats more per slice; the down projection's dY is the operand staged as bf16,
-    # and the staging pass takes the sums, one partial per 64 k and column.
+    # bf16 on the 256 x 256 kernel: the sums ride in it where dY reaches it as fp32 (x^T staged, for
+    # the head, or nothing staged), N floats more per slice; the down projection's dY is the operand
+    # staged as bf16, and the staging pass takes the sums, one partial per 64 k and column.
     for inputs, outputs in ((768, 2304), (768, 768), (768, 3072), (768, 16384)):
         bf16 = MatmulSpec.new(inputs, outputs, 32768).left_transposed().accumulate().with_precision(Precision.Bf16)
         product, fused = gemm.plan(bf16), gemm.plan_column_sums(bf16)
@@ -137,11 +137,14 @@ def test_weight_gradients_take_the_column_sums_into_the_product():
         assert (fused.splits, fused.tiles_m, fused.tiles_n) == (product.splits, product.tiles_m, product.tiles_n)
         extra = fused.splits * outputs * 4 if fused.splits > 1 else 0
         assert fused.workspace_bytes == product.workspace_bytes + extra
+    # (The plain down product, read by 12 tile rows, rounds dY as it loads it; the fused one stages it
+    # for the sums whatever the reuse.)
     down = MatmulSpec.new(3072, 768, 32768).left_transposed().accumulate().with_precision(Precision.Bf16)
     product, fused = gemm.plan(down), gemm.plan_column_sums(down)
     assert fused.path == gemm.PATH_BF16_WIDE_SUMS
-    assert (fused.splits, fused.tiles_m, fused.tiles_n) == (product.splits, product.tiles_m, product.tiles_n)
-    assert fused.workspace_bytes == product.workspace_bytes + (32768 // 64) * 768 * 4
+    assert product.workspace_bytes == product.splits * 3072 * 768 * 4 * (product.splits > 1)
+    assert fused.workspace_bytes == (768 * 32768 * 2 + fused.splits * 3072 * 768 * 4 * (fused.splits > 1)
+                                     + (32768 // 64) * 768 * 4)
     odd = MatmulSpec.new(96, 50, 300).left_transposed()
     assert gemm.plan_column_sums(odd).path == gemm.PATH_F32_REGISTER
     # The unsupported forms are rejected by the planner as by the call.
@@ -159,18 +162,23 @@ def test_configs_take_the_expected_kernel_families():
     assert forward.splits == 1 and forward.workspace_bytes == 2304 * 768 * 2  # the staged weight
     wgrad = gemm.plan(MatmulSpec.new(768, 2304, 32768).left_transposed().with_precision(Precision.Bf16))
     assert wgrad.path == gemm.PATH_BF16_WIDE and wgrad.splits > 1
+    # x^T is staged only where at least 32 tiles read it: the head's weight gradient (64 tile columns),
+    # not the qkv one's (9), whose workspace holds only the partial sums.
+    assert wgrad.workspace_bytes == wgrad.splits * 768 * 2304 * 4
+    head = gemm.plan(MatmulSpec.new(768, 16384, 32768).left_transposed().with_precision(Precision.Bf16))
+    assert head.workspace_bytes == head.splits * 768 * 16384 * 4 * (head.splits > 1) + 768 * 32768 * 2
     dgrad = gemm.plan(MatmulSpec.new(32768, 768, 2304).right_transposed().with_precision(Precision.Bf16))
     assert dgrad.path == gemm.PATH_BF16_WIDE and dgrad.workspace_bytes == 768 * 2304 * 2
     # The staged operand is blocked by 32-deep steps (each step's tile rows one 16 KB run), so its
     # loads need no offsets across K: with K in the millions the weight gradient still stages x^T
     # (rows padded to 256, K to 32), beside the partial sums.
-    huge = gemm.plan(MatmulSpec.new(256, 640, 5_000_000).left_transposed().with_precision(Precision.Bf16),
+    huge = gemm.plan(MatmulSpec.new(256, 8192, 5_000_000).left_transposed().with_precision(Precision.Bf16),
                      workspace_bytes=1 << 40)
     assert huge.path == gemm.PATH_BF16_WIDE
-    assert huge.workspace_bytes == huge.splits * 256 * 640 * 4 + 256 * 5_000_000 * 2
-    long_k = gemm.plan(MatmulSpec.new(200, 640, 500_001).left_transposed().with_precision(Precision.Bf16),
+    assert huge.workspace_bytes == huge.splits * 256 * 8192 * 4 * (huge.splits > 1) + 256 * 5_000_000 * 2
+    long_k = gemm.plan(MatmulSpec.new(200, 8192, 500_001).left_transposed().with_precision(Precision.Bf16),
                        workspace_bytes=1 << 40)
-    assert long_k.workspace_bytes == long_k.splits * 200 * 640 * 4 + 256 * 500_032 * 2  # x^T staged, padded
+    assert long_k.workspace_bytes == long_k.splits * 200 * 8192 * 4 * (long_k.splits > 1) + 256 * 500_032 * 2
     # Too small for the wide tiles, and fewer 128 x 128 tiles than CUs: no staging pass, 64 x 64 tiles
     # rounding fp32 fragments as they are read.
     tiny = gemm.plan(MatmulSpec.new(96, 2304, 768).with_precision(Precision.Bf16))

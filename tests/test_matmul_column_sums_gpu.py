@@ -159,7 +159,8 @@ def test_weight_gradient_at_config_2_scale(gpu):
 # product exact in any order: it is compared in full with the exact integer product (float64
 # arithmetic), and the sums with the oracle's row-order sums, bit for bit.
 @pytest.mark.parametrize("inputs,outputs,rows", [
-    (768, 2304, 32768),   # the qkv weight gradient: x^T staged as bf16, 9 K slices
+    (768, 2304, 32768),   # the qkv weight gradient: x^T rounded as loaded (9 tile columns read it), 9 K slices
+    (768, 8192, 8192),    # x^T staged as bf16 (32 tile columns read it)
     (768, 768, 32768),    # the out projection's: nothing staged, 28 slices
     (772, 2312, 20010),   # ragged tiles both ways, a K tail
     (3072, 768, 32768),   # the down projection's: dY staged as bf16, the staging pass takes the sums
@@ -184,7 +185,7 @@ def test_bf16_fused_sums_are_exact_on_integers(gpu, inputs, outputs, rows):
     assert np.array_equal(out, want_out)
 
 
-@pytest.mark.parametrize("inputs,outputs", [(768, 2304), (3072, 768)])  # x^T staged; dY staged
+@pytest.mark.parametrize("inputs,outputs", [(768, 2304), (3072, 768)])  # nothing staged; dY staged
 def test_bf16_fused_product_is_sn_matmul_and_sums_within_tolerance(gpu, inputs, outputs):
     rows = 32768
     print(f"bf16 column sums random {inputs}x{outputs}x{rows}", flush=True)
