@@ -194,7 +194,10 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 }
 
 // The same for 16-byte-aligned outputs with M*N a multiple of 4: four
-// consecutive outputs per thread, 16-byte loads, 8 splits in flight.
+// consecutive outputs per thread, 8 splits' 16-byte loads in flight
+// (non-temporal: each partial is read once), and the output read (when
+// accumulating) and written 16 bytes at a time; each element's combine is
+// write_output's, rounded as it rounds.
 __global__ __launch_bounds__(256) void splitk_reduce4_kernel(const f32x4* __restrict__ ws, float* c,
                                                              int64_t per_matrix, int64_t n, int64_t batches,
                                                              int splits, int64_t stride_c, float scale,
@@ -209,10 +212,18 @@ __global__ __launch_bounds__(256) void splitk_reduce4_kernel(const f32x4* __rest
         const f32x4* src = ws + bat * splits * per_matrix4 + e4;
         f32x4 sum = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 8
-        for (int s = 0; s < splits; ++s) sum = sum + src[s * per_matrix4];
-        float* dst = c + bat * stride_c + 4 * e4;
+        for (int s = 0; s < splits; ++s) sum = sum + __builtin_nontemporal_load(src + s * per_matrix4);
+        f32x4* dst = reinterpret_cast<f32x4*>(c + bat * stride_c + 4 * e4);
+        const f32x4 prior = accumulate ? *dst : f32x4{0.f, 0.f, 0.f, 0.f};
+        f32x4 out;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) write_output(dst + j, sum[j], scale, accumulate != 0, bias, (4 * e4 + j) % n);
+        for (int j = 0; j < 4; ++j) {
+            const float scaled = scale * sum[j];
+            float value = accumulate ? prior[j] + scaled : scaled;
+            if (bias != nullptr) value = value + bias[(4 * e4 + j) % n];
+            out[j] = value;
+        }
+        *dst = out;
     }
 }
 
