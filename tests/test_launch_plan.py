@@ -142,6 +142,9 @@ def test_weight_gradients_take_the_column_sums_into_the_product():
     down = MatmulSpec.new(3072, 768, 32768).left_transposed().accumulate().with_precision(Precision.Bf16)
     product, fused = gemm.plan(down), gemm.plan_column_sums(down)
     assert fused.path == gemm.PATH_BF16_WIDE_SUMS
+    # The same slices (the same summation order, so sn_matmul's bits) with dY staged or not.
+    assert (fused.splits, fused.k_per_split, fused.tiles_m, fused.tiles_n) == \
+        (product.splits, product.k_per_split, product.tiles_m, product.tiles_n)
     assert product.workspace_bytes == product.splits * 3072 * 768 * 4 * (product.splits > 1)
     assert fused.workspace_bytes == (768 * 32768 * 2 + fused.splits * 3072 * 768 * 4 * (fused.splits > 1)
                                      + (32768 // 64) * 768 * 4)
