@@ -1069,23 +1069,26 @@ __global__ __launch_bounds__(256) void attention_dq_sum_kernel(DqSumArgs a) {
     const int64_t blocks = (a.keys + kKeyBlock - 1) / kKeyBlock;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     int64_t before = 0;  // rows of the blocks before
-    // Four blocks' loads in flight at a time, added in block order.
-    for (int64_t b = 0; b < blocks; b += 4) {
-        f32x4 x[4];
-        bool ok[4];
+    // Eight blocks' loads in flight at a time (non-temporal: each partial is
+    // read once), added in block order.
+    constexpr int kInFlight = 8;
+    for (int64_t b = 0; b < blocks; b += kInFlight) {
+        f32x4 x[kInFlight];
+        bool ok[kInFlight];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < kInFlight; ++u) {
             const int64_t first = stage_begin(b + u, a.query_offset);
             ok[u] = b + u < blocks && first <= q;
-            x[u] = ok[u] ? *reinterpret_cast<const f32x4*>(base + (before + q - first) * H) : f32x4{0.f, 0.f, 0.f, 0.f};
+            x[u] = ok[u] ? __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(base + (before + q - first) * H))
+                         : f32x4{0.f, 0.f, 0.f, 0.f};
             if (ok[u]) before += a.queries - first;
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int u = 0; u < kInFlight; ++u)
             if (ok[u])
 #pragma unroll
                 for (int s = 0; s < 4; ++s) acc[s] = acc[s] + x[u][s];
-        if (!ok[3]) break;
+        if (!ok[kInFlight - 1]) break;
     }
     f32x4 out;
 #pragma unroll
